@@ -1,0 +1,293 @@
+#!/usr/bin/env python3
+"""Benchmark of the KernRT HIP backend on one MI355X.
+
+Headline (BASELINE.json `configs[1]`): greedy decode of a synthetic
+SmolLM2-360M-shaped Llama with Q8_0x4 weights, KV cache pre-filled to 512
+positions, one decode step = one token. Reported beside it:
+  * the Q8_0 decode GEMV at SmolLM2-1.7B projection shapes, as HBM GB/s
+    against the 8 TB/s peak (the `roofline` object: the dominant kernel);
+  * the 128-token Q8_0 prefill at 1.7B shapes (`configs[2]`), its
+    projection-kernel time and int8 ops rate against the 5.0 POPS peak;
+  * the CPU baseline: the oracle's restatement of the reference cpu backend
+    timed on this host on a bounded sample of the same decode.
+
+Prints one JSON line on stdout; progress goes to stderr.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+import numpy as np  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0
+METRIC = "decode tok/s + Q8_0 GEMV HBM GB/s (% peak); prefill int8 MFMA util, 1 GPU"
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+# SmolLM2-360M shape
+CFG2 = dict(dim=960, hidden_dim=2560, n_layers=32, n_heads=15, n_kv_heads=5, vocab_size=49152, seq_len=1024,
+            rms_eps=1e-5, rope_theta=100_000.0, rope_interleaved=False, head_dim=64)
+# SmolLM2-1.7B shape
+CFG3 = dict(dim=2048, hidden_dim=8192, n_layers=24, n_heads=32, n_kv_heads=32, vocab_size=49152, seq_len=256,
+            rms_eps=1e-5, rope_theta=130_000.0, rope_interleaved=False, head_dim=64)
+PREFILL_POS = 512
+
+
+def synthetic_model(K, cfg: dict, storage: str, seed: int):
+    """Device-generated N(0, 0.02) Q8 weights (tied classifier), unit norms."""
+    hip = K.open("hip")
+    c = K.Config(**cfg)
+    layers, handles = [], []
+    s = seed
+    for l in range(c.n_layers):
+        shapes = {"q": (c.q_dim, c.dim), "k": (c.kv_dim, c.dim), "v": (c.kv_dim, c.dim), "o": (c.dim, c.q_dim),
+                  "gate": (c.hidden_dim, c.dim), "up": (c.hidden_dim, c.dim), "down": (c.dim, c.hidden_dim)}
+        h = {}
+        for name, (n, k) in shapes.items():
+            s += 1
+            h[name] = hip.synthetic_matrix(storage, n, k, s)
+        handles.append(h)
+        layers.append(K.LayerWeights(np.ones(c.dim, np.float32), np.ones(c.dim, np.float32)))
+    emb = hip.synthetic_matrix(storage, c.vocab_size, c.dim, seed + 100_000)
+    hip.bind_handles(emb, 0xFFFFFFFF, handles)
+    model = K.Model(c, hip, None, layers=layers, rms_final=np.ones(c.dim, np.float32))
+    return hip, model, c
+
+
+def bench_decode(K, steps: int, warmup: int):
+    log("decode: building the 360M-shaped Q8_0x4 model on the device")
+    hip, model, c = synthetic_model(K, CFG2, "q8_0x4", seed=2)
+    hip.kv_synthetic(PREFILL_POS, seed=5)
+    token0 = int(np.random.default_rng(2).integers(0, c.vocab_size))
+    hip.synchronize()
+    log(f"decode: warmup {warmup} tokens (captures the step graph)")
+    model.generate_greedy(token0, PREFILL_POS, max(warmup, 1))
+    hip.synchronize()
+    log(f"decode: timing {steps} greedy tokens from position {PREFILL_POS}")
+    t0 = time.perf_counter()
+    toks = model.generate_greedy(token0, PREFILL_POS, steps)
+    hip.synchronize()
+    dt = time.perf_counter() - t0
+    # the per-call forward() path (logits back to the host each token)
+    t1 = time.perf_counter()
+    n_fwd = min(32, steps)
+    for i in range(n_fwd):
+        model.forward(token0, PREFILL_POS + i)
+    fwd_dt = time.perf_counter() - t1
+    weights = sum(n * k for n, k in [(c.q_dim, c.dim), (c.kv_dim, c.dim), (c.kv_dim, c.dim), (c.dim, c.q_dim),
+                                     (c.hidden_dim, c.dim), (c.hidden_dim, c.dim),
+                                     (c.dim, c.hidden_dim)]) * c.n_layers + c.vocab_size * c.dim
+    p_mean = PREFILL_POS + steps / 2
+    kv_bytes = 2 * c.n_layers * (p_mean + 1) * c.kv_dim * 4
+    bytes_tok = weights * (1 + 2 / 32) + kv_bytes  # int8 + f16 scales per 32-block
+    out = dict(tok_s=steps / dt, ms_per_tok=dt * 1e3 / steps, forward_tok_s=n_fwd / fwd_dt,
+               bytes_per_token=bytes_tok, hbm_gbs_per_token_model=bytes_tok * steps / dt / 1e9,
+               first_tokens=[int(t) for t in toks[:8]])
+    model.close()
+    hip.close()
+    return out
+
+
+def bench_gemv(K, reps: int = 3):
+    """Q8_0 GEMV, M = 1, over every 1.7B projection shape, rotating through
+    24 layers of distinct weights (1.6 GB > 256 MB MALL)."""
+    log("gemv: building 24 layers of 1.7B-shaped Q8_0 matrices")
+    hip = K.open("hip")
+    c = K.Config(**CFG3)
+    shapes = [(c.q_dim, c.dim), (c.kv_dim, c.dim), (c.kv_dim, c.dim), (c.dim, c.q_dim), (c.hidden_dim, c.dim),
+              (c.hidden_dim, c.dim), (c.dim, c.hidden_dim)]
+    mats = [[hip.synthetic_matrix("q8_0", n, k, 1000 * l + i) for i, (n, k) in enumerate(shapes)]
+            for l in range(c.n_layers)]
+    rng = np.random.default_rng(3)
+    xs = {k: hip.upload(rng.normal(size=k).astype(np.float32)) for k in {k for _, k in shapes}}
+    ys = {n: hip.alloc(n) for n in {n for n, _ in shapes}}
+
+    def algo_bytes(n, k):
+        nb = k // 32
+        return n * k + n * nb * 4 + k + nb * 4 + n * 4
+
+    per_shape = {}
+    total_bytes, total_ms, total_launches = 0.0, 0.0, 0
+    for i, (n, k) in enumerate(shapes):
+        hip.quantize_rows(xs[k], 1, k)
+        for l in range(c.n_layers):  # warm
+            hip.matmul_quantized(mats[l][i], ys[n], 1)
+        hip.synchronize()
+        hip.timer_start()
+        for _ in range(reps):
+            for l in range(c.n_layers):
+                hip.matmul_quantized(mats[l][i], ys[n], 1)
+        ms = hip.timer_stop()
+        launches = reps * c.n_layers
+        avg_us = ms * 1e3 / launches
+        b = algo_bytes(n, k)
+        per_shape[f"{n}x{k}"] = dict(avg_us=avg_us, gbs=b / (avg_us * 1e-6) / 1e9)
+        total_bytes += b * launches
+        total_ms += ms
+        total_launches += launches
+    gbs = total_bytes / (total_ms * 1e-3) / 1e9
+    # one GEMV at SmolLM2-135M's gate shape, 1536x576
+    m1 = hip.synthetic_matrix("q8_0", 1536, 576, 77)
+    x1 = hip.upload(rng.normal(size=576).astype(np.float32))
+    y1 = hip.alloc(1536)
+    for _ in range(10):
+        hip.matmul(m1, x1, y1, 1)
+    hip.synchronize()
+    hip.timer_start()
+    for _ in range(200):
+        hip.matmul(m1, x1, y1, 1)
+    cfg1_us = hip.timer_stop() * 1e3 / 200
+    hip.close()
+    return dict(achieved_gbs=gbs, avg_launch_us=total_ms * 1e3 / total_launches,
+                bytes_per_launch=total_bytes / total_launches, per_shape=per_shape,
+                cfg1_1536x576_us=cfg1_us, cfg1_bytes=1_003_776)
+
+
+def bench_prefill(K):
+    """128-token Q8_0 prefill at 1.7B projection shapes: time the projection
+    kernels (quantize + int8 GEMM) over all 24 layers."""
+    log("prefill: 128-row Q8_0 projections at 1.7B shapes")
+    hip = K.open("hip")
+    c = K.Config(**CFG3)
+    m_rows = 128
+    shapes = [(c.q_dim, c.dim), (c.kv_dim, c.dim), (c.kv_dim, c.dim), (c.dim, c.q_dim), (c.hidden_dim, c.dim),
+              (c.hidden_dim, c.dim), (c.dim, c.hidden_dim)]
+    mats = [[hip.synthetic_matrix("q8_0", n, k, 5000 * l + i) for i, (n, k) in enumerate(shapes)]
+            for l in range(c.n_layers)]
+    rng = np.random.default_rng(4)
+    xs = {k: hip.upload(rng.normal(size=m_rows * k).astype(np.float32)) for k in {k for _, k in shapes}}
+    ys = {n: hip.alloc(m_rows * n) for n in {n for n, _ in shapes}}
+
+    def run():
+        for l in range(c.n_layers):
+            for i, (n, k) in enumerate(shapes):
+                hip.matmul(mats[l][i], xs[k], ys[n], m_rows)
+
+    run()
+    hip.synchronize()
+    hip.timer_start()
+    run()
+    ms = hip.timer_stop()
+    ops = 2 * m_rows * sum(n * k for n, k in shapes) * c.n_layers
+    tops = ops / (ms * 1e-3) / 1e12
+    hip.close()
+    return dict(rows=m_rows, projection_ms=ms, int8_tops=tops, mfma_util=tops / INT8_PEAK_TOPS, ops=ops)
+
+
+def bench_cpu_baseline(seconds_budget: float = 20.0):
+    """The oracle's cpu backend (the reference's x86 Q8_0x4 path) on 1 core:
+    cfg2 decode steps from a cache pre-filled to 512 positions."""
+    import oracle as O
+    log("cpu baseline: building the 360M-shaped Q8_0x4 model on the host")
+    c = O.Config(**CFG2)
+    rng = np.random.default_rng(9)
+    w = O.Weights(c.n_layers)
+
+    def mat(n, k):
+        return O.Matrix(rng.standard_normal(size=(n, k), dtype=np.float32) * np.float32(0.02), "q8_0x4")
+
+    for l in range(c.n_layers):
+        for name, (n, k) in {"q": (c.q_dim, c.dim), "k": (c.kv_dim, c.dim), "v": (c.kv_dim, c.dim),
+                             "o": (c.dim, c.q_dim), "gate": (c.hidden_dim, c.dim), "up": (c.hidden_dim, c.dim),
+                             "down": (c.dim, c.hidden_dim)}.items():
+            w.set_proj(l, name, mat(n, k))
+        w.set_norm(l, "att", np.ones(c.dim, np.float32))
+        w.set_norm(l, "ffn", np.ones(c.dim, np.float32))
+    w.set_embedding(mat(c.vocab_size, c.dim))
+    w.set_final_norm(np.ones(c.dim, np.float32))
+    w.set_classifier(None)
+    model = O.Model(c, w, "cpu")
+    model.kv_fill(PREFILL_POS, 5)
+    log("cpu baseline: timing decode steps on one core")
+    tok, n, t0 = 1, 0, time.perf_counter()
+    times = []
+    while True:
+        s = time.perf_counter()
+        logits = model.forward(tok, PREFILL_POS + n)
+        times.append(time.perf_counter() - s)
+        tok = O.argmax(logits)
+        n += 1
+        if time.perf_counter() - t0 > seconds_budget or n >= 64:
+            break
+    times.sort()
+    median = times[len(times) // 2]
+    return dict(value=1.0 / median, unit="tok/s", cores=1, kind="port",
+                sample=f"{n} greedy decode steps of the cfg2 360M-shaped Q8_0x4 model at positions "
+                       f"{PREFILL_POS}-{PREFILL_POS + n - 1} (cache pre-filled), oracle cpu backend, 1 thread, "
+                       f"median step {median * 1e3:.1f} ms")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--only", choices=["decode", "gemv", "prefill"], default=None)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (the design note in DESIGN.md "
+              "says how the projections would shard).", file=sys.stderr)
+        sys.exit(2)
+    import kernrt_amd as K
+
+    res = {}
+    if args.only in (None, "decode"):
+        res["decode"] = bench_decode(K, args.steps, args.warmup)
+        log(f"decode: {res['decode']['tok_s']:.1f} tok/s")
+    if args.only in (None, "gemv"):
+        res["gemv"] = bench_gemv(K)
+        log(f"gemv: {res['gemv']['achieved_gbs']:.0f} GB/s")
+    if args.only in (None, "prefill"):
+        res["prefill"] = bench_prefill(K)
+        log(f"prefill: {res['prefill']['int8_tops']:.1f} TOPS")
+    cpu = None if args.skip_cpu or args.only else bench_cpu_baseline()
+
+    d, g, p = res.get("decode"), res.get("gemv"), res.get("prefill")
+    line = {
+        "metric": METRIC,
+        "value": d["tok_s"] if d else None,
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": d["ms_per_tok"] if d else None,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {"workload": "cfg2: SmolLM2-360M-shaped Llama, Q8_0x4 weights N(0,0.02), KV pre-filled to 512, "
+                               f"{args.steps} greedy decode tokens (one step = one token)",
+                   "seq_len": CFG2["seq_len"], "start_pos": PREFILL_POS},
+    }
+    if g:
+        line["roofline"] = {"bound": "hbm", "achieved": round(g["achieved_gbs"], 1), "peak": HBM_PEAK_GBS,
+                            "unit": "GB/s", "frac": round(g["achieved_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                            "kernel": "k_gemv (Q8_0, M=1) over the 7 SmolLM2-1.7B projection shapes x 24 layers",
+                            "avg_launch_us": round(g["avg_launch_us"], 3),
+                            "bytes_per_launch": round(g["bytes_per_launch"])}
+        line["gemv"] = g
+    if p:
+        line["prefill"] = p
+    if d:
+        line["decode"] = d
+    if cpu:
+        line["cpu_baseline"] = cpu
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,179 @@
+/*
+ * kernrt_hip.h — C ABI of libkernrt_hip.so, the MI355X (gfx950) backend for
+ * KernRT's `Backend` trait (reference: src/backends/mod.rs:264-404).
+ *
+ * One `kr_ctx` is one backend instance: one device, one in-order HIP stream,
+ * its activation buffers, its weights and its key/value cache. Calls are
+ * stream-ordered and may return before the device has finished; `kr_read` is
+ * the barrier (mod.rs:262-282). A context is used from one thread at a time
+ * (the trait is `Send`, not `Sync`).
+ *
+ * Every entry returns KR_OK or an error code; `kr_last_error` gives the text.
+ * The reference trait panics on misuse (cpu.rs:134, :366); a binding maps a
+ * non-zero status to that panic. Only `kr_open` distinguishes "no device"
+ * (KR_ERR_NO_DEVICE, detail "no HIP device ...") from other failures, which is
+ * what `BackendError::detail` carries (mod.rs:190-213).
+ *
+ * Plain C types only; host slices (positions, slots, windows) are copied
+ * before the call returns, so the caller may reuse them immediately.
+ */
+#ifndef KERNRT_HIP_H
+#define KERNRT_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct kr_ctx kr_ctx;
+/* A handle to activation memory (mod.rs:40-42 `Buf`). */
+typedef uint32_t kr_buf;
+/* A device-resident weight matrix (one `Matrix`, quant.rs:502-520). */
+typedef uint32_t kr_mat;
+#define KR_NO_MAT ((kr_mat)0xffffffffu)
+
+enum {
+    KR_OK = 0,
+    KR_ERR_NO_DEVICE = 1, /* open: no usable gfx950 device */
+    KR_ERR_INVALID = 2,   /* bad handle, shape or argument */
+    KR_ERR_HIP = 3,       /* a HIP runtime call failed */
+    KR_ERR_OOM = 4,       /* device allocation failed */
+    KR_ERR_STATE = 5      /* call out of order (e.g. compute before prepare) */
+};
+
+/* Projection index, `Proj::index` (mod.rs:100-112). */
+enum {
+    KR_PROJ_Q = 0, KR_PROJ_K = 1, KR_PROJ_V = 2, KR_PROJ_O = 3, KR_PROJ_GATE = 4,
+    KR_PROJ_DOWN = 5, KR_PROJ_UP = 6, KR_PROJ_CONV_IN = 7, KR_PROJ_CONV_OUT = 8
+};
+
+/* Weight storage kinds (`Matrix` variants, quant.rs:502-520). */
+enum { KR_STORAGE_Q8_0 = 2, KR_STORAGE_Q8_0X4 = 3 };
+
+/* `Window` (mod.rs:181-188): own range [att_start, slot], plus the shared
+ * range [shared_start, shared_end) scored first. */
+typedef struct {
+    size_t att_start, slot, shared_start, shared_end;
+} kr_window;
+
+/* `AttnSpec` (mod.rs:158-167). */
+typedef struct {
+    size_t n_heads, kv_mul, head_size, kv_dim, seq_len;
+} kr_attn_spec;
+
+/* `RopeSpec` (mod.rs:149-155). */
+typedef struct {
+    size_t head_size;
+    float theta;
+    int interleaved;
+} kr_rope_spec;
+
+/* ---- lifetime (backends::open, mod.rs:228-244; Backend::name/storage :266-269) */
+int kr_open(int device, kr_ctx** out, char* detail, size_t detail_len);
+void kr_close(kr_ctx* ctx);
+const char* kr_last_error(const kr_ctx* ctx);
+const char* kr_name(const kr_ctx* ctx);    /* "hip" */
+const char* kr_storage(const kr_ctx* ctx); /* the embedding's storage, like cpu.rs:196 */
+int kr_device_name(const kr_ctx* ctx, char* out, size_t len);
+
+/* ---- weights: the material `prepare` receives (mod.rs:271-272, 131-145) */
+/* Matrix::Q8_0 (quant.rs:512-517): row-major int8 quants, one f32 scale per 32-block. */
+int kr_matrix_q8_0(kr_ctx* ctx, size_t out_dim, size_t in_dim, const int8_t* quants,
+                   const float* scales, kr_mat* out);
+/* Matrix::Q8_0x4 (quant.rs:103-118): (out_dim/4)*(in_dim/32) packed 136-byte
+ * blocks {u16 scales[4]; i8 quants[128]}, de-interleaved on upload. */
+int kr_matrix_q8_0x4(kr_ctx* ctx, size_t out_dim, size_t in_dim, const void* blocks, kr_mat* out);
+/* Synthetic weights for benchmarks: N(0, stddev) from a counter-based
+ * generator on the device, quantized with the same arithmetic as
+ * Matrix::from_f32_q8_0 / Q8_0x4::from_f32 (quant.rs:544-557, 124-164). */
+int kr_matrix_synthetic(kr_ctx* ctx, int storage, size_t out_dim, size_t in_dim, uint64_t seed,
+                        float stddev, kr_mat* out);
+int kr_matrix_free(kr_ctx* ctx, kr_mat m);
+
+/* Bind matrices into the model layout, then `prepare` (mod.rs:272). */
+int kr_bind_embedding(kr_ctx* ctx, kr_mat m);
+int kr_bind_classifier(kr_ctx* ctx, kr_mat m); /* KR_NO_MAT: tied to the embedding */
+int kr_bind_proj(kr_ctx* ctx, size_t layer, int proj, kr_mat m);
+int kr_prepare(kr_ctx* ctx, size_t n_layers, size_t kv_dim, size_t seq_len); /* KvSpec mod.rs:170-177 */
+
+/* ---- memory (mod.rs:274-282) */
+int kr_alloc(kr_ctx* ctx, size_t len, kr_buf* out);                   /* Backend::alloc, zeroed */
+int kr_upload(kr_ctx* ctx, const float* data, size_t len, kr_buf* out); /* Backend::upload */
+int kr_read(kr_ctx* ctx, kr_buf src, float* out, size_t len);          /* Backend::read: the barrier */
+
+/* ---- ops (mod.rs:284-403) */
+int kr_embed(kr_ctx* ctx, size_t token, kr_buf out, size_t offset);                     /* :285 */
+int kr_copy(kr_ctx* ctx, kr_buf src, size_t src_offset, kr_buf dst, size_t dst_offset,  /* :288 */
+            size_t len);
+int kr_rms_norm(kr_ctx* ctx, kr_buf out, kr_buf x, kr_buf weight, size_t rows, size_t dim,  /* :291 */
+                float eps);
+int kr_qk_norm(kr_ctx* ctx, kr_buf v, size_t rows, size_t width, size_t head_size,          /* :294-302 */
+               kr_buf weight, float eps);
+int kr_rope(kr_ctx* ctx, kr_buf q, kr_buf k, size_t q_width, size_t kv_width, size_t rows,  /* :306-315 */
+            const size_t* positions, const kr_rope_spec* spec);
+int kr_project(kr_ctx* ctx, size_t layer, int proj, kr_buf x, kr_buf y, size_t rows);     /* :318 */
+int kr_project_qkv(kr_ctx* ctx, size_t layer, kr_buf x, kr_buf q, kr_buf k, kr_buf v,     /* :326-330 */
+                   size_t rows);
+int kr_project_gate_up(kr_ctx* ctx, size_t layer, kr_buf x, kr_buf gate, kr_buf up,       /* :334-337 */
+                       size_t rows);
+int kr_kv_write(kr_ctx* ctx, size_t layer, const size_t* slots, kr_buf k, kr_buf v,       /* :344 */
+                size_t rows);
+int kr_attention(kr_ctx* ctx, kr_buf q, kr_buf out, kr_buf att, size_t layer,             /* :351-359 */
+                 const kr_window* windows, size_t n_windows, const kr_attn_spec* spec);
+int kr_add_in_place(kr_ctx* ctx, kr_buf dst, kr_buf src, size_t len);                    /* :362 */
+int kr_mul(kr_ctx* ctx, kr_buf out, size_t out_off, kr_buf a, size_t a_off, kr_buf b,    /* :370-379 */
+           size_t b_off, size_t len);
+int kr_conv_prefill(kr_ctx* ctx, kr_buf out, kr_buf x, kr_buf kernel, size_t rows,        /* :388 */
+                    size_t dim, size_t k);
+int kr_conv_decode(kr_ctx* ctx, kr_buf out, kr_buf x, kr_buf kernel, kr_buf state,        /* :397 */
+                   size_t dim, size_t k);
+int kr_silu_mul(kr_ctx* ctx, kr_buf gate, kr_buf up, size_t len);                        /* :400 */
+int kr_logits(kr_ctx* ctx, kr_buf x, kr_buf y);                                          /* :403 */
+
+/* ---- the same kernels on an unbound matrix (no model needed) */
+/* Cpu::project arithmetic (cpu.rs:304-371 with the int8 path): rows of x
+ * [rows, in_dim] -> y [rows, out_dim]. */
+int kr_matmul(kr_ctx* ctx, kr_mat w, kr_buf x, kr_buf y, size_t rows);
+/* Cpu::logits arithmetic (cpu.rs:501-514) with `w` as the classifier. */
+int kr_classify(kr_ctx* ctx, kr_mat w, kr_buf x, kr_buf y);
+
+/* The two halves of kr_matmul, as Cpu::project runs them (quantize_rows,
+ * cpu.rs:143-158, then the batched kernel): quantize rows of x into the
+ * context's activation workspace, then run the projection kernel on it. */
+int kr_quantize_rows(kr_ctx* ctx, kr_buf x, size_t rows, size_t width);
+int kr_matmul_quantized(kr_ctx* ctx, kr_mat w, kr_buf y, size_t rows);
+
+/* Stream-ordered timing: events recorded on the context's stream. */
+int kr_timer_start(kr_ctx* ctx);
+int kr_timer_stop(kr_ctx* ctx, float* ms); /* waits for the stop event */
+
+/* ---- parity probes for the bit-exact int8 stages */
+/* Activation quantization of `rows` rows of `width` (cpu.rs:143-158 /
+ * quant.rs:856-874): quants [rows*width], scales [rows*width/32], f16 bits. */
+int kr_dbg_quantize(kr_ctx* ctx, kr_buf x, size_t rows, size_t width, int8_t* quants,
+                    float* scales, uint16_t* scales_f16);
+/* Per-block exact i32 dot products of `w`'s rows with the quantized rows of
+ * x: out [rows][out_dim][in_dim/32], through the same dot code as kr_matmul. */
+int kr_dbg_block_dots(kr_ctx* ctx, kr_mat w, kr_buf x, size_t rows, int32_t* out);
+
+/* ---- key/value cache access, for benchmarks that start from a filled cache */
+/* which: 0 keys, 1 values; element offset into [n_layers, seq_len, kv_dim]. */
+int kr_kv_upload(kr_ctx* ctx, int which, size_t offset, const float* data, size_t len);
+int kr_kv_synthetic(kr_ctx* ctx, size_t slots, uint64_t seed); /* N(0,1) into slots [0,slots) */
+
+/* ---- device-side helpers for on-device greedy decoding */
+/* argmax with the reference's tie rule (generate.rs:70-77) of buf[0..len),
+ * written as an integer into tokens[index] (a device token ring). */
+int kr_argmax(kr_ctx* ctx, kr_buf x, size_t len, size_t index);
+/* Host copy of the device token ring. */
+int kr_read_tokens(kr_ctx* ctx, size_t* out, size_t n);
+
+int kr_synchronize(kr_ctx* ctx);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KERNRT_HIP_H */

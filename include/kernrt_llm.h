@@ -1,0 +1,86 @@
+/*
+ * kernrt_llm.h — the model drivers above the backend seam, in C++ with a C
+ * ABI: the host-side mirror of the reference's `Llama`
+ * (src/arch/llm/llama.rs:169-863) and `Lfm2` (src/arch/llm/lfm2.rs:118-641),
+ * driving a `kr_ctx` through the calls of include/kernrt_hip.h exactly as the
+ * reference drivers drive `dyn Backend`.
+ *
+ * The reference is Rust; with no Rust toolchain in this build's image the
+ * driver is C++, and the Rust `backends/hip.rs` arm that a maintainer would
+ * add over kernrt_hip.h is shown in INTEGRATION.md.
+ */
+#ifndef KERNRT_LLM_H
+#define KERNRT_LLM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "kernrt_hip.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct krl_model krl_model;
+
+/* arch/llm/llama.rs:26-67 `Config`. */
+typedef struct {
+    size_t dim, hidden_dim, n_layers, n_heads, n_kv_heads, vocab_size, seq_len;
+    float rms_eps, rope_theta;
+    int rope_interleaved;
+    size_t head_dim;
+} krl_config;
+
+/* The small f32 tensors of one `LayerWeights` (formats/llama2c.rs:49-76);
+ * the matrices are bound on the backend with kr_bind_proj beforehand. */
+typedef struct {
+    const float* rms_att;     /* [dim] (LFM2: operator_norm) */
+    const float* rms_ffn;     /* [dim] */
+    const float* rms_q;       /* [head_dim] or NULL */
+    const float* rms_k;       /* [head_dim] or NULL */
+    const float* conv_kernel; /* LFM2 conv layers: [dim, conv_k]; else NULL */
+    size_t conv_k;
+    int is_attention;
+} krl_layer;
+
+typedef struct {
+    const krl_layer* layers; /* n_layers entries */
+    const float* rms_final;  /* [dim] */
+} krl_weights;
+
+/* Llama::with_backend (llama.rs:364-415) / Lfm2::with_backend (lfm2.rs:276-366):
+ * calls kr_prepare on `backend` (matrices must be bound), uploads the norms,
+ * allocates the decode state. The model borrows `backend`; close it after
+ * krl_free. */
+int krl_llama_new(kr_ctx* backend, const krl_config* cfg, const krl_weights* w, krl_model** out);
+int krl_lfm2_new(kr_ctx* backend, const krl_config* cfg, const krl_weights* w, krl_model** out);
+void krl_free(krl_model* m);
+const char* krl_last_error(const krl_model* m);
+
+/* forward(token, pos) -> logits (llama.rs:786-862, lfm2.rs:380-477). */
+int krl_forward(krl_model* m, size_t token, size_t pos, float* logits);
+/* prefill(tokens, start) -> logits of the last row (llama.rs:473-492,
+ * lfm2.rs:481-498). Every storage runs batched here (the HIP kernels give
+ * per-row results identical to the decode loop, so the reference's Q8_0
+ * per-token fallback is not needed). */
+int krl_prefill(krl_model* m, const size_t* tokens, size_t n, size_t start, float* logits);
+/* prefill_multi / prefill_shared (llama.rs:552-647): sequences flattened,
+ * `lens[i]` tokens each; one final-normed hidden row [dim] per sequence. */
+int krl_prefill_multi(krl_model* m, const size_t* tokens, const size_t* lens, size_t n_seq, float* hiddens);
+int krl_prefill_shared(krl_model* m, const size_t* prefix, size_t n_prefix, const size_t* tokens,
+                       const size_t* lens, size_t n_seq, float* hiddens);
+
+/* Greedy decoding of `n_steps` tokens after `token` at position `pos`, with
+ * the argmax (generate.rs:70-77 tie rule) on the device. Each step is the
+ * forward pass with its token and position read from device memory; with
+ * `use_graph` the step is captured once as a HIP graph and replayed.
+ * out_tokens[i] is the token chosen at step i (its logits came from position
+ * pos + i). */
+int krl_generate_greedy(krl_model* m, size_t token, size_t pos, size_t n_steps, size_t* out_tokens,
+                        int use_graph);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KERNRT_LLM_H */

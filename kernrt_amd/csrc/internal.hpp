@@ -1,0 +1,39 @@
+// Backend entry points used by the in-library model driver (llm.cpp) but not
+// part of the public C ABI: decode-step variants whose per-token scalars
+// (token id, position) live in device memory, so a whole decode step is a
+// fixed launch sequence that can be captured once in a HIP graph and
+// replayed per token.
+//
+// Device step record (uint32_t[8]):
+//   [0] token  [1] att_start  [2] slot == position  [3] shared_start
+//   [4] shared_end  [5] step index into the token ring  [6..7] unused
+// so &s[1] is a window {att_start, slot, shared_start, shared_end}, &s[2] the
+// position and the KV slot, &s[0] the token.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "../../include/kernrt_hip.h"
+
+namespace kri {
+
+hipStream_t stream(kr_ctx* c);
+int set_error(kr_ctx* c, int code, const char* msg);
+int device_u32(kr_ctx* c, size_t n, uint32_t** out);
+void device_free(void* p);
+uint32_t* token_ring(kr_ctx* c);
+// changes whenever the backend reallocates a buffer that captured kernels may
+// reference; a cached graph from an older epoch must be re-captured
+uint64_t epoch(kr_ctx* c);
+size_t token_ring_len();
+
+int embed_dev(kr_ctx* c, const uint32_t* token_dev, kr_buf out, size_t offset);
+int rope_dev(kr_ctx* c, kr_buf q, kr_buf k, size_t qw, size_t kvw, const uint32_t* pos_dev,
+             const kr_rope_spec* spec);
+int kv_write_dev(kr_ctx* c, size_t layer, const uint32_t* slot_dev, kr_buf k, kr_buf v);
+int attention_dev(kr_ctx* c, kr_buf q, kr_buf out, kr_buf att, size_t layer, const uint32_t* window_dev,
+                  const kr_attn_spec* spec);
+// argmax of logits -> s[0] and ring[s[5]]; then s[2] += 1, s[5] += 1
+int greedy_step(kr_ctx* c, kr_buf logits, size_t len, uint32_t* step);
+
+}  // namespace kri

@@ -1,0 +1,787 @@
+// gfx950 kernels of the KernRT HIP backend.
+//
+// Exactness contract: every kernel reproduces the f32 rounding sequence of
+// the reference KernRT CPU backend on x86 (src/backends/cpu.rs and the ops it
+// calls), so results are bit-identical to it, not merely close. Integer work
+// (quantized dots) is order-free; floating-point reductions keep the
+// reference's order, and only order-free work (per-element products,
+// per-block integer dots, maxima) is spread across lanes. Build with
+// -ffp-contract=off; fma appears only where the reference writes `mul_add`.
+#include <hip/hip_runtime.h>
+
+#include "kernels.hpp"
+#include "numerics.hpp"
+
+namespace kr {
+
+static constexpr int kStorageQ8_0 = 2;
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+// Correctly rounded f32 division and square root, as the reference's x86 SSE
+// arithmetic gives. The IEEE double operation rounded once to f32 is the
+// correctly rounded f32 result (53 >= 2*24 + 2 makes the double rounding
+// innocuous for / and sqrt); the f32 library forms are not exact here.
+__device__ __forceinline__ float div_rn(float a, float b) { return (float)((double)a / (double)b); }
+__device__ __forceinline__ float sqrt_rn(float a) { return (float)__builtin_sqrt((double)a); }
+
+// ---------------------------------------------------------------------------
+// Activation quantization (quant.rs:856-874 per row, cpu.rs:143-158 batched).
+// One 32-lane half-wave per Q8 block: lanes load one element each, the block
+// amax is a 32-lane max reduction (max is order-free), then every lane
+// rounds its own element.
+__global__ __launch_bounds__(256) void k_quantize(const float* __restrict__ x, size_t total_blocks,
+                                                  uint32_t nb, uint32_t k, size_t x_stride,
+                                                  int8_t* __restrict__ q, float* __restrict__ s,
+                                                  uint16_t* __restrict__ h) {
+    size_t gid = (size_t)blockIdx.x * 256 + threadIdx.x;
+    size_t blk = gid >> 5;
+    int lane = threadIdx.x & 31;
+    bool valid = blk < total_blocks;
+    size_t row = valid ? blk / nb : 0, b = valid ? blk % nb : 0;
+    float v = valid ? x[row * x_stride + b * 32 + lane] : 0.0f;
+    float m = fmaxf(0.0f, fabsf(v));  // fold(0.0, max(|v|)), NaN-ignoring
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 32));
+    float d = div_rn(m, 127.0f);
+    float inv = d > 0.0f ? div_rn(1.0f, d) : 0.0f;
+    if (valid) {
+        q[row * k + b * 32 + lane] = q8_round(v * inv);
+        if (lane == 0) {
+            s[blk] = d;
+            h[blk] = f32_to_f16_bits(d);
+        }
+    }
+}
+
+hipError_t launch_quantize(hipStream_t st, const float* x, size_t rows, size_t k, size_t x_stride,
+                           int8_t* q, float* s, uint16_t* h) {
+    size_t nb = k / 32, total = rows * nb;
+    if (total == 0) return hipSuccess;
+    size_t threads = total * 32;
+    dim3 grid((unsigned)((threads + 255) / 256));
+    hipLaunchKernelGGL(k_quantize, grid, dim3(256), 0, st, x, total, (uint32_t)nb, (uint32_t)k, x_stride,
+                       q, s, h);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Quantized GEMV (M <= 4 activation rows).
+//
+// A workgroup owns a tile of R consecutive weight rows, i.e. R*K contiguous
+// bytes of the row-major int8 matrix, streamed with 16-byte loads that are
+// fully coalesced across the wave (one wave load = 1 KiB). A lane pair holds
+// one 32-byte Q8 block: each lane does four v_dot4_i32_i8 on its half and the
+// pair sums with one lane swap, so the per-block i32 is exact. The even lane
+// turns it into the reference's per-block epilogue operand and parks it in
+// LDS; after a barrier one lane per (row, output) walks the blocks in order,
+// reproducing the reference's f32 accumulation sequence exactly.
+template <int SEM, int M>
+__global__ __launch_bounds__(256) void k_gemv(const int8_t* __restrict__ W, const void* __restrict__ WS,
+                                              QuantAct x, float* __restrict__ Y, uint32_t N, uint32_t K,
+                                              uint32_t R, uint32_t ldy, int32_t* __restrict__ dbg) {
+    extern __shared__ __align__(16) char smem[];
+    const uint32_t nb = K >> 5;
+    const uint32_t row0 = blockIdx.x * R;
+    const uint32_t rows = min(R, N - row0);
+    int8_t* xs_l = (int8_t*)smem;                      // [M][K]
+    float* res = (float*)(smem + M * K);               // per (m, block) epilogue operands
+    const uint32_t nblk = rows * nb;                   // blocks in this tile
+
+    for (uint32_t i = threadIdx.x; i < M * K / 16; i += 256) ((int4*)xs_l)[i] = ((const int4*)x.q)[i];
+    __syncthreads();
+
+    const int8_t* wt = W + (size_t)row0 * K;
+    const uint32_t C = nblk * 2;  // 16-byte chunks
+    const bool even = (threadIdx.x & 1) == 0;
+    constexpr int U = 4;
+    const uint32_t iters = (C + 256 * U - 1) / (256 * U);
+    for (uint32_t it = 0; it < iters; it++) {
+        v4i wv[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            uint32_t c = threadIdx.x + 256 * (it * U + u);
+            wv[u] = c < C ? __builtin_nontemporal_load((const v4i*)(wt + 16 * (size_t)c)) : v4i{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            uint32_t c = threadIdx.x + 256 * (it * U + u);
+            bool valid = c < C;
+            uint32_t col = valid ? (16 * c) % K : 0;
+            uint32_t g = c >> 1;           // block index within the tile
+            uint32_t r = valid ? g / nb : 0, b = valid ? g % nb : 0;
+#pragma unroll
+            for (int m = 0; m < M; m++) {
+                v4i xv = *(const v4i*)(xs_l + m * K + col);
+                int acc = 0;
+                acc = __builtin_amdgcn_sdot4(wv[u].x, xv.x, acc, false);
+                acc = __builtin_amdgcn_sdot4(wv[u].y, xv.y, acc, false);
+                acc = __builtin_amdgcn_sdot4(wv[u].z, xv.z, acc, false);
+                acc = __builtin_amdgcn_sdot4(wv[u].w, xv.w, acc, false);
+                int isum = acc + __shfl_xor(acc, 1);
+                if (valid && even) {
+                    size_t wsi = (size_t)(row0 + r) * nb + b;
+                    uint32_t xsi = m * nb + b;
+                    if (dbg) dbg[((size_t)m * N + row0 + r) * nb + b] = isum;
+                    if (SEM == SEM_FMA_CHAIN) {
+                        float xsf = f16w(x.h[xsi]);
+                        float ws = f16w(((const uint16_t*)WS)[wsi]) * xsf;
+                        ((float2*)res)[m * nblk + g] = make_float2((float)isum, ws);
+                    } else {
+                        float sa = SEM == SEM_FOUR_PARTIALS_F32 ? ((const float*)WS)[wsi]
+                                                                : f16w(((const uint16_t*)WS)[wsi]);
+                        float sb = x.s[xsi];
+                        res[m * nblk + g] = (sa * sb) * (float)isum;
+                    }
+                }
+            }
+        }
+    }
+    __syncthreads();
+
+    for (uint32_t t = threadIdx.x; t < M * rows; t += 256) {
+        uint32_t m = t / rows, r = t % rows;
+        float out;
+        if (SEM == SEM_FMA_CHAIN) {
+            const float2* e = (const float2*)res + m * nblk + r * nb;
+            float slot = 0.0f;
+            for (uint32_t b = 0; b < nb; b++) slot = __builtin_fmaf(e[b].x, e[b].y, slot);
+            out = slot;
+        } else {
+            const float* e = res + m * nblk + r * nb;
+            float t0 = 0.0f, t1 = 0.0f, t2 = 0.0f, t3 = 0.0f;
+            uint32_t b = 0;
+            for (; b + 4 <= nb; b += 4) {
+                t0 += e[b];
+                t1 += e[b + 1];
+                t2 += e[b + 2];
+                t3 += e[b + 3];
+            }
+            if (b < nb) t0 += e[b++];
+            if (b < nb) t1 += e[b++];
+            if (b < nb) t2 += e[b++];
+            out = ((t0 + t1) + t2) + t3;
+        }
+        Y[(size_t)m * ldy + row0 + r] = out;
+    }
+}
+
+// LDS budget of one GEMV workgroup: the staged activations (M*K bytes, at
+// most kGemvActBytes) plus the per-block epilogue operands of its tile.
+static constexpr size_t kGemvLds = 64 * 1024;
+static constexpr size_t kGemvActBytes = 32 * 1024;
+
+static size_t gemv_rows_per_tile(size_t n, size_t k) {
+    size_t r = 32768 / k;
+    if (r < 1) r = 1;
+    size_t cap = n / 512;  // keep >= ~2 tiles per CU when the matrix allows
+    if (cap < 1) cap = 1;
+    if (r > cap) r = cap;
+    if (r > 256) r = 256;
+    return r;
+}
+
+template <int SEM, int M>
+static hipError_t gemv_launch(hipStream_t st, const DevMatrix& w, QuantAct x, float* y, size_t ldy,
+                              int32_t* dbg) {
+    size_t nb = w.k / 32;
+    size_t per_row = (SEM == SEM_FMA_CHAIN ? 8 : 4) * M * nb;  // LDS bytes of epilogue operands per row
+    size_t R = gemv_rows_per_tile(w.n, w.k);
+    size_t r_cap = (kGemvLds - M * w.k) / per_row;
+    if (R > r_cap) R = r_cap;
+    size_t tiles = (w.n + R - 1) / R;
+    size_t lds = M * w.k + per_row * R;
+    hipLaunchKernelGGL((k_gemv<SEM, M>), dim3((unsigned)tiles), dim3(256), lds, st, w.q, w.s, x, y,
+                       (uint32_t)w.n, (uint32_t)w.k, (uint32_t)R, (uint32_t)ldy, dbg);
+    return hipGetLastError();
+}
+
+template <int SEM>
+static hipError_t gemv_rows(hipStream_t st, const DevMatrix& w, QuantAct x, size_t rows, float* y, size_t ldy,
+                            int32_t* dbg) {
+    size_t nb = w.k / 32;
+    size_t done = 0;
+    while (done < rows) {
+        size_t m = rows - done;
+        QuantAct xm{x.q + done * w.k, x.s + done * nb, x.h + done * nb};
+        float* ym = y + done * ldy;
+        int32_t* dm = dbg ? dbg + done * w.n * nb : nullptr;
+        hipError_t e;
+        size_t m_cap = kGemvActBytes / w.k;
+        if (m > m_cap) m = m_cap;
+        if (m >= 4) {
+            e = gemv_launch<SEM, 4>(st, w, xm, ym, ldy, dm);
+            m = 4;
+        } else if (m == 3) {
+            e = gemv_launch<SEM, 3>(st, w, xm, ym, ldy, dm);
+        } else if (m == 2) {
+            e = gemv_launch<SEM, 2>(st, w, xm, ym, ldy, dm);
+        } else {
+            e = gemv_launch<SEM, 1>(st, w, xm, ym, ldy, dm);
+        }
+        if (e != hipSuccess) return e;
+        done += m;
+    }
+    return hipSuccess;
+}
+
+hipError_t launch_project(hipStream_t st, int sem, const DevMatrix& w, QuantAct x, size_t rows, float* y,
+                          size_t ldy, int32_t* dbg) {
+    switch (sem) {
+        case SEM_FMA_CHAIN: return gemv_rows<SEM_FMA_CHAIN>(st, w, x, rows, y, ldy, dbg);
+        case SEM_FOUR_PARTIALS_F32: return gemv_rows<SEM_FOUR_PARTIALS_F32>(st, w, x, rows, y, ldy, dbg);
+        case SEM_FOUR_PARTIALS_F16: return gemv_rows<SEM_FOUR_PARTIALS_F16>(st, w, x, rows, y, ldy, dbg);
+    }
+    return hipErrorInvalidValue;
+}
+
+// ---------------------------------------------------------------------------
+// RMSNorm (cpu.rs:633-644): ss is a left-to-right f32 sum of x*x, so squares
+// are formed in parallel and one lane adds them in order.
+__global__ __launch_bounds__(256) void k_rms_norm(float* __restrict__ out, const float* __restrict__ x,
+                                                  const float* __restrict__ w, uint32_t dim, float eps) {
+    extern __shared__ float sq[];
+    __shared__ float s_scale;
+    const float* xr = x + (size_t)blockIdx.x * dim;
+    float* orow = out + (size_t)blockIdx.x * dim;
+    for (uint32_t i = threadIdx.x; i < dim; i += 256) {
+        float v = xr[i];
+        sq[i] = v * v;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float ss = 0.0f;
+        uint32_t i = 0;
+        for (; i + 4 <= dim; i += 4) {
+            float4 p = *(const float4*)(sq + i);
+            ss += p.x;
+            ss += p.y;
+            ss += p.z;
+            ss += p.w;
+        }
+        for (; i < dim; i++) ss += sq[i];
+        ss = div_rn(ss, (float)dim);
+        ss += eps;
+        s_scale = div_rn(1.0f, sqrt_rn(ss));
+    }
+    __syncthreads();
+    float scale = s_scale;
+    for (uint32_t i = threadIdx.x; i < dim; i += 256) orow[i] = w[i] * (scale * xr[i]);
+}
+
+hipError_t launch_rms_norm(hipStream_t st, float* out, const float* x, const float* w, size_t rows,
+                           size_t dim, float eps) {
+    if (rows == 0) return hipSuccess;
+    size_t lds = ((dim + 3) & ~(size_t)3) * sizeof(float);
+    hipLaunchKernelGGL(k_rms_norm, dim3((unsigned)rows), dim3(256), lds, st, out, x, w, (uint32_t)dim, eps);
+    return hipGetLastError();
+}
+
+// Per-head RMSNorm (cpu.rs:647-661): one lane per (row, head), in order.
+__global__ __launch_bounds__(256) void k_qk_norm(float* __restrict__ v, uint32_t rows, uint32_t width,
+                                                 uint32_t head, const float* __restrict__ w, float eps) {
+    uint32_t heads = width / head;
+    uint32_t id = blockIdx.x * 256 + threadIdx.x;
+    if (id >= rows * heads) return;
+    float* hd = v + (size_t)(id / heads) * width + (size_t)(id % heads) * head;
+    float ss = 0.0f;
+    for (uint32_t i = 0; i < head; i++) {
+        float a = hd[i];
+        ss += a * a;
+    }
+    ss = div_rn(ss, (float)head);
+    ss += eps;
+    float scale = div_rn(1.0f, sqrt_rn(ss));
+    for (uint32_t i = 0; i < head; i++) hd[i] = w[i] * (scale * hd[i]);
+}
+
+hipError_t launch_qk_norm(hipStream_t st, float* v, size_t rows, size_t width, size_t head, const float* w,
+                          float eps) {
+    size_t n = rows * (width / head);
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_qk_norm, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, v, (uint32_t)rows,
+                       (uint32_t)width, (uint32_t)head, w, eps);
+    return hipGetLastError();
+}
+
+// RoPE (cpu.rs:664-705). (cos, sin) of every (position, frequency) come from
+// a table the host builds with the same libm calls as the reference, so only
+// the rotation itself runs here: two products and a difference/sum, unfused.
+__global__ __launch_bounds__(256) void k_rope(float* __restrict__ q, float* __restrict__ k, uint32_t qw,
+                                              uint32_t kvw, uint32_t rows, const uint32_t* __restrict__ pos,
+                                              const float2* __restrict__ tab, uint32_t hs, int interleaved) {
+    uint32_t half = hs / 2;
+    uint32_t qpairs = interleaved ? qw / 2 : (qw / hs) * half;
+    uint32_t kpairs = interleaved ? 0 : (kvw / hs) * half;
+    uint32_t per_row = qpairs + kpairs;
+    uint32_t id = blockIdx.x * 256 + threadIdx.x;
+    if (id >= rows * per_row) return;
+    uint32_t row = id / per_row, p = id % per_row;
+    const float2* tr = tab + (size_t)pos[row] * half;
+    if (interleaved) {
+        uint32_t i = 2 * p;
+        float2 cs = tr[(i % hs) / 2];
+        float c = cs.x, s = cs.y;
+        float* qv = q + (size_t)row * qw;
+        float q0 = qv[i], q1 = qv[i + 1];
+        qv[i] = q0 * c - q1 * s;
+        qv[i + 1] = q0 * s + q1 * c;
+        if (i < kvw) {
+            float* kv = k + (size_t)row * kvw;
+            float k0 = kv[i], k1 = kv[i + 1];
+            kv[i] = k0 * c - k1 * s;
+            kv[i + 1] = k0 * s + k1 * c;
+        }
+        return;
+    }
+    float* vec;
+    uint32_t pp;
+    if (p < qpairs) {
+        vec = q + (size_t)row * qw;
+        pp = p;
+    } else {
+        vec = k + (size_t)row * kvw;
+        pp = p - qpairs;
+    }
+    uint32_t head = pp / half, i = pp % half;
+    float2 cs = tr[i];
+    float c = cs.x, s = cs.y;
+    float* hd = vec + (size_t)head * hs;
+    float lo = hd[i], hi = hd[i + half];
+    hd[i] = lo * c - hi * s;
+    hd[i + half] = lo * s + hi * c;
+}
+
+hipError_t launch_rope(hipStream_t st, float* q, float* k, size_t qw, size_t kvw, size_t rows,
+                       const uint32_t* positions, const float2* table, size_t hs, int interleaved) {
+    size_t half = hs / 2;
+    size_t per_row = interleaved ? qw / 2 : (qw / hs) * half + (kvw / hs) * half;
+    size_t n = rows * per_row;
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_rope, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, q, k, (uint32_t)qw,
+                       (uint32_t)kvw, (uint32_t)rows, positions, table, (uint32_t)hs, interleaved);
+    return hipGetLastError();
+}
+
+__global__ __launch_bounds__(256) void k_kv_write(float* __restrict__ kc, float* __restrict__ vc, size_t base,
+                                                  uint32_t kv_dim, const uint32_t* __restrict__ slots,
+                                                  const float* __restrict__ k, const float* __restrict__ v,
+                                                  uint32_t rows) {
+    uint32_t id = blockIdx.x * 256 + threadIdx.x;
+    if (id >= rows * kv_dim) return;
+    uint32_t row = id / kv_dim, e = id % kv_dim;
+    size_t at = base + (size_t)slots[row] * kv_dim + e;
+    kc[at] = k[id];
+    vc[at] = v[id];
+}
+
+hipError_t launch_kv_write(hipStream_t st, float* kc, float* vc, size_t layer, size_t seq_len, size_t kv_dim,
+                           const uint32_t* slots, const float* k, const float* v, size_t rows) {
+    size_t n = rows * kv_dim;
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_kv_write, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, kc, vc,
+                       layer * seq_len * kv_dim, (uint32_t)kv_dim, slots, k, v, (uint32_t)rows);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Attention for one (row, head) per workgroup (cpu.rs:575-630).
+//  1. scores: each lane scores whole cache rows with the reference's
+//     four-chain FMA dot (dot.rs:350-366), times the scale;
+//  2. max (order-free), exp via glibc's expf restated;
+//  3. the softmax sum is left-to-right (one lane), then each score / sum;
+//  4. out[e] = sum_t p_t * v_t[e], one lane per element e, t in order.
+// Scores live in LDS when they fit, otherwise in the caller's `att` rows.
+__device__ __forceinline__ uint32_t win_slot(const DevWindow& w, uint32_t n_shared, uint32_t i) {
+    return i < n_shared ? w.shared_start + i : w.att_start + (i - n_shared);
+}
+
+__global__ __launch_bounds__(256) void k_attention(const float* __restrict__ q, float* __restrict__ out,
+                                                   float* __restrict__ att, const float* __restrict__ kc,
+                                                   const float* __restrict__ vc, size_t loff,
+                                                   const DevWindow* __restrict__ windows, uint32_t n_heads,
+                                                   uint32_t kv_mul, uint32_t hs, uint32_t kv_dim,
+                                                   uint32_t seq_len, float scale, uint32_t lds_scores) {
+    extern __shared__ float sm[];  // [hs] query, then scores if they fit
+    __shared__ float red[8];
+    __shared__ float s_bcast;
+    const uint32_t h = blockIdx.x, row = blockIdx.y;
+    const DevWindow w = windows[row];
+    const uint32_t n_shared = w.shared_end - w.shared_start;
+    const uint32_t count = n_shared + w.slot - w.att_start + 1;
+    const uint32_t width = n_heads * hs;
+    const float* qh = q + (size_t)row * width + (size_t)h * hs;
+    const uint32_t kvo = (h / kv_mul) * hs;
+    float* qs = sm;
+    float* sc = count <= lds_scores ? sm + ((hs + 3) & ~3u)
+                                    : att + (size_t)row * n_heads * seq_len + (size_t)h * seq_len;
+    for (uint32_t e = threadIdx.x; e < hs; e += 256) qs[e] = qh[e];
+    __syncthreads();
+
+    float mx = -INFINITY;
+    for (uint32_t i = threadIdx.x; i < count; i += 256) {
+        const float* kr = kc + loff + (size_t)win_slot(w, n_shared, i) * kv_dim + kvo;
+        float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+        uint32_t e = 0;
+        for (; e + 4 <= hs; e += 4) {
+            float4 kk = *(const float4*)(kr + e);
+            a0 = __builtin_fmaf(qs[e], kk.x, a0);
+            a1 = __builtin_fmaf(qs[e + 1], kk.y, a1);
+            a2 = __builtin_fmaf(qs[e + 2], kk.z, a2);
+            a3 = __builtin_fmaf(qs[e + 3], kk.w, a3);
+        }
+        float d = (a0 + a1) + (a2 + a3);
+        for (; e < hs; e++) d = __builtin_fmaf(qs[e], kr[e], d);
+        float s = d * scale;
+        sc[i] = s;
+        mx = fmaxf(mx, s);
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    for (uint32_t i = threadIdx.x; i < count; i += 256) sc[i] = glibc_expf(sc[i] - mx);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float sum = 0.0f;
+        uint32_t i = 0;
+        for (; i + 4 <= count; i += 4) {
+            sum += sc[i];
+            sum += sc[i + 1];
+            sum += sc[i + 2];
+            sum += sc[i + 3];
+        }
+        for (; i < count; i++) sum += sc[i];
+        s_bcast = sum;
+    }
+    __syncthreads();
+    const float sum = s_bcast;
+    for (uint32_t i = threadIdx.x; i < count; i += 256) sc[i] = div_rn(sc[i], sum);
+    __syncthreads();
+    float* orow = out + (size_t)row * width + (size_t)h * hs;
+    for (uint32_t e = threadIdx.x; e < hs; e += 256) {
+        float acc = 0.0f;
+        const float* vb = vc + loff + kvo + e;
+        for (uint32_t i = 0; i < count; i++) acc += sc[i] * vb[(size_t)win_slot(w, n_shared, i) * kv_dim];
+        orow[e] = acc;
+    }
+    // Leave the probabilities in `att` like the reference does.
+    if (count <= lds_scores) {
+        float* ag = att + (size_t)row * n_heads * seq_len + (size_t)h * seq_len;
+        for (uint32_t i = threadIdx.x; i < count; i += 256) ag[i] = sc[i];
+    }
+}
+
+hipError_t launch_attention(hipStream_t st, const float* q, float* out, float* att, const float* kc,
+                            const float* vc, size_t layer, const DevWindow* windows, size_t n_rows,
+                            size_t max_count, size_t n_heads, size_t kv_mul, size_t hs, size_t kv_dim,
+                            size_t seq_len, float scale) {
+    if (n_rows == 0) return hipSuccess;
+    const size_t lds_cap = 48 * 1024;
+    size_t qbytes = ((hs + 3) & ~(size_t)3) * sizeof(float);
+    size_t lds_scores = max_count * sizeof(float) + qbytes <= lds_cap ? max_count : 0;
+    size_t lds = qbytes + lds_scores * sizeof(float);
+    hipLaunchKernelGGL(k_attention, dim3((unsigned)n_heads, (unsigned)n_rows), dim3(256), lds, st, q, out, att,
+                       kc, vc, layer * seq_len * kv_dim, windows, (uint32_t)n_heads, (uint32_t)kv_mul,
+                       (uint32_t)hs, (uint32_t)kv_dim, (uint32_t)seq_len, scale, (uint32_t)lds_scores);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Elementwise ops.
+__global__ void k_add(float* __restrict__ d, const float* __restrict__ s, size_t n) {
+    size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) d[i] += s[i];
+}
+hipError_t launch_add(hipStream_t st, float* d, const float* s, size_t n) {
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_add, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, d, s, n);
+    return hipGetLastError();
+}
+
+__global__ void k_mul(float* o, const float* a, const float* b, size_t n) {
+    size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) {
+        float x = a[i], y = b[i];
+        o[i] = x * y;
+    }
+}
+// Overlapping output/input ranges at different offsets: the reference reads
+// and writes element by element in order (cpu.rs:424-431), which only a
+// sequential loop reproduces.
+__global__ void k_mul_seq(float* o, const float* a, const float* b, size_t n) {
+    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    for (size_t i = 0; i < n; i++) {
+        float x = a[i], y = b[i];
+        o[i] = x * y;
+    }
+}
+hipError_t launch_mul(hipStream_t st, float* o, const float* a, const float* b, size_t n, int sequential) {
+    if (n == 0) return hipSuccess;
+    if (sequential)
+        hipLaunchKernelGGL(k_mul_seq, dim3(1), dim3(64), 0, st, o, a, b, n);
+    else
+        hipLaunchKernelGGL(k_mul, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, o, a, b, n);
+    return hipGetLastError();
+}
+
+__global__ void k_copy(float* __restrict__ d, const float* __restrict__ s, size_t n) {
+    size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) d[i] = s[i];
+}
+hipError_t launch_copy(hipStream_t st, float* d, const float* s, size_t n) {
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_copy, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, d, s, n);
+    return hipGetLastError();
+}
+
+// silu (cpu.rs:708-710): x / (1 + exp(-x)), then * up.
+__global__ void k_silu_mul(float* __restrict__ g, const float* __restrict__ u, size_t n) {
+    size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) {
+        float x = g[i];
+        float s = div_rn(x, 1.0f + glibc_expf(-x));
+        g[i] = s * u[i];
+    }
+}
+hipError_t launch_silu_mul(hipStream_t st, float* g, const float* u, size_t n) {
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_silu_mul, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, g, u, n);
+    return hipGetLastError();
+}
+
+// Causal depthwise conv (cpu.rs:557-571).
+__global__ void k_conv_prefill(float* __restrict__ out, const float* __restrict__ x,
+                               const float* __restrict__ kern, uint32_t rows, uint32_t dim, uint32_t k) {
+    size_t id = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (id >= (size_t)rows * dim) return;
+    uint32_t r = id / dim, i = id % dim;
+    float acc = 0.0f;
+    for (uint32_t j = 0; j < k; j++) {
+        long h = (long)r - ((long)k - 1) + (long)j;
+        if (h >= 0) acc += kern[(size_t)i * k + j] * x[(size_t)h * dim + i];
+    }
+    out[id] = acc;
+}
+hipError_t launch_conv_prefill(hipStream_t st, float* out, const float* x, const float* kern, size_t rows,
+                               size_t dim, size_t k) {
+    size_t n = rows * dim;
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_conv_prefill, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, out, x, kern,
+                       (uint32_t)rows, (uint32_t)dim, (uint32_t)k);
+    return hipGetLastError();
+}
+
+// Single-row conv through the ring (cpu.rs:469-492): the output is the last
+// row of the conv over [state; x], then the ring shifts by one row. All reads
+// of element i happen before its writes, so `out` may alias `x`.
+__global__ void k_conv_decode(float* out, const float* x, const float* __restrict__ kern, float* state,
+                              uint32_t dim, uint32_t k) {
+    uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= dim) return;
+    uint32_t hist = k - 1;
+    float xi = x[i];
+    float acc = 0.0f;
+    for (uint32_t j = 0; j < k; j++) {
+        float hv = j < hist ? state[(size_t)j * dim + i] : xi;
+        acc += kern[(size_t)i * k + j] * hv;
+    }
+    if (hist > 0) {
+        for (uint32_t j = 0; j + 1 < hist; j++) state[(size_t)j * dim + i] = state[(size_t)(j + 1) * dim + i];
+        state[(size_t)(hist - 1) * dim + i] = xi;
+    }
+    out[i] = acc;
+}
+hipError_t launch_conv_decode(hipStream_t st, float* out, const float* x, const float* kern, float* state,
+                              size_t dim, size_t k) {
+    if (dim == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_conv_decode, dim3((unsigned)((dim + 255) / 256)), dim3(256), 0, st, out, x, kern, state,
+                       (uint32_t)dim, (uint32_t)k);
+    return hipGetLastError();
+}
+
+// Embedding row (Matrix::decode_row, quant.rs:670-691): q * scale, exact.
+__global__ void k_embed(const int8_t* __restrict__ q, const void* __restrict__ s, int f16, uint32_t k,
+                        size_t token, const uint32_t* __restrict__ token_dev, float* __restrict__ out) {
+    uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= k) return;
+    size_t t = token_dev ? (size_t)token_dev[0] : token;
+    size_t si = t * (k / 32) + i / 32;
+    float scale = f16 ? f16w(((const uint16_t*)s)[si]) : ((const float*)s)[si];
+    out[i] = (float)q[t * k + i] * scale;
+}
+hipError_t launch_embed(hipStream_t st, const DevMatrix& e, size_t token, const uint32_t* token_dev, float* out) {
+    hipLaunchKernelGGL(k_embed, dim3((unsigned)((e.k + 255) / 256)), dim3(256), 0, st, e.q, e.s,
+                       e.storage == kStorageQ8_0 ? 0 : 1, (uint32_t)e.k, token, token_dev, out);
+    return hipGetLastError();
+}
+
+// argmax with Iterator::max_by(total_cmp) semantics: the largest total-order
+// key wins and, among equal keys, the largest index (generate.rs:70-77).
+__global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ x, uint32_t n, uint32_t* out) {
+    __shared__ int32_t skey[16];
+    __shared__ uint32_t sidx[16];
+    int32_t best = INT32_MIN;
+    uint32_t bi = 0;
+    bool any = false;
+    for (uint32_t i = threadIdx.x; i < n; i += 1024) {
+        int32_t k = total_order_key(x[i]);
+        if (!any || k >= best) {
+            best = k;
+            bi = i;
+            any = true;
+        }
+    }
+    if (!any) {
+        best = INT32_MIN;
+        bi = 0;
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        int32_t ok = __shfl_xor(best, off);
+        uint32_t oi = __shfl_xor(bi, off);
+        if (ok > best || (ok == best && oi > bi)) {
+            best = ok;
+            bi = oi;
+        }
+    }
+    if ((threadIdx.x & 63) == 0) {
+        skey[threadIdx.x >> 6] = best;
+        sidx[threadIdx.x >> 6] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int32_t b = skey[0];
+        uint32_t idx = sidx[0];
+        for (int w = 1; w < 16; w++)
+            if (skey[w] > b || (skey[w] == b && sidx[w] > idx)) {
+                b = skey[w];
+                idx = sidx[w];
+            }
+        out[0] = idx;
+    }
+}
+hipError_t launch_argmax(hipStream_t st, const float* x, size_t n, uint32_t* out) {
+    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, st, x, (uint32_t)n, out);
+    return hipGetLastError();
+}
+
+// Greedy decode bookkeeping after the argmax: the chosen token feeds the next
+// step's embedding and is recorded in the ring; position and ring index
+// advance. Runs as one lane after k_argmax has written step[0].
+__global__ void k_step_advance(uint32_t* step, uint32_t* ring, uint32_t ring_len) {
+    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    uint32_t i = step[5];
+    if (i < ring_len) ring[i] = step[0];
+    step[5] = i + 1;
+    step[2] = step[2] + 1;
+}
+hipError_t launch_greedy_step(hipStream_t st, const float* logits, size_t n, uint32_t* step, uint32_t* ring,
+                              size_t ring_len) {
+    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, st, logits, (uint32_t)n, step);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_step_advance, dim3(1), dim3(64), 0, st, step, ring, (uint32_t)ring_len);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Synthetic data for benchmarks: splitmix64 per element, Box-Muller.
+__device__ __forceinline__ uint64_t splitmix64(uint64_t z) {
+    z += 0x9e3779b97f4a7c15ull;
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+}
+__device__ __forceinline__ float normal_at(uint64_t seed, uint64_t i) {
+    uint64_t z = splitmix64(seed ^ splitmix64(i));
+    float u1 = ((float)(z >> 40) + 0.5f) * (1.0f / 16777216.0f);
+    float u2 = (float)((z >> 16) & 0xffffffu) * (1.0f / 16777216.0f);
+    return sqrtf(-2.0f * logf(u1)) * cosf(6.283185307179586f * u2);
+}
+
+// One thread per 32-block: draw, then quantize exactly as Q8Vec::quantize /
+// Q8_0x4::from_f32 do (f32 scale for Q8_0, f16 bits for Q8_0x4, quants from
+// the f32 reciprocal in both).
+__global__ void k_synth_q8(int8_t* __restrict__ q, void* __restrict__ s, int f16, size_t blocks, uint64_t seed,
+                           float stddev) {
+    size_t b = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (b >= blocks) return;
+    float v[32];
+    float amax = 0.0f;
+    for (int i = 0; i < 32; i++) {
+        v[i] = normal_at(seed, b * 32 + i) * stddev;
+        amax = fmaxf(amax, fabsf(v[i]));
+    }
+    float d = div_rn(amax, 127.0f);
+    float inv = d > 0.0f ? div_rn(1.0f, d) : 0.0f;
+    for (int i = 0; i < 32; i++) q[b * 32 + i] = q8_round(v[i] * inv);
+    if (f16)
+        ((uint16_t*)s)[b] = f32_to_f16_bits(d);
+    else
+        ((float*)s)[b] = d;
+}
+hipError_t launch_synthetic_q8(hipStream_t st, const DevMatrix& m, uint64_t seed, float stddev) {
+    size_t blocks = m.n * m.k / 32;
+    hipLaunchKernelGGL(k_synth_q8, dim3((unsigned)((blocks + 255) / 256)), dim3(256), 0, st, m.q, m.s,
+                       m.storage == kStorageQ8_0 ? 0 : 1, blocks, seed, stddev);
+    return hipGetLastError();
+}
+
+__global__ void k_synth_normal(float* __restrict__ out, size_t n, uint64_t seed) {
+    size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) out[i] = normal_at(seed, i);
+}
+hipError_t launch_synthetic_normal(hipStream_t st, float* out, size_t n, uint64_t seed) {
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_synth_normal, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, out, n, seed);
+    return hipGetLastError();
+}
+
+// x86 logits over a Q8_0x4 classifier re-quantize each decoded row
+// (quant.rs:232-235). With every block's max |q| in {0, 127} that gives back
+// the stored quants and the widened f16 scale; count the blocks where not.
+__global__ void k_requant_check(const int8_t* __restrict__ q, size_t blocks, unsigned int* counter) {
+    size_t b = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (b >= blocks) return;
+    int m = 0;
+    for (int i = 0; i < 32; i++) {
+        int a = q[b * 32 + i];
+        a = a < 0 ? -a : a;
+        m = a > m ? a : m;
+    }
+    if (m != 0 && m != 127) atomicAdd(counter, 1u);
+}
+hipError_t launch_requant_check(hipStream_t st, const DevMatrix& m, unsigned int* counter) {
+    size_t blocks = m.n * m.k / 32;
+    hipLaunchKernelGGL(k_requant_check, dim3((unsigned)((blocks + 255) / 256)), dim3(256), 0, st, m.q, blocks,
+                       counter);
+    return hipGetLastError();
+}
+
+// The literal re-quantization, for classifiers where the identity fails.
+__global__ void k_requantize(const int8_t* __restrict__ q, const uint16_t* __restrict__ s, int8_t* __restrict__ q2,
+                             float* __restrict__ s2, size_t blocks) {
+    size_t b = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (b >= blocks) return;
+    float sc = f16w(s[b]);
+    float v[32];
+    float amax = 0.0f;
+    for (int i = 0; i < 32; i++) {
+        v[i] = (float)q[b * 32 + i] * sc;
+        amax = fmaxf(amax, fabsf(v[i]));
+    }
+    float d = div_rn(amax, 127.0f);
+    float inv = d > 0.0f ? div_rn(1.0f, d) : 0.0f;
+    for (int i = 0; i < 32; i++) q2[b * 32 + i] = q8_round(v[i] * inv);
+    s2[b] = d;
+}
+hipError_t launch_requantize(hipStream_t st, const DevMatrix& src, const DevMatrix& dst) {
+    size_t blocks = src.n * src.k / 32;
+    hipLaunchKernelGGL(k_requantize, dim3((unsigned)((blocks + 255) / 256)), dim3(256), 0, st, src.q,
+                       (const uint16_t*)src.s, dst.q, (float*)dst.s, blocks);
+    return hipGetLastError();
+}
+
+}  // namespace kr

@@ -1,0 +1,80 @@
+// Launchers for the gfx950 kernels of the KernRT HIP backend. Every launcher
+// enqueues on the given stream and returns the hipError_t of the launch; the
+// host side (backend.cpp) validates shapes before calling any of them.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace kr {
+
+// Output-order semantics of a quantized projection (the reference's f32
+// epilogue per 32-block; the per-block integer dots are the same for all):
+enum Sem {
+    // Q8_0x4 project (quant.rs:276-288): slot = fma(f32(isum), f16w(ws)*f16w(xs), slot)
+    SEM_FMA_CHAIN = 0,
+    // Q8_0 dot (dot.rs:34-45): t[b&3] += (ws*xs)*f32(isum), f32 scales
+    SEM_FOUR_PARTIALS_F32 = 1,
+    // Q8_0x4 logits on x86 (quant.rs:223-236): as above with f16w(ws)
+    SEM_FOUR_PARTIALS_F16 = 2,
+};
+
+struct QuantAct {  // one quantized activation batch, row-major
+    const int8_t* q;     // [rows][K]
+    const float* s;      // [rows][K/32] f32 scales (Q8Vec::scales)
+    const uint16_t* h;   // [rows][K/32] f16 bits  (Q8Vec::scales_f16)
+};
+
+struct DevMatrix {  // device layout of one Q8 matrix
+    int storage;         // KR_STORAGE_Q8_0 or KR_STORAGE_Q8_0X4
+    size_t n, k;         // out_dim, in_dim
+    int8_t* q;           // [n][k] row-major quants
+    void* s;             // [n][k/32]: float (Q8_0) or uint16_t f16 bits (Q8_0x4)
+};
+
+hipError_t launch_quantize(hipStream_t st, const float* x, size_t rows, size_t k, size_t x_stride,
+                           int8_t* q, float* s, uint16_t* h);
+
+// y[m*ldy + n] for m < rows. Uses the GEMV path (rows <= 4) or the MFMA GEMM.
+hipError_t launch_project(hipStream_t st, int sem, const DevMatrix& w, QuantAct x, size_t rows,
+                          float* y, size_t ldy, int32_t* dbg_block_dots);
+
+hipError_t launch_rms_norm(hipStream_t st, float* out, const float* x, const float* w, size_t rows,
+                           size_t dim, float eps);
+hipError_t launch_qk_norm(hipStream_t st, float* v, size_t rows, size_t width, size_t head,
+                          const float* w, float eps);
+// table: [n_pos][head_size/2] of (cos, sin)
+hipError_t launch_rope(hipStream_t st, float* q, float* k, size_t qw, size_t kvw, size_t rows,
+                       const uint32_t* positions, const float2* table, size_t head_size, int interleaved);
+hipError_t launch_kv_write(hipStream_t st, float* kc, float* vc, size_t layer, size_t seq_len,
+                           size_t kv_dim, const uint32_t* slots, const float* k, const float* v,
+                           size_t rows);
+struct DevWindow { uint32_t att_start, slot, shared_start, shared_end; };
+hipError_t launch_attention(hipStream_t st, const float* q, float* out, float* att, const float* kc,
+                            const float* vc, size_t layer, const DevWindow* windows, size_t n_rows,
+                            size_t max_count, size_t n_heads, size_t kv_mul, size_t head_size,
+                            size_t kv_dim, size_t seq_len, float scale);
+hipError_t launch_add(hipStream_t st, float* dst, const float* src, size_t n);
+hipError_t launch_mul(hipStream_t st, float* out, const float* a, const float* b, size_t n,
+                      int sequential);
+hipError_t launch_copy(hipStream_t st, float* dst, const float* src, size_t n);
+hipError_t launch_silu_mul(hipStream_t st, float* g, const float* u, size_t n);
+hipError_t launch_conv_prefill(hipStream_t st, float* out, const float* x, const float* kernel,
+                               size_t rows, size_t dim, size_t k);
+hipError_t launch_conv_decode(hipStream_t st, float* out, const float* x, const float* kernel,
+                              float* state, size_t dim, size_t k);
+// token from `token_dev` when non-null, else `token`
+hipError_t launch_embed(hipStream_t st, const DevMatrix& e, size_t token, const uint32_t* token_dev,
+                        float* out);
+hipError_t launch_argmax(hipStream_t st, const float* x, size_t n, uint32_t* out);
+hipError_t launch_greedy_step(hipStream_t st, const float* logits, size_t n, uint32_t* step, uint32_t* ring,
+                              size_t ring_len);
+hipError_t launch_synthetic_q8(hipStream_t st, const DevMatrix& m, uint64_t seed, float stddev);
+hipError_t launch_synthetic_normal(hipStream_t st, float* out, size_t n, uint64_t seed);
+// counts Q8_0x4 blocks whose max |q| is neither 0 nor 127
+hipError_t launch_requant_check(hipStream_t st, const DevMatrix& m, unsigned int* counter);
+// x86 `gemv_q8_0x4` re-quantization of every row into a Q8_0 matrix (quant.rs:232-235)
+hipError_t launch_requantize(hipStream_t st, const DevMatrix& src, const DevMatrix& dst);
+
+}  // namespace kr

@@ -29,10 +29,15 @@ PROJ = {"q": 0, "k": 1, "v": 2, "o": 3, "gate": 4, "down": 5, "up": 6, "conv_in"
 _lib = None
 
 
+SOURCES = ("oracle.cpp", "capi.cpp", "oracle.hpp", "Makefile")
+
+
 def build(force: bool = False) -> str:
     """Compile the oracle with its Makefile (g++, -O2 -ffp-contract=off)."""
-    if force or not os.path.exists(LIB_PATH):
-        subprocess.run(["make", "-s", "-C", HERE], check=True)
+    stale = not os.path.exists(LIB_PATH) or any(
+        os.path.getmtime(os.path.join(HERE, s)) > os.path.getmtime(LIB_PATH) for s in SOURCES)
+    if force or stale:
+        subprocess.run(["make", "-s", "-B" if force else "-s", "-C", HERE], check=True)
     return LIB_PATH
 
 
@@ -74,6 +79,8 @@ def lib():
         L.or_softmax.argtypes = [vp, sz]
         L.or_matrix_from_f32.argtypes = [vp, sz, sz, C.c_int, C.POINTER(vp)]
         L.or_matrix_free.argtypes = [vp]
+        L.or_matrix_from_q8_0.argtypes = [vp, vp, sz, sz, C.POINTER(vp)]
+        L.or_matrix_from_q8_0x4_blocks.argtypes = [vp, sz, sz, C.POINTER(vp)]
         L.or_matrix_info.argtypes = [vp, C.POINTER(C.c_int), C.POINTER(sz), C.POINTER(sz)]
         L.or_matrix_decode_row.argtypes = [vp, sz, vp]
         L.or_matrix_q8_0_data.argtypes = [vp, vp, vp]
@@ -95,6 +102,7 @@ def lib():
         L.or_llama_new.argtypes = [C.POINTER(OracleConfig), vp, C.c_char_p, C.POINTER(vp)]
         L.or_lfm2_new.argtypes = [C.POINTER(OracleConfig), vp, vp, C.c_char_p, C.POINTER(vp)]
         L.or_model_free.argtypes = [vp]
+        L.or_model_kv_fill.argtypes = [vp, sz, C.c_uint64]
         L.or_model_forward.argtypes = [vp, sz, sz, vp, sz]
         L.or_model_prefill.argtypes = [vp, vp, sz, sz, vp, sz]
         L.or_llama_prefill_multi.argtypes = [vp, vp, vp, sz, vp, sz]
@@ -203,6 +211,25 @@ class Matrix:
         self.h = h
         self.out_dim, self.in_dim = data.shape
         self.storage = storage
+
+    @staticmethod
+    def from_q8_0(quants, scales, out_dim, in_dim) -> "Matrix":
+        m = Matrix.__new__(Matrix)
+        q = np.ascontiguousarray(quants, np.int8)
+        s = np.ascontiguousarray(scales, np.float32)
+        h = C.c_void_p()
+        _check(lib().or_matrix_from_q8_0(_ptr(q), _ptr(s), out_dim, in_dim, C.byref(h)))
+        m.h, m.out_dim, m.in_dim, m.storage = h, out_dim, in_dim, "q8_0"
+        return m
+
+    @staticmethod
+    def from_q8_0x4_blocks(blocks, out_dim, in_dim) -> "Matrix":
+        m = Matrix.__new__(Matrix)
+        b = np.ascontiguousarray(blocks, np.uint8)
+        h = C.c_void_p()
+        _check(lib().or_matrix_from_q8_0x4_blocks(_ptr(b), out_dim, in_dim, C.byref(h)))
+        m.h, m.out_dim, m.in_dim, m.storage = h, out_dim, in_dim, "q8_0x4"
+        return m
 
     @staticmethod
     def try_new(data, storage):
@@ -444,6 +471,10 @@ class Model:
         if getattr(self, "h", None) is not None and _lib is not None:
             _lib.or_model_free(self.h)
             self.h = None
+
+    def kv_fill(self, slots: int, seed: int):
+        """Benchmark set-up: N(0,1) into cache slots [0, slots) of every layer."""
+        _check(lib().or_model_kv_fill(self.h, slots, seed))
 
     def forward(self, token: int, pos: int) -> np.ndarray:
         out = np.empty(self.config.vocab_size, np.float32)

@@ -102,6 +102,35 @@ int or_matrix_from_f32(const float* data, size_t out, size_t in, int kind, void*
     });
 }
 
+// Matrices straight from quantized bytes (the `Matrix::Q8_0` fields, or
+// Q8Block4 records), for tests that need blocks no f32 input produces.
+int or_matrix_from_q8_0(const int8_t* quants, const float* scales, size_t out, size_t in, void** handle) {
+    return guard([&] {
+        if (in % Q8_0_BLOCK != 0) throw std::runtime_error("in_dim must be a multiple of 32");
+        Matrix* m = new Matrix();
+        m->kind = Matrix::Q8_0;
+        m->out_dim = out;
+        m->in_dim = in;
+        m->quants.assign(quants, quants + out * in);
+        m->scales.assign(scales, scales + out * in / Q8_0_BLOCK);
+        *handle = m;
+    });
+}
+
+int or_matrix_from_q8_0x4_blocks(const void* blocks, size_t out, size_t in, void** handle) {
+    return guard([&] {
+        if (in % Q8_0_BLOCK != 0 || out % 4 != 0) throw std::runtime_error("bad Q8_0x4 shape");
+        Matrix* m = new Matrix();
+        m->kind = Matrix::Q8_0X4;
+        m->out_dim = out;
+        m->in_dim = in;
+        size_t n = (out / 4) * (in / Q8_0_BLOCK);
+        m->blocks.resize(n);
+        std::memcpy(m->blocks.data(), blocks, n * sizeof(Q8Block4));
+        *handle = m;
+    });
+}
+
 void or_matrix_free(void* h) { delete (Matrix*)h; }
 
 void or_matrix_info(void* h, int* kind, size_t* out, size_t* in) {
@@ -290,6 +319,13 @@ int or_lfm2_new(const or_config* c, const int* is_attention, void* w, const char
 }
 
 void or_model_free(void* m) { delete (OModel*)m; }
+
+int or_model_kv_fill(void* mp, size_t slots, uint64_t seed) {
+    return guard([&] {
+        OModel* m = (OModel*)mp;
+        fill_kv(m->llama ? m->llama->backend() : m->lfm2->backend(), slots, seed);
+    });
+}
 
 int or_model_forward(void* mp, size_t token, size_t pos, float* logits, size_t n) {
     return guard([&] {

@@ -4,6 +4,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <random>
 #include <cstring>
 #include <stdexcept>
 
@@ -631,6 +632,16 @@ public:
             std::memcpy(s + (hist_len - 1) * dim, xv.data(), dim * sizeof(float));
         }
     }
+    void fill_kv(size_t slots, uint64_t seed) {
+        std::mt19937_64 rng(seed);
+        std::normal_distribution<float> nd(0.0f, 1.0f);
+        for (size_t l = 0; l < kv_.n_layers; l++)
+            for (size_t i = 0; i < slots * kv_.kv_dim; i++) {
+                size_t at = l * kv_.seq_len * kv_.kv_dim + i;
+                kc_[at] = nd(rng);
+                vc_[at] = nd(rng);
+            }
+    }
     void silu_mul(Buf gate, Buf up, size_t len) override {
         float* g = bufs_.at(gate).data();
         const float* u = bufs_.at(up).data();
@@ -814,6 +825,7 @@ public:
 };
 
 std::unique_ptr<Backend> make_cpu() { return std::unique_ptr<Backend>(new Cpu()); }
+void fill_kv(Backend& b, size_t slots, uint64_t seed) { dynamic_cast<HostBackend&>(b).fill_kv(slots, seed); }
 std::unique_ptr<Backend> make_reference() { return std::unique_ptr<Backend>(new Reference()); }
 
 // ---------------------------------------------------------------------------

@@ -180,6 +180,9 @@ struct Backend {
 std::unique_ptr<Backend> make_cpu();
 // reference.rs:44-415
 std::unique_ptr<Backend> make_reference();
+// Benchmark set-up only: fill cache slots [0, slots) of every layer with
+// N(0, 1) draws (the cpu baseline starts decoding from a pre-filled cache).
+void fill_kv(Backend& b, size_t slots, uint64_t seed);
 
 // arch/llm/llama.rs:26-67
 struct Config {
@@ -230,6 +233,7 @@ public:
     const std::vector<float>& forward(size_t token, size_t pos);                    // :380-477
     const std::vector<float>& prefill(const size_t* tokens, size_t n, size_t start);  // :481-498
     const char* storage() const { return backend_->storage(); }
+    Backend& backend() { return *backend_; }
 
 private:
     struct PrefillBuffers { size_t n_tok; Buf x, xb, q, k, v, attn, o, bcx, h, co, cy, gate, up, att; };

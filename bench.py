@@ -66,18 +66,18 @@ def synthetic_model(K, cfg: dict, storage: str, seed: int):
     return hip, model, c
 
 
-def bench_decode(K, steps: int, warmup: int):
+def bench_decode(K, steps: int, warmup: int, use_graph: bool = True):
     log("decode: building the 360M-shaped Q8_0x4 model on the device")
     hip, model, c = synthetic_model(K, CFG2, "q8_0x4", seed=2)
     hip.kv_synthetic(PREFILL_POS, seed=5)
     token0 = int(np.random.default_rng(2).integers(0, c.vocab_size))
     hip.synchronize()
     log(f"decode: warmup {warmup} tokens (captures the step graph)")
-    model.generate_greedy(token0, PREFILL_POS, max(warmup, 1))
+    model.generate_greedy(token0, PREFILL_POS, max(warmup, 1), use_graph=use_graph)
     hip.synchronize()
     log(f"decode: timing {steps} greedy tokens from position {PREFILL_POS}")
     t0 = time.perf_counter()
-    toks = model.generate_greedy(token0, PREFILL_POS, steps)
+    toks = model.generate_greedy(token0, PREFILL_POS, steps, use_graph=use_graph)
     hip.synchronize()
     dt = time.perf_counter() - t0
     # the per-call forward() path (logits back to the host each token)
@@ -236,6 +236,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--only", choices=["decode", "gemv", "prefill"], default=None)
+    ap.add_argument("--no-graph", action="store_true",
+                    help="launch each decode step's kernels directly instead of replaying a captured HIP graph "
+                         "(same kernels; for profilers that cannot trace graph launches)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the design note in DESIGN.md "
@@ -245,7 +248,7 @@ def main():
 
     res = {}
     if args.only in (None, "decode"):
-        res["decode"] = bench_decode(K, args.steps, args.warmup)
+        res["decode"] = bench_decode(K, args.steps, args.warmup, use_graph=not args.no_graph)
         log(f"decode: {res['decode']['tok_s']:.1f} tok/s")
     if args.only in (None, "gemv"):
         res["gemv"] = bench_gemv(K)

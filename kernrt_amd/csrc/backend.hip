@@ -697,6 +697,7 @@ int kr_attention(kr_ctx* c, kr_buf q, kr_buf out, kr_buf att, size_t layer, cons
     CHECK(c, layer < c->n_layers, "layer %zu out of range", layer);
     CHECK(c, sp && sp->kv_dim == c->kv_dim && sp->seq_len == c->seq_len,
           "attention spec does not match the prepared cache");
+    CHECK(c, sp->head_size % 4 == 0 && sp->head_size <= 256, "head_size must be a multiple of 4, at most 256");
     CHECK(c, sp->head_size > 0 && sp->kv_mul > 0 && sp->n_heads % sp->kv_mul == 0 &&
                  (sp->n_heads / sp->kv_mul) * sp->head_size <= sp->kv_dim,
           "attention geometry is inconsistent");
@@ -978,6 +979,166 @@ int attention_dev(kr_ctx* c, kr_buf q, kr_buf out, kr_buf att, size_t layer, con
     HIPCHK(c, kr::launch_attention(c->stream, qb->p, ob->p, ab->p, c->kc, c->vc, layer,
                                    (const kr::DevWindow*)window_dev, 1, c->seq_len, sp->n_heads, sp->kv_mul,
                                    sp->head_size, sp->kv_dim, sp->seq_len, scale));
+    return KR_OK;
+}
+
+int norm_quant(kr_ctx* c, kr_buf x, kr_buf add, kr_buf w, kr_buf out, size_t rows, size_t dim, float eps) {
+    CHECK(c, dim % 32 == 0 && dim <= 8000, "fused norm needs dim %% 32 == 0 and dim <= 8000 (got %zu)", dim);
+    BUF(xb, x, rows * dim);
+    BUF(wb, w, dim);
+    BUF(ob, out, rows * dim);
+    const float* ap = nullptr;
+    if (add != KR_NO_BUF) {
+        BUF(ab, add, rows * dim);
+        ap = ab->p;
+    }
+    int rc = ensure_workspace(c, rows, dim);
+    if (rc) return rc;
+    HIPCHK(c, kr::launch_add_rms_quant(c->stream, xb->p, ap, wb->p, ob->p, rows, dim, eps, c->wq, c->ws, c->wh));
+    c->q_rows = rows;
+    c->q_width = dim;
+    return KR_OK;
+}
+
+int project_q(kr_ctx* c, size_t layer, const int* projs, const kr_buf* ys, int n, size_t rows) {
+    CHECK(c, c->prepared && layer < c->n_layers, "layer %zu out of range", layer);
+    CHECK(c, n >= 1 && n <= 3, "1 to 3 projections per launch");
+    const DevMatrix* ms[3];
+    float* yp[3];
+    bool same = true;
+    for (int i = 0; i < n; i++) {
+        const Mat* m = proj_mat(c, layer, projs[i]);
+        CHECK(c, m != nullptr, "projection %d is not live on layer %zu", projs[i], layer);
+        ms[i] = &m->m;
+        CHECK(c, rows <= c->q_rows && ms[i]->k == c->q_width, "the workspace holds %zu rows of %zu, not %zu of %zu",
+              c->q_rows, c->q_width, rows, ms[i]->k);
+        BUF(yb, ys[i], rows * ms[i]->n);
+        yp[i] = yb->p;
+        same = same && ms[i]->storage == ms[0]->storage;
+    }
+    if (rows == 0) return KR_OK;
+    if (same) {
+        HIPCHK(c, kr::launch_project_set(c->stream, sem_for_project(*ms[0]), ms, yp, n, act(c), rows, nullptr));
+    } else {
+        for (int i = 0; i < n; i++)
+            HIPCHK(c, kr::launch_project(c->stream, sem_for_project(*ms[i]), *ms[i], act(c), rows, yp[i], ms[i]->n,
+                                         nullptr));
+    }
+    return KR_OK;
+}
+
+int silu_quant(kr_ctx* c, kr_buf gate, kr_buf up, size_t rows, size_t width) {
+    CHECK(c, width % 32 == 0, "fused silu needs width %% 32 == 0");
+    BUF(g, gate, rows * width);
+    BUF(u, up, rows * width);
+    int rc = ensure_workspace(c, rows, width);
+    if (rc) return rc;
+    HIPCHK(c, kr::launch_silu_quant(c->stream, g->p, u->p, rows, width, c->wq, c->ws, c->wh));
+    c->q_rows = rows;
+    c->q_width = width;
+    return KR_OK;
+}
+
+int rope_kv(kr_ctx* c, kr_buf q, kr_buf k, kr_buf v, size_t qw, size_t kvw, size_t rows, const size_t* pos_host,
+            const size_t* slot_host, const uint32_t* pos_dev, size_t layer, const kr_rope_spec* spec) {
+    CHECK(c, c->prepared && layer < c->n_layers, "layer %zu out of range", layer);
+    CHECK(c, spec && spec->head_size >= 2 && spec->head_size % 2 == 0, "rope head_size must be even");
+    CHECK(c, kvw == c->kv_dim && kvw % spec->head_size == 0 && qw % spec->head_size == 0,
+          "fused rope/kv_write needs whole heads and kv_width == kv_dim");
+    BUF(qb, q, rows * qw);
+    BUF(kb, k, rows * kvw);
+    BUF(vb, v, rows * kvw);
+    if (rows == 0) return KR_OK;
+    const uint32_t* pd;
+    const uint32_t* sd;
+    const float2* tab;
+    int rc;
+    if (pos_dev) {
+        CHECK(c, rows == 1, "device positions are for one row");
+        rc = rope_table(c, spec->theta, spec->head_size, c->seq_len, &tab);
+        if (rc) return rc;
+        pd = pos_dev;
+        sd = pos_dev;
+    } else {
+        size_t maxp = 0;
+        for (size_t i = 0; i < rows; i++) {
+            maxp = pos_host[i] > maxp ? pos_host[i] : maxp;
+            CHECK(c, slot_host[i] < c->seq_len, "slot %zu out of range", slot_host[i]);
+        }
+        CHECK(c, maxp < (1u << 24), "rope position %zu too large", maxp);
+        rc = rope_table(c, spec->theta, spec->head_size, maxp + 1, &tab);
+        if (rc) return rc;
+        std::vector<uint32_t> p = to_u32(pos_host, rows), sl = to_u32(slot_host, rows);
+        rc = stage(c, c->st_pos, p.data(), rows, &pd);
+        if (rc) return rc;
+        rc = stage(c, c->st_slots, sl.data(), rows, &sd);
+        if (rc) return rc;
+    }
+    HIPCHK(c, kr::launch_rope_kv(c->stream, qb->p, kb->p, vb->p, qw, kvw, rows, pd, sd, tab, spec->head_size,
+                                 spec->interleaved, c->kc, c->vc, layer, c->seq_len));
+    return KR_OK;
+}
+
+int attention_quant(kr_ctx* c, kr_buf q, kr_buf out, kr_buf att, size_t layer, const kr_window* windows, size_t n,
+                    const uint32_t* window_dev, const kr_attn_spec* sp) {
+    CHECK(c, c->prepared && layer < c->n_layers, "layer %zu out of range", layer);
+    CHECK(c, sp && sp->kv_dim == c->kv_dim && sp->seq_len == c->seq_len,
+          "attention spec does not match the prepared cache");
+    CHECK(c, sp->head_size % 32 == 0 && sp->head_size <= 256, "fused attention needs head_size %% 32 == 0");
+    CHECK(c, sp->kv_mul > 0 && sp->n_heads % sp->kv_mul == 0 && (sp->n_heads / sp->kv_mul) * sp->head_size <= sp->kv_dim,
+          "attention geometry is inconsistent");
+    size_t width = sp->n_heads * sp->head_size;
+    BUF(qb, q, n * width);
+    BUF(ob, out, n * width);
+    BUF(ab, att, n * sp->n_heads * sp->seq_len);
+    if (n == 0) return KR_OK;
+    const uint32_t* wd;
+    size_t max_count;
+    if (window_dev) {
+        CHECK(c, n == 1, "a device window is for one row");
+        wd = window_dev;
+        max_count = c->seq_len;
+    } else {
+        std::vector<uint32_t> w(4 * n);
+        max_count = 0;
+        for (size_t i = 0; i < n; i++) {
+            const kr_window& x = windows[i];
+            CHECK(c, x.att_start <= x.slot && x.slot < c->seq_len && x.shared_start <= x.shared_end &&
+                         x.shared_end <= c->seq_len,
+                  "window %zu out of range", i);
+            size_t count = (x.shared_end - x.shared_start) + x.slot - x.att_start + 1;
+            CHECK(c, count <= c->seq_len, "window %zu attends more than seq_len slots", i);
+            max_count = count > max_count ? count : max_count;
+            w[4 * i] = (uint32_t)x.att_start;
+            w[4 * i + 1] = (uint32_t)x.slot;
+            w[4 * i + 2] = (uint32_t)x.shared_start;
+            w[4 * i + 3] = (uint32_t)x.shared_end;
+        }
+        int rc = stage(c, c->st_win, w.data(), 4 * n, &wd);
+        if (rc) return rc;
+    }
+    int rc = ensure_workspace(c, n, width);
+    if (rc) return rc;
+    float scale = 1.0f / sqrtf((float)sp->head_size);
+    HIPCHK(c, kr::launch_attention(c->stream, qb->p, ob->p, ab->p, c->kc, c->vc, layer, (const kr::DevWindow*)wd, n,
+                                   max_count, sp->n_heads, sp->kv_mul, sp->head_size, sp->kv_dim, sp->seq_len, scale,
+                                   c->wq, c->ws, c->wh));
+    c->q_rows = n;
+    c->q_width = width;
+    return KR_OK;
+}
+
+int logits_q(kr_ctx* c, kr_buf y) {
+    CHECK(c, c->prepared, "prepare() runs before any compute");
+    Mat* mt = mat_of(c, c->classifier != KR_NO_MAT ? c->classifier : c->embedding);
+    CHECK(c, mt != nullptr, "no classifier bound");
+    const DevMatrix* m;
+    int sem;
+    int rc = classifier_matrix(c, mt, &m, &sem);
+    if (rc) return rc;
+    CHECK(c, c->q_rows >= 1 && c->q_width == m->k, "the workspace does not hold the classifier input");
+    BUF(yb, y, m->n);
+    HIPCHK(c, kr::launch_project(c->stream, sem, *m, act(c), 1, yb->p, m->n, nullptr));
     return KR_OK;
 }
 

@@ -36,4 +36,24 @@ int attention_dev(kr_ctx* c, kr_buf q, kr_buf out, kr_buf att, size_t layer, con
 // argmax of logits -> s[0] and ring[s[5]]; then s[2] += 1, s[5] += 1
 int greedy_step(kr_ctx* c, kr_buf logits, size_t len, uint32_t* step);
 
+// Fused driver steps. Each leaves the Q8 quantization of its output rows in
+// the backend's activation workspace, which project_q / logits_q consume.
+// x += add (add may be KR_NO_BUF), out = rms_norm(x, w), quantize(out)
+constexpr kr_buf KR_NO_BUF = 0xffffffffu;
+int norm_quant(kr_ctx* c, kr_buf x, kr_buf add, kr_buf w, kr_buf out, size_t rows, size_t dim, float eps);
+// projections of the quantized workspace rows; one launch when they share in_dim and storage
+int project_q(kr_ctx* c, size_t layer, const int* projs, const kr_buf* ys, int n, size_t rows);
+// gate = silu(gate) * up, quantized
+int silu_quant(kr_ctx* c, kr_buf gate, kr_buf up, size_t rows, size_t width);
+// rope of q and k, then k and v into the cache; positions and slots from the
+// host (pos_host/slot_host) or one device position (pos_dev, rows == 1)
+int rope_kv(kr_ctx* c, kr_buf q, kr_buf k, kr_buf v, size_t qw, size_t kvw, size_t rows, const size_t* pos_host,
+            const size_t* slot_host, const uint32_t* pos_dev, size_t layer, const kr_rope_spec* spec);
+// attention whose output rows are also quantized; windows from the host, or
+// one device window (window_dev, n == 1)
+int attention_quant(kr_ctx* c, kr_buf q, kr_buf out, kr_buf att, size_t layer, const kr_window* windows,
+                    size_t n, const uint32_t* window_dev, const kr_attn_spec* spec);
+// the classifier over the quantized workspace row
+int logits_q(kr_ctx* c, kr_buf y);
+
 }  // namespace kri

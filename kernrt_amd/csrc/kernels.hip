@@ -25,6 +25,129 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ float div_rn(float a, float b) { return (float)((double)a / (double)b); }
 __device__ __forceinline__ float sqrt_rn(float a) { return (float)__builtin_sqrt((double)a); }
 
+// Serial f32 chains, software-pipelined: operands are fetched kPipe elements
+// ahead into registers so each dependent add waits only on the previous add,
+// never on a memory read. The accumulation order is exactly left to right.
+static constexpr int kPipe = 16;
+
+// ((0 + a[0]) + a[1]) + ... + a[n-1]
+__device__ __forceinline__ float seq_sum(const float* __restrict__ a, uint32_t n) {
+    float s = 0.0f;
+    uint32_t full = n & ~(uint32_t)(kPipe - 1), i = 0;
+    if (full) {
+        float cur[kPipe];
+#pragma unroll
+        for (int j = 0; j < kPipe; j++) cur[j] = a[j];
+        for (i = kPipe; i < full; i += kPipe) {
+            float nxt[kPipe];
+#pragma unroll
+            for (int j = 0; j < kPipe; j++) nxt[j] = a[i + j];
+#pragma unroll
+            for (int j = 0; j < kPipe; j++) s += cur[j];
+#pragma unroll
+            for (int j = 0; j < kPipe; j++) cur[j] = nxt[j];
+        }
+#pragma unroll
+        for (int j = 0; j < kPipe; j++) s += cur[j];
+        i = full;
+    }
+    for (; i < n; i++) s += a[i];
+    return s;
+}
+
+// acc += p[j] * t[j * stride] for j in order (mul then add, unfused)
+__device__ __forceinline__ float seq_dot(float acc, const float* __restrict__ p, const float* __restrict__ t,
+                                         uint32_t stride, uint32_t n) {
+    uint32_t full = n & ~(uint32_t)(kPipe - 1), i = 0;
+    if (full) {
+        float cur[kPipe];
+#pragma unroll
+        for (int j = 0; j < kPipe; j++) cur[j] = p[j] * t[j * stride];
+        for (i = kPipe; i < full; i += kPipe) {
+            float nxt[kPipe];
+#pragma unroll
+            for (int j = 0; j < kPipe; j++) nxt[j] = p[i + j] * t[(i + j) * stride];
+#pragma unroll
+            for (int j = 0; j < kPipe; j++) acc += cur[j];
+#pragma unroll
+            for (int j = 0; j < kPipe; j++) cur[j] = nxt[j];
+        }
+#pragma unroll
+        for (int j = 0; j < kPipe; j++) acc += cur[j];
+        i = full;
+    }
+    for (; i < n; i++) acc += p[i] * t[i * stride];
+    return acc;
+}
+
+// slot = fma(e[b].x, e[b].y, slot) for b in order (quant.rs:287)
+__device__ __forceinline__ float seq_fma(const float2* __restrict__ e, uint32_t n) {
+    float slot = 0.0f;
+    uint32_t full = n & ~(uint32_t)(kPipe - 1), i = 0;
+    if (full) {
+        float2 cur[kPipe];
+#pragma unroll
+        for (int j = 0; j < kPipe; j++) cur[j] = e[j];
+        for (i = kPipe; i < full; i += kPipe) {
+            float2 nxt[kPipe];
+#pragma unroll
+            for (int j = 0; j < kPipe; j++) nxt[j] = e[i + j];
+#pragma unroll
+            for (int j = 0; j < kPipe; j++) slot = __builtin_fmaf(cur[j].x, cur[j].y, slot);
+#pragma unroll
+            for (int j = 0; j < kPipe; j++) cur[j] = nxt[j];
+        }
+#pragma unroll
+        for (int j = 0; j < kPipe; j++) slot = __builtin_fmaf(cur[j].x, cur[j].y, slot);
+        i = full;
+    }
+    for (; i < n; i++) slot = __builtin_fmaf(e[i].x, e[i].y, slot);
+    return slot;
+}
+
+// t[b & 3] += e[b] for b in order, then ((t0 + t1) + t2) + t3 (dot.rs:35-44)
+__device__ __forceinline__ float seq_four(const float* __restrict__ e, uint32_t n) {
+    float t[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    uint32_t full = n & ~(uint32_t)(kPipe - 1), i = 0;
+    if (full) {
+        float cur[kPipe];
+#pragma unroll
+        for (int j = 0; j < kPipe; j++) cur[j] = e[j];
+        for (i = kPipe; i < full; i += kPipe) {
+            float nxt[kPipe];
+#pragma unroll
+            for (int j = 0; j < kPipe; j++) nxt[j] = e[i + j];
+#pragma unroll
+            for (int j = 0; j < kPipe; j++) t[j & 3] += cur[j];
+#pragma unroll
+            for (int j = 0; j < kPipe; j++) cur[j] = nxt[j];
+        }
+#pragma unroll
+        for (int j = 0; j < kPipe; j++) t[j & 3] += cur[j];
+        i = full;
+    }
+    for (; i < n; i++) t[i & 3] += e[i];
+    return ((t[0] + t[1]) + t[2]) + t[3];
+}
+
+// Quantize one f32 value per lane as part of a 32-lane Q8 block (lanes
+// 32k..32k+31 hold one block), exactly as Q8Vec::quantize_into does
+// (quant.rs:864-873). Every lane of the half-wave must call this.
+__device__ __forceinline__ void quant_lane(float v, bool valid, int8_t* q, float* s, uint16_t* h) {
+    float m = fmaxf(0.0f, fabsf(v));
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 32));
+    float d = div_rn(m, 127.0f);
+    float inv = d > 0.0f ? div_rn(1.0f, d) : 0.0f;
+    if (valid) {
+        *q = q8_round(v * inv);
+        if ((threadIdx.x & 31) == 0) {
+            *s = d;
+            *h = f32_to_f16_bits(d);
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Activation quantization (quant.rs:856-874 per row, cpu.rs:143-158 batched).
 // One 32-lane half-wave per Q8 block: lanes load one element each, the block
@@ -76,17 +199,34 @@ hipError_t launch_quantize(hipStream_t st, const float* x, size_t rows, size_t k
 // turns it into the reference's per-block epilogue operand and parks it in
 // LDS; after a barrier one lane per (row, output) walks the blocks in order,
 // reproducing the reference's f32 accumulation sequence exactly.
+//
+// One launch may cover up to three matrices with the same K (q/k/v, or
+// gate/up): the grid is the concatenation of their tile ranges.
+struct MatSet {
+    const int8_t* q[3];
+    const void* s[3];
+    float* y[3];
+    uint32_t n[3];
+    uint32_t ld[3];
+    uint32_t tile_end[3];  // cumulative tile counts
+    int count;
+};
+
 template <int SEM, int M>
-__global__ __launch_bounds__(256) void k_gemv(const int8_t* __restrict__ W, const void* __restrict__ WS,
-                                              QuantAct x, float* __restrict__ Y, uint32_t N, uint32_t K,
-                                              uint32_t R, uint32_t ldy, int32_t* __restrict__ dbg) {
+__global__ __launch_bounds__(256) void k_gemv(MatSet ms, QuantAct x, uint32_t K, uint32_t R,
+                                              int32_t* __restrict__ dbg) {
     extern __shared__ __align__(16) char smem[];
+    const int mi = blockIdx.x < ms.tile_end[0] ? 0 : (blockIdx.x < ms.tile_end[1] ? 1 : 2);
+    const uint32_t tile = blockIdx.x - (mi == 0 ? 0 : ms.tile_end[mi - 1]);
+    const int8_t* __restrict__ W = ms.q[mi];
+    const void* __restrict__ WS = ms.s[mi];
+    const uint32_t N = ms.n[mi];
     const uint32_t nb = K >> 5;
-    const uint32_t row0 = blockIdx.x * R;
+    const uint32_t row0 = tile * R;
     const uint32_t rows = min(R, N - row0);
-    int8_t* xs_l = (int8_t*)smem;                      // [M][K]
-    float* res = (float*)(smem + M * K);               // per (m, block) epilogue operands
-    const uint32_t nblk = rows * nb;                   // blocks in this tile
+    int8_t* xs_l = (int8_t*)smem;         // [M][K]
+    float* res = (float*)(smem + M * K);  // per (m, block) epilogue operands
+    const uint32_t nblk = rows * nb;      // blocks in this tile
 
     for (uint32_t i = threadIdx.x; i < M * K / 16; i += 256) ((int4*)xs_l)[i] = ((const int4*)x.q)[i];
     __syncthreads();
@@ -108,7 +248,7 @@ __global__ __launch_bounds__(256) void k_gemv(const int8_t* __restrict__ W, cons
             uint32_t c = threadIdx.x + 256 * (it * U + u);
             bool valid = c < C;
             uint32_t col = valid ? (16 * c) % K : 0;
-            uint32_t g = c >> 1;           // block index within the tile
+            uint32_t g = c >> 1;  // block index within the tile
             uint32_t r = valid ? g / nb : 0, b = valid ? g % nb : 0;
 #pragma unroll
             for (int m = 0; m < M; m++) {
@@ -139,30 +279,16 @@ __global__ __launch_bounds__(256) void k_gemv(const int8_t* __restrict__ W, cons
     }
     __syncthreads();
 
+    float* Y = ms.y[mi];
+    const uint32_t ld = ms.ld[mi];
     for (uint32_t t = threadIdx.x; t < M * rows; t += 256) {
         uint32_t m = t / rows, r = t % rows;
         float out;
-        if (SEM == SEM_FMA_CHAIN) {
-            const float2* e = (const float2*)res + m * nblk + r * nb;
-            float slot = 0.0f;
-            for (uint32_t b = 0; b < nb; b++) slot = __builtin_fmaf(e[b].x, e[b].y, slot);
-            out = slot;
-        } else {
-            const float* e = res + m * nblk + r * nb;
-            float t0 = 0.0f, t1 = 0.0f, t2 = 0.0f, t3 = 0.0f;
-            uint32_t b = 0;
-            for (; b + 4 <= nb; b += 4) {
-                t0 += e[b];
-                t1 += e[b + 1];
-                t2 += e[b + 2];
-                t3 += e[b + 3];
-            }
-            if (b < nb) t0 += e[b++];
-            if (b < nb) t1 += e[b++];
-            if (b < nb) t2 += e[b++];
-            out = ((t0 + t1) + t2) + t3;
-        }
-        Y[(size_t)m * ldy + row0 + r] = out;
+        if (SEM == SEM_FMA_CHAIN)
+            out = seq_fma((const float2*)res + m * nblk + r * nb, nb);
+        else
+            out = seq_four(res + m * nblk + r * nb, nb);
+        Y[(size_t)m * ld + row0 + r] = out;
     }
 }
 
@@ -182,42 +308,46 @@ static size_t gemv_rows_per_tile(size_t n, size_t k) {
 }
 
 template <int SEM, int M>
-static hipError_t gemv_launch(hipStream_t st, const DevMatrix& w, QuantAct x, float* y, size_t ldy,
-                              int32_t* dbg) {
-    size_t nb = w.k / 32;
+static hipError_t gemv_launch(hipStream_t st, MatSet ms, size_t k, QuantAct x, int32_t* dbg) {
+    size_t nb = k / 32;
     size_t per_row = (SEM == SEM_FMA_CHAIN ? 8 : 4) * M * nb;  // LDS bytes of epilogue operands per row
-    size_t R = gemv_rows_per_tile(w.n, w.k);
-    size_t r_cap = (kGemvLds - M * w.k) / per_row;
+    size_t n_max = 0;
+    for (int i = 0; i < ms.count; i++) n_max = ms.n[i] > n_max ? ms.n[i] : n_max;
+    size_t R = gemv_rows_per_tile(n_max, k);
+    size_t r_cap = (kGemvLds - M * k) / per_row;
     if (R > r_cap) R = r_cap;
-    size_t tiles = (w.n + R - 1) / R;
-    size_t lds = M * w.k + per_row * R;
-    hipLaunchKernelGGL((k_gemv<SEM, M>), dim3((unsigned)tiles), dim3(256), lds, st, w.q, w.s, x, y,
-                       (uint32_t)w.n, (uint32_t)w.k, (uint32_t)R, (uint32_t)ldy, dbg);
+    uint32_t total = 0;
+    for (int i = 0; i < 3; i++) {
+        if (i < ms.count) total += (uint32_t)((ms.n[i] + R - 1) / R);
+        ms.tile_end[i] = total;
+    }
+    size_t lds = M * k + per_row * R;
+    hipLaunchKernelGGL((k_gemv<SEM, M>), dim3(total), dim3(256), lds, st, ms, x, (uint32_t)k, (uint32_t)R, dbg);
     return hipGetLastError();
 }
 
 template <int SEM>
-static hipError_t gemv_rows(hipStream_t st, const DevMatrix& w, QuantAct x, size_t rows, float* y, size_t ldy,
-                            int32_t* dbg) {
-    size_t nb = w.k / 32;
+static hipError_t gemv_rows(hipStream_t st, const MatSet& ms, size_t k, QuantAct x, size_t rows, int32_t* dbg) {
+    size_t nb = k / 32;
     size_t done = 0;
     while (done < rows) {
         size_t m = rows - done;
-        QuantAct xm{x.q + done * w.k, x.s + done * nb, x.h + done * nb};
-        float* ym = y + done * ldy;
-        int32_t* dm = dbg ? dbg + done * w.n * nb : nullptr;
-        hipError_t e;
-        size_t m_cap = kGemvActBytes / w.k;
+        size_t m_cap = kGemvActBytes / k;
         if (m > m_cap) m = m_cap;
+        QuantAct xm{x.q + done * k, x.s + done * nb, x.h + done * nb};
+        MatSet mm = ms;
+        for (int i = 0; i < ms.count; i++) mm.y[i] = ms.y[i] + done * ms.ld[i];
+        int32_t* dm = dbg ? dbg + done * ms.n[0] * nb : nullptr;
+        hipError_t e;
         if (m >= 4) {
-            e = gemv_launch<SEM, 4>(st, w, xm, ym, ldy, dm);
+            e = gemv_launch<SEM, 4>(st, mm, k, xm, dm);
             m = 4;
         } else if (m == 3) {
-            e = gemv_launch<SEM, 3>(st, w, xm, ym, ldy, dm);
+            e = gemv_launch<SEM, 3>(st, mm, k, xm, dm);
         } else if (m == 2) {
-            e = gemv_launch<SEM, 2>(st, w, xm, ym, ldy, dm);
+            e = gemv_launch<SEM, 2>(st, mm, k, xm, dm);
         } else {
-            e = gemv_launch<SEM, 1>(st, w, xm, ym, ldy, dm);
+            e = gemv_launch<SEM, 1>(st, mm, k, xm, dm);
         }
         if (e != hipSuccess) return e;
         done += m;
@@ -225,14 +355,34 @@ static hipError_t gemv_rows(hipStream_t st, const DevMatrix& w, QuantAct x, size
     return hipSuccess;
 }
 
-hipError_t launch_project(hipStream_t st, int sem, const DevMatrix& w, QuantAct x, size_t rows, float* y,
-                          size_t ldy, int32_t* dbg) {
+hipError_t launch_project_set(hipStream_t st, int sem, const DevMatrix* const* w, float* const* y, int count,
+                              QuantAct x, size_t rows, int32_t* dbg) {
+    if (count < 1 || count > 3) return hipErrorInvalidValue;
+    MatSet ms{};
+    ms.count = count;
+    for (int i = 0; i < count; i++) {
+        if (w[i]->k != w[0]->k || w[i]->storage != w[0]->storage) return hipErrorInvalidValue;
+        ms.q[i] = w[i]->q;
+        ms.s[i] = w[i]->s;
+        ms.y[i] = y[i];
+        ms.n[i] = (uint32_t)w[i]->n;
+        ms.ld[i] = (uint32_t)w[i]->n;
+    }
+    size_t k = w[0]->k;
     switch (sem) {
-        case SEM_FMA_CHAIN: return gemv_rows<SEM_FMA_CHAIN>(st, w, x, rows, y, ldy, dbg);
-        case SEM_FOUR_PARTIALS_F32: return gemv_rows<SEM_FOUR_PARTIALS_F32>(st, w, x, rows, y, ldy, dbg);
-        case SEM_FOUR_PARTIALS_F16: return gemv_rows<SEM_FOUR_PARTIALS_F16>(st, w, x, rows, y, ldy, dbg);
+        case SEM_FMA_CHAIN: return gemv_rows<SEM_FMA_CHAIN>(st, ms, k, x, rows, dbg);
+        case SEM_FOUR_PARTIALS_F32: return gemv_rows<SEM_FOUR_PARTIALS_F32>(st, ms, k, x, rows, dbg);
+        case SEM_FOUR_PARTIALS_F16: return gemv_rows<SEM_FOUR_PARTIALS_F16>(st, ms, k, x, rows, dbg);
     }
     return hipErrorInvalidValue;
+}
+
+hipError_t launch_project(hipStream_t st, int sem, const DevMatrix& w, QuantAct x, size_t rows, float* y,
+                          size_t ldy, int32_t* dbg) {
+    if (ldy != w.n) return hipErrorInvalidValue;
+    const DevMatrix* ws[1] = {&w};
+    float* ys[1] = {y};
+    return launch_project_set(st, sem, ws, ys, 1, x, rows, dbg);
 }
 
 // ---------------------------------------------------------------------------
@@ -250,16 +400,7 @@ __global__ __launch_bounds__(256) void k_rms_norm(float* __restrict__ out, const
     }
     __syncthreads();
     if (threadIdx.x == 0) {
-        float ss = 0.0f;
-        uint32_t i = 0;
-        for (; i + 4 <= dim; i += 4) {
-            float4 p = *(const float4*)(sq + i);
-            ss += p.x;
-            ss += p.y;
-            ss += p.z;
-            ss += p.w;
-        }
-        for (; i < dim; i++) ss += sq[i];
+        float ss = seq_sum(sq, dim);
         ss = div_rn(ss, (float)dim);
         ss += eps;
         s_scale = div_rn(1.0f, sqrt_rn(ss));
@@ -385,106 +526,334 @@ hipError_t launch_kv_write(hipStream_t st, float* kc, float* vc, size_t layer, s
 }
 
 // ---------------------------------------------------------------------------
-// Attention for one (row, head) per workgroup (cpu.rs:575-630).
-//  1. scores: each lane scores whole cache rows with the reference's
-//     four-chain FMA dot (dot.rs:350-366), times the scale;
-//  2. max (order-free), exp via glibc's expf restated;
-//  3. the softmax sum is left-to-right (one lane), then each score / sum;
-//  4. out[e] = sum_t p_t * v_t[e], one lane per element e, t in order.
+// Attention (cpu.rs:575-630), one workgroup per (query row, KV head): the
+// kv_mul query heads that share a KV head are served together, so each K and
+// V row is read once for all of them.
+//  1. scores: one lane per cache row runs the reference's four-chain FMA dot
+//     (dot.rs:350-366) against every query head of the group, times scale;
+//  2. per-head max (order-free); exp via glibc's expf restated;
+//  3. each head's softmax sum is left to right (one lane per head, side by
+//     side in one wave), then every score / sum;
+//  4. out[h][e] = sum_t p_t * v_t[e], one lane per (head, e), t in order.
+//     V rows stream through two LDS tiles filled by all lanes; the first
+//     tile's loads are issued together with the K loads of step 1.
 // Scores live in LDS when they fit, otherwise in the caller's `att` rows.
+static constexpr uint32_t kAttnThreads = 512;
+static constexpr size_t kAttnLds = 150 * 1024;
+
 __device__ __forceinline__ uint32_t win_slot(const DevWindow& w, uint32_t n_shared, uint32_t i) {
     return i < n_shared ? w.shared_start + i : w.att_start + (i - n_shared);
 }
 
-__global__ __launch_bounds__(256) void k_attention(const float* __restrict__ q, float* __restrict__ out,
+__global__ __launch_bounds__(512) void k_attention(const float* __restrict__ q, float* __restrict__ out,
                                                    float* __restrict__ att, const float* __restrict__ kc,
                                                    const float* __restrict__ vc, size_t loff,
                                                    const DevWindow* __restrict__ windows, uint32_t n_heads,
                                                    uint32_t kv_mul, uint32_t hs, uint32_t kv_dim,
-                                                   uint32_t seq_len, float scale, uint32_t lds_scores) {
-    extern __shared__ float sm[];  // [hs] query, then scores if they fit
-    __shared__ float red[8];
-    __shared__ float s_bcast;
-    const uint32_t h = blockIdx.x, row = blockIdx.y;
+                                                   uint32_t seq_len, float scale, uint32_t G, uint32_t lds_scores,
+                                                   uint32_t tile_rows, int8_t* __restrict__ qo,
+                                                   float* __restrict__ so, uint16_t* __restrict__ ho) {
+    // LDS: q [kv_mul][hs] | V tiles [2][tile_rows*hs] | scores [kv_mul][lds_scores]
+    extern __shared__ float sm[];
+    __shared__ float red[16][8];
+    __shared__ float s_sum[8];
+    // this workgroup: query heads [h0, h0 + G), G | kv_mul, all on one KV head
+    const uint32_t row = blockIdx.y, T = kAttnThreads;
     const DevWindow w = windows[row];
     const uint32_t n_shared = w.shared_end - w.shared_start;
     const uint32_t count = n_shared + w.slot - w.att_start + 1;
     const uint32_t width = n_heads * hs;
-    const float* qh = q + (size_t)row * width + (size_t)h * hs;
-    const uint32_t kvo = (h / kv_mul) * hs;
+    const uint32_t h0 = blockIdx.x * G;
+    const uint32_t kvo = (h0 / kv_mul) * hs;
+    const uint32_t qn = G * hs;
     float* qs = sm;
-    float* sc = count <= lds_scores ? sm + ((hs + 3) & ~3u)
-                                    : att + (size_t)row * n_heads * seq_len + (size_t)h * seq_len;
-    for (uint32_t e = threadIdx.x; e < hs; e += 256) qs[e] = qh[e];
+    float* vt = sm + ((qn + 3) & ~3u);
+    const uint32_t tile_f = tile_rows * hs;
+    const bool sc_lds = count <= lds_scores;
+    float* sc_base = sc_lds ? vt + 2 * tile_f : att + (size_t)row * n_heads * seq_len + (size_t)h0 * seq_len;
+    const uint32_t sc_stride = sc_lds ? lds_scores : seq_len;  // per query head
+    for (uint32_t e = threadIdx.x; e < qn; e += T) qs[e] = q[(size_t)row * width + (size_t)h0 * hs + e];
+
+    // V tile loader: float4 f of the tile -> (row j, column col)
+    const uint32_t tile_f4 = tile_f / 4;
+    const uint32_t ntiles = (count + tile_rows - 1) / tile_rows;
+    const float* vbase = vc + loff + kvo;
+    constexpr int VPT = 8;  // float4 per lane per tile, enough for 16K floats
+    float4 pre[VPT];
+    auto load_tile = [&](uint32_t c) {
+#pragma unroll
+        for (int u = 0; u < VPT; u++) {
+            uint32_t f = threadIdx.x + T * u;
+            pre[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (f < tile_f4) {
+                uint32_t j = (4 * f) / hs, col = (4 * f) % hs, i = c * tile_rows + j;
+                if (i < count) pre[u] = *(const float4*)(vbase + (size_t)win_slot(w, n_shared, i) * kv_dim + col);
+            }
+        }
+    };
+    auto store_tile = [&](uint32_t buf) {
+#pragma unroll
+        for (int u = 0; u < VPT; u++) {
+            uint32_t f = threadIdx.x + T * u;
+            if (f < tile_f4) *(float4*)(vt + buf * tile_f + 4 * f) = pre[u];
+        }
+    };
+    load_tile(0);  // in flight while the scores are computed
     __syncthreads();
 
-    float mx = -INFINITY;
-    for (uint32_t i = threadIdx.x; i < count; i += 256) {
+    // 1. scores
+    float mx[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) mx[j] = -INFINITY;
+    for (uint32_t i = threadIdx.x; i < count; i += T) {
         const float* kr = kc + loff + (size_t)win_slot(w, n_shared, i) * kv_dim + kvo;
-        float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
-        uint32_t e = 0;
-        for (; e + 4 <= hs; e += 4) {
-            float4 kk = *(const float4*)(kr + e);
-            a0 = __builtin_fmaf(qs[e], kk.x, a0);
-            a1 = __builtin_fmaf(qs[e + 1], kk.y, a1);
-            a2 = __builtin_fmaf(qs[e + 2], kk.z, a2);
-            a3 = __builtin_fmaf(qs[e + 3], kk.w, a3);
+        for (uint32_t j = 0; j < G; j++) {
+            const float* qh = qs + j * hs;
+            float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+            uint32_t e = 0;
+#pragma unroll 8
+            for (; e + 4 <= hs; e += 4) {
+                float4 kk = *(const float4*)(kr + e);
+                a0 = __builtin_fmaf(qh[e], kk.x, a0);
+                a1 = __builtin_fmaf(qh[e + 1], kk.y, a1);
+                a2 = __builtin_fmaf(qh[e + 2], kk.z, a2);
+                a3 = __builtin_fmaf(qh[e + 3], kk.w, a3);
+            }
+            float d = (a0 + a1) + (a2 + a3);
+            for (; e < hs; e++) d = __builtin_fmaf(qh[e], kr[e], d);
+            float sv = d * scale;
+            sc_base[j * sc_stride + i] = sv;
+            if (j < 8) mx[j] = fmaxf(mx[j], sv);
         }
-        float d = (a0 + a1) + (a2 + a3);
-        for (; e < hs; e++) d = __builtin_fmaf(qs[e], kr[e], d);
-        float s = d * scale;
-        sc[i] = s;
-        mx = fmaxf(mx, s);
+    }
+    store_tile(0);
+    for (uint32_t j = 0; j < G; j++) {
+        float m = mx[j < 8 ? j : 0];
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6][j] = m;
+    }
+    __syncthreads();
+    // 2. exp per (head, row) with the head's max
+    for (uint32_t t = threadIdx.x; t < G * count; t += T) {
+        uint32_t j = t / count, i = t % count;
+        float m = red[0][j];
+        for (uint32_t wv = 1; wv < T / 64; wv++) m = fmaxf(m, red[wv][j]);
+        float* sc = sc_base + j * sc_stride;
+        sc[i] = glibc_expf(sc[i] - m);
+    }
+    __syncthreads();
+    // 3. per-head sums, lanes 0..kv_mul-1 of wave 0 in lockstep
+    if (threadIdx.x < G) s_sum[threadIdx.x] = seq_sum(sc_base + threadIdx.x * sc_stride, count);
+    __syncthreads();
+    for (uint32_t t = threadIdx.x; t < G * count; t += T) {
+        uint32_t j = t / count, i = t % count;
+        float* sc = sc_base + j * sc_stride;
+        sc[i] = div_rn(sc[i], s_sum[j]);
+    }
+    __syncthreads();
+
+    // 4. weighted V sums: lane (j, e) for j < kv_mul, e < hs
+    float acc[2] = {0.0f, 0.0f};  // lanes cover kv_mul*hs <= 2*T
+    for (uint32_t c = 0; c < ntiles; c++) {
+        if (c + 1 < ntiles) load_tile(c + 1);
+        uint32_t rows = min(tile_rows, count - c * tile_rows);
+#pragma unroll
+        for (int r = 0; r < 2; r++) {
+            uint32_t t = threadIdx.x + r * T;
+            if (t < qn) {
+                uint32_t j = t / hs, e = t % hs;
+                acc[r] = seq_dot(acc[r], sc_base + j * sc_stride + c * tile_rows, vt + (c & 1) * tile_f + e, hs, rows);
+            }
+        }
+        if (c + 1 < ntiles) store_tile((c + 1) & 1);
+        __syncthreads();
     }
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
-    __syncthreads();
-    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    for (uint32_t i = threadIdx.x; i < count; i += 256) sc[i] = glibc_expf(sc[i] - mx);
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        float sum = 0.0f;
-        uint32_t i = 0;
-        for (; i + 4 <= count; i += 4) {
-            sum += sc[i];
-            sum += sc[i + 1];
-            sum += sc[i + 2];
-            sum += sc[i + 3];
-        }
-        for (; i < count; i++) sum += sc[i];
-        s_bcast = sum;
-    }
-    __syncthreads();
-    const float sum = s_bcast;
-    for (uint32_t i = threadIdx.x; i < count; i += 256) sc[i] = div_rn(sc[i], sum);
-    __syncthreads();
-    float* orow = out + (size_t)row * width + (size_t)h * hs;
-    for (uint32_t e = threadIdx.x; e < hs; e += 256) {
-        float acc = 0.0f;
-        const float* vb = vc + loff + kvo + e;
-        for (uint32_t i = 0; i < count; i++) acc += sc[i] * vb[(size_t)win_slot(w, n_shared, i) * kv_dim];
-        orow[e] = acc;
+    for (int r = 0; r < 2; r++) {
+        uint32_t t = threadIdx.x + r * T;
+        bool live = t < qn;
+        size_t o = (size_t)row * width + (size_t)h0 * hs + t;
+        if (live) out[o] = acc[r];
+        // head outputs are whole Q8 blocks (hs % 32 == 0): quantize for o_proj
+        if (qo && t < ((qn + 31) & ~31u)) quant_lane(acc[r], live, qo + o, so + o / 32, ho + o / 32);
     }
     // Leave the probabilities in `att` like the reference does.
-    if (count <= lds_scores) {
-        float* ag = att + (size_t)row * n_heads * seq_len + (size_t)h * seq_len;
-        for (uint32_t i = threadIdx.x; i < count; i += 256) ag[i] = sc[i];
+    if (sc_lds) {
+        for (uint32_t t = threadIdx.x; t < G * count; t += T) {
+            uint32_t j = t / count, i = t % count;
+            att[(size_t)row * n_heads * seq_len + (size_t)(h0 + j) * seq_len + i] = sc_base[j * sc_stride + i];
+        }
     }
 }
 
 hipError_t launch_attention(hipStream_t st, const float* q, float* out, float* att, const float* kc,
                             const float* vc, size_t layer, const DevWindow* windows, size_t n_rows,
                             size_t max_count, size_t n_heads, size_t kv_mul, size_t hs, size_t kv_dim,
-                            size_t seq_len, float scale) {
+                            size_t seq_len, float scale, int8_t* qo, float* so, uint16_t* ho) {
     if (n_rows == 0) return hipSuccess;
-    const size_t lds_cap = 48 * 1024;
-    size_t qbytes = ((hs + 3) & ~(size_t)3) * sizeof(float);
-    size_t lds_scores = max_count * sizeof(float) + qbytes <= lds_cap ? max_count : 0;
-    size_t lds = qbytes + lds_scores * sizeof(float);
-    hipLaunchKernelGGL(k_attention, dim3((unsigned)n_heads, (unsigned)n_rows), dim3(256), lds, st, q, out, att,
-                       kc, vc, layer * seq_len * kv_dim, windows, (uint32_t)n_heads, (uint32_t)kv_mul,
-                       (uint32_t)hs, (uint32_t)kv_dim, (uint32_t)seq_len, scale, (uint32_t)lds_scores);
+    if (hs == 0 || hs > 256 || hs % 4 != 0 || kv_mul == 0 || n_heads % kv_mul != 0) return hipErrorInvalidValue;
+    if (qo && hs % 32 != 0) return hipErrorInvalidValue;
+    size_t G = 1;  // heads per workgroup: the largest divisor of kv_mul that fits
+    for (size_t g = 1; g <= 8 && g <= kv_mul; g++)
+        if (kv_mul % g == 0 && g * hs <= 2 * kAttnThreads) G = g;
+    size_t qn = G * hs;
+    size_t qbytes = ((qn + 3) & ~(size_t)3) * sizeof(float);
+    // V tiles: as many rows as the window needs, at most 8 float4 per lane
+    size_t tile_rows = (8 * 4 * kAttnThreads) / hs;
+    size_t need_rows = max_count < tile_rows ? max_count : tile_rows;
+    if (need_rows < 1) need_rows = 1;
+    size_t vbytes = 2 * need_rows * hs * sizeof(float);
+    size_t lds_scores = qbytes + vbytes + G * max_count * sizeof(float) <= kAttnLds ? max_count : 0;
+    size_t lds = qbytes + vbytes + G * lds_scores * sizeof(float);
+    hipLaunchKernelGGL(k_attention, dim3((unsigned)(n_heads / G), (unsigned)n_rows), dim3(kAttnThreads), lds, st, q,
+                       out, att, kc, vc, layer * seq_len * kv_dim, windows, (uint32_t)n_heads, (uint32_t)kv_mul,
+                       (uint32_t)hs, (uint32_t)kv_dim, (uint32_t)seq_len, scale, (uint32_t)G, (uint32_t)lds_scores,
+                       (uint32_t)need_rows, qo, so, ho);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Fused steps of the model driver. Each reproduces, in one launch, the exact
+// arithmetic of a short run of separate ops.
+
+// add_in_place (cpu.rs:405-410) + rms_norm (cpu.rs:633-644) + the Q8
+// quantization of the normed row (quant.rs:856-874), one row per workgroup.
+template <bool ADD>
+__global__ __launch_bounds__(256) void k_add_rms_quant(float* __restrict__ x, const float* __restrict__ add,
+                                                       const float* __restrict__ w, float* __restrict__ out,
+                                                       uint32_t dim, float eps, int8_t* __restrict__ q,
+                                                       float* __restrict__ s, uint16_t* __restrict__ h) {
+    extern __shared__ float sm[];  // xs[dim] | sq[dim]
+    __shared__ float s_scale;
+    float* xs = sm;
+    float* sq = sm + dim;
+    const size_t row = blockIdx.x;
+    float* xr = x + row * dim;
+    for (uint32_t i = threadIdx.x; i < dim; i += 256) {
+        float v = xr[i];
+        if (ADD) {
+            v = v + add[row * dim + i];
+            xr[i] = v;
+        }
+        xs[i] = v;
+        sq[i] = v * v;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float ss = seq_sum(sq, dim);
+        ss = div_rn(ss, (float)dim);
+        ss += eps;
+        s_scale = div_rn(1.0f, sqrt_rn(ss));
+    }
+    __syncthreads();
+    const float scale = s_scale;
+    const uint32_t nb = dim / 32;
+    for (uint32_t base = 0; base < dim; base += 256) {
+        uint32_t i = base + threadIdx.x;
+        bool valid = i < dim;  // dim % 32 == 0: half-waves are all valid or all not
+        float o = valid ? w[i] * (scale * xs[i]) : 0.0f;
+        if (valid) out[row * dim + i] = o;
+        quant_lane(o, valid, q + row * dim + i, s + row * nb + i / 32, h + row * nb + i / 32);
+    }
+}
+
+hipError_t launch_add_rms_quant(hipStream_t st, float* x, const float* add, const float* w, float* out,
+                                size_t rows, size_t dim, float eps, int8_t* q, float* s, uint16_t* h) {
+    if (rows == 0) return hipSuccess;
+    if (dim % 32 != 0) return hipErrorInvalidValue;
+    size_t lds = 2 * dim * sizeof(float);
+    if (add)
+        hipLaunchKernelGGL(k_add_rms_quant<true>, dim3((unsigned)rows), dim3(256), lds, st, x, add, w, out,
+                           (uint32_t)dim, eps, q, s, h);
+    else
+        hipLaunchKernelGGL(k_add_rms_quant<false>, dim3((unsigned)rows), dim3(256), lds, st, x, add, w, out,
+                           (uint32_t)dim, eps, q, s, h);
+    return hipGetLastError();
+}
+
+// silu_mul (cpu.rs:494-499) + quantization of the gated rows.
+__global__ __launch_bounds__(256) void k_silu_quant(float* __restrict__ g, const float* __restrict__ u, size_t n,
+                                                    int8_t* __restrict__ q, float* __restrict__ s,
+                                                    uint16_t* __restrict__ h) {
+    size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    bool valid = i < n;  // n % 32 == 0
+    float r = 0.0f;
+    if (valid) {
+        float xv = g[i];
+        r = div_rn(xv, 1.0f + glibc_expf(-xv)) * u[i];
+        g[i] = r;
+    }
+    quant_lane(r, valid, q + i, s + i / 32, h + i / 32);
+}
+
+hipError_t launch_silu_quant(hipStream_t st, float* g, const float* u, size_t rows, size_t width, int8_t* q,
+                             float* s, uint16_t* h) {
+    size_t n = rows * width;
+    if (n == 0) return hipSuccess;
+    if (width % 32 != 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_silu_quant, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, g, u, n, q, s, h);
+    return hipGetLastError();
+}
+
+// rope (cpu.rs:274-302) then kv_write (cpu.rs:238-246): each lane rotates one
+// q or k pair and writes rotated k pairs into the cache; v is copied as is.
+__global__ __launch_bounds__(256) void k_rope_kv(float* __restrict__ q, float* __restrict__ k,
+                                                 const float* __restrict__ v, uint32_t qw, uint32_t kvw,
+                                                 uint32_t rows, const uint32_t* __restrict__ pos,
+                                                 const uint32_t* __restrict__ slots,
+                                                 const float2* __restrict__ tab, uint32_t hs, int interleaved,
+                                                 float* __restrict__ kc, float* __restrict__ vc, size_t base) {
+    const uint32_t half = hs / 2;
+    const uint32_t qpairs = interleaved ? qw / 2 : (qw / hs) * half;
+    const uint32_t kpairs = interleaved ? kvw / 2 : (kvw / hs) * half;
+    const uint32_t per_row = qpairs + kpairs + kvw;
+    uint32_t id = blockIdx.x * 256 + threadIdx.x;
+    if (id >= rows * per_row) return;
+    uint32_t row = id / per_row, p = id % per_row;
+    float* crow_k = kc + base + (size_t)slots[row] * kvw;
+    if (p >= qpairs + kpairs) {  // v copy
+        uint32_t e = p - qpairs - kpairs;
+        vc[base + (size_t)slots[row] * kvw + e] = v[(size_t)row * kvw + e];
+        return;
+    }
+    const float2* tr = tab + (size_t)pos[row] * half;
+    bool is_k = p >= qpairs;
+    uint32_t pp = is_k ? p - qpairs : p;
+    float* vec = is_k ? k + (size_t)row * kvw : q + (size_t)row * qw;
+    uint32_t i0, i1;
+    float2 cs;
+    if (interleaved) {
+        i0 = 2 * pp;
+        i1 = i0 + 1;
+        cs = tr[(i0 % hs) / 2];
+    } else {
+        uint32_t head = pp / half, i = pp % half;
+        i0 = head * hs + i;
+        i1 = i0 + half;
+        cs = tr[i];
+    }
+    float a = vec[i0], b = vec[i1];
+    float r0 = a * cs.x - b * cs.y;
+    float r1 = a * cs.y + b * cs.x;
+    vec[i0] = r0;
+    vec[i1] = r1;
+    if (is_k) {
+        crow_k[i0] = r0;
+        crow_k[i1] = r1;
+    }
+}
+
+hipError_t launch_rope_kv(hipStream_t st, float* q, float* k, const float* v, size_t qw, size_t kvw, size_t rows,
+                          const uint32_t* positions, const uint32_t* slots, const float2* table, size_t hs,
+                          int interleaved, float* kc, float* vc, size_t layer, size_t seq_len) {
+    size_t half = hs / 2;
+    size_t per_row = interleaved ? qw / 2 + kvw / 2 + kvw : (qw / hs) * half + (kvw / hs) * half + kvw;
+    size_t n = rows * per_row;
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_rope_kv, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, q, k, v, (uint32_t)qw,
+                       (uint32_t)kvw, (uint32_t)rows, positions, slots, table, (uint32_t)hs, interleaved, kc, vc,
+                       layer * seq_len * kvw);
     return hipGetLastError();
 }
 

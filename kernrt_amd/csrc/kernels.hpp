@@ -36,6 +36,23 @@ struct DevMatrix {  // device layout of one Q8 matrix
 hipError_t launch_quantize(hipStream_t st, const float* x, size_t rows, size_t k, size_t x_stride,
                            int8_t* q, float* s, uint16_t* h);
 
+// One launch over up to three matrices with the same in_dim and storage
+// (q/k/v, gate/up): output y[i] gets w[i]'s rows, row stride w[i]->n.
+hipError_t launch_project_set(hipStream_t st, int sem, const DevMatrix* const* w, float* const* y, int count,
+                              QuantAct x, size_t rows, int32_t* dbg_block_dots);
+
+// Fused decode/prefill steps (same arithmetic as the separate ops):
+// x += add (when add != null), out = rms_norm(x) and its Q8 quantization.
+hipError_t launch_add_rms_quant(hipStream_t st, float* x, const float* add, const float* w, float* out,
+                                size_t rows, size_t dim, float eps, int8_t* q, float* s, uint16_t* h);
+// g = silu(g) * u and its Q8 quantization, rows of `width`
+hipError_t launch_silu_quant(hipStream_t st, float* g, const float* u, size_t rows, size_t width, int8_t* q,
+                             float* s, uint16_t* h);
+// RoPE of q and k, then k and v into the cache at slots[row]
+hipError_t launch_rope_kv(hipStream_t st, float* q, float* k, const float* v, size_t qw, size_t kvw,
+                          size_t rows, const uint32_t* positions, const uint32_t* slots, const float2* table,
+                          size_t head_size, int interleaved, float* kc, float* vc, size_t layer, size_t seq_len);
+
 // y[m*ldy + n] for m < rows. Uses the GEMV path (rows <= 4) or the MFMA GEMM.
 hipError_t launch_project(hipStream_t st, int sem, const DevMatrix& w, QuantAct x, size_t rows,
                           float* y, size_t ldy, int32_t* dbg_block_dots);
@@ -54,7 +71,8 @@ struct DevWindow { uint32_t att_start, slot, shared_start, shared_end; };
 hipError_t launch_attention(hipStream_t st, const float* q, float* out, float* att, const float* kc,
                             const float* vc, size_t layer, const DevWindow* windows, size_t n_rows,
                             size_t max_count, size_t n_heads, size_t kv_mul, size_t head_size,
-                            size_t kv_dim, size_t seq_len, float scale);
+                            size_t kv_dim, size_t seq_len, float scale, int8_t* qo = nullptr,
+                            float* so = nullptr, uint16_t* ho = nullptr);
 hipError_t launch_add(hipStream_t st, float* dst, const float* src, size_t n);
 hipError_t launch_mul(hipStream_t st, float* out, const float* a, const float* b, size_t n,
                       int sequential);

@@ -3,6 +3,7 @@
 // issuing the same backend calls in the same order through the C ABI of
 // include/kernrt_hip.h, plus an on-device greedy loop.
 #include <hip/hip_runtime.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <algorithm>
@@ -48,6 +49,7 @@ struct krl_model {
     hipGraph_t graph = nullptr;  // one captured decode step
     hipGraphExec_t graph_exec = nullptr;
     uint64_t graph_epoch = 0;
+    bool fused = true;  // KERNRT_HIP_UNFUSED=1 runs the reference's op-by-op schedule
 };
 
 namespace {
@@ -82,6 +84,8 @@ int construct(krl_model* m, const krl_weights* w) {
     const krl_config& c = m->c;
     size_t kv_dim = c.n_kv_heads * c.head_dim, q_dim = c.n_heads * c.head_dim, dim = c.dim;
     KRC(m, kr_prepare(m->b, c.n_layers, kv_dim, c.seq_len));
+    const char* unfused = getenv("KERNRT_HIP_UNFUSED");
+    m->fused = !(unfused && unfused[0] == '1');
     for (size_t l = 0; l < c.n_layers; l++) {
         const krl_layer& L = w->layers[l];
         Norms n{};
@@ -163,9 +167,71 @@ Geometry geometry(const krl_config& c) {
     return g;
 }
 
+// The decode step with fused kernels: same values as the op-by-op schedule
+// below. Each residual add_in_place is folded into the rms_norm that follows
+// it, and every projection input is quantized by the kernel that produces it.
+int decode_step_fused(krl_model* m, size_t token, size_t pos, bool dev) {
+    kr_ctx* b = m->b;
+    Geometry g = geometry(m->c);
+    const uint32_t* s = m->step;
+    if (dev)
+        KRC(m, kri::embed_dev(b, s + 0, m->x, 0));
+    else
+        KRC(m, kr_embed(b, token, m->x, 0));
+    size_t positions[1] = {pos};
+    kr_window win{0, pos, 0, 0};
+    kr_buf pending = kri::KR_NO_BUF;  // the residual still to add into x
+    for (size_t l = 0; l < m->c.n_layers; l++) {
+        const Norms& n = m->norms[l];
+        KRC(m, kri::norm_quant(b, m->x, pending, n.att, m->xb, 1, g.dim, g.eps));
+        if (m->is_attention[l]) {
+            int qkv[3] = {KR_PROJ_Q, KR_PROJ_K, KR_PROJ_V};
+            kr_buf ys[3] = {m->q, m->k, m->v};
+            KRC(m, kri::project_q(b, l, qkv, ys, 3, 1));
+            if (n.has_q) KRC(m, kr_qk_norm(b, m->q, 1, g.q_dim, g.hs, n.q, g.eps));
+            if (n.has_k) KRC(m, kr_qk_norm(b, m->k, 1, g.kv_dim, g.hs, n.k, g.eps));
+            KRC(m, kri::rope_kv(b, m->q, m->k, m->v, g.q_dim, g.kv_dim, 1, dev ? nullptr : positions,
+                                dev ? nullptr : positions, dev ? s + 2 : nullptr, l, &g.rs));
+            if (g.hs % 32 == 0) {
+                KRC(m, kri::attention_quant(b, m->q, m->attn, m->att, l, dev ? nullptr : &win, 1,
+                                            dev ? s + 1 : nullptr, &g.as));
+            } else {  // head outputs are not whole Q8 blocks: quantize the row after
+                if (dev)
+                    KRC(m, kri::attention_dev(b, m->q, m->attn, m->att, l, s + 1, &g.as));
+                else
+                    KRC(m, kr_attention(b, m->q, m->attn, m->att, l, &win, 1, &g.as));
+                KRC(m, kr_quantize_rows(b, m->attn, 1, g.q_dim));
+            }
+            int o[1] = {KR_PROJ_O};
+            KRC(m, kri::project_q(b, l, o, &m->o, 1, 1));
+        } else {
+            int ci[1] = {KR_PROJ_CONV_IN};
+            KRC(m, kri::project_q(b, l, ci, &m->bcx, 1, 1));
+            KRC(m, kr_mul(b, m->h, 0, m->bcx, 0, m->bcx, 2 * g.dim, g.dim));
+            KRC(m, kr_conv_decode(b, m->co, m->h, (kr_buf)m->conv_kernels[l], (kr_buf)m->conv_state[l], g.dim,
+                                  m->conv_k[l]));
+            KRC(m, kr_mul(b, m->cy, 0, m->bcx, g.dim, m->co, 0, g.dim));
+            KRC(m, kr_project(b, l, KR_PROJ_CONV_OUT, m->cy, m->o, 1));
+        }
+        KRC(m, kri::norm_quant(b, m->x, m->o, n.ffn, m->xb, 1, g.dim, g.eps));
+        int gu[2] = {KR_PROJ_GATE, KR_PROJ_UP};
+        kr_buf gys[2] = {m->gate, m->up};
+        KRC(m, kri::project_q(b, l, gu, gys, 2, 1));
+        KRC(m, kri::silu_quant(b, m->gate, m->up, 1, g.hidden));
+        int dn[1] = {KR_PROJ_DOWN};
+        KRC(m, kri::project_q(b, l, dn, &m->mlp, 1, 1));
+        pending = m->mlp;
+    }
+    KRC(m, kri::norm_quant(b, m->x, pending, m->rms_final, m->xb, 1, g.dim, g.eps));
+    KRC(m, kri::logits_q(b, m->logits));
+    if (dev) KRC(m, kri::greedy_step(b, m->logits, m->c.vocab_size, m->step));
+    return KR_OK;
+}
+
 // One decode step, llama.rs:816-859 / lfm2.rs:414-474. With `dev`, the
 // token, position and window come from the device step record.
 int decode_step(krl_model* m, size_t token, size_t pos, bool dev) {
+    if (m->fused) return decode_step_fused(m, token, pos, dev);
     kr_ctx* b = m->b;
     Geometry g = geometry(m->c);
     const uint32_t* s = m->step;
@@ -255,6 +321,58 @@ int prefill_rows(krl_model* m, const std::vector<Row>& rows) {
     TRY(ensure_prefill(m, n_tok));
     PrefillBuffers& p = m->pb;
     for (size_t r = 0; r < n_tok; r++) KRC(m, kr_embed(b, rows[r].token, p.x, r * g.dim));
+    if (m->fused) {
+        // prefill_rows with the fused kernels (see decode_step_fused); the
+        // last residual add is applied here because the final norm reads one row
+        kr_buf pending = kri::KR_NO_BUF;
+        for (size_t l = 0; l < m->c.n_layers; l++) {
+            const Norms& n = m->norms[l];
+            KRC(m, kri::norm_quant(b, p.x, pending, n.att, p.xb, n_tok, g.dim, g.eps));
+            if (m->is_attention[l]) {
+                int qkv[3] = {KR_PROJ_Q, KR_PROJ_K, KR_PROJ_V};
+                kr_buf ys[3] = {p.q, p.k, p.v};
+                KRC(m, kri::project_q(b, l, qkv, ys, 3, n_tok));
+                if (n.has_q) KRC(m, kr_qk_norm(b, p.q, n_tok, g.q_dim, g.hs, n.q, g.eps));
+                if (n.has_k) KRC(m, kr_qk_norm(b, p.k, n_tok, g.kv_dim, g.hs, n.k, g.eps));
+                KRC(m, kri::rope_kv(b, p.q, p.k, p.v, g.q_dim, g.kv_dim, n_tok, positions.data(), slots.data(), nullptr,
+                                    l, &g.rs));
+                if (g.hs % 32 == 0) {
+                    KRC(m, kri::attention_quant(b, p.q, p.attn, p.att, l, windows.data(), windows.size(), nullptr,
+                                                &g.as));
+                } else {
+                    KRC(m, kr_attention(b, p.q, p.attn, p.att, l, windows.data(), windows.size(), &g.as));
+                    KRC(m, kr_quantize_rows(b, p.attn, n_tok, g.q_dim));
+                }
+                int o[1] = {KR_PROJ_O};
+                KRC(m, kri::project_q(b, l, o, &p.o, 1, n_tok));
+            } else {
+                int ci[1] = {KR_PROJ_CONV_IN};
+                KRC(m, kri::project_q(b, l, ci, &p.bcx, 1, n_tok));
+                for (size_t r = 0; r < n_tok; r++)
+                    KRC(m, kr_mul(b, p.h, r * g.dim, p.bcx, r * 3 * g.dim, p.bcx, r * 3 * g.dim + 2 * g.dim, g.dim));
+                size_t k = m->conv_k[l];
+                KRC(m, kr_conv_prefill(b, p.co, p.h, (kr_buf)m->conv_kernels[l], n_tok, g.dim, k));
+                if (m->conv_state[l] >= 0) {
+                    size_t take = std::min(n_tok, k - 1);
+                    KRC(m, kr_copy(b, p.h, (n_tok - take) * g.dim, (kr_buf)m->conv_state[l], (k - 1 - take) * g.dim,
+                                   take * g.dim));
+                }
+                for (size_t r = 0; r < n_tok; r++)
+                    KRC(m, kr_mul(b, p.cy, r * g.dim, p.bcx, r * 3 * g.dim + g.dim, p.co, r * g.dim, g.dim));
+                KRC(m, kr_project(b, l, KR_PROJ_CONV_OUT, p.cy, p.o, n_tok));
+            }
+            KRC(m, kri::norm_quant(b, p.x, p.o, n.ffn, p.xb, n_tok, g.dim, g.eps));
+            int gu[2] = {KR_PROJ_GATE, KR_PROJ_UP};
+            kr_buf gys[2] = {p.gate, p.up};
+            KRC(m, kri::project_q(b, l, gu, gys, 2, n_tok));
+            KRC(m, kri::silu_quant(b, p.gate, p.up, n_tok, g.hidden));
+            int dn[1] = {KR_PROJ_DOWN};
+            KRC(m, kri::project_q(b, l, dn, &p.o, 1, n_tok));
+            pending = p.o;
+        }
+        KRC(m, kr_add_in_place(b, p.x, pending, n_tok * g.dim));
+        return KR_OK;
+    }
     for (size_t l = 0; l < m->c.n_layers; l++) {
         const Norms& n = m->norms[l];
         KRC(m, kr_rms_norm(b, p.xb, p.x, n.att, n_tok, g.dim, g.eps));

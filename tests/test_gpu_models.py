@@ -16,6 +16,17 @@ from helpers import assert_bits_equal, gaussian_weights, gpu_model
 
 pytestmark = pytest.mark.gpu
 
+
+@pytest.fixture(autouse=True, params=["fused", "unfused"])
+def driver_mode(request, monkeypatch):
+    """Every model test runs through both driver schedules: the fused kernels
+    and the reference's op-by-op sequence of backend calls."""
+    if request.param == "unfused":
+        monkeypatch.setenv("KERNRT_HIP_UNFUSED", "1")
+    else:
+        monkeypatch.delenv("KERNRT_HIP_UNFUSED", raising=False)
+    return request.param
+
 PROMPT = [5, 11, 2, 30, 7, 7, 19, 1, 24]
 
 

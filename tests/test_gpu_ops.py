@@ -201,6 +201,12 @@ def test_attention_decode_windows():
     _attention_case(1024, 15, 5, 64, [(0, 0, 0, 0), (0, 511, 0, 0), (0, 767, 0, 0)], 15)
 
 
+@pytest.mark.parametrize("n_heads,n_kv,hs", [(32, 32, 64), (16, 8, 128), (16, 1, 64), (12, 1, 32), (24, 8, 64)])
+def test_attention_head_groupings(n_heads, n_kv, hs):
+    # kv_mul 1 (1.7B), 2 (Qwen3), 16 and 12 (multi-query), 3 (LFM2)
+    _attention_case(600, n_heads, n_kv, hs, [(0, 599, 0, 0), (0, 37, 0, 0), (10, 300, 0, 5)], n_heads + hs)
+
+
 def test_attention_shared_and_multi_windows():
     # prefill_shared / prefill_multi windows (llama.rs:552-647)
     _attention_case(64, 4, 2, 8, [(0, 2, 0, 0), (3, 4, 0, 3), (5, 8, 0, 3), (9, 9, 0, 3), (10, 20, 0, 0)], 16)

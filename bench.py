@@ -155,9 +155,10 @@ def bench_gemv(K, reps: int = 3):
                 cfg1_1536x576_us=cfg1_us, cfg1_bytes=1_003_776)
 
 
-def bench_prefill(K):
-    """128-token Q8_0 prefill at 1.7B projection shapes: time the projection
-    kernels (quantize + int8 GEMM) over all 24 layers."""
+def bench_prefill(K, reps: int = 2):
+    """128-token Q8_0 prefill at 1.7B projection shapes (`configs[2]`): the
+    int8 MFMA GEMM kernels alone (activations quantized beforehand), and the
+    projections with their activation quantization, over all 24 layers."""
     log("prefill: 128-row Q8_0 projections at 1.7B shapes")
     hip = K.open("hip")
     c = K.Config(**CFG3)
@@ -179,11 +180,50 @@ def bench_prefill(K):
     hip.synchronize()
     hip.timer_start()
     run()
-    ms = hip.timer_stop()
+    proj_ms = hip.timer_stop()
+    # GEMM kernels only: one shape at a time over the 24 layers' matrices
+    gemm_ms, per_shape = 0.0, {}
+    for i, (n, k) in enumerate(shapes):
+        hip.quantize_rows(xs[k], m_rows, k)
+        for l in range(c.n_layers):
+            hip.matmul_quantized(mats[l][i], ys[n], m_rows)
+        hip.synchronize()
+        hip.timer_start()
+        for _ in range(reps):
+            for l in range(c.n_layers):
+                hip.matmul_quantized(mats[l][i], ys[n], m_rows)
+        ms = hip.timer_stop() / reps
+        gemm_ms += ms
+        us = ms * 1e3 / c.n_layers
+        per_shape[f"{n}x{k}"] = dict(avg_us=us, tops=2 * m_rows * n * k / (us * 1e-6) / 1e12,
+                                     weight_gbs=n * k * (1 + 4 / 32) / (us * 1e-6) / 1e9)
     ops = 2 * m_rows * sum(n * k for n, k in shapes) * c.n_layers
-    tops = ops / (ms * 1e-3) / 1e12
+    tops = ops / (gemm_ms * 1e-3) / 1e12
     hip.close()
-    return dict(rows=m_rows, projection_ms=ms, int8_tops=tops, mfma_util=tops / INT8_PEAK_TOPS, ops=ops)
+    return dict(rows=m_rows, gemm_ms=gemm_ms, int8_tops=tops, mfma_util=tops / INT8_PEAK_TOPS, ops=ops,
+                projection_ms_with_quantize=proj_ms, per_shape=per_shape)
+
+
+def bench_prefill_model(K, n_tokens: int = 128, reps: int = 5):
+    """`configs[2]` end to end: a 128-token prefill of the synthetic
+    SmolLM2-1.7B-shaped Llama with Q8_0 weights, seeded random token ids.
+    As the reference's prefill_rate harness does, the first call is timed
+    apart and the best of the following calls is reported."""
+    log("prefill model: building the 1.7B-shaped Q8_0 model on the device")
+    hip, model, c = synthetic_model(K, CFG3, "q8_0", seed=7)
+    toks = [int(t) for t in np.random.default_rng(8).integers(0, c.vocab_size, size=n_tokens)]
+    t0 = time.perf_counter()
+    model.prefill(toks, 0)
+    first = time.perf_counter() - t0
+    best = None
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        model.prefill(toks, 0)
+        dt = time.perf_counter() - t0
+        best = dt if best is None else min(best, dt)
+    model.close()
+    hip.close()
+    return dict(tokens=n_tokens, tok_s=n_tokens / best, best_ms=best * 1e3, first_call_ms=first * 1e3)
 
 
 def bench_cpu_baseline(seconds_budget: float = 20.0):
@@ -255,7 +295,9 @@ def main():
         log(f"gemv: {res['gemv']['achieved_gbs']:.0f} GB/s")
     if args.only in (None, "prefill"):
         res["prefill"] = bench_prefill(K)
-        log(f"prefill: {res['prefill']['int8_tops']:.1f} TOPS")
+        log(f"prefill: {res['prefill']['int8_tops']:.1f} TOPS in the GEMM kernels")
+        res["prefill"]["model"] = bench_prefill_model(K)
+        log(f"prefill model: {res['prefill']['model']['tok_s']:.0f} tok/s")
     cpu = None if args.skip_cpu or args.only else bench_cpu_baseline()
 
     d, g, p = res.get("decode"), res.get("gemv"), res.get("prefill")

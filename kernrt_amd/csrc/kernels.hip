@@ -296,6 +296,8 @@ __global__ __launch_bounds__(256) void k_gemv(MatSet ms, QuantAct x, uint32_t K,
 // most kGemvActBytes) plus the per-block epilogue operands of its tile.
 static constexpr size_t kGemvLds = 64 * 1024;
 static constexpr size_t kGemvActBytes = 32 * 1024;
+// the GEMM stages 32 rows x K/32 f32 activation scales in LDS (128 KB at most)
+static constexpr size_t kGemmMaxK = 32768;
 
 static size_t gemv_rows_per_tile(size_t n, size_t k) {
     size_t r = 32768 / k;
@@ -326,8 +328,336 @@ static hipError_t gemv_launch(hipStream_t st, MatSet ms, size_t k, QuantAct x, i
     return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// Quantized GEMM on int8 MFMA (prefill and batched rows, M >= kGemmMinRows).
+//
+// v_mfma_i32_32x32x32_i8 multiplies a 32x32 int8 tile of activations by a
+// 32x32 int8 tile of weights over K = 32, exactly one Q8 block, so each
+// instruction yields the exact i32 block dots of a 32x32 output tile. Every
+// block's dots go straight into the reference's f32 epilogue, so each output
+// keeps the per-row path's rounding sequence (quant.rs:276-288 for Q8_0x4,
+// dot.rs:35-44 for Q8_0).
+//
+// Operand layout: lane l feeds row l % 32 of the activation tile and column
+// l % 32 of the weight tile with bytes 16*(l/32) .. +16 of the block; both
+// operands use the same byte map, so the integer sum covers the block once.
+// Accumulator v of lane l is output (row 8*(v/4) + 4*(l/32) + v%4, col l%32).
+//
+// Operands are staged through LDS in chunks of KC blocks: every row's KC*32
+// bytes are read with coalesced 16-byte loads (whole cache lines), several
+// chunks ahead in registers, and written to a double-buffered LDS tile whose
+// rows are padded by 16 bytes so that the fragment reads of 32 consecutive
+// rows spread over all banks. One barrier per chunk.
+//
+// Two workgroup shapes, both 4 waves:
+//  * four partial sums (Q8_0, dot.rs:35-44): t[b & 3] are independent chains,
+//    so the 4 waves share one 32x32 output tile and wave j runs chain j over
+//    the blocks b = j, j+4, ...; the chains meet in LDS and are summed in the
+//    reference order ((t0 + t1) + t2) + t3. This is a 4-way split of K that
+//    changes no rounding. KC = 8.
+//  * one FMA chain (Q8_0x4, quant.rs:276-288): the chain is serial, so each
+//    wave owns its own 32x32 tile over all of K; the workgroup tile is 32x128
+//    and the 4 waves share the activation chunk. KC = 4.
+//
+// Workgroups are numbered XCD-aware: the row tiles that share a column tile
+// of weights run on one XCD and share its L2.
+typedef int v16i __attribute__((ext_vector_type(16)));
+static constexpr size_t kGemmMinRows = 8;
+// chunks each thread keeps in flight in registers (even: LDS buffer parity)
+static constexpr int kGemmStages = 4;
+
+// Workgroup ids are dispatched round-robin over the 8 XCDs; map them so that
+// consecutive logical tiles run on one XCD.
+__device__ __forceinline__ uint32_t xcd_tile(uint32_t id, uint32_t count) {
+    const uint32_t per = count >> 3, rem = count & 7, xcd = id & 7, k = id >> 3;
+    return xcd < rem ? xcd * (per + 1) + k : rem * (per + 1) + (xcd - rem) * per + k;
+}
+
+// One column tile of a matrix in the set; tile_end counts column tiles of
+// width `cols`.
+struct GemmPos {
+    int mi;
+    uint32_t m0, n0;
+};
+__device__ __forceinline__ GemmPos gemm_pos(const MatSet& ms, uint32_t mtiles, uint32_t cols) {
+    const uint32_t L = xcd_tile(blockIdx.x, gridDim.x);
+    const uint32_t mt = L % mtiles, nt = L / mtiles;
+    const int mi = nt < ms.tile_end[0] ? 0 : (nt < ms.tile_end[1] ? 1 : 2);
+    const uint32_t tile = nt - (mi == 0 ? 0 : ms.tile_end[mi - 1]);
+    return GemmPos{mi, mt * 32, tile * cols};
+}
+
+__device__ __forceinline__ float gemm_wscale(int sem, const void* ws, size_t i) {
+    return sem == SEM_FOUR_PARTIALS_F32 ? ((const float*)ws)[i] : f16w(((const uint16_t*)ws)[i]);
+}
+
+// A scale as loaded: f32 bits, or f16 bits widened only when stored to LDS
+// (widening right after the load would make the load's wait immediate).
+__device__ __forceinline__ uint32_t scale_bits(bool f16, const void* p, size_t i) {
+    return f16 ? (uint32_t)((const uint16_t*)p)[i] : f2u(((const float*)p)[i]);
+}
+__device__ __forceinline__ float scale_value(bool f16, uint32_t bits) {
+    return f16 ? f16w((uint16_t)bits) : u2f(bits);
+}
+
+// The 16 activation scales of accumulator rows 8g + 4*half + (0..3).
+__device__ __forceinline__ void gemm_row_scales(float (&xs)[16], const float* col) {
+    const float4* q = (const float4*)col;
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+        const float4 f = q[2 * g];
+        xs[4 * g] = f.x, xs[4 * g + 1] = f.y, xs[4 * g + 2] = f.z, xs[4 * g + 3] = f.w;
+    }
+}
+
+// The chunk pipeline shared by both GEMM kernels. At chunk c, the register
+// stage (c + 1) % NS holds chunk c + 1 and LDS buffer c & 1 holds chunk c.
+// The chunk count is padded to a multiple of NS and every load and store is
+// unconditional (loads clamp to the last chunk, compute skips blocks past
+// the end), so all paths issue the same loads and each wait covers only the
+// chunk about to be stored.
+template <int NS, typename Stage, typename Load, typename Store, typename Compute>
+__device__ __forceinline__ void gemm_pipeline(uint32_t nchunks, Load&& gload, Store&& lstore, Compute&& compute) {
+    static_assert(NS % 2 == 0, "the LDS buffer parity follows the register stage");
+    Stage st[NS];
+#pragma unroll
+    for (int s = 0; s < NS; s++) gload(st[s], s);
+    lstore(st[0], 0);
+    gload(st[0], NS);
+    __syncthreads();
+    const uint32_t steps = (nchunks + NS - 1) / NS * NS;
+    for (uint32_t c0 = 0; c0 < steps; c0 += NS) {
+#pragma unroll
+        for (int u = 0; u < NS; u++) {
+            compute(u & 1, c0 + u);
+            lstore(st[(u + 1) % NS], (u + 1) & 1);
+            gload(st[(u + 1) % NS], c0 + u + 1 + NS);
+            __syncthreads();
+        }
+    }
+}
+
+template <int SEM, bool DBG>
+__global__ __launch_bounds__(256, 2) void k_gemm_four(MatSet ms, QuantAct x, uint32_t M, uint32_t K,
+                                                      uint32_t mtiles, int32_t* __restrict__ dbg) {
+    constexpr int KC = 8, ROW = KC * 32 + 16, NS = kGemmStages;
+    __shared__ __align__(16) int8_t sA[2][32 * ROW];
+    __shared__ __align__(16) int8_t sB[2][32 * ROW];
+    __shared__ __align__(16) float sX[2][KC * 32];  // [block][row]
+    __shared__ __align__(16) float sW[2][KC * 32];  // [block][col]
+    const uint32_t nb = K >> 5, nchunks = (nb + KC - 1) / KC;
+    const GemmPos p = gemm_pos(ms, mtiles, 32);
+    const int8_t* __restrict__ W = ms.q[p.mi];
+    const void* __restrict__ WS = ms.s[p.mi];
+    const uint32_t N = ms.n[p.mi];
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: block checks branch on SGPRs
+    const uint32_t r = lane & 31, half = lane >> 5;
+
+    // loader map: operand pieces (row tid/16 and tid/16 + 16, 16-byte column
+    // tid%16), scale entries (row or column tid/8, block tid%8). Rows past M
+    // or N read the last row; their outputs are never stored.
+    const uint32_t lr = tid >> 4, lc = (tid & 15) * 16, sr = tid >> 3, sb = tid & 7;
+    const int8_t* ga0 = x.q + (size_t)min(p.m0 + lr, M - 1) * K;
+    const int8_t* ga1 = x.q + (size_t)min(p.m0 + lr + 16, M - 1) * K;
+    const int8_t* gb0 = W + (size_t)min(p.n0 + lr, N - 1) * K;
+    const int8_t* gb1 = W + (size_t)min(p.n0 + lr + 16, N - 1) * K;
+    const float* gx = x.s + (size_t)min(p.m0 + sr, M - 1) * nb;
+    const size_t gw = (size_t)min(p.n0 + sr, N - 1) * nb;
+    constexpr bool WF16 = SEM == SEM_FOUR_PARTIALS_F16;
+
+    struct Stage {
+        v4i a0, a1, b0, b1;
+        float xs;
+        uint32_t ws;
+    };
+    auto gload = [&](Stage& st, uint32_t c) {
+        c = c < nchunks ? c : nchunks - 1;
+        const uint32_t col = min(c * KC * 32 + lc, K - 16);  // past the row end: a piece no block uses
+        st.a0 = *(const v4i*)(ga0 + col), st.a1 = *(const v4i*)(ga1 + col);
+        st.b0 = *(const v4i*)(gb0 + col), st.b1 = *(const v4i*)(gb1 + col);
+        const uint32_t blk = min(c * KC + sb, nb - 1);
+        st.xs = gx[blk];
+        st.ws = scale_bits(WF16, WS, gw + blk);
+    };
+    auto lstore = [&](const Stage& st, int buf) {
+        *(v4i*)(sA[buf] + lr * ROW + lc) = st.a0, *(v4i*)(sA[buf] + (lr + 16) * ROW + lc) = st.a1;
+        *(v4i*)(sB[buf] + lr * ROW + lc) = st.b0, *(v4i*)(sB[buf] + (lr + 16) * ROW + lc) = st.b1;
+        sX[buf][sb * 32 + sr] = st.xs;
+        sW[buf][sb * 32 + sr] = scale_value(WF16, st.ws);
+    };
+
+    const v16i zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    float t[16];
+#pragma unroll
+    for (int v = 0; v < 16; v++) t[v] = 0.0f;
+    // wave j: blocks j and j + 4 of each chunk, i.e. chain t[j] in order
+    auto compute = [&](int buf, uint32_t c) {
+#pragma unroll
+        for (int i = 0; i < KC / 4; i++) {
+            const uint32_t blk = wave + 4 * i, b = c * KC + blk;
+            if (b >= nb) break;
+            const v4i a = *(const v4i*)(sA[buf] + r * ROW + blk * 32 + 16 * half);
+            const v4i bq = *(const v4i*)(sB[buf] + r * ROW + blk * 32 + 16 * half);
+            const v16i d = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bq, zero, 0, 0, 0);
+            const float w = sW[buf][blk * 32 + r];
+            float xs[16];
+            gemm_row_scales(xs, sX[buf] + blk * 32 + 4 * half);
+            if (DBG && p.n0 + r < N) {
+#pragma unroll
+                for (int v = 0; v < 16; v++) {
+                    const uint32_t m = p.m0 + 8 * (v >> 2) + 4 * half + (v & 3);
+                    if (m < M) dbg[((size_t)m * N + p.n0 + r) * nb + b] = d[v];
+                }
+            }
+            // dot.rs: t[b & 3] += (sa * sb) * (isum as f32), with sa the weight scale
+#pragma unroll
+            for (int v = 0; v < 16; v++) t[v] += (w * xs[v]) * (float)d[v];
+        }
+    };
+
+    gemm_pipeline<NS, Stage>(nchunks, gload, lstore, compute);
+
+    float* part = (float*)&sA[0][0];  // [4 waves][16][64], after the last barrier
+#pragma unroll
+    for (int v = 0; v < 16; v++) part[(wave * 16 + v) * 64 + lane] = t[v];
+    __syncthreads();
+    float* Y = ms.y[p.mi];
+    const uint32_t ld = ms.ld[p.mi];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t o = tid + 256 * i;  // (v, lane)
+        const uint32_t v = o >> 6, l = o & 63;
+        const uint32_t m = p.m0 + 8 * (v >> 2) + 4 * (l >> 5) + (v & 3), n = p.n0 + (l & 31);
+        if (m >= M || n >= N) continue;
+        const float sum = ((part[(0 * 16 + v) * 64 + l] + part[(1 * 16 + v) * 64 + l]) + part[(2 * 16 + v) * 64 + l]) +
+                          part[(3 * 16 + v) * 64 + l];
+        Y[(size_t)m * ld + n] = sum;
+    }
+}
+
+template <bool DBG>
+__global__ __launch_bounds__(256, 2) void k_gemm_chain(MatSet ms, QuantAct x, uint32_t M, uint32_t K,
+                                                       uint32_t mtiles, int32_t* __restrict__ dbg) {
+    constexpr int KC = 4, ROW = KC * 32 + 16, NS = kGemmStages;
+    __shared__ __align__(16) int8_t sA[2][32 * ROW];
+    __shared__ __align__(16) int8_t sB[2][128 * ROW];
+    __shared__ __align__(16) float sX[2][KC * 32];   // [block][row]
+    __shared__ __align__(16) float sW[2][KC * 128];  // [block][col]
+    const uint32_t nb = K >> 5, nchunks = (nb + KC - 1) / KC;
+    const GemmPos p = gemm_pos(ms, mtiles, 128);
+    const int8_t* __restrict__ W = ms.q[p.mi];
+    const uint16_t* __restrict__ WS = (const uint16_t*)ms.s[p.mi];
+    const uint32_t N = ms.n[p.mi];
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: block checks branch on SGPRs
+    const uint32_t r = lane & 31, half = lane >> 5;
+    const uint32_t n = p.n0 + 32 * wave + r;       // this lane's output column
+    const bool active = p.n0 + 32 * wave < N;       // uniform per wave
+
+    // loader map: activation piece (row tid/8, 16-byte column tid%8), weight
+    // pieces (rows tid/8 + 32i), activation scale (row (tid/4)%32, block
+    // tid%4; the upper half of the workgroup repeats the lower), weight
+    // scales (columns tid/4 + 64i, block tid%4).
+    const uint32_t lr = tid >> 3, lc = (tid & 7) * 16, xr = (tid >> 2) & 31, wc = tid >> 2, sb = tid & 3;
+    const int8_t* ga = x.q + (size_t)min(p.m0 + lr, M - 1) * K;
+    const int8_t* gb[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) gb[i] = W + (size_t)min(p.n0 + lr + 32 * i, N - 1) * K;
+    const uint16_t* gx = x.h + (size_t)min(p.m0 + xr, M - 1) * nb;
+    const size_t gw0 = (size_t)min(p.n0 + wc, N - 1) * nb, gw1 = (size_t)min(p.n0 + wc + 64, N - 1) * nb;
+
+    struct Stage {
+        v4i a, b[4];
+        uint32_t xs, w0, w1;
+    };
+    auto gload = [&](Stage& st, uint32_t c) {
+        c = c < nchunks ? c : nchunks - 1;
+        const uint32_t col = min(c * KC * 32 + lc, K - 16);  // past the row end: a piece no block uses
+        st.a = *(const v4i*)(ga + col);
+#pragma unroll
+        for (int i = 0; i < 4; i++) st.b[i] = *(const v4i*)(gb[i] + col);
+        const uint32_t blk = min(c * KC + sb, nb - 1);
+        st.xs = gx[blk];
+        st.w0 = WS[gw0 + blk], st.w1 = WS[gw1 + blk];
+    };
+    auto lstore = [&](const Stage& st, int buf) {
+        *(v4i*)(sA[buf] + lr * ROW + lc) = st.a;
+#pragma unroll
+        for (int i = 0; i < 4; i++) *(v4i*)(sB[buf] + (lr + 32 * i) * ROW + lc) = st.b[i];
+        sX[buf][sb * 32 + xr] = f16w((uint16_t)st.xs);
+        sW[buf][sb * 128 + wc] = f16w((uint16_t)st.w0);
+        sW[buf][sb * 128 + wc + 64] = f16w((uint16_t)st.w1);
+    };
+
+    const v16i zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    float slot[16];
+#pragma unroll
+    for (int v = 0; v < 16; v++) slot[v] = 0.0f;
+    auto compute = [&](int buf, uint32_t c) {
+        if (!active) return;
+#pragma unroll
+        for (int blk = 0; blk < KC; blk++) {
+            const uint32_t b = c * KC + blk;
+            if (b >= nb) break;
+            const v4i a = *(const v4i*)(sA[buf] + r * ROW + blk * 32 + 16 * half);
+            const v4i bq = *(const v4i*)(sB[buf] + (32 * wave + r) * ROW + blk * 32 + 16 * half);
+            const v16i d = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bq, zero, 0, 0, 0);
+            const float w = sW[buf][blk * 128 + 32 * wave + r];
+            float xs[16];
+            gemm_row_scales(xs, sX[buf] + blk * 32 + 4 * half);
+            if (DBG && n < N) {
+#pragma unroll
+                for (int v = 0; v < 16; v++) {
+                    const uint32_t m = p.m0 + 8 * (v >> 2) + 4 * half + (v & 3);
+                    if (m < M) dbg[((size_t)m * N + n) * nb + b] = d[v];
+                }
+            }
+            // quant.rs: slot = (isum as f32).mul_add(f16w(ws) * f16w(xs), slot)
+#pragma unroll
+            for (int v = 0; v < 16; v++) slot[v] = __builtin_fmaf((float)d[v], w * xs[v], slot[v]);
+        }
+    };
+
+    gemm_pipeline<NS, Stage>(nchunks, gload, lstore, compute);
+    if (!active || n >= N) return;
+    float* Y = ms.y[p.mi];
+    const uint32_t ld = ms.ld[p.mi];
+#pragma unroll
+    for (int v = 0; v < 16; v++) {
+        const uint32_t m = p.m0 + 8 * (v >> 2) + 4 * half + (v & 3);
+        if (m < M) Y[(size_t)m * ld + n] = slot[v];
+    }
+}
+
+template <int SEM>
+static hipError_t gemm_launch(hipStream_t st, MatSet ms, size_t k, QuantAct x, size_t rows, int32_t* dbg) {
+    const uint32_t cols = SEM == SEM_FMA_CHAIN ? 128 : 32;
+    uint32_t total = 0;
+    for (int i = 0; i < 3; i++) {
+        if (i < ms.count) total += (uint32_t)((ms.n[i] + cols - 1) / cols);
+        ms.tile_end[i] = total;
+    }
+    const uint32_t mtiles = (uint32_t)((rows + 31) / 32);
+    dim3 grid(total * mtiles);
+    const uint32_t m = (uint32_t)rows, kk = (uint32_t)k;
+    if (SEM == SEM_FMA_CHAIN) {
+        if (dbg)
+            hipLaunchKernelGGL(k_gemm_chain<true>, grid, dim3(256), 0, st, ms, x, m, kk, mtiles, dbg);
+        else
+            hipLaunchKernelGGL(k_gemm_chain<false>, grid, dim3(256), 0, st, ms, x, m, kk, mtiles, dbg);
+    } else {
+        if (dbg)
+            hipLaunchKernelGGL((k_gemm_four<SEM, true>), grid, dim3(256), 0, st, ms, x, m, kk, mtiles, dbg);
+        else
+            hipLaunchKernelGGL((k_gemm_four<SEM, false>), grid, dim3(256), 0, st, ms, x, m, kk, mtiles, dbg);
+    }
+    return hipGetLastError();
+}
+
 template <int SEM>
 static hipError_t gemv_rows(hipStream_t st, const MatSet& ms, size_t k, QuantAct x, size_t rows, int32_t* dbg) {
+    if (rows >= kGemmMinRows && k <= kGemmMaxK) return gemm_launch<SEM>(st, ms, k, x, rows, dbg);
     size_t nb = k / 32;
     size_t done = 0;
     while (done < rows) {

@@ -86,6 +86,39 @@ def test_matmul_matches_cpu_project(hip, storage, shape, rows):
     hip.free_matrix(mat)
 
 
+# Row counts that take the int8 MFMA GEMM: partial and whole 32-row tiles.
+@pytest.mark.parametrize("storage", ["q8_0", "q8_0x4"])
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("rows", [8, 33, 128])
+def test_gemm_matches_cpu_project(hip, storage, shape, rows):
+    test_matmul_matches_cpu_project(hip, storage, shape, rows)
+
+
+@pytest.mark.parametrize("storage", ["q8_0", "q8_0x4"])
+@pytest.mark.parametrize("shape", [(1536, 576), (100, 96), (36, 8192), (260, 128)])
+def test_gemm_block_dots_are_exact(hip, storage, shape):
+    n, k = shape
+    if storage == "q8_0x4" and n % 4:
+        pytest.skip("Q8_0x4 needs out_dim % 4 == 0")
+    rows = 37
+    rng = np.random.default_rng(n * 29 + k)
+    m = O.Matrix(rng.normal(0, 0.02, size=(n, k)).astype(np.float32), storage)
+    x = (rng.normal(size=(rows, k)) * rng.uniform(0.01, 10, size=(rows, 1))).astype(np.float32)
+    x[3] = 0.0
+    mat = hip.upload_matrix(product_matrix(m))
+    got = hip.dbg_block_dots(mat, hip.upload(x), rows, n, k)
+    xq = np.concatenate([O.quantize(x[r])[0] for r in range(rows)])
+    assert np.array_equal(got, m.block_dots(xq))
+    hip.free_matrix(mat)
+
+
+@pytest.mark.parametrize("storage", ["q8_0", "q8_0x4"])
+@pytest.mark.parametrize("shape", [(2048, 8192), (8192, 2048)])
+def test_gemm_at_1p7b_shapes(hip, storage, shape):
+    # SmolLM2-1.7B down and gate/up projections with a 128-token prompt
+    test_matmul_matches_cpu_project(hip, storage, shape, 128)
+
+
 @pytest.mark.parametrize("storage", ["q8_0", "q8_0x4"])
 def test_classify_matches_cpu_logits(hip, storage):
     rng = np.random.default_rng(11)

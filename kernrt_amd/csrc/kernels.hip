@@ -192,13 +192,18 @@ hipError_t launch_quantize(hipStream_t st, const float* x, size_t rows, size_t k
 // Quantized GEMV (M <= 4 activation rows).
 //
 // A workgroup owns a tile of R consecutive weight rows, i.e. R*K contiguous
-// bytes of the row-major int8 matrix, streamed with 16-byte loads that are
-// fully coalesced across the wave (one wave load = 1 KiB). A lane pair holds
-// one 32-byte Q8 block: each lane does four v_dot4_i32_i8 on its half and the
-// pair sums with one lane swap, so the per-block i32 is exact. The even lane
-// turns it into the reference's per-block epilogue operand and parks it in
-// LDS; after a barrier one lane per (row, output) walks the blocks in order,
-// reproducing the reference's f32 accumulation sequence exactly.
+// bytes of the row-major int8 matrix. Thread t takes the 16-byte chunks
+// t, t+256, t+512, ... of the tile, so every wave load is 1 KiB, fully
+// coalesced. All of a thread's loads are issued before any is used -- its
+// weight chunks, the matching activation chunks and the two scales of each
+// chunk's block -- and none sits behind a branch, so a tile costs one memory
+// round trip. A lane pair holds one 32-byte Q8 block: each lane does four
+// v_dot4_i32_i8 on its half and the pair sums with one lane swap, so the
+// per-block i32 is exact. The even lane turns it into the reference's
+// epilogue operand and parks it in LDS; after one barrier the f32 chains run
+// in the reference order: one lane per output for the FMA chain
+// (quant.rs:276-288), four lanes per output for the four partial sums
+// (dot.rs:35-44), which are joined as ((t0 + t1) + t2) + t3.
 //
 // One launch may cover up to three matrices with the same K (q/k/v, or
 // gate/up): the grid is the concatenation of their tile ranges.
@@ -212,68 +217,117 @@ struct MatSet {
     int count;
 };
 
-template <int SEM, int M>
-__global__ __launch_bounds__(256) void k_gemv(MatSet ms, QuantAct x, uint32_t K, uint32_t R,
-                                              int32_t* __restrict__ dbg) {
-    extern __shared__ __align__(16) char smem[];
+// A scale as loaded: f32 bits, or f16 bits that are widened only where the
+// value is used (widening right after the load would make its wait immediate).
+__device__ __forceinline__ uint32_t scale_bits(bool f16, const void* p, size_t i) {
+    return f16 ? (uint32_t)((const uint16_t*)p)[i] : f2u(((const float*)p)[i]);
+}
+__device__ __forceinline__ float scale_value(bool f16, uint32_t bits) {
+    return f16 ? f16w((uint16_t)bits) : u2f(bits);
+}
+
+// LDS layout of the epilogue operands of one output (one weight row for one
+// activation row). Four partial sums: residue j of the blocks at
+// [j*q4p, j*q4p + count_j), q4p = ceil(nb/4) + 1 (odd, so the four lanes
+// of an output and neighbouring outputs hit different banks). FMA chain:
+// (isum, scale) pairs, nb + 1 of them per output.
+__host__ __device__ inline uint32_t gemv_q4p(uint32_t nb) { return (nb + 3) / 4 + 1; }
+__host__ __device__ inline uint32_t gemv_out_floats(int sem, uint32_t nb) {
+    return sem == SEM_FMA_CHAIN ? 2 * (nb + 1) : 4 * gemv_q4p(nb);
+}
+
+// Serial f32 sum of n LDS values in order, with loads kept ahead.
+__device__ __forceinline__ float lds_sum(const float* e, uint32_t n) {
+    float t = 0.0f;
+    uint32_t i = 0;
+    for (; i + 8 <= n; i += 8) {
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[j] = e[i + j];
+#pragma unroll
+        for (int j = 0; j < 8; j++) t += v[j];
+    }
+    for (; i < n; i++) t += e[i];
+    return t;
+}
+
+template <int SEM, int M, int CPT>
+__global__ __launch_bounds__(256) void k_gemv(MatSet ms, QuantAct x, uint32_t K, uint32_t R, uint32_t step_rows,
+                                              uint32_t step_cols, int32_t* __restrict__ dbg) {
+    extern __shared__ __align__(16) float res[];
     const int mi = blockIdx.x < ms.tile_end[0] ? 0 : (blockIdx.x < ms.tile_end[1] ? 1 : 2);
     const uint32_t tile = blockIdx.x - (mi == 0 ? 0 : ms.tile_end[mi - 1]);
     const int8_t* __restrict__ W = ms.q[mi];
     const void* __restrict__ WS = ms.s[mi];
     const uint32_t N = ms.n[mi];
-    const uint32_t nb = K >> 5;
+    const uint32_t nb = K >> 5, kc = K >> 4;  // blocks and 16-byte chunks per row
     const uint32_t row0 = tile * R;
     const uint32_t rows = min(R, N - row0);
-    int8_t* xs_l = (int8_t*)smem;         // [M][K]
-    float* res = (float*)(smem + M * K);  // per (m, block) epilogue operands
-    const uint32_t nblk = rows * nb;      // blocks in this tile
-
-    for (uint32_t i = threadIdx.x; i < M * K / 16; i += 256) ((int4*)xs_l)[i] = ((const int4*)x.q)[i];
-    __syncthreads();
-
+    const uint32_t C = rows * kc;  // chunks in this tile
+    const uint32_t tid = threadIdx.x;
+    constexpr bool WF16 = SEM != SEM_FOUR_PARTIALS_F32;
+    constexpr bool XF16 = SEM == SEM_FMA_CHAIN;
     const int8_t* wt = W + (size_t)row0 * K;
-    const uint32_t C = nblk * 2;  // 16-byte chunks
-    const bool even = (threadIdx.x & 1) == 0;
-    constexpr int U = 4;
-    const uint32_t iters = (C + 256 * U - 1) / (256 * U);
-    for (uint32_t it = 0; it < iters; it++) {
-        v4i wv[U];
+
+    // chunk tid + 256u sits at (row, col) of the tile; 256 chunks further is
+    // (step_rows, step_cols) further, with carry
+    uint32_t row = tid / kc, col = tid - (tid / kc) * kc;
+    v4i wv[CPT], xv[CPT][M];
+    uint32_t wsb[CPT], xsb[CPT][M], rowu[CPT], blku[CPT];
 #pragma unroll
-        for (int u = 0; u < U; u++) {
-            uint32_t c = threadIdx.x + 256 * (it * U + u);
-            wv[u] = c < C ? __builtin_nontemporal_load((const v4i*)(wt + 16 * (size_t)c)) : v4i{0, 0, 0, 0};
+    for (int u = 0; u < CPT; u++) {
+        const bool in = tid + 256 * u < C;
+        const uint32_t rr = in ? row : rows - 1, cc = in ? col : kc - 1;  // clamped: no branch
+        const uint32_t b = cc >> 1;
+        rowu[u] = rr, blku[u] = b;
+        wv[u] = __builtin_nontemporal_load((const v4i*)(wt + (size_t)rr * K + cc * 16));
+        wsb[u] = scale_bits(WF16, WS, (size_t)(row0 + rr) * nb + b);
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            xv[u][m] = *(const v4i*)(x.q + (size_t)m * K + cc * 16);
+            xsb[u][m] = XF16 ? (uint32_t)x.h[m * nb + b] : f2u(x.s[m * nb + b]);
         }
+        col += step_cols;
+        row += step_rows;
+        if (col >= kc) col -= kc, row += 1;
+    }
+
+    const uint32_t per = gemv_out_floats(SEM, nb), q4p = gemv_q4p(nb);
+    const uint32_t dummy = M * rows * per;  // LDS slot for the stores of lanes that own no block
+    const bool even = (tid & 1) == 0;
 #pragma unroll
-        for (int u = 0; u < U; u++) {
-            uint32_t c = threadIdx.x + 256 * (it * U + u);
-            bool valid = c < C;
-            uint32_t col = valid ? (16 * c) % K : 0;
-            uint32_t g = c >> 1;  // block index within the tile
-            uint32_t r = valid ? g / nb : 0, b = valid ? g % nb : 0;
+    for (int u = 0; u < CPT; u++) {
+        const bool valid = tid + 256 * u < C;
+        const uint32_t r = rowu[u], b = blku[u];
+        const float ws = scale_value(WF16, wsb[u]);
 #pragma unroll
-            for (int m = 0; m < M; m++) {
-                v4i xv = *(const v4i*)(xs_l + m * K + col);
-                int acc = 0;
-                acc = __builtin_amdgcn_sdot4(wv[u].x, xv.x, acc, false);
-                acc = __builtin_amdgcn_sdot4(wv[u].y, xv.y, acc, false);
-                acc = __builtin_amdgcn_sdot4(wv[u].z, xv.z, acc, false);
-                acc = __builtin_amdgcn_sdot4(wv[u].w, xv.w, acc, false);
-                int isum = acc + __shfl_xor(acc, 1);
-                if (valid && even) {
-                    size_t wsi = (size_t)(row0 + r) * nb + b;
-                    uint32_t xsi = m * nb + b;
-                    if (dbg) dbg[((size_t)m * N + row0 + r) * nb + b] = isum;
-                    if (SEM == SEM_FMA_CHAIN) {
-                        float xsf = f16w(x.h[xsi]);
-                        float ws = f16w(((const uint16_t*)WS)[wsi]) * xsf;
-                        ((float2*)res)[m * nblk + g] = make_float2((float)isum, ws);
-                    } else {
-                        float sa = SEM == SEM_FOUR_PARTIALS_F32 ? ((const float*)WS)[wsi]
-                                                                : f16w(((const uint16_t*)WS)[wsi]);
-                        float sb = x.s[xsi];
-                        res[m * nblk + g] = (sa * sb) * (float)isum;
-                    }
-                }
+        for (int m = 0; m < M; m++) {
+            int acc = 0;
+            acc = __builtin_amdgcn_sdot4(wv[u].x, xv[u][m].x, acc, false);
+            acc = __builtin_amdgcn_sdot4(wv[u].y, xv[u][m].y, acc, false);
+            acc = __builtin_amdgcn_sdot4(wv[u].z, xv[u][m].z, acc, false);
+            acc = __builtin_amdgcn_sdot4(wv[u].w, xv[u][m].w, acc, false);
+            const int isum = acc + __shfl_xor(acc, 1);
+            // every lane forms the operand and stores it (lanes that own no
+            // block to a dummy slot): with no branch around the use, the
+            // scale loads stay at the top of the kernel
+            float v0, v1 = 0.0f;
+            if (SEM == SEM_FMA_CHAIN) {
+                // quant.rs: slot = (isum as f32).mul_add(f16w(ws) * f16w(xs), slot)
+                v0 = (float)isum;
+                v1 = ws * f16w((uint16_t)xsb[u][m]);
+            } else {
+                // dot.rs: t[b & 3] += (sa * sb) * (isum as f32)
+                v0 = (ws * u2f(xsb[u][m])) * (float)isum;
+            }
+            const bool own = valid && even;
+            if (dbg && own) dbg[((size_t)m * N + row0 + r) * nb + b] = isum;
+            const uint32_t base = (m * rows + r) * per;
+            if (SEM == SEM_FMA_CHAIN) {
+                float2* o = (float2*)(res + (own ? base + 2 * b : dummy));
+                *o = make_float2(v0, v1);
+            } else {
+                res[own ? base + (b & 3) * q4p + (b >> 2) : dummy] = v0;
             }
         }
     }
@@ -281,50 +335,71 @@ __global__ __launch_bounds__(256) void k_gemv(MatSet ms, QuantAct x, uint32_t K,
 
     float* Y = ms.y[mi];
     const uint32_t ld = ms.ld[mi];
-    for (uint32_t t = threadIdx.x; t < M * rows; t += 256) {
-        uint32_t m = t / rows, r = t % rows;
-        float out;
-        if (SEM == SEM_FMA_CHAIN)
-            out = seq_fma((const float2*)res + m * nblk + r * nb, nb);
-        else
-            out = seq_four(res + m * nblk + r * nb, nb);
-        Y[(size_t)m * ld + row0 + r] = out;
+    const uint32_t outs = M * rows;
+    if (SEM == SEM_FMA_CHAIN) {
+        for (uint32_t o = tid; o < outs; o += 256) {
+            const uint32_t m = o / rows, r = o - m * rows;
+            Y[(size_t)m * ld + row0 + r] = seq_fma((const float2*)(res + (size_t)o * per), nb);
+        }
+    } else {
+        // lanes 4o .. 4o+3 run the four chains of output o
+        for (uint32_t base = 0; base < 4 * outs; base += 256) {
+            const uint32_t i = base + tid, o = i >> 2, j = i & 3;
+            float t = 0.0f;
+            if (o < outs && j < nb) t = lds_sum(res + (size_t)o * per + j * q4p, (nb - j + 3) / 4);
+            const uint32_t lane0 = (tid & 63) & ~3u;
+            const float t0 = __shfl(t, lane0), t1 = __shfl(t, lane0 + 1), t2 = __shfl(t, lane0 + 2),
+                        t3 = __shfl(t, lane0 + 3);
+            if (o < outs && j == 0) {
+                const uint32_t m = o / rows, r = o - m * rows;
+                Y[(size_t)m * ld + row0 + r] = ((t0 + t1) + t2) + t3;
+            }
+        }
     }
 }
 
-// LDS budget of one GEMV workgroup: the staged activations (M*K bytes, at
-// most kGemvActBytes) plus the per-block epilogue operands of its tile.
-static constexpr size_t kGemvLds = 64 * 1024;
-static constexpr size_t kGemvActBytes = 32 * 1024;
-// the GEMM stages 32 rows x K/32 f32 activation scales in LDS (128 KB at most)
-static constexpr size_t kGemmMaxK = 32768;
-
+// Rows per workgroup tile: about 4 chunks per thread, but at least ~2 tiles
+// per CU when the matrix allows.
 static size_t gemv_rows_per_tile(size_t n, size_t k) {
-    size_t r = 32768 / k;
+    const size_t kc = k / 16;
+    size_t r = 1024 / kc;
     if (r < 1) r = 1;
-    size_t cap = n / 512;  // keep >= ~2 tiles per CU when the matrix allows
+    size_t cap = n / 512;
     if (cap < 1) cap = 1;
     if (r > cap) r = cap;
     if (r > 256) r = 256;
     return r;
 }
 
+template <int SEM, int M, int CPT>
+static void gemv_go(hipStream_t st, const MatSet& ms, QuantAct x, uint32_t k, uint32_t R, uint32_t total,
+                    size_t lds, int32_t* dbg) {
+    const uint32_t kc = k / 16;
+    hipLaunchKernelGGL((k_gemv<SEM, M, CPT>), dim3(total), dim3(256), lds, st, ms, x, k, R, 256 / kc, 256 % kc,
+                       dbg);
+}
+
 template <int SEM, int M>
 static hipError_t gemv_launch(hipStream_t st, MatSet ms, size_t k, QuantAct x, int32_t* dbg) {
-    size_t nb = k / 32;
-    size_t per_row = (SEM == SEM_FMA_CHAIN ? 8 : 4) * M * nb;  // LDS bytes of epilogue operands per row
     size_t n_max = 0;
     for (int i = 0; i < ms.count; i++) n_max = ms.n[i] > n_max ? ms.n[i] : n_max;
-    size_t R = gemv_rows_per_tile(n_max, k);
-    size_t r_cap = (kGemvLds - M * k) / per_row;
-    if (R > r_cap) R = r_cap;
+    const size_t R = gemv_rows_per_tile(n_max, k);
     uint32_t total = 0;
     for (int i = 0; i < 3; i++) {
         if (i < ms.count) total += (uint32_t)((ms.n[i] + R - 1) / R);
         ms.tile_end[i] = total;
     }
-    size_t lds = M * k + per_row * R;
-    hipLaunchKernelGGL((k_gemv<SEM, M>), dim3(total), dim3(256), lds, st, ms, x, (uint32_t)k, (uint32_t)R, dbg);
+    const size_t lds = ((size_t)M * R * gemv_out_floats(SEM, (uint32_t)(k / 32)) + 2) * sizeof(float);
+    const size_t chunks = R * (k / 16);
+    const size_t cpt = (chunks + 255) / 256;
+    if (cpt <= 2)
+        gemv_go<SEM, M, 2>(st, ms, x, (uint32_t)k, (uint32_t)R, total, lds, dbg);
+    else if (cpt <= 4)
+        gemv_go<SEM, M, 4>(st, ms, x, (uint32_t)k, (uint32_t)R, total, lds, dbg);
+    else if (cpt <= 8)
+        gemv_go<SEM, M, 8>(st, ms, x, (uint32_t)k, (uint32_t)R, total, lds, dbg);
+    else
+        return hipErrorInvalidValue;  // k > 32768: rejected when the matrix is made
     return hipGetLastError();
 }
 
@@ -391,14 +466,6 @@ __device__ __forceinline__ float gemm_wscale(int sem, const void* ws, size_t i) 
     return sem == SEM_FOUR_PARTIALS_F32 ? ((const float*)ws)[i] : f16w(((const uint16_t*)ws)[i]);
 }
 
-// A scale as loaded: f32 bits, or f16 bits widened only when stored to LDS
-// (widening right after the load would make the load's wait immediate).
-__device__ __forceinline__ uint32_t scale_bits(bool f16, const void* p, size_t i) {
-    return f16 ? (uint32_t)((const uint16_t*)p)[i] : f2u(((const float*)p)[i]);
-}
-__device__ __forceinline__ float scale_value(bool f16, uint32_t bits) {
-    return f16 ? f16w((uint16_t)bits) : u2f(bits);
-}
 
 // The 16 activation scales of accumulator rows 8g + 4*half + (0..3).
 __device__ __forceinline__ void gemm_row_scales(float (&xs)[16], const float* col) {
@@ -657,13 +724,11 @@ static hipError_t gemm_launch(hipStream_t st, MatSet ms, size_t k, QuantAct x, s
 
 template <int SEM>
 static hipError_t gemv_rows(hipStream_t st, const MatSet& ms, size_t k, QuantAct x, size_t rows, int32_t* dbg) {
-    if (rows >= kGemmMinRows && k <= kGemmMaxK) return gemm_launch<SEM>(st, ms, k, x, rows, dbg);
+    if (rows >= kGemmMinRows) return gemm_launch<SEM>(st, ms, k, x, rows, dbg);
     size_t nb = k / 32;
     size_t done = 0;
     while (done < rows) {
         size_t m = rows - done;
-        size_t m_cap = kGemvActBytes / k;
-        if (m > m_cap) m = m_cap;
         QuantAct xm{x.q + done * k, x.s + done * nb, x.h + done * nb};
         MatSet mm = ms;
         for (int i = 0; i < ms.count; i++) mm.y[i] = ms.y[i] + done * ms.ld[i];

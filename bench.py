@@ -149,10 +149,21 @@ def bench_gemv(K, reps: int = 3):
     for _ in range(200):
         hip.matmul(m1, x1, y1, 1)
     cfg1_us = hip.timer_stop() * 1e3 / 200
+    # a plain 64 MiB device copy (k_copy): the reference for scaling the HBM
+    # byte counters of a profiler run, and a practical streaming rate
+    n_copy = 16 << 20
+    src, dst = hip.alloc(n_copy), hip.alloc(n_copy)
+    hip.copy(src, 0, dst, 0, n_copy)
+    hip.synchronize()
+    hip.timer_start()
+    for _ in range(10):
+        hip.copy(src, 0, dst, 0, n_copy)
+    copy_us = hip.timer_stop() * 1e3 / 10
     hip.close()
     return dict(achieved_gbs=gbs, avg_launch_us=total_ms * 1e3 / total_launches,
                 bytes_per_launch=total_bytes / total_launches, per_shape=per_shape,
-                cfg1_1536x576_us=cfg1_us, cfg1_bytes=1_003_776)
+                cfg1_1536x576_us=cfg1_us, cfg1_bytes=1_003_776,
+                copy_64mib_us=copy_us, copy_gbs=2 * 4 * n_copy / (copy_us * 1e-6) / 1e9)
 
 
 def bench_prefill(K, reps: int = 2):
@@ -269,6 +280,23 @@ def bench_cpu_baseline(seconds_budget: float = 20.0):
                        f"median step {median * 1e3:.1f} ms")
 
 
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "k_gemv_q8_0_1p7b_pmc.md")
+
+
+def measured_traffic():
+    """HBM bytes per GEMV launch from the committed rocprofv3 PMC summary
+    (FETCH_SIZE and WRITE_SIZE runs of `bench.py --only gemv`, scaled by the
+    same counters on a 64 MiB copy); None if the summary is absent."""
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch"):
+                    return float(line.split("=")[1])
+    except OSError:
+        pass
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -319,8 +347,11 @@ def main():
                    "seq_len": CFG2["seq_len"], "start_pos": PREFILL_POS},
     }
     if g:
+        traffic = measured_traffic()
         line["roofline"] = {"bound": "hbm", "achieved": round(g["achieved_gbs"], 1), "peak": HBM_PEAK_GBS,
-                            "unit": "GB/s", "frac": round(g["achieved_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                            "unit": "GB/s", "frac": round(g["achieved_gbs"] / HBM_PEAK_GBS, 4),
+                            "traffic": round(traffic) if traffic else None,
+                            "traffic_source": os.path.relpath(TRAFFIC_PROFILE, ROOT) if traffic else None,
                             "kernel": "k_gemv (Q8_0, M=1) over the 7 SmolLM2-1.7B projection shapes x 24 layers",
                             "avg_launch_us": round(g["avg_launch_us"], 3),
                             "bytes_per_launch": round(g["bytes_per_launch"])}

@@ -9,6 +9,8 @@
 // -ffp-contract=off; fma appears only where the reference writes `mul_add`.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include "kernels.hpp"
 #include "numerics.hpp"
 
@@ -1082,6 +1084,250 @@ __global__ __launch_bounds__(512) void k_attention(const float* __restrict__ q, 
     }
 }
 
+// ---------------------------------------------------------------------------
+// Attention, latency-first form (the same arithmetic as k_attention).
+//
+// A decode step runs one query row against a few hundred cache rows, so the
+// time is the critical path, not the work: the two serial chains per head
+// (the softmax sum and the weighted V sum, each `count` dependent adds) plus
+// the memory round trips before them. This form keeps the round trips few
+// and off the chains:
+//  * workgroup (head group, d-slice, row): the G query heads of one KV head
+//    and DW of their HS output dims; the HS / DW slices of a group redo the
+//    scores (cheap, parallel) so that each needs only count * DW floats of V;
+//  * K rows are copied HBM -> LDS by the gfx950 LDS DMA
+//    (global_load_lds_dwordx4), 16 bytes per lane, fully coalesced; the
+//    float4 u of row r lands in slot u ^ (r % F) of its row (F float4 per
+//    row), so when every lane then reads its own row the 16 lanes of a read
+//    phase hit 16 different bank groups;
+//  * one lane per cache row runs the reference dot (four FMA chains) for
+//    every head of the group;
+//  * the V slice is DMA'd into the same LDS by waves 1.. while wave 0 runs
+//    the softmax sums, so its latency is hidden behind them;
+//  * both chains read LDS in runs of 32-64 values per wait, at compile-time
+//    offsets, which keeps a dependent add about every 8 cycles.
+static constexpr uint32_t kAttnFastThreads = 512;
+
+template <int G, int HS, int DW>
+__global__ __launch_bounds__(512) void k_attention_fast(
+    const float* __restrict__ q, float* __restrict__ out, float* __restrict__ att, const float* __restrict__ kc,
+    const float* __restrict__ vc, size_t loff, const DevWindow* __restrict__ windows, uint32_t n_heads,
+    uint32_t kv_mul, uint32_t kv_dim, uint32_t seq_len, float scale, uint32_t scs, uint32_t kcap, uint32_t vcap,
+    int8_t* __restrict__ qo, float* __restrict__ so, uint16_t* __restrict__ ho) {
+    constexpr uint32_t T = kAttnFastThreads, S = HS / DW, F = HS / 4, FV = DW / 4;
+    // LDS: q [G][HS] | scores [G][scs] | work: K chunk [kcap][HS], later V [vcap][DW]
+    extern __shared__ __align__(16) float sm[];
+    __shared__ float red[T / 64][G];
+    __shared__ float s_sum[G];
+    __shared__ uint64_t etab[32];  // the exp table, off the global memory path
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t row = blockIdx.y, hg = blockIdx.x / S, sidx = blockIdx.x % S;
+    const DevWindow w = windows[row];
+    const uint32_t n_shared = w.shared_end - w.shared_start;
+    const uint32_t count = n_shared + w.slot - w.att_start + 1;  // <= scs: sized for the longest window
+    const uint32_t width = n_heads * HS, d0 = sidx * DW;
+    const uint32_t h0 = hg * G, kvo = (h0 / kv_mul) * HS;
+    float* qs = sm;
+    float* sc = sm + G * HS;
+    float* work = sc + G * scs;
+    for (uint32_t e = tid; e < G * HS; e += T) qs[e] = q[(size_t)row * width + (size_t)h0 * HS + e];
+    if (tid < 32) etab[tid] = kExp2Tab[tid];
+
+    // 1. scores, K in chunks of kcap <= T rows
+    const float* kbase = kc + loff + kvo;
+    float mx[G];
+#pragma unroll
+    for (int j = 0; j < G; j++) mx[j] = -INFINITY;
+    for (uint32_t r0 = 0; r0 < count; r0 += kcap) {
+        const uint32_t nr = count - r0 < kcap ? count - r0 : kcap, slots = nr * F;
+        __syncthreads();  // q is in place / the previous chunk is consumed
+        for (uint32_t base = wave * 64; base < slots; base += T) {
+            const uint32_t s = base + lane;
+            if (s < slots) {
+                const uint32_t r = s / F, u = (s % F) ^ (r % F);
+                __builtin_amdgcn_global_load_lds(kbase + (size_t)win_slot(w, n_shared, r0 + r) * kv_dim + 4 * u,
+                                                 work + 4 * base, 16, 0, 0);
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0);  // this lane's LDS loads have landed
+        __syncthreads();
+        if (tid < nr) {
+            const float* kr = work + tid * HS;
+            const uint32_t sw = tid % F;
+            float acc[G][4];
+#pragma unroll
+            for (int j = 0; j < G; j++) acc[j][0] = acc[j][1] = acc[j][2] = acc[j][3] = 0.0f;
+#pragma unroll
+            for (int c = 0; c < (int)F; c += 16) {  // 16 float4 of the row at a time
+                constexpr int U = F < 16 ? F : 16;
+                float4 kk[U];
+#pragma unroll
+                for (int u = 0; u < U; u++) kk[u] = *(const float4*)(kr + 4 * ((c + u) ^ sw));
+#pragma unroll
+                for (int j = 0; j < G; j++) {
+#pragma unroll
+                    for (int u = 0; u < U; u++) {
+                        const float4 qq = *(const float4*)(qs + j * HS + 4 * (c + u));
+                        acc[j][0] = __builtin_fmaf(qq.x, kk[u].x, acc[j][0]);
+                        acc[j][1] = __builtin_fmaf(qq.y, kk[u].y, acc[j][1]);
+                        acc[j][2] = __builtin_fmaf(qq.z, kk[u].z, acc[j][2]);
+                        acc[j][3] = __builtin_fmaf(qq.w, kk[u].w, acc[j][3]);
+                    }
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < G; j++) {
+                // dot.rs:360: (acc0 + acc1) + (acc2 + acc3), then * scale (cpu.rs:609)
+                const float sv = ((acc[j][0] + acc[j][1]) + (acc[j][2] + acc[j][3])) * scale;
+                sc[j * scs + r0 + tid] = sv;
+                mx[j] = fmaxf(mx[j], sv);
+            }
+        }
+    }
+
+    // 2. per-head max (order-free), then exp with it
+#pragma unroll
+    for (int j = 0; j < G; j++) {
+        float m = mx[j];
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+        if (lane == 0) red[wave][j] = m;
+    }
+    __syncthreads();
+    for (uint32_t t = tid; t < G * count; t += T) {
+        const uint32_t j = t / count, i = t - j * count;
+        float m = red[0][j];
+#pragma unroll
+        for (uint32_t wv = 1; wv < T / 64; wv++) m = fmaxf(m, red[wv][j]);
+        float* p = sc + j * scs + i;
+        *p = glibc_expf(*p - m, etab);
+    }
+    __syncthreads();
+
+    // 3. V slice rows by LDS DMA (unit f = row f / FV, float4 f % FV, at
+    // work[4 f]); the first chunk from waves 1.. while wave 0 runs the sums
+    const float* vbase = vc + loff + kvo + d0;
+    auto v_dma = [&](uint32_t r0, uint32_t nrows, uint32_t wave0) {
+        const uint32_t units = nrows * FV;
+        for (uint32_t base = (wave - wave0) * 64; base < units; base += T - 64 * wave0) {
+            const uint32_t f = base + lane;
+            if (f < units) {
+                const uint32_t r = f / FV, col = f - r * FV;
+                __builtin_amdgcn_global_load_lds(vbase + (size_t)win_slot(w, n_shared, r0 + r) * kv_dim + 4 * col,
+                                                 work + 4 * base, 16, 0, 0);
+            }
+        }
+    };
+    if (wave > 0) v_dma(0, count < vcap ? count : vcap, 1);
+    // softmax sums, left to right: lane j of wave 0 for head j
+    if (tid < G) {
+        const float* e = sc + tid * scs;
+        float s = 0.0f;
+        uint32_t i = 0;
+        for (; i + 64 <= count; i += 64) {
+            float4 r[16];
+#pragma unroll
+            for (int u = 0; u < 16; u++) r[u] = *(const float4*)(e + i + 4 * u);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int u = 0; u < 16; u++) {
+                s += r[u].x;
+                s += r[u].y;
+                s += r[u].z;
+                s += r[u].w;
+            }
+        }
+        for (; i < count; i++) s += e[i];
+        s_sum[tid] = s;
+    }
+    __syncthreads();
+    for (uint32_t t = tid; t < G * count; t += T) {
+        const uint32_t j = t / count, i = t - j * count;
+        float* p = sc + j * scs + i;
+        const float pv = div_rn(*p, s_sum[j]);
+        *p = pv;
+        // the probabilities stay in `att`, as the reference leaves them
+        if (sidx == 0) att[(size_t)row * n_heads * seq_len + (size_t)(h0 + j) * seq_len + i] = pv;
+    }
+
+    // 4. out[h][d0 + e] = sum_i p_i * v_i[e], lane (j, e), i in order
+    constexpr uint32_t lanes = G * DW;
+    const uint32_t j = tid / DW, e = tid % DW;
+    const float* pj = sc + (j < G ? j : 0) * scs;
+    float o = 0.0f;
+    for (uint32_t r0 = 0; r0 < count; r0 += vcap) {
+        const uint32_t nrows = count - r0 < vcap ? count - r0 : vcap;
+        if (r0 > 0) {  // a window longer than the V capacity: the next chunk
+            __syncthreads();  // every lane is done with the previous one
+            v_dma(r0, nrows, 0);
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (tid < lanes) {
+            const float* pp = pj + r0;
+            const float* vv = work + e;
+            uint32_t i = 0;
+            for (; i + 32 <= nrows; i += 32) {
+                float4 p4[8];
+                float v[32];
+#pragma unroll
+                for (int u = 0; u < 8; u++) p4[u] = *(const float4*)(pp + i + 4 * u);
+#pragma unroll
+                for (int u = 0; u < 32; u++) v[u] = vv[(i + u) * DW];
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    o += p4[u].x * v[4 * u];
+                    o += p4[u].y * v[4 * u + 1];
+                    o += p4[u].z * v[4 * u + 2];
+                    o += p4[u].w * v[4 * u + 3];
+                }
+            }
+            for (; i < nrows; i++) o += pp[i] * vv[i * DW];
+        }
+    }
+    if (tid < lanes) {
+        const size_t oi = (size_t)row * width + (size_t)(h0 + j) * HS + d0 + e;
+        out[oi] = o;
+        // DW % 32 == 0: each 32-lane group is one Q8 block of the head output
+        if (qo) quant_lane(o, true, qo + oi, so + oi / 32, ho + oi / 32);
+    }
+}
+
+// LDS budget of the latency-first attention and its shape for one call:
+// slice width DW (32 or 64), K chunk and V chunk capacities.
+static constexpr size_t kAttnFastLds = 150 * 1024;
+struct AttnFastShape {
+    bool ok;
+    uint32_t dw, scs, kcap, vcap;
+    size_t lds;
+};
+static AttnFastShape attn_fast_shape(size_t max_count, size_t G, size_t hs) {
+    AttnFastShape r{false, 0, 0, 0, 0, 0};
+    if ((hs != 32 && hs != 64 && hs != 128) || G > 8 || max_count == 0) return r;
+    const size_t scs = (max_count + 3) & ~(size_t)3;
+    const size_t fixed = G * hs + G * scs;  // floats
+    if (fixed * 4 + 32 * hs * 4 > kAttnFastLds) return r;
+    const size_t work = kAttnFastLds / 4 - fixed;
+    size_t kcap = work / hs;
+    if (kcap > kAttnFastThreads) kcap = kAttnFastThreads;
+    // the widest slice whose V window fits in one chunk; else 32 wide, chunked
+    size_t dw = 32, vcap = work / 32;
+    if (hs >= 64 && work / 64 >= max_count && G * 64 <= kAttnFastThreads) dw = 64, vcap = work / 64;
+    if (G * dw > kAttnFastThreads) return r;
+    if (vcap >= max_count)
+        vcap = max_count;
+    else
+        vcap &= ~(size_t)31;  // chunk starts stay 16-byte aligned
+    r.ok = true;
+    r.dw = (uint32_t)dw;
+    r.scs = (uint32_t)scs;
+    r.kcap = (uint32_t)kcap;
+    r.vcap = (uint32_t)vcap;
+    r.lds = (fixed + std::max(kcap * hs, vcap * dw)) * 4;
+    return r;
+}
+
 hipError_t launch_attention(hipStream_t st, const float* q, float* out, float* att, const float* kc,
                             const float* vc, size_t layer, const DevWindow* windows, size_t n_rows,
                             size_t max_count, size_t n_heads, size_t kv_mul, size_t hs, size_t kv_dim,
@@ -1089,6 +1335,45 @@ hipError_t launch_attention(hipStream_t st, const float* q, float* out, float* a
     if (n_rows == 0) return hipSuccess;
     if (hs == 0 || hs > 256 || hs % 4 != 0 || kv_mul == 0 || n_heads % kv_mul != 0) return hipErrorInvalidValue;
     if (qo && hs % 32 != 0) return hipErrorInvalidValue;
+    if (max_count > seq_len) max_count = seq_len;
+    {
+        // heads per workgroup: the largest of 8, 4, 3, 2, 1 dividing kv_mul
+        size_t G = 1;
+        for (size_t g : {8, 4, 3, 2})
+            if (kv_mul % g == 0) {
+                G = g;
+                break;
+            }
+        const AttnFastShape f = attn_fast_shape(max_count, G, hs);
+        if (f.ok) {
+            const dim3 grid((unsigned)(n_heads / G * (hs / f.dw)), (unsigned)n_rows);
+#define KR_ATTN_FAST(g, h, d)                                                                                    \
+    hipLaunchKernelGGL((k_attention_fast<g, h, d>), grid, dim3(kAttnFastThreads), f.lds, st, q, out, att, kc, vc, \
+                       layer * seq_len * kv_dim, windows, (uint32_t)n_heads, (uint32_t)kv_mul, (uint32_t)kv_dim,  \
+                       (uint32_t)seq_len, scale, f.scs, f.kcap, f.vcap, qo, so, ho)
+#define KR_ATTN_FAST_G(g)                   \
+    if (hs == 32)                           \
+        KR_ATTN_FAST(g, 32, 32);            \
+    else if (hs == 64 && f.dw == 32)        \
+        KR_ATTN_FAST(g, 64, 32);            \
+    else if (hs == 64)                      \
+        KR_ATTN_FAST(g, 64, 64);            \
+    else if (f.dw == 32)                    \
+        KR_ATTN_FAST(g, 128, 32);           \
+    else                                    \
+        KR_ATTN_FAST(g, 128, 64);
+            switch (G) {
+                case 8: KR_ATTN_FAST_G(8) break;
+                case 4: KR_ATTN_FAST_G(4) break;
+                case 3: KR_ATTN_FAST_G(3) break;
+                case 2: KR_ATTN_FAST_G(2) break;
+                default: KR_ATTN_FAST_G(1) break;
+            }
+#undef KR_ATTN_FAST_G
+#undef KR_ATTN_FAST
+            return hipGetLastError();
+        }
+    }
     size_t G = 1;  // heads per workgroup: the largest divisor of kv_mul that fits
     for (size_t g = 1; g <= 8 && g <= kv_mul; g++)
         if (kv_mul % g == 0 && g * hs <= 2 * kAttnThreads) G = g;

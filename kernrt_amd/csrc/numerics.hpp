@@ -105,7 +105,8 @@ static const uint64_t kExp2Tab[32] = {
     0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
 };
 
-KR_HD float glibc_expf(float x) {
+// `tab` holds kExp2Tab; a kernel may pass a copy in LDS.
+KR_HD float glibc_expf(float x, const uint64_t* tab) {
     const double N = 32.0;
     const double InvLn2N = 0x1.71547652b82fep+0 * N;
     const double Shift = 0x1.8p+52;
@@ -126,7 +127,7 @@ KR_HD float glibc_expf(float x) {
     uint64_t ki = d2u(kd);
     kd -= Shift;
     double r = __builtin_fma(InvLn2N, xd, -kd);
-    uint64_t t = kExp2Tab[ki % 32] + (ki << 47);
+    uint64_t t = tab[ki % 32] + (ki << 47);
     double s = u2d(t);
     double p = __builtin_fma(C0, r, C1);
     double r2 = r * r;
@@ -135,5 +136,7 @@ KR_HD float glibc_expf(float x) {
     y = y * s;
     return (float)y;
 }
+
+KR_HD float glibc_expf(float x) { return glibc_expf(x, kExp2Tab); }
 
 }  // namespace kr

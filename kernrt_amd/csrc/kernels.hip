@@ -1399,56 +1399,122 @@ hipError_t launch_attention(hipStream_t st, const float* q, float* out, float* a
 
 // add_in_place (cpu.rs:405-410) + rms_norm (cpu.rs:633-644) + the Q8
 // quantization of the normed row (quant.rs:856-874), one row per workgroup.
-template <bool ADD>
+// Thread t holds float4 t, t + 256, ... of the row in registers: the residual
+// sum, the norm weight (loaded before the chain, off its critical path) and
+// the squares, which go to LDS for the serial sum. Wave 0 runs that sum, all
+// 64 lanes in lockstep on the same values (uniform control flow), reading
+// LDS in runs of 64 values per wait. A Q8 block is 8 consecutive threads.
+template <bool ADD, int VPT>
 __global__ __launch_bounds__(256) void k_add_rms_quant(float* __restrict__ x, const float* __restrict__ add,
                                                        const float* __restrict__ w, float* __restrict__ out,
                                                        uint32_t dim, float eps, int8_t* __restrict__ q,
                                                        float* __restrict__ s, uint16_t* __restrict__ h) {
-    extern __shared__ float sm[];  // xs[dim] | sq[dim]
+    extern __shared__ __align__(16) float sq[];  // [dim]
     __shared__ float s_scale;
-    float* xs = sm;
-    float* sq = sm + dim;
+    const uint32_t tid = threadIdx.x, n4 = dim / 4;
     const size_t row = blockIdx.x;
-    float* xr = x + row * dim;
-    for (uint32_t i = threadIdx.x; i < dim; i += 256) {
-        float v = xr[i];
-        if (ADD) {
-            v = v + add[row * dim + i];
-            xr[i] = v;
+    float4* xr = (float4*)(x + row * dim);
+    float4 v[VPT], wv[VPT];
+#pragma unroll
+    for (int u = 0; u < VPT; u++) {
+        const uint32_t f = tid + 256 * u;
+        if (f < n4) {
+            v[u] = xr[f];
+            wv[u] = ((const float4*)w)[f];
+            if (ADD) {
+                const float4 a = ((const float4*)(add + row * dim))[f];
+                v[u] = make_float4(v[u].x + a.x, v[u].y + a.y, v[u].z + a.z, v[u].w + a.w);
+            }
         }
-        xs[i] = v;
-        sq[i] = v * v;
+    }
+#pragma unroll
+    for (int u = 0; u < VPT; u++) {
+        const uint32_t f = tid + 256 * u;
+        if (f < n4) {
+            if (ADD) xr[f] = v[u];
+            ((float4*)sq)[f] = make_float4(v[u].x * v[u].x, v[u].y * v[u].y, v[u].z * v[u].z, v[u].w * v[u].w);
+        }
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        float ss = seq_sum(sq, dim);
+    if (tid < 64) {
+        // rms_norm_row (cpu.rs:635-641): ss = sum of squares left to right,
+        // ss /= dim, ss += eps, scale = 1 / sqrt(ss)
+        float ss = 0.0f;
+        uint32_t i = 0;
+        for (; i + 64 <= dim; i += 64) {
+            float4 r[16];
+#pragma unroll
+            for (int u = 0; u < 16; u++) r[u] = *(const float4*)(sq + i + 4 * u);
+#pragma unroll
+            for (int u = 0; u < 16; u++) {
+                ss += r[u].x;
+                ss += r[u].y;
+                ss += r[u].z;
+                ss += r[u].w;
+            }
+        }
+        for (; i < dim; i++) ss += sq[i];
         ss = div_rn(ss, (float)dim);
         ss += eps;
-        s_scale = div_rn(1.0f, sqrt_rn(ss));
+        if (tid == 0) s_scale = div_rn(1.0f, sqrt_rn(ss));
     }
     __syncthreads();
     const float scale = s_scale;
     const uint32_t nb = dim / 32;
-    for (uint32_t base = 0; base < dim; base += 256) {
-        uint32_t i = base + threadIdx.x;
-        bool valid = i < dim;  // dim % 32 == 0: half-waves are all valid or all not
-        float o = valid ? w[i] * (scale * xs[i]) : 0.0f;
-        if (valid) out[row * dim + i] = o;
-        quant_lane(o, valid, q + row * dim + i, s + row * nb + i / 32, h + row * nb + i / 32);
+#pragma unroll
+    for (int u = 0; u < VPT; u++) {
+        const uint32_t f = tid + 256 * u;
+        // dim % 32 == 0: the 8 threads of a block are all in range or all out
+        if (f < n4) {
+            // cpu.rs:643: out = w * (scale * x)
+            const float4 o = make_float4(wv[u].x * (scale * v[u].x), wv[u].y * (scale * v[u].y),
+                                         wv[u].z * (scale * v[u].z), wv[u].w * (scale * v[u].w));
+            ((float4*)(out + row * dim))[f] = o;
+            // Q8Vec::quantize_into (quant.rs:864-873) on the block of 8 threads
+            float m = fmaxf(fmaxf(fmaxf(fmaxf(0.0f, fabsf(o.x)), fabsf(o.y)), fabsf(o.z)), fabsf(o.w));
+#pragma unroll
+            for (int off = 4; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 8));
+            const float d = div_rn(m, 127.0f);
+            const float inv = d > 0.0f ? div_rn(1.0f, d) : 0.0f;
+            char4 qq;
+            qq.x = q8_round(o.x * inv);
+            qq.y = q8_round(o.y * inv);
+            qq.z = q8_round(o.z * inv);
+            qq.w = q8_round(o.w * inv);
+            ((char4*)(q + row * dim))[f] = qq;
+            if ((f & 7) == 0) {
+                s[row * nb + f / 8] = d;
+                h[row * nb + f / 8] = f32_to_f16_bits(d);
+            }
+        }
     }
 }
 
 hipError_t launch_add_rms_quant(hipStream_t st, float* x, const float* add, const float* w, float* out,
                                 size_t rows, size_t dim, float eps, int8_t* q, float* s, uint16_t* h) {
     if (rows == 0) return hipSuccess;
-    if (dim % 32 != 0) return hipErrorInvalidValue;
-    size_t lds = 2 * dim * sizeof(float);
-    if (add)
-        hipLaunchKernelGGL(k_add_rms_quant<true>, dim3((unsigned)rows), dim3(256), lds, st, x, add, w, out,
-                           (uint32_t)dim, eps, q, s, h);
-    else
-        hipLaunchKernelGGL(k_add_rms_quant<false>, dim3((unsigned)rows), dim3(256), lds, st, x, add, w, out,
-                           (uint32_t)dim, eps, q, s, h);
+    if (dim % 32 != 0 || dim > 8192) return hipErrorInvalidValue;
+    const size_t lds = dim * sizeof(float);
+    const size_t vpt = (dim / 4 + 255) / 256;
+#define KR_NORM_GO(A, V)                                                                                        \
+    hipLaunchKernelGGL((k_add_rms_quant<A, V>), dim3((unsigned)rows), dim3(256), lds, st, x, add, w, out,      \
+                       (uint32_t)dim, eps, q, s, h)
+#define KR_NORM_V(A)          \
+    if (vpt <= 1)             \
+        KR_NORM_GO(A, 1);     \
+    else if (vpt <= 2)        \
+        KR_NORM_GO(A, 2);     \
+    else if (vpt <= 4)        \
+        KR_NORM_GO(A, 4);     \
+    else                      \
+        KR_NORM_GO(A, 8);
+    if (add) {
+        KR_NORM_V(true)
+    } else {
+        KR_NORM_V(false)
+    }
+#undef KR_NORM_V
+#undef KR_NORM_GO
     return hipGetLastError();
 }
 

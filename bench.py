@@ -100,44 +100,104 @@ def bench_decode(K, steps: int, warmup: int, use_graph: bool = True):
     return out
 
 
-def bench_gemv(K, reps: int = 3):
-    """Q8_0 GEMV, M = 1, over every 1.7B projection shape, rotating through
-    24 layers of distinct weights (1.6 GB > 256 MB MALL)."""
+def gemv_algo_bytes(n: int, k: int) -> int:
+    """Algorithmic HBM bytes of one Q8_0 GEMV launch over n weight rows of
+    in_dim k at M = 1: int8 weights, f32 block scales, the quantized
+    activation row with its f32 scales, and the f32 outputs."""
+    nb = k // 32
+    return n * k + n * nb * 4 + k + nb * 4 + n * 4
+
+
+def bench_gemv(K, reps: int = 3, use_graph: bool = True):
+    """Q8_0 decode GEMVs (M = 1) at SmolLM2-1.7B shapes, launched as a decode
+    step launches them: per layer the fused QKV (3 x 2048x2048, one launch),
+    O 2048x2048, the fused gate+up (2 x 8192x2048, one launch) and down
+    2048x8192, over 24 layers of distinct weights, plus the 49152x2048
+    classifier. One pass streams 1.93 GB of weights, far beyond the 256 MB
+    MALL, so every launch reads its weights from HBM. Launches are grouped by
+    in_dim (the activation workspace holds one quantized row): first every
+    in_dim-2048 launch of all layers, then every down projection."""
     log("gemv: building 24 layers of 1.7B-shaped Q8_0 matrices")
     hip = K.open("hip")
     c = K.Config(**CFG3)
-    shapes = [(c.q_dim, c.dim), (c.kv_dim, c.dim), (c.kv_dim, c.dim), (c.dim, c.q_dim), (c.hidden_dim, c.dim),
-              (c.hidden_dim, c.dim), (c.dim, c.hidden_dim)]
-    mats = [[hip.synthetic_matrix("q8_0", n, k, 1000 * l + i) for i, (n, k) in enumerate(shapes)]
-            for l in range(c.n_layers)]
+    d, hdim = c.dim, c.hidden_dim
+    seed = 1000
+    layers = []
+    for l in range(c.n_layers):
+        m = {}
+        for name, (n, k) in {"q": (d, d), "k": (d, d), "v": (d, d), "o": (d, d), "gate": (hdim, d),
+                             "up": (hdim, d), "down": (d, hdim)}.items():
+            seed += 1
+            m[name] = hip.synthetic_matrix("q8_0", n, k, seed)
+        layers.append(m)
+    cls = hip.synthetic_matrix("q8_0", c.vocab_size, d, 99)
     rng = np.random.default_rng(3)
-    xs = {k: hip.upload(rng.normal(size=k).astype(np.float32)) for k in {k for _, k in shapes}}
-    ys = {n: hip.alloc(n) for n in {n for n, _ in shapes}}
+    x_d = hip.upload(rng.normal(size=d).astype(np.float32))
+    x_h = hip.upload(rng.normal(size=hdim).astype(np.float32))
+    y = {n: [hip.alloc(n) for _ in range(3)] for n in (d, hdim, c.vocab_size)}
+    # (matrices, out rows per matrix, in_dim) per launch, in launch order
+    group_a = []
+    for m in layers:
+        group_a += [([m["q"], m["k"], m["v"]], d, d), ([m["o"]], d, d), ([m["gate"], m["up"]], hdim, d)]
+    group_a.append(([cls], c.vocab_size, d))
+    group_b = [([m["down"]], d, hdim) for m in layers]
 
-    def algo_bytes(n, k):
-        nb = k // 32
-        return n * k + n * nb * 4 + k + nb * 4 + n * 4
+    # launch arguments prepared once: the host must issue launches faster than
+    # the GPU retires them, or the events would time the host
+    import ctypes as C
+    fn, ctx = hip._L.kr_matmul_quantized_set, hip.ctx
+    prepared = {}
+    for g in group_a + group_b:
+        mats, n, _ = g
+        prepared[id(g)] = ((C.c_uint32 * len(mats))(*mats), (C.c_uint32 * len(mats))(*y[n][:len(mats)]), len(mats))
 
-    per_shape = {}
-    total_bytes, total_ms, total_launches = 0.0, 0.0, 0
-    for i, (n, k) in enumerate(shapes):
-        hip.quantize_rows(xs[k], 1, k)
-        for l in range(c.n_layers):  # warm
-            hip.matmul_quantized(mats[l][i], ys[n], 1)
+    def run(group):
+        for g in group:
+            ws, ys, nm = prepared[id(g)]
+            if fn(ctx, ws, ys, nm, 1) != 0:
+                raise RuntimeError(hip._L.kr_last_error(ctx).decode())
+
+    def timed(group, passes):
+        """One pass captured into a HIP graph, as the decode driver replays its
+        step; the graph is then replayed `passes` times between two events.
+        Without graphs (for profilers), the launches are issued directly."""
+        run(group)  # warm-up pass (also evicts the other group from the MALL)
+        if not use_graph:
+            hip.synchronize()
+            hip.timer_start()
+            for _ in range(passes):
+                run(group)
+            return hip.timer_stop()
+        hip.capture_begin()
+        run(group)
+        hip.capture_end()
+        hip.replay(1)
         hip.synchronize()
+        hip.replay(1)  # keeps the GPU busy while the timed launches are submitted
         hip.timer_start()
-        for _ in range(reps):
-            for l in range(c.n_layers):
-                hip.matmul_quantized(mats[l][i], ys[n], 1)
-        ms = hip.timer_stop()
-        launches = reps * c.n_layers
-        avg_us = ms * 1e3 / launches
-        b = algo_bytes(n, k)
-        per_shape[f"{n}x{k}"] = dict(avg_us=avg_us, gbs=b / (avg_us * 1e-6) / 1e9)
-        total_bytes += b * launches
+        hip.replay(passes)
+        return hip.timer_stop()
+
+    kinds = {}
+    total_ms, total_bytes, total_launches = 0.0, 0, 0
+    for x, width, group in ((x_d, d, group_a), (x_h, hdim, group_b)):
+        hip.quantize_rows(x, 1, width)
+        ms = timed(group, reps)
         total_ms += ms
-        total_launches += launches
+        total_launches += reps * len(group)
+        for mats, n, k in group:
+            total_bytes += reps * gemv_algo_bytes(n * len(mats), k)
+            kinds.setdefault(f"{len(mats)}x{n}x{k}", [0, gemv_algo_bytes(n * len(mats), k)])[0] += 1
     gbs = total_bytes / (total_ms * 1e-3) / 1e9
+    # per launch shape: time each kind alone over the same distinct matrices
+    per_shape = {}
+    for key, (count, b) in kinds.items():
+        nm, n, k = (int(t) for t in key.split("x"))
+        group = [g for g in group_a + group_b if len(g[0]) == nm and g[1] == n and g[2] == k]
+        hip.quantize_rows(x_d if k == d else x_h, 1, k)
+        us = timed(group, 4) * 1e3 / (4 * len(group))
+        per_shape[key] = dict(launches_per_pass=count, bytes=b, avg_us=round(us, 3),
+                              gbs=round(b / (us * 1e-6) / 1e9, 1))
     # BASELINE.json configs[0]: one GEMV at SmolLM2-135M's gate shape, 1536x576
     m1 = hip.synthetic_matrix("q8_0", 1536, 576, 77)
     x1 = hip.upload(rng.normal(size=576).astype(np.float32))
@@ -161,7 +221,8 @@ def bench_gemv(K, reps: int = 3):
     copy_us = hip.timer_stop() * 1e3 / 10
     hip.close()
     return dict(achieved_gbs=gbs, avg_launch_us=total_ms * 1e3 / total_launches,
-                bytes_per_launch=total_bytes / total_launches, per_shape=per_shape,
+                bytes_per_launch=total_bytes / total_launches, launches_per_pass=len(group_a) + len(group_b),
+                bytes_per_pass=total_bytes // reps, per_shape=per_shape,
                 cfg1_1536x576_us=cfg1_us, cfg1_bytes=1_003_776,
                 copy_64mib_us=copy_us, copy_gbs=2 * 4 * n_copy / (copy_us * 1e-6) / 1e9)
 
@@ -305,8 +366,8 @@ def main():
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--only", choices=["decode", "gemv", "prefill"], default=None)
     ap.add_argument("--no-graph", action="store_true",
-                    help="launch each decode step's kernels directly instead of replaying a captured HIP graph "
-                         "(same kernels; for profilers that cannot trace graph launches)")
+                    help="launch the decode step's and the GEMV passes' kernels directly instead of replaying "
+                         "captured HIP graphs (same kernels; for profilers that cannot trace graph launches)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the design note in DESIGN.md "
@@ -319,7 +380,7 @@ def main():
         res["decode"] = bench_decode(K, args.steps, args.warmup, use_graph=not args.no_graph)
         log(f"decode: {res['decode']['tok_s']:.1f} tok/s")
     if args.only in (None, "gemv"):
-        res["gemv"] = bench_gemv(K)
+        res["gemv"] = bench_gemv(K, use_graph=not args.no_graph)
         log(f"gemv: {res['gemv']['achieved_gbs']:.0f} GB/s")
     if args.only in (None, "prefill"):
         res["prefill"] = bench_prefill(K)
@@ -352,7 +413,8 @@ def main():
                             "unit": "GB/s", "frac": round(g["achieved_gbs"] / HBM_PEAK_GBS, 4),
                             "traffic": round(traffic) if traffic else None,
                             "traffic_source": os.path.relpath(TRAFFIC_PROFILE, ROOT) if traffic else None,
-                            "kernel": "k_gemv (Q8_0, M=1) over the 7 SmolLM2-1.7B projection shapes x 24 layers",
+                            "kernel": "k_gemv (Q8_0, M=1): the decode launches of a SmolLM2-1.7B-shaped model "
+                                      "(fused QKV, O, fused gate+up, down x 24 layers + classifier), cold",
                             "avg_launch_us": round(g["avg_launch_us"], 3),
                             "bytes_per_launch": round(g["bytes_per_launch"])}
         line["gemv"] = g

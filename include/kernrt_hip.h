@@ -144,6 +144,20 @@ int kr_classify(kr_ctx* ctx, kr_mat w, kr_buf x, kr_buf y);
  * context's activation workspace, then run the projection kernel on it. */
 int kr_quantize_rows(kr_ctx* ctx, kr_buf x, size_t rows, size_t width);
 int kr_matmul_quantized(kr_ctx* ctx, kr_mat w, kr_buf y, size_t rows);
+/* The fused launch behind project_qkv / project_gate_up (mod.rs:326-337):
+ * n (1..3) matrices with the same in_dim and storage, one kernel launch over
+ * all their rows, on the quantized workspace rows; y[i] gets w[i]'s output. */
+int kr_matmul_quantized_set(kr_ctx* ctx, const kr_mat* w, const kr_buf* y, int n, size_t rows);
+
+/* Launch capture: the ops issued between kr_capture_begin and
+ * kr_capture_end are recorded into one HIP graph instead of running (so
+ * their inputs must stay alive and unchanged); kr_replay launches that
+ * graph `times` times on the context's stream. No counterpart in the
+ * reference; it lets a benchmark issue a fixed op sequence the way the
+ * model driver's captured decode step does. */
+int kr_capture_begin(kr_ctx* ctx);
+int kr_capture_end(kr_ctx* ctx);
+int kr_replay(kr_ctx* ctx, size_t times);
 
 /* Stream-ordered timing: events recorded on the context's stream. */
 int kr_timer_start(kr_ctx* ctx);

@@ -84,6 +84,10 @@ _SIGS = {
     "kr_classify": (i32, [vp, u32, u32, u32]),
     "kr_quantize_rows": (i32, [vp, u32, sz, sz]),
     "kr_matmul_quantized": (i32, [vp, u32, u32, sz]),
+    "kr_matmul_quantized_set": (i32, [vp, C.POINTER(u32), C.POINTER(u32), i32, sz]),
+    "kr_capture_begin": (i32, [vp]),
+    "kr_capture_end": (i32, [vp]),
+    "kr_replay": (i32, [vp, sz]),
     "kr_timer_start": (i32, [vp]),
     "kr_timer_stop": (i32, [vp, C.POINTER(C.c_float)]),
     "kr_dbg_quantize": (i32, [vp, u32, sz, sz, vp, vp, vp]),

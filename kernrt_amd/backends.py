@@ -308,6 +308,25 @@ class Hip:
     def matmul_quantized(self, mat: int, y: Buf, rows: int):
         self._ck(self._L.kr_matmul_quantized(self.ctx, mat, y, rows))
 
+    def matmul_quantized_set(self, mats, ys, rows: int):
+        """One fused launch over 1-3 matrices with the same in_dim (the kernel
+        behind project_qkv / project_gate_up), on the quantized workspace."""
+        n = len(mats)
+        ws = (C.c_uint32 * n)(*mats)
+        yb = (C.c_uint32 * n)(*ys)
+        self._ck(self._L.kr_matmul_quantized_set(self.ctx, ws, yb, n, rows))
+
+    def capture_begin(self):
+        """Record the following ops into one HIP graph instead of running them."""
+        self._ck(self._L.kr_capture_begin(self.ctx))
+
+    def capture_end(self):
+        self._ck(self._L.kr_capture_end(self.ctx))
+
+    def replay(self, times: int = 1):
+        """Launch the captured graph `times` times on the context's stream."""
+        self._ck(self._L.kr_replay(self.ctx, times))
+
     def timer_start(self):
         self._ck(self._L.kr_timer_start(self.ctx))
 

@@ -92,6 +92,10 @@ struct kr_ctx {
     uint64_t epoch = 0;
     size_t q_rows = 0, q_width = 0;  // what the activation workspace holds
     hipEvent_t t0 = nullptr, t1 = nullptr;
+    // one captured launch sequence (kr_capture_begin / kr_capture_end)
+    bool capturing = false;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t graph_exec = nullptr;
 };
 
 namespace {
@@ -443,6 +447,8 @@ void kr_close(kr_ctx* c) {
         if (p) (void)hipFree(p);
     if (c->t0) (void)hipEventDestroy(c->t0);
     if (c->t1) (void)hipEventDestroy(c->t1);
+    if (c->graph_exec) (void)hipGraphExecDestroy(c->graph_exec);
+    if (c->graph) (void)hipGraphDestroy(c->graph);
     if (c->stream) (void)hipStreamDestroy(c->stream);
     delete c;
 }
@@ -809,6 +815,51 @@ int kr_matmul_quantized(kr_ctx* c, kr_mat w, kr_buf y, size_t rows) {
     BUF(yb, y, rows * m->m.n);
     if (rows == 0) return KR_OK;
     HIPCHK(c, kr::launch_project(c->stream, sem_for_project(m->m), m->m, act(c), rows, yb->p, m->m.n, nullptr));
+    return KR_OK;
+}
+
+int kr_matmul_quantized_set(kr_ctx* c, const kr_mat* w, const kr_buf* y, int n, size_t rows) {
+    CHECK(c, n >= 1 && n <= 3 && w && y, "1 to 3 matrices per launch");
+    const DevMatrix* ms[3];
+    float* yp[3];
+    for (int i = 0; i < n; i++) {
+        Mat* m = mat_of(c, w[i]);
+        CHECK(c, m != nullptr, "unknown matrix %u", (unsigned)w[i]);
+        ms[i] = &m->m;
+        CHECK(c, rows <= c->q_rows && ms[i]->k == c->q_width, "the workspace holds %zu rows of %zu, not %zu of %zu",
+              c->q_rows, c->q_width, rows, ms[i]->k);
+        CHECK(c, ms[i]->storage == ms[0]->storage, "the matrices of one launch share their storage");
+        BUF(yb, y[i], rows * ms[i]->n);
+        yp[i] = yb->p;
+    }
+    if (rows == 0) return KR_OK;
+    HIPCHK(c, kr::launch_project_set(c->stream, sem_for_project(*ms[0]), ms, yp, n, act(c), rows, nullptr));
+    return KR_OK;
+}
+
+int kr_capture_begin(kr_ctx* c) {
+    CHECK(c, !c->capturing, "a capture is already open");
+    if (c->graph_exec) (void)hipGraphExecDestroy(c->graph_exec);
+    if (c->graph) (void)hipGraphDestroy(c->graph);
+    c->graph_exec = nullptr;
+    c->graph = nullptr;
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    HIPCHK(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+    c->capturing = true;
+    return KR_OK;
+}
+
+int kr_capture_end(kr_ctx* c) {
+    CHECK(c, c->capturing, "no capture is open");
+    c->capturing = false;
+    HIPCHK(c, hipStreamEndCapture(c->stream, &c->graph));
+    HIPCHK(c, hipGraphInstantiate(&c->graph_exec, c->graph, nullptr, nullptr, 0));
+    return KR_OK;
+}
+
+int kr_replay(kr_ctx* c, size_t times) {
+    CHECK(c, c->graph_exec != nullptr, "nothing was captured");
+    for (size_t i = 0; i < times; i++) HIPCHK(c, hipGraphLaunch(c->graph_exec, c->stream));
     return KR_OK;
 }
 

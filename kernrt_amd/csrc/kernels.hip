@@ -238,19 +238,33 @@ __host__ __device__ inline uint32_t gemv_out_floats(int sem, uint32_t nb) {
     return sem == SEM_FMA_CHAIN ? 2 * (nb + 1) : 4 * gemv_q4p(nb);
 }
 
-// Serial f32 sum of n LDS values in order, with loads kept ahead.
+// Serial f32 sum of n LDS values in order: each run of 16 loads is issued
+// at once and then summed, one LDS round trip per 16 values.
 __device__ __forceinline__ float lds_sum(const float* e, uint32_t n) {
     float t = 0.0f;
     uint32_t i = 0;
-    for (; i + 8 <= n; i += 8) {
-        float v[8];
+    for (; i + 16 <= n; i += 16) {
+        float v[16];
 #pragma unroll
-        for (int j = 0; j < 8; j++) v[j] = e[i + j];
+        for (int j = 0; j < 16; j++) v[j] = e[i + j];
 #pragma unroll
-        for (int j = 0; j < 8; j++) t += v[j];
+        for (int j = 0; j < 16; j++) t += v[j];
     }
-    for (; i < n; i++) t += e[i];
+    if (i < n) {
+        float v[16];
+#pragma unroll
+        for (int j = 0; j < 16; j++) v[j] = i + j < n ? e[i + j] : 0.0f;
+#pragma unroll
+        for (int j = 0; j < 16; j++)
+            if (i + j < n) t += v[j];
+    }
     return t;
+}
+
+// Lane k (0..3) of each quad, to every lane of the quad (DPP quad_perm).
+template <int K>
+__device__ __forceinline__ float quad_bcast(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), K * 0x55, 0xf, 0xf, false));
 }
 
 template <int SEM, int M, int CPT>
@@ -349,9 +363,7 @@ __global__ __launch_bounds__(256) void k_gemv(MatSet ms, QuantAct x, uint32_t K,
             const uint32_t i = base + tid, o = i >> 2, j = i & 3;
             float t = 0.0f;
             if (o < outs && j < nb) t = lds_sum(res + (size_t)o * per + j * q4p, (nb - j + 3) / 4);
-            const uint32_t lane0 = (tid & 63) & ~3u;
-            const float t0 = __shfl(t, lane0), t1 = __shfl(t, lane0 + 1), t2 = __shfl(t, lane0 + 2),
-                        t3 = __shfl(t, lane0 + 3);
+            const float t0 = quad_bcast<0>(t), t1 = quad_bcast<1>(t), t2 = quad_bcast<2>(t), t3 = quad_bcast<3>(t);
             if (o < outs && j == 0) {
                 const uint32_t m = o / rows, r = o - m * rows;
                 Y[(size_t)m * ld + row0 + r] = ((t0 + t1) + t2) + t3;
@@ -360,15 +372,13 @@ __global__ __launch_bounds__(256) void k_gemv(MatSet ms, QuantAct x, uint32_t K,
     }
 }
 
-// Rows per workgroup tile: about 4 chunks per thread, but at least ~2 tiles
-// per CU when the matrix allows.
+// Rows per workgroup tile: about 8 KiB of weights, two 16-byte chunks per
+// thread (a sweep over R at the 360M and 1.7B shapes: 8 KiB tiles were the
+// fastest or within 3% of it at every shape, from 960x960 to 16384x2048).
 static size_t gemv_rows_per_tile(size_t n, size_t k) {
-    const size_t kc = k / 16;
-    size_t r = 1024 / kc;
+    size_t r = 8192 / k;
     if (r < 1) r = 1;
-    size_t cap = n / 512;
-    if (cap < 1) cap = 1;
-    if (r > cap) r = cap;
+    if (r > n) r = n;
     if (r > 256) r = 256;
     return r;
 }

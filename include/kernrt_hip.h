@@ -149,6 +149,11 @@ int kr_matmul_quantized(kr_ctx* ctx, kr_mat w, kr_buf y, size_t rows);
  * all their rows, on the quantized workspace rows; y[i] gets w[i]'s output. */
 int kr_matmul_quantized_set(kr_ctx* ctx, const kr_mat* w, const kr_buf* y, int n, size_t rows);
 
+/* A bare streaming read of len floats of src from `offset` (both multiples
+ * of 4): the practical ceiling of a read-dominated kernel of that size, for
+ * benchmarks. No counterpart in the reference. */
+int kr_stream_read(kr_ctx* ctx, kr_buf src, size_t offset, size_t len);
+
 /* Launch capture: the ops issued between kr_capture_begin and
  * kr_capture_end are recorded into one HIP graph instead of running (so
  * their inputs must stay alive and unchanged); kr_replay launches that

@@ -316,6 +316,10 @@ class Hip:
         yb = (C.c_uint32 * n)(*ys)
         self._ck(self._L.kr_matmul_quantized_set(self.ctx, ws, yb, n, rows))
 
+    def stream_read(self, src: Buf, offset: int, n: int):
+        """Read n floats of src and discard them (a bandwidth reference)."""
+        self._ck(self._L.kr_stream_read(self.ctx, src, offset, n))
+
     def capture_begin(self):
         """Record the following ops into one HIP graph instead of running them."""
         self._ck(self._L.kr_capture_begin(self.ctx))

@@ -837,6 +837,13 @@ int kr_matmul_quantized_set(kr_ctx* c, const kr_mat* w, const kr_buf* y, int n, 
     return KR_OK;
 }
 
+int kr_stream_read(kr_ctx* c, kr_buf src, size_t offset, size_t len) {
+    BUF(s, src, offset + len);
+    CHECK(c, offset % 4 == 0 && len % 4 == 0, "offset and length are multiples of 4 floats");
+    HIPCHK(c, kr::launch_stream_read(c->stream, s->p + offset, len, (int*)c->counter));
+    return KR_OK;
+}
+
 int kr_capture_begin(kr_ctx* c) {
     CHECK(c, !c->capturing, "a capture is already open");
     if (c->graph_exec) (void)hipGraphExecDestroy(c->graph_exec);

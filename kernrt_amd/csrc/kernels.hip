@@ -1661,6 +1661,25 @@ hipError_t launch_copy(hipStream_t st, float* d, const float* s, size_t n) {
     return hipGetLastError();
 }
 
+// A bare streaming read, the practical ceiling a read-dominated kernel of the
+// same size can reach: two 16-byte loads per lane, issued together, folded
+// into a value that is stored only if it matches an impossible pattern.
+__global__ __launch_bounds__(256) void k_stream_read(const v4i* __restrict__ p, size_t n16, int* __restrict__ sink) {
+    const size_t i = (size_t)blockIdx.x * 512 + threadIdx.x;
+    const v4i a = __builtin_nontemporal_load(p + (i < n16 ? i : 0));
+    const v4i b = __builtin_nontemporal_load(p + (i + 256 < n16 ? i + 256 : 0));
+    const v4i c = a ^ b;
+    if (c.x == 0x7eadbeef && c.y == 0x1b2c3d4e && c.z == c.w) sink[0] = c.x;
+}
+
+hipError_t launch_stream_read(hipStream_t st, const float* p, size_t n, int* sink) {
+    const size_t n16 = n / 4;
+    if (n16 == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_stream_read, dim3((unsigned)((n16 + 511) / 512)), dim3(256), 0, st, (const v4i*)p, n16,
+                       sink);
+    return hipGetLastError();
+}
+
 // silu (cpu.rs:708-710): x / (1 + exp(-x)), then * up.
 __global__ void k_silu_mul(float* __restrict__ g, const float* __restrict__ u, size_t n) {
     size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;

@@ -77,6 +77,8 @@ hipError_t launch_add(hipStream_t st, float* dst, const float* src, size_t n);
 hipError_t launch_mul(hipStream_t st, float* out, const float* a, const float* b, size_t n,
                       int sequential);
 hipError_t launch_copy(hipStream_t st, float* dst, const float* src, size_t n);
+// reads n floats (n % 4 == 0) and discards them; `sink` is never written in practice
+hipError_t launch_stream_read(hipStream_t st, const float* p, size_t n, int* sink);
 hipError_t launch_silu_mul(hipStream_t st, float* g, const float* u, size_t n);
 hipError_t launch_conv_prefill(hipStream_t st, float* out, const float* x, const float* kernel,
                                size_t rows, size_t dim, size_t k);

@@ -1200,6 +1200,73 @@ int logits_q(kr_ctx* c, kr_buf y) {
     return KR_OK;
 }
 
+// The fused decode producers (launch_project_pro): one row, M = 1.
+bool pro_fusable(size_t k) { return k % 32 == 0 && k <= 8192 && 8192 / k * (k / 16) <= 512; }
+
+int norm_project(kr_ctx* c, size_t layer, const int* projs, const kr_buf* ys, int n, kr_buf x, kr_buf add, kr_buf w,
+                 kr_buf x_out, size_t dim, float eps) {
+    CHECK(c, c->prepared && layer < c->n_layers, "layer %zu out of range", layer);
+    CHECK(c, n >= 1 && n <= 3 && pro_fusable(dim), "fused norm + projection: 1-3 matrices, dim %zu", dim);
+    const DevMatrix* ms[3];
+    float* yp[3];
+    for (int i = 0; i < n; i++) {
+        const Mat* m = proj_mat(c, layer, projs[i]);
+        CHECK(c, m != nullptr, "projection %d is not live on layer %zu", projs[i], layer);
+        ms[i] = &m->m;
+        CHECK(c, ms[i]->k == dim && ms[i]->storage == ms[0]->storage, "fused projections share in_dim and storage");
+        BUF(yb, ys[i], ms[i]->n);
+        yp[i] = yb->p;
+    }
+    BUF(xb, x, dim);
+    BUF(wb, w, dim);
+    BUF(ob, x_out, dim);
+    CHECK(c, x_out != x, "the updated residual goes to a second buffer");
+    const float* ap = nullptr;
+    if (add != KR_NO_BUF) {
+        BUF(ab, add, dim);
+        ap = ab->p;
+    }
+    HIPCHK(c, kr::launch_project_pro(c->stream, sem_for_project(*ms[0]), ms, yp, n, 1, xb->p, ap, wb->p, ob->p, eps));
+    return KR_OK;
+}
+
+int norm_logits(kr_ctx* c, kr_buf x, kr_buf add, kr_buf w, kr_buf y, size_t dim, float eps) {
+    CHECK(c, c->prepared, "prepare() runs before any compute");
+    Mat* mt = mat_of(c, c->classifier != KR_NO_MAT ? c->classifier : c->embedding);
+    CHECK(c, mt != nullptr, "no classifier bound");
+    CHECK(c, pro_fusable(dim) && mt->m.k == dim, "fused norm + logits: dim %zu", dim);
+    const DevMatrix* m;
+    int sem;
+    int rc = classifier_matrix(c, mt, &m, &sem);
+    if (rc) return rc;
+    BUF(yb, y, m->n);
+    BUF(xb, x, dim);
+    BUF(wb, w, dim);
+    const float* ap = nullptr;
+    if (add != KR_NO_BUF) {
+        BUF(ab, add, dim);
+        ap = ab->p;
+    }
+    float* yp = yb->p;
+    HIPCHK(c, kr::launch_project_pro(c->stream, sem, &m, &yp, 1, 1, xb->p, ap, wb->p, nullptr, eps));
+    return KR_OK;
+}
+
+int silu_project(kr_ctx* c, size_t layer, int proj, kr_buf gate, kr_buf up, kr_buf y, size_t width) {
+    CHECK(c, c->prepared && layer < c->n_layers, "layer %zu out of range", layer);
+    CHECK(c, pro_fusable(width), "fused silu + projection: width %zu", width);
+    const Mat* m = proj_mat(c, layer, proj);
+    CHECK(c, m != nullptr && m->m.k == width, "projection %d is not live on layer %zu", proj, layer);
+    BUF(g, gate, width);
+    BUF(u, up, width);
+    BUF(yb, y, m->m.n);
+    const DevMatrix* ms = &m->m;
+    float* yp = yb->p;
+    HIPCHK(c, kr::launch_project_pro(c->stream, sem_for_project(m->m), &ms, &yp, 1, 2, g->p, u->p, nullptr, nullptr,
+                                     0.0f));
+    return KR_OK;
+}
+
 int greedy_step(kr_ctx* c, kr_buf logits, size_t len, uint32_t* step) {
     BUF(l, logits, len);
     CHECK(c, len > 0, "argmax of an empty buffer");

@@ -56,4 +56,17 @@ int attention_quant(kr_ctx* c, kr_buf q, kr_buf out, kr_buf att, size_t layer, c
 // the classifier over the quantized workspace row
 int logits_q(kr_ctx* c, kr_buf y);
 
+// One decode row with the producer of the projection input fused into the
+// projection launch (results identical to the separate steps above):
+// whether a row of width k can take this path
+bool pro_fusable(size_t k);
+// x_out = x + add (add may be KR_NO_BUF), then the projections of
+// Q8(rms_norm(x_out, w)); x_out must not be x
+int norm_project(kr_ctx* c, size_t layer, const int* projs, const kr_buf* ys, int n, kr_buf x, kr_buf add, kr_buf w,
+                 kr_buf x_out, size_t dim, float eps);
+// the classifier of Q8(rms_norm(x + add, w)) (the updated x is not kept)
+int norm_logits(kr_ctx* c, kr_buf x, kr_buf add, kr_buf w, kr_buf y, size_t dim, float eps);
+// the projection of Q8(silu(gate) * up)
+int silu_project(kr_ctx* c, size_t layer, int proj, kr_buf gate, kr_buf up, kr_buf y, size_t width);
+
 }  // namespace kri

@@ -416,6 +416,257 @@ static hipError_t gemv_launch(hipStream_t st, MatSet ms, size_t k, QuantAct x, i
 }
 
 // ---------------------------------------------------------------------------
+// Decode GEMV with the producer of its activation fused in front (M = 1).
+//
+// A decode step alternates a short serial producer (the residual add +
+// RMSNorm + quantization, or SiLU(gate) * up + quantization) with a GEMV that
+// must wait for it. Run as two launches, the GEMV's weight fetch cannot start
+// until the producer ends. Here every workgroup issues the producer's loads
+// (L2-resident, a few KiB), then its weight loads, and computes the producer
+// while the weights are in flight: the serial RMS sum (dim dependent adds,
+// the reference order) overlaps the HBM round trip instead of preceding it.
+// The quantized row is built in LDS with the exact arithmetic of the
+// standalone kernels (k_add_rms_quant, k_silu_quant), so the results are
+// bit-identical to running those and then k_gemv. Workgroup 0 writes the
+// updated residual row to a second buffer (the other workgroups still read
+// the old one).
+struct GemvPro {
+    const float* a;  // PRO_NORM: residual row x; PRO_SILU: gate row
+    const float* b;  // PRO_NORM: the add into x (may be null); PRO_SILU: up row
+    const float* w;  // PRO_NORM: norm weight
+    float* x_out;    // PRO_NORM: x + add, written by workgroup 0 (may be null)
+    float eps;
+};
+static constexpr int PRO_NORM = 1, PRO_SILU = 2;
+
+template <int SEM, int PRO, int VPT>
+__global__ __launch_bounds__(256) void k_gemv_pro(MatSet ms, GemvPro pro, uint32_t K, uint32_t R,
+                                                  uint32_t step_rows, uint32_t step_cols) {
+    constexpr int CPT = 2;  // rows per tile keep R * K <= 8 KiB
+    // LDS: x quants [K] | x scale bits [nb] | scratch: squares [K], then the epilogue operands
+    extern __shared__ __align__(16) float sm[];
+    __shared__ float s_scale;
+    const int mi = blockIdx.x < ms.tile_end[0] ? 0 : (blockIdx.x < ms.tile_end[1] ? 1 : 2);
+    const uint32_t tile = blockIdx.x - (mi == 0 ? 0 : ms.tile_end[mi - 1]);
+    const int8_t* __restrict__ W = ms.q[mi];
+    const void* __restrict__ WS = ms.s[mi];
+    const uint32_t nb = K >> 5, kc = K >> 4, n4 = K >> 2;
+    const uint32_t row0 = tile * R;
+    const uint32_t rows = min(R, ms.n[mi] - row0);
+    const uint32_t C = rows * kc;
+    const uint32_t tid = threadIdx.x;
+    constexpr bool WF16 = SEM != SEM_FOUR_PARTIALS_F32;
+    constexpr bool XF16 = SEM == SEM_FMA_CHAIN;
+    int8_t* xq = (int8_t*)sm;
+    uint32_t* xsb = (uint32_t*)(sm + n4);
+    float* scratch = sm + ((n4 + nb + 3) & ~3u);
+
+    // 1. the producer's inputs first, so waiting for them never waits for the weights
+    float4 va[VPT], vb[VPT], vw[VPT];
+#pragma unroll
+    for (int u = 0; u < VPT; u++) {
+        const uint32_t f = tid + 256 * u;
+        if (f < n4) {
+            va[u] = ((const float4*)pro.a)[f];
+            vb[u] = pro.b ? ((const float4*)pro.b)[f] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (PRO == PRO_NORM) vw[u] = ((const float4*)pro.w)[f];
+        }
+    }
+    // 2. the weight tile, as k_gemv loads it
+    const int8_t* wt = W + (size_t)row0 * K;
+    uint32_t row = tid / kc, col = tid - (tid / kc) * kc;
+    v4i wv[CPT];
+    uint32_t wsb[CPT], rowu[CPT], colu[CPT];
+#pragma unroll
+    for (int u = 0; u < CPT; u++) {
+        const bool in = tid + 256 * u < C;
+        const uint32_t rr = in ? row : rows - 1, cc = in ? col : kc - 1;
+        rowu[u] = rr, colu[u] = cc;
+        wv[u] = __builtin_nontemporal_load((const v4i*)(wt + (size_t)rr * K + cc * 16));
+        wsb[u] = scale_bits(WF16, WS, (size_t)(row0 + rr) * nb + (cc >> 1));
+        col += step_cols;
+        row += step_rows;
+        if (col >= kc) col -= kc, row += 1;
+    }
+
+    // 3. the producer, while the weights are in flight
+    float4 o[VPT];
+    if (PRO == PRO_NORM) {
+#pragma unroll
+        for (int u = 0; u < VPT; u++) {
+            const uint32_t f = tid + 256 * u;
+            if (f < n4) {
+                float4 v = va[u];
+                if (pro.b) v = make_float4(v.x + vb[u].x, v.y + vb[u].y, v.z + vb[u].z, v.w + vb[u].w);
+                va[u] = v;
+                if (blockIdx.x == 0 && pro.x_out) ((float4*)pro.x_out)[f] = v;
+                ((float4*)scratch)[f] = make_float4(v.x * v.x, v.y * v.y, v.z * v.z, v.w * v.w);
+            }
+        }
+        __syncthreads();
+        if (tid == 0) {  // rms_norm_row (cpu.rs:635-641)
+            float ss = 0.0f;
+            uint32_t i = 0;
+            for (; i + 64 <= K; i += 64) {
+                float4 r[16];
+#pragma unroll
+                for (int u = 0; u < 16; u++) r[u] = *(const float4*)(scratch + i + 4 * u);
+#pragma unroll
+                for (int u = 0; u < 16; u++) {
+                    ss += r[u].x;
+                    ss += r[u].y;
+                    ss += r[u].z;
+                    ss += r[u].w;
+                }
+            }
+            for (; i < K; i++) ss += scratch[i];
+            ss = div_rn(ss, (float)K);
+            ss += pro.eps;
+            s_scale = div_rn(1.0f, sqrt_rn(ss));
+        }
+        __syncthreads();
+        const float scale = s_scale;
+#pragma unroll
+        for (int u = 0; u < VPT; u++) {
+            const float4 v = va[u], wq = vw[u];
+            o[u] = make_float4(wq.x * (scale * v.x), wq.y * (scale * v.y), wq.z * (scale * v.z), wq.w * (scale * v.w));
+        }
+    } else {
+#pragma unroll
+        for (int u = 0; u < VPT; u++) {  // silu (cpu.rs:708-710), then * up (cpu.rs:494-499)
+            const float4 g = va[u], up = vb[u];
+            o[u] = make_float4(div_rn(g.x, 1.0f + glibc_expf(-g.x)) * up.x, div_rn(g.y, 1.0f + glibc_expf(-g.y)) * up.y,
+                               div_rn(g.z, 1.0f + glibc_expf(-g.z)) * up.z, div_rn(g.w, 1.0f + glibc_expf(-g.w)) * up.w);
+        }
+    }
+    // Q8Vec::quantize_into (quant.rs:864-873) into LDS; a block is 8 threads
+#pragma unroll
+    for (int u = 0; u < VPT; u++) {
+        const uint32_t f = tid + 256 * u;
+        if (f < n4) {  // K % 32 == 0: the 8 threads of a block are all in range or all out
+            const float4 v = o[u];
+            float m = fmaxf(fmaxf(fmaxf(fmaxf(0.0f, fabsf(v.x)), fabsf(v.y)), fabsf(v.z)), fabsf(v.w));
+#pragma unroll
+            for (int off = 4; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 8));
+            const float d = div_rn(m, 127.0f);
+            const float inv = d > 0.0f ? div_rn(1.0f, d) : 0.0f;
+            char4 qq;
+            qq.x = q8_round(v.x * inv);
+            qq.y = q8_round(v.y * inv);
+            qq.z = q8_round(v.z * inv);
+            qq.w = q8_round(v.w * inv);
+            ((char4*)xq)[f] = qq;
+            if ((f & 7) == 0) xsb[f / 8] = XF16 ? (uint32_t)f32_to_f16_bits(d) : f2u(d);
+        }
+    }
+    __syncthreads();
+
+    // 4. block dots against the LDS row, then the epilogue of k_gemv
+    const uint32_t per = gemv_out_floats(SEM, nb), q4p = gemv_q4p(nb);
+    float* res = scratch;
+    const uint32_t dummy = rows * per;
+    const bool even = (tid & 1) == 0;
+#pragma unroll
+    for (int u = 0; u < CPT; u++) {
+        const bool valid = tid + 256 * u < C;
+        const uint32_t r = rowu[u], b = colu[u] >> 1;
+        const float ws = scale_value(WF16, wsb[u]);
+        const v4i xv = *(const v4i*)(xq + colu[u] * 16);
+        const uint32_t xs = xsb[b];
+        int acc = 0;
+        acc = __builtin_amdgcn_sdot4(wv[u].x, xv.x, acc, false);
+        acc = __builtin_amdgcn_sdot4(wv[u].y, xv.y, acc, false);
+        acc = __builtin_amdgcn_sdot4(wv[u].z, xv.z, acc, false);
+        acc = __builtin_amdgcn_sdot4(wv[u].w, xv.w, acc, false);
+        const int isum = acc + __shfl_xor(acc, 1);
+        const bool own = valid && even;
+        const uint32_t base = r * per;
+        if (SEM == SEM_FMA_CHAIN) {
+            float2* op = (float2*)(res + (own ? base + 2 * b : dummy));
+            *op = make_float2((float)isum, ws * f16w((uint16_t)xs));
+        } else {
+            res[own ? base + (b & 3) * q4p + (b >> 2) : dummy] = (ws * u2f(xs)) * (float)isum;
+        }
+    }
+    __syncthreads();
+    float* Y = ms.y[mi];
+    if (SEM == SEM_FMA_CHAIN) {
+        for (uint32_t oi = tid; oi < rows; oi += 256) Y[row0 + oi] = seq_fma((const float2*)(res + (size_t)oi * per), nb);
+    } else {
+        for (uint32_t base = 0; base < 4 * rows; base += 256) {
+            const uint32_t i = base + tid, oi = i >> 2, j = i & 3;
+            float t = 0.0f;
+            if (oi < rows && j < nb) t = lds_sum(res + (size_t)oi * per + j * q4p, (nb - j + 3) / 4);
+            const float t0 = quad_bcast<0>(t), t1 = quad_bcast<1>(t), t2 = quad_bcast<2>(t), t3 = quad_bcast<3>(t);
+            if (oi < rows && j == 0) Y[row0 + oi] = ((t0 + t1) + t2) + t3;
+        }
+    }
+}
+
+template <int SEM, int PRO>
+static hipError_t gemv_pro_go(hipStream_t st, MatSet ms, size_t k, const GemvPro& pro) {
+    size_t n_max = 0;
+    for (int i = 0; i < ms.count; i++) n_max = ms.n[i] > n_max ? ms.n[i] : n_max;
+    const size_t R = gemv_rows_per_tile(n_max, k);
+    if (R * (k / 16) > 512) return hipErrorInvalidValue;
+    uint32_t total = 0;
+    for (int i = 0; i < 3; i++) {
+        if (i < ms.count) total += (uint32_t)((ms.n[i] + R - 1) / R);
+        ms.tile_end[i] = total;
+    }
+    const size_t nb = k / 32, head = (k / 4 + nb + 3) & ~(size_t)3;
+    const size_t ops = R * gemv_out_floats(SEM, (uint32_t)nb) + 2;
+    const size_t lds = (head + (ops > k ? ops : k)) * sizeof(float);
+    const size_t vpt = (k / 4 + 255) / 256;
+    const uint32_t kc = (uint32_t)(k / 16);
+#define KR_PRO_GO(V)                                                                                            \
+    hipLaunchKernelGGL((k_gemv_pro<SEM, PRO, V>), dim3(total), dim3(256), lds, st, ms, pro, (uint32_t)k,         \
+                       (uint32_t)R, 256 / kc, 256 % kc)
+    if (vpt <= 1)
+        KR_PRO_GO(1);
+    else if (vpt <= 2)
+        KR_PRO_GO(2);
+    else if (vpt <= 4)
+        KR_PRO_GO(4);
+    else
+        KR_PRO_GO(8);
+#undef KR_PRO_GO
+    return hipGetLastError();
+}
+
+hipError_t launch_project_pro(hipStream_t st, int sem, const DevMatrix* const* w, float* const* y, int count,
+                              int pro_kind, const float* a, const float* b, const float* norm_w, float* x_out,
+                              float eps) {
+    if (count < 1 || count > 3 || (pro_kind != PRO_NORM && pro_kind != PRO_SILU)) return hipErrorInvalidValue;
+    const size_t k = w[0]->k;
+    if (k % 32 != 0 || k > 8192) return hipErrorInvalidValue;
+    MatSet ms{};
+    ms.count = count;
+    for (int i = 0; i < count; i++) {
+        if (w[i]->k != k || w[i]->storage != w[0]->storage) return hipErrorInvalidValue;
+        ms.q[i] = w[i]->q;
+        ms.s[i] = w[i]->s;
+        ms.y[i] = y[i];
+        ms.n[i] = (uint32_t)w[i]->n;
+        ms.ld[i] = (uint32_t)w[i]->n;
+    }
+    GemvPro pro{a, b, norm_w, x_out, eps};
+#define KR_PRO_SEM(P)                                                                          \
+    switch (sem) {                                                                             \
+        case SEM_FMA_CHAIN: return gemv_pro_go<SEM_FMA_CHAIN, P>(st, ms, k, pro);              \
+        case SEM_FOUR_PARTIALS_F32: return gemv_pro_go<SEM_FOUR_PARTIALS_F32, P>(st, ms, k, pro); \
+        case SEM_FOUR_PARTIALS_F16: return gemv_pro_go<SEM_FOUR_PARTIALS_F16, P>(st, ms, k, pro); \
+    }
+    if (pro_kind == PRO_NORM) {
+        KR_PRO_SEM(PRO_NORM)
+    } else {
+        KR_PRO_SEM(PRO_SILU)
+    }
+#undef KR_PRO_SEM
+    return hipErrorInvalidValue;
+}
+
+// ---------------------------------------------------------------------------
 // Quantized GEMM on int8 MFMA (prefill and batched rows, M >= kGemmMinRows).
 //
 // v_mfma_i32_32x32x32_i8 multiplies a 32x32 int8 tile of activations by a
@@ -1137,10 +1388,9 @@ __global__ __launch_bounds__(512) void k_attention_fast(
     const uint32_t count = n_shared + w.slot - w.att_start + 1;  // <= scs: sized for the longest window
     const uint32_t width = n_heads * HS, d0 = sidx * DW;
     const uint32_t h0 = hg * G, kvo = (h0 / kv_mul) * HS;
-    float* qs = sm;
+    const float* __restrict__ qg = q + (size_t)row * width + (size_t)h0 * HS;
     float* sc = sm + G * HS;
     float* work = sc + G * scs;
-    for (uint32_t e = tid; e < G * HS; e += T) qs[e] = q[(size_t)row * width + (size_t)h0 * HS + e];
     if (tid < 32) etab[tid] = kExp2Tab[tid];
 
     // 1. scores, K in chunks of kcap <= T rows
@@ -1177,7 +1427,8 @@ __global__ __launch_bounds__(512) void k_attention_fast(
                 for (int j = 0; j < G; j++) {
 #pragma unroll
                     for (int u = 0; u < U; u++) {
-                        const float4 qq = *(const float4*)(qs + j * HS + 4 * (c + u));
+                        // the same q for every lane: scalar loads into SGPRs
+                        const float4 qq = *(const float4*)(qg + j * HS + 4 * (c + u));
                         acc[j][0] = __builtin_fmaf(qq.x, kk[u].x, acc[j][0]);
                         acc[j][1] = __builtin_fmaf(qq.y, kk[u].y, acc[j][1]);
                         acc[j][2] = __builtin_fmaf(qq.z, kk[u].z, acc[j][2]);
@@ -1411,9 +1662,10 @@ hipError_t launch_attention(hipStream_t st, const float* q, float* out, float* a
 // quantization of the normed row (quant.rs:856-874), one row per workgroup.
 // Thread t holds float4 t, t + 256, ... of the row in registers: the residual
 // sum, the norm weight (loaded before the chain, off its critical path) and
-// the squares, which go to LDS for the serial sum. Wave 0 runs that sum, all
-// 64 lanes in lockstep on the same values (uniform control flow), reading
-// LDS in runs of 64 values per wait. A Q8 block is 8 consecutive threads.
+// the squares, which go to LDS for the serial sum. Lane 0 alone runs that
+// sum, reading LDS in runs of 64 values per wait (one active lane: the same
+// loop on all 64 lanes of a wave ran 2.5x slower when other work shared the
+// CU). A Q8 block is 8 consecutive threads.
 template <bool ADD, int VPT>
 __global__ __launch_bounds__(256) void k_add_rms_quant(float* __restrict__ x, const float* __restrict__ add,
                                                        const float* __restrict__ w, float* __restrict__ out,
@@ -1446,7 +1698,7 @@ __global__ __launch_bounds__(256) void k_add_rms_quant(float* __restrict__ x, co
         }
     }
     __syncthreads();
-    if (tid < 64) {
+    if (tid == 0) {
         // rms_norm_row (cpu.rs:635-641): ss = sum of squares left to right,
         // ss /= dim, ss += eps, scale = 1 / sqrt(ss)
         float ss = 0.0f;
@@ -1466,7 +1718,7 @@ __global__ __launch_bounds__(256) void k_add_rms_quant(float* __restrict__ x, co
         for (; i < dim; i++) ss += sq[i];
         ss = div_rn(ss, (float)dim);
         ss += eps;
-        if (tid == 0) s_scale = div_rn(1.0f, sqrt_rn(ss));
+        s_scale = div_rn(1.0f, sqrt_rn(ss));
     }
     __syncthreads();
     const float scale = s_scale;
@@ -1763,32 +2015,46 @@ hipError_t launch_embed(hipStream_t st, const DevMatrix& e, size_t token, const 
 
 // argmax with Iterator::max_by(total_cmp) semantics: the largest total-order
 // key wins and, among equal keys, the largest index (generate.rs:70-77).
-__global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ x, uint32_t n, uint32_t* out) {
+// Each thread loads its float4s of a 16-float4-per-thread stripe at once, then
+// scans them in index order; the stripes, threads and waves then reduce with
+// the same tie rule. With `ring`, thread 0 also does the greedy bookkeeping:
+// the token feeds the next step (out[0]), is recorded in the ring, and the
+// position (out[2]) and ring index (out[5]) advance.
+__device__ __forceinline__ void argmax_take(int32_t k, uint32_t i, int32_t& best, uint32_t& bi) {
+    if (k > best || (k == best && i > bi)) best = k, bi = i;
+}
+__global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ x, uint32_t n, uint32_t* out,
+                                                 uint32_t* ring, uint32_t ring_len) {
     __shared__ int32_t skey[16];
     __shared__ uint32_t sidx[16];
+    constexpr uint32_t T = 1024, U = 16;
     int32_t best = INT32_MIN;
     uint32_t bi = 0;
-    bool any = false;
-    for (uint32_t i = threadIdx.x; i < n; i += 1024) {
-        int32_t k = total_order_key(x[i]);
-        if (!any || k >= best) {
-            best = k;
-            bi = i;
-            any = true;
+    const uint32_t n4 = n / 4;
+    for (uint32_t base = 0; base < n4; base += T * U) {
+        float4 v[U];
+#pragma unroll
+        for (uint32_t u = 0; u < U; u++) {
+            const uint32_t f = base + u * T + threadIdx.x;
+            v[u] = ((const float4*)x)[f < n4 ? f : 0];
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < U; u++) {
+            const uint32_t f = base + u * T + threadIdx.x;
+            if (f < n4) {
+                argmax_take(total_order_key(v[u].x), 4 * f, best, bi);
+                argmax_take(total_order_key(v[u].y), 4 * f + 1, best, bi);
+                argmax_take(total_order_key(v[u].z), 4 * f + 2, best, bi);
+                argmax_take(total_order_key(v[u].w), 4 * f + 3, best, bi);
+            }
         }
     }
-    if (!any) {
-        best = INT32_MIN;
-        bi = 0;
-    }
+    for (uint32_t i = 4 * n4 + threadIdx.x; i < n; i += T) argmax_take(total_order_key(x[i]), i, best, bi);
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
-        int32_t ok = __shfl_xor(best, off);
-        uint32_t oi = __shfl_xor(bi, off);
-        if (ok > best || (ok == best && oi > bi)) {
-            best = ok;
-            bi = oi;
-        }
+        const int32_t ok = __shfl_xor(best, off);
+        const uint32_t oi = __shfl_xor(bi, off);
+        argmax_take(ok, oi, best, bi);
     }
     if ((threadIdx.x & 63) == 0) {
         skey[threadIdx.x >> 6] = best;
@@ -1798,35 +2064,26 @@ __global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ x, ui
     if (threadIdx.x == 0) {
         int32_t b = skey[0];
         uint32_t idx = sidx[0];
-        for (int w = 1; w < 16; w++)
-            if (skey[w] > b || (skey[w] == b && sidx[w] > idx)) {
-                b = skey[w];
-                idx = sidx[w];
-            }
+        for (int w = 1; w < 16; w++) argmax_take(skey[w], sidx[w], b, idx);
         out[0] = idx;
+        if (ring) {
+            const uint32_t i = out[5];
+            if (i < ring_len) ring[i] = idx;
+            out[5] = i + 1;
+            out[2] = out[2] + 1;
+        }
     }
 }
 hipError_t launch_argmax(hipStream_t st, const float* x, size_t n, uint32_t* out) {
-    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, st, x, (uint32_t)n, out);
+    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, st, x, (uint32_t)n, out, nullptr, 0u);
     return hipGetLastError();
 }
 
-// Greedy decode bookkeeping after the argmax: the chosen token feeds the next
-// step's embedding and is recorded in the ring; position and ring index
-// advance. Runs as one lane after k_argmax has written step[0].
-__global__ void k_step_advance(uint32_t* step, uint32_t* ring, uint32_t ring_len) {
-    if (threadIdx.x != 0 || blockIdx.x != 0) return;
-    uint32_t i = step[5];
-    if (i < ring_len) ring[i] = step[0];
-    step[5] = i + 1;
-    step[2] = step[2] + 1;
-}
+// Greedy decode: argmax into step[0] plus the ring / position bookkeeping,
+// one launch.
 hipError_t launch_greedy_step(hipStream_t st, const float* logits, size_t n, uint32_t* step, uint32_t* ring,
                               size_t ring_len) {
-    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, st, logits, (uint32_t)n, step);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k_step_advance, dim3(1), dim3(64), 0, st, step, ring, (uint32_t)ring_len);
+    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, st, logits, (uint32_t)n, step, ring, (uint32_t)ring_len);
     return hipGetLastError();
 }
 

@@ -54,6 +54,12 @@ hipError_t launch_rope_kv(hipStream_t st, float* q, float* k, const float* v, si
                           size_t head_size, int interleaved, float* kc, float* vc, size_t layer, size_t seq_len);
 
 // y[m*ldy + n] for m < rows. Uses the GEMV path (rows <= 4) or the MFMA GEMM.
+// One decode row (M = 1) of 1-3 projections with the producer of their input
+// fused in front: pro_kind 1 = x (+= add) -> rms_norm(w, eps) -> Q8 (the
+// updated x row goes to x_out when non-null), 2 = silu(a) * b -> Q8.
+hipError_t launch_project_pro(hipStream_t st, int sem, const DevMatrix* const* w, float* const* y, int count,
+                              int pro_kind, const float* a, const float* b, const float* norm_w, float* x_out,
+                              float eps);
 hipError_t launch_project(hipStream_t st, int sem, const DevMatrix& w, QuantAct x, size_t rows,
                           float* y, size_t ldy, int32_t* dbg_block_dots);
 

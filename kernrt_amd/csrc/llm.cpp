@@ -41,7 +41,7 @@ struct krl_model {
     std::vector<Norms> norms;
     std::vector<long> conv_kernels, conv_state;
     kr_buf rms_final = 0;
-    kr_buf x, xb, q, k, v, attn, o, bcx, h, co, cy, gate, up, mlp, hidden, att, logits;
+    kr_buf x, x2, xb, q, k, v, attn, o, bcx, h, co, cy, gate, up, mlp, hidden, att, logits;
     std::vector<float> logits_host;
     bool has_prefill = false;
     PrefillBuffers pb;
@@ -120,6 +120,7 @@ int construct(krl_model* m, const krl_weights* w) {
         }
     }
     TRY(alloc(m, dim, &m->x));
+    TRY(alloc(m, dim, &m->x2));
     TRY(alloc(m, dim, &m->xb));
     TRY(alloc(m, q_dim, &m->q));
     TRY(alloc(m, kv_dim, &m->k));
@@ -170,10 +171,17 @@ Geometry geometry(const krl_config& c) {
 // The decode step with fused kernels: same values as the op-by-op schedule
 // below. Each residual add_in_place is folded into the rms_norm that follows
 // it, and every projection input is quantized by the kernel that produces it.
+// Where the width allows, the attention and FFN norms run inside the launch
+// of the projection that consumes them; the residual row then alternates
+// between two buffers, because that launch's workgroups all still read the
+// old row while one of them writes the new one.
 int decode_step_fused(krl_model* m, size_t token, size_t pos, bool dev) {
     kr_ctx* b = m->b;
     Geometry g = geometry(m->c);
     const uint32_t* s = m->step;
+    const bool pro = kri::pro_fusable(g.dim);
+    kr_buf X[2] = {m->x, m->x2};
+    int cur = 0;
     if (dev)
         KRC(m, kri::embed_dev(b, s + 0, m->x, 0));
     else
@@ -181,13 +189,23 @@ int decode_step_fused(krl_model* m, size_t token, size_t pos, bool dev) {
     size_t positions[1] = {pos};
     kr_window win{0, pos, 0, 0};
     kr_buf pending = kri::KR_NO_BUF;  // the residual still to add into x
+    // norm(x + add) feeding the projections projs -> ys
+    auto norm_then = [&](kr_buf add, kr_buf w, size_t l, const int* projs, const kr_buf* ys, int n) -> int {
+        if (pro) {
+            KRC(m, kri::norm_project(b, l, projs, ys, n, X[cur], add, w, X[cur ^ 1], g.dim, g.eps));
+            cur ^= 1;
+        } else {
+            KRC(m, kri::norm_quant(b, X[cur], add, w, m->xb, 1, g.dim, g.eps));
+            KRC(m, kri::project_q(b, l, projs, ys, n, 1));
+        }
+        return KR_OK;
+    };
     for (size_t l = 0; l < m->c.n_layers; l++) {
         const Norms& n = m->norms[l];
-        KRC(m, kri::norm_quant(b, m->x, pending, n.att, m->xb, 1, g.dim, g.eps));
         if (m->is_attention[l]) {
             int qkv[3] = {KR_PROJ_Q, KR_PROJ_K, KR_PROJ_V};
             kr_buf ys[3] = {m->q, m->k, m->v};
-            KRC(m, kri::project_q(b, l, qkv, ys, 3, 1));
+            TRY(norm_then(pending, n.att, l, qkv, ys, 3));
             if (n.has_q) KRC(m, kr_qk_norm(b, m->q, 1, g.q_dim, g.hs, n.q, g.eps));
             if (n.has_k) KRC(m, kr_qk_norm(b, m->k, 1, g.kv_dim, g.hs, n.k, g.eps));
             KRC(m, kri::rope_kv(b, m->q, m->k, m->v, g.q_dim, g.kv_dim, 1, dev ? nullptr : positions,
@@ -206,23 +224,26 @@ int decode_step_fused(krl_model* m, size_t token, size_t pos, bool dev) {
             KRC(m, kri::project_q(b, l, o, &m->o, 1, 1));
         } else {
             int ci[1] = {KR_PROJ_CONV_IN};
-            KRC(m, kri::project_q(b, l, ci, &m->bcx, 1, 1));
+            TRY(norm_then(pending, n.att, l, ci, &m->bcx, 1));
             KRC(m, kr_mul(b, m->h, 0, m->bcx, 0, m->bcx, 2 * g.dim, g.dim));
             KRC(m, kr_conv_decode(b, m->co, m->h, (kr_buf)m->conv_kernels[l], (kr_buf)m->conv_state[l], g.dim,
                                   m->conv_k[l]));
             KRC(m, kr_mul(b, m->cy, 0, m->bcx, g.dim, m->co, 0, g.dim));
             KRC(m, kr_project(b, l, KR_PROJ_CONV_OUT, m->cy, m->o, 1));
         }
-        KRC(m, kri::norm_quant(b, m->x, m->o, n.ffn, m->xb, 1, g.dim, g.eps));
         int gu[2] = {KR_PROJ_GATE, KR_PROJ_UP};
         kr_buf gys[2] = {m->gate, m->up};
-        KRC(m, kri::project_q(b, l, gu, gys, 2, 1));
+        TRY(norm_then(m->o, n.ffn, l, gu, gys, 2));
+        // SiLU * up and the final norm stay separate launches: every workgroup
+        // of a fused launch would redo 'hidden' double-precision exp/divisions,
+        // or (classifier) 49k rows' worth of workgroups the serial norm sum;
+        // both measured slower than the two-launch form
         KRC(m, kri::silu_quant(b, m->gate, m->up, 1, g.hidden));
         int dn[1] = {KR_PROJ_DOWN};
         KRC(m, kri::project_q(b, l, dn, &m->mlp, 1, 1));
         pending = m->mlp;
     }
-    KRC(m, kri::norm_quant(b, m->x, pending, m->rms_final, m->xb, 1, g.dim, g.eps));
+    KRC(m, kri::norm_quant(b, X[cur], pending, m->rms_final, m->xb, 1, g.dim, g.eps));
     KRC(m, kri::logits_q(b, m->logits));
     if (dev) KRC(m, kri::greedy_step(b, m->logits, m->c.vocab_size, m->step));
     return KR_OK;

@@ -92,6 +92,9 @@ struct kr_ctx {
     uint64_t epoch = 0;
     size_t q_rows = 0, q_width = 0;  // what the activation workspace holds
     hipEvent_t t0 = nullptr, t1 = nullptr;
+    // decode attention scratch: scores and per-chunk maxima
+    float* attn_scratch = nullptr;
+    size_t cap_attn_scratch = 0;
     // one captured launch sequence (kr_capture_begin / kr_capture_end)
     bool capturing = false;
     hipGraph_t graph = nullptr;
@@ -442,7 +445,7 @@ void kr_close(kr_ctx* c) {
     free_stage(c->st_pos);
     free_stage(c->st_slots);
     free_stage(c->st_win);
-    void* ptrs[] = {c->kc, c->vc, c->wq, c->ws, c->wh, c->tmp, c->tokens, c->counter};
+    void* ptrs[] = {c->kc, c->vc, c->wq, c->ws, c->wh, c->tmp, c->tokens, c->counter, c->attn_scratch};
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
     if (c->t0) (void)hipEventDestroy(c->t0);
@@ -1264,6 +1267,75 @@ int silu_project(kr_ctx* c, size_t layer, int proj, kr_buf gate, kr_buf up, kr_b
     float* yp = yb->p;
     HIPCHK(c, kr::launch_project_pro(c->stream, sem_for_project(m->m), &ms, &yp, 1, 2, g->p, u->p, nullptr, nullptr,
                                      0.0f));
+    return KR_OK;
+}
+
+bool split_attention_ok(kr_ctx* c, const kr_attn_spec* sp) {
+    return sp && c->prepared && sp->seq_len == c->seq_len &&
+           kr::attention_split_ok(c->seq_len, sp->kv_mul, sp->head_size);
+}
+
+int rope_attention(kr_ctx* c, kr_buf q, kr_buf k, kr_buf v, kr_buf out, kr_buf att, size_t layer, size_t pos_host,
+                   const uint32_t* step_dev, const kr_attn_spec* sp, const kr_rope_spec* rs) {
+    CHECK(c, c->prepared && layer < c->n_layers, "layer %zu out of range", layer);
+    CHECK(c, split_attention_ok(c, sp) && sp->kv_dim == c->kv_dim && sp->n_heads % sp->kv_mul == 0,
+          "split decode attention does not apply to this geometry");
+    CHECK(c, rs && rs->head_size == sp->head_size, "rope and attention head sizes differ");
+    const size_t width = sp->n_heads * sp->head_size;
+    BUF(qb, q, width);
+    BUF(kb, k, c->kv_dim);
+    BUF(vb, v, c->kv_dim);
+    BUF(ob, out, width);
+    BUF(ab, att, sp->n_heads * sp->seq_len);
+    const size_t need = kr::attention_split_scratch(sp->n_heads, c->seq_len);
+    if (need > c->cap_attn_scratch) {
+        if (c->attn_scratch) HIPCHK(c, hipFree(c->attn_scratch));
+        c->attn_scratch = nullptr;
+        HIPCHK(c, hipMalloc(&c->attn_scratch, need * sizeof(float)));
+        c->cap_attn_scratch = need;
+        c->epoch++;
+    }
+    const float2* tab;
+    const uint32_t* wd;
+    const uint32_t* pd;
+    size_t max_count;
+    int rc;
+    if (step_dev) {  // window at step[1..4], position (== slot) at step[2]
+        rc = rope_table(c, rs->theta, rs->head_size, c->seq_len, &tab);
+        if (rc) return rc;
+        wd = step_dev + 1;
+        pd = step_dev + 2;
+        max_count = c->seq_len;
+    } else {
+        CHECK(c, pos_host < c->seq_len, "position %zu out of range", pos_host);
+        rc = rope_table(c, rs->theta, rs->head_size, pos_host + 1, &tab);
+        if (rc) return rc;
+        uint32_t w[4] = {0, (uint32_t)pos_host, 0, 0};
+        rc = stage(c, c->st_win, w, 4, &wd);
+        if (rc) return rc;
+        uint32_t p = (uint32_t)pos_host;
+        rc = stage(c, c->st_pos, &p, 1, &pd);
+        if (rc) return rc;
+        max_count = pos_host + 1;
+    }
+    const float scale = 1.0f / sqrtf((float)sp->head_size);  // cpu.rs:591
+    HIPCHK(c, kr::launch_attention_split(c->stream, qb->p, kb->p, vb->p, ob->p, ab->p, c->kc, c->vc, layer,
+                                         (const kr::DevWindow*)wd, pd, tab, rs->interleaved, max_count, sp->n_heads,
+                                         sp->kv_mul, sp->head_size, c->kv_dim, c->seq_len, scale, c->attn_scratch));
+    return KR_OK;
+}
+
+int quant_project(kr_ctx* c, size_t layer, int proj, kr_buf x, kr_buf y, size_t width) {
+    CHECK(c, c->prepared && layer < c->n_layers, "layer %zu out of range", layer);
+    CHECK(c, pro_fusable(width), "fused quantize + projection: width %zu", width);
+    const Mat* m = proj_mat(c, layer, proj);
+    CHECK(c, m != nullptr && m->m.k == width, "projection %d is not live on layer %zu", proj, layer);
+    BUF(xb, x, width);
+    BUF(yb, y, m->m.n);
+    const DevMatrix* ms = &m->m;
+    float* yp = yb->p;
+    HIPCHK(c, kr::launch_project_pro(c->stream, sem_for_project(m->m), &ms, &yp, 1, 3, xb->p, nullptr, nullptr,
+                                     nullptr, 0.0f));
     return KR_OK;
 }
 

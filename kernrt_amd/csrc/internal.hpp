@@ -68,5 +68,16 @@ int norm_project(kr_ctx* c, size_t layer, const int* projs, const kr_buf* ys, in
 int norm_logits(kr_ctx* c, kr_buf x, kr_buf add, kr_buf w, kr_buf y, size_t dim, float eps);
 // the projection of Q8(silu(gate) * up)
 int silu_project(kr_ctx* c, size_t layer, int proj, kr_buf gate, kr_buf up, kr_buf y, size_t width);
+// the projection of Q8(x) (x one f32 row of `width`)
+int quant_project(kr_ctx* c, size_t layer, int proj, kr_buf x, kr_buf y, size_t width);
+
+// Decode attention of one row as two launches that spread the cache reads
+// over many CUs, with rope of q and k and the kv_write of k and v folded in:
+// the same values as rope_kv + attention. Whether it applies to `spec`:
+bool split_attention_ok(kr_ctx* c, const kr_attn_spec* spec);
+// window {0, pos, 0, 0} and position from the host (pos_host), or from the
+// device step record (step_dev: window at step[1..4], position at step[2])
+int rope_attention(kr_ctx* c, kr_buf q, kr_buf k, kr_buf v, kr_buf out, kr_buf att, size_t layer, size_t pos_host,
+                   const uint32_t* step_dev, const kr_attn_spec* spec, const kr_rope_spec* rope);
 
 }  // namespace kri

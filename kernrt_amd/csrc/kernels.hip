@@ -267,6 +267,24 @@ __device__ __forceinline__ float quad_bcast(float v) {
     return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), K * 0x55, 0xf, 0xf, false));
 }
 
+// NaN-ignoring max over the 64 lanes of a wave, returned to every lane: DPP
+// swaps within quads, half-rows and rows, then row broadcasts 15 and 31 into
+// lane 63 (a few cycles each, no LDS round trip). Max is order-free.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float dpp_max_step(float v) {
+    return fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, ROWS, 0xf,
+                                                               false)));
+}
+__device__ __forceinline__ float wave_max(float v) {
+    v = dpp_max_step<0xB1, 0xf>(v);   // quad_perm [1,0,3,2]
+    v = dpp_max_step<0x4E, 0xf>(v);   // quad_perm [2,3,0,1]
+    v = dpp_max_step<0x141, 0xf>(v);  // row_half_mirror
+    v = dpp_max_step<0x140, 0xf>(v);  // row_mirror
+    v = dpp_max_step<0x142, 0xa>(v);  // row_bcast:15 into rows 1, 3
+    v = dpp_max_step<0x143, 0xc>(v);  // row_bcast:31 into rows 2, 3
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
 template <int SEM, int M, int CPT>
 __global__ __launch_bounds__(256) void k_gemv(MatSet ms, QuantAct x, uint32_t K, uint32_t R, uint32_t step_rows,
                                               uint32_t step_cols, int32_t* __restrict__ dbg) {
@@ -437,7 +455,7 @@ struct GemvPro {
     float* x_out;    // PRO_NORM: x + add, written by workgroup 0 (may be null)
     float eps;
 };
-static constexpr int PRO_NORM = 1, PRO_SILU = 2;
+static constexpr int PRO_NORM = 1, PRO_SILU = 2, PRO_QUANT = 3;
 
 template <int SEM, int PRO, int VPT>
 __global__ __launch_bounds__(256) void k_gemv_pro(MatSet ms, GemvPro pro, uint32_t K, uint32_t R,
@@ -531,6 +549,9 @@ __global__ __launch_bounds__(256) void k_gemv_pro(MatSet ms, GemvPro pro, uint32
             const float4 v = va[u], wq = vw[u];
             o[u] = make_float4(wq.x * (scale * v.x), wq.y * (scale * v.y), wq.z * (scale * v.z), wq.w * (scale * v.w));
         }
+    } else if (PRO == PRO_QUANT) {
+#pragma unroll
+        for (int u = 0; u < VPT; u++) o[u] = va[u];
     } else {
 #pragma unroll
         for (int u = 0; u < VPT; u++) {  // silu (cpu.rs:708-710), then * up (cpu.rs:494-499)
@@ -637,7 +658,7 @@ static hipError_t gemv_pro_go(hipStream_t st, MatSet ms, size_t k, const GemvPro
 hipError_t launch_project_pro(hipStream_t st, int sem, const DevMatrix* const* w, float* const* y, int count,
                               int pro_kind, const float* a, const float* b, const float* norm_w, float* x_out,
                               float eps) {
-    if (count < 1 || count > 3 || (pro_kind != PRO_NORM && pro_kind != PRO_SILU)) return hipErrorInvalidValue;
+    if (count < 1 || count > 3 || pro_kind < PRO_NORM || pro_kind > PRO_QUANT) return hipErrorInvalidValue;
     const size_t k = w[0]->k;
     if (k % 32 != 0 || k > 8192) return hipErrorInvalidValue;
     MatSet ms{};
@@ -659,6 +680,8 @@ hipError_t launch_project_pro(hipStream_t st, int sem, const DevMatrix* const* w
     }
     if (pro_kind == PRO_NORM) {
         KR_PRO_SEM(PRO_NORM)
+    } else if (pro_kind == PRO_QUANT) {
+        KR_PRO_SEM(PRO_QUANT)
     } else {
         KR_PRO_SEM(PRO_SILU)
     }
@@ -1553,6 +1576,260 @@ __global__ __launch_bounds__(512) void k_attention_fast(
         // DW % 32 == 0: each 32-lane group is one Q8 block of the head output
         if (qo) quant_lane(o, true, qo + oi, so + oi / 32, ho + oi / 32);
     }
+}
+
+// ---------------------------------------------------------------------------
+// Decode attention, split in two launches so that the KV reads spread over
+// many CUs (one CU pulls only ~40 GB/s, so a head's whole K and V through one
+// workgroup is the critical path otherwise). Same arithmetic as k_attention.
+//
+// k_attn_scores, workgroup = (KV head, 64 cache rows): RoPE of the head's
+// query heads and of the new key (cpu.rs:274-302, the host-built cos/sin
+// table), the kv_write of the new key and value (cpu.rs:238-246, by the
+// chunk-0 workgroup), then one lane per cache row runs the four-chain dot for
+// every query head; the scores go to a scratch row per head.
+// The new position's key is taken from LDS, not from the cache being written.
+template <int G, int HS>
+__global__ __launch_bounds__(64) void k_attn_scores(const float* __restrict__ q, const float* __restrict__ kin,
+                                                    const float* __restrict__ vin, float* __restrict__ kc,
+                                                    float* __restrict__ vc, size_t loff,
+                                                    const DevWindow* __restrict__ win, const uint32_t* __restrict__ pos,
+                                                    const float2* __restrict__ tab, int interleaved, uint32_t kv_dim,
+                                                    float scale, float* __restrict__ sc, uint32_t ss) {
+    constexpr uint32_t F = HS / 4, HALF = HS / 2;
+    __shared__ __align__(16) float qs[G * HS];
+    __shared__ __align__(16) float kn[HS];
+    const uint32_t lane = threadIdx.x, hk = blockIdx.x, chunk = blockIdx.y;
+    const DevWindow w = win[0];
+    const uint32_t n_shared = w.shared_end - w.shared_start;
+    const uint32_t count = n_shared + w.slot - w.att_start + 1;
+    const uint32_t r0 = chunk * 64;
+    if (r0 >= count && chunk != 0) return;
+    const float2* tr = tab + (size_t)pos[0] * HALF;
+    const float* qh = q + (size_t)hk * G * HS;
+    for (uint32_t t = lane; t < (G + 1) * HALF; t += 64) {
+        const uint32_t hh = t / HALF, i = t - hh * HALF;
+        const float* src = hh < G ? qh + hh * HS : kin + (size_t)hk * HS;
+        float* dst = hh < G ? qs + hh * HS : kn;
+        const uint32_t i0 = interleaved ? 2 * i : i, i1 = interleaved ? 2 * i + 1 : i + HALF;
+        const float2 cs = tr[i];
+        const float a = src[i0], b = src[i1];
+        dst[i0] = a * cs.x - b * cs.y;
+        dst[i1] = a * cs.y + b * cs.x;
+    }
+    __syncthreads();
+    if (chunk == 0) {
+        const size_t at = loff + (size_t)w.slot * kv_dim + (size_t)hk * HS;
+        for (uint32_t e = lane; e < HS; e += 64) {
+            kc[at + e] = kn[e];
+            vc[at + e] = vin[(size_t)hk * HS + e];
+        }
+        if (r0 >= count) return;
+    }
+    const uint32_t i = r0 + lane;
+    const bool live = i < count;
+    const uint32_t ic = live ? i : count - 1;
+    float4 kk[F];
+    const float4* krow = (const float4*)(kc + loff + (size_t)win_slot(w, n_shared, ic) * kv_dim + (size_t)hk * HS);
+#pragma unroll
+    for (uint32_t u = 0; u < F; u++) kk[u] = krow[u];
+    if (ic == count - 1) {  // the new position: its key is the one just rotated
+#pragma unroll
+        for (uint32_t u = 0; u < F; u++) kk[u] = ((const float4*)kn)[u];
+    }
+#pragma unroll
+    for (int j = 0; j < G; j++) {
+        float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+#pragma unroll
+        for (uint32_t u = 0; u < F; u++) {
+            const float4 qq = ((const float4*)(qs + j * HS))[u];
+            a0 = __builtin_fmaf(qq.x, kk[u].x, a0);
+            a1 = __builtin_fmaf(qq.y, kk[u].y, a1);
+            a2 = __builtin_fmaf(qq.z, kk[u].z, a2);
+            a3 = __builtin_fmaf(qq.w, kk[u].w, a3);
+        }
+        // dot.rs:360: (acc0 + acc1) + (acc2 + acc3), then * scale (cpu.rs:609)
+        const float sv = ((a0 + a1) + (a2 + a3)) * scale;
+        if (live) sc[(size_t)(hk * G + j) * ss + i] = sv;
+    }
+}
+
+// k_attn_softmax_v, workgroup = (KV head, DW of its HS output dims): the V
+// slice of the whole window goes HBM -> LDS by DMA first, and lands while the
+// maxima, exp and the serial softmax sums (one lane per head) run; then one
+// lane per (query head, dim) runs the weighted V sum in position order. The
+// probabilities are left in `att` (slice 0), as the reference leaves them.
+template <int G, int HS, int DW>
+__global__ __launch_bounds__(1024) void k_attn_softmax_v(const float* __restrict__ sc_in, uint32_t ss,
+                                                         const float* __restrict__ vc, size_t loff,
+                                                         const DevWindow* __restrict__ win, uint32_t kv_dim,
+                                                         uint32_t seq_len, uint32_t scs, float* __restrict__ att,
+                                                         float* __restrict__ out) {
+    constexpr uint32_t S = HS / DW, FV = DW / 4, T = 1024;
+    extern __shared__ __align__(16) float sm[];  // probabilities [G][scs] | V slice [count][DW]
+    __shared__ float red[T / 64][G];
+    __shared__ float s_sum[G];
+    __shared__ uint64_t etab[32];
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t hk = blockIdx.x / S, sidx = blockIdx.x % S, d0 = sidx * DW;
+    const DevWindow w = win[0];
+    const uint32_t n_shared = w.shared_end - w.shared_start;
+    const uint32_t count = n_shared + w.slot - w.att_start + 1;  // <= scs
+    float* ps = sm;
+    float* vt = sm + G * scs;
+    // the G score rows go to LDS by DMA (16-byte units; rows padded to a
+    // multiple of 4 floats in both places) and are waited for at once ...
+    const uint32_t c4 = (count + 3) / 4, srow = scs / 4;
+    for (uint32_t base = wave * 64; base < G * srow; base += T) {
+        const uint32_t f = base + lane, j = f / srow, u = f - j * srow;
+        if (f < G * srow && u < c4)
+            __builtin_amdgcn_global_load_lds(sc_in + (size_t)(hk * G + j) * ss + 4 * u, ps + 4 * base, 16, 0, 0);
+    }
+    if (tid < 32) etab[tid] = kExp2Tab[tid];
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    // ... the V slice likewise, but its wait is just before the V sums: it
+    // lands while the max, exp, serial sums and divisions run
+    const float* vbase = vc + loff + (size_t)hk * HS + d0;
+    const uint32_t units = count * FV;
+    for (uint32_t base = wave * 64; base < units; base += T) {
+        const uint32_t f = base + lane;
+        if (f < units) {
+            const uint32_t r = f / FV, col = f - r * FV;
+            __builtin_amdgcn_global_load_lds(vbase + (size_t)win_slot(w, n_shared, r) * kv_dim + 4 * col,
+                                             vt + 4 * base, 16, 0, 0);
+        }
+    }
+    // per-head max (order-free), then exp with it
+#pragma unroll
+    for (int j = 0; j < G; j++) {
+        float m = -INFINITY;
+        for (uint32_t i = tid; i < count; i += T) m = fmaxf(m, ps[j * scs + i]);
+        m = wave_max(m);
+        if (lane == 0) red[wave][j] = m;
+    }
+    __syncthreads();
+    float mx[G];
+#pragma unroll
+    for (int j = 0; j < G; j++) {
+        float m = red[0][j];
+#pragma unroll
+        for (uint32_t wv = 1; wv < T / 64; wv++) m = fmaxf(m, red[wv][j]);
+        mx[j] = m;
+    }
+    for (uint32_t t = tid; t < G * count; t += T) {
+        const uint32_t j = t / count, i = t - j * count;
+        float m = mx[0];
+#pragma unroll
+        for (int jj = 1; jj < G; jj++)
+            if ((uint32_t)jj == j) m = mx[jj];
+        ps[j * scs + i] = glibc_expf(ps[j * scs + i] - m, etab);
+    }
+    __syncthreads();
+    if (tid < G) {  // softmax sum, left to right (elementwise.rs:81-91)
+        const float* e = ps + tid * scs;
+        float s = 0.0f;
+        uint32_t i = 0;
+        for (; i + 64 <= count; i += 64) {
+            float4 r[16];
+#pragma unroll
+            for (int u = 0; u < 16; u++) r[u] = *(const float4*)(e + i + 4 * u);
+#pragma unroll
+            for (int u = 0; u < 16; u++) {
+                s += r[u].x;
+                s += r[u].y;
+                s += r[u].z;
+                s += r[u].w;
+            }
+        }
+        for (; i < count; i++) s += e[i];
+        s_sum[tid] = s;
+    }
+    __syncthreads();
+    for (uint32_t t = tid; t < G * count; t += T) {
+        const uint32_t j = t / count, i = t - j * count;
+        const float pv = div_rn(ps[j * scs + i], s_sum[j]);
+        ps[j * scs + i] = pv;
+        if (sidx == 0) att[(size_t)(hk * G + j) * seq_len + i] = pv;
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // this lane's V DMA has landed
+    __syncthreads();
+    if (tid < G * DW) {
+        const uint32_t j = tid / DW, e = tid % DW;
+        const float* pp = ps + j * scs;
+        const float* vv = vt + e;
+        float o = 0.0f;
+        uint32_t i = 0;
+        for (; i + 32 <= count; i += 32) {
+            float4 p4[8];
+            float v[32];
+#pragma unroll
+            for (int u = 0; u < 8; u++) p4[u] = *(const float4*)(pp + i + 4 * u);
+#pragma unroll
+            for (int u = 0; u < 32; u++) v[u] = vv[(i + u) * DW];
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                o += p4[u].x * v[4 * u];
+                o += p4[u].y * v[4 * u + 1];
+                o += p4[u].z * v[4 * u + 2];
+                o += p4[u].w * v[4 * u + 3];
+            }
+        }
+        for (; i < count; i++) o += pp[i] * vv[i * DW];
+        out[(size_t)(hk * G + j) * HS + d0 + e] = o;
+    }
+}
+
+static constexpr uint32_t kAttnSplitDW = 16;
+static constexpr size_t kAttnSplitLds = 150 * 1024;
+
+bool attention_split_ok(size_t max_count, size_t kv_mul, size_t hs) {
+    if (kv_mul != 1 && kv_mul != 2 && kv_mul != 3 && kv_mul != 4 && kv_mul != 8) return false;
+    if (hs != 32 && hs != 64 && hs != 128) return false;
+    const size_t scs = (max_count + 3) & ~(size_t)3;
+    return max_count >= 1 && (kv_mul * scs + max_count * kAttnSplitDW) * 4 <= kAttnSplitLds;
+}
+
+size_t attention_split_scratch(size_t n_heads, size_t seq_len) { return n_heads * ((seq_len + 3) & ~(size_t)3); }
+
+hipError_t launch_attention_split(hipStream_t st, const float* q, const float* k, const float* v, float* out,
+                                  float* att, float* kc, float* vc, size_t layer, const DevWindow* window,
+                                  const uint32_t* pos, const float2* table, int interleaved, size_t max_count,
+                                  size_t n_heads, size_t kv_mul, size_t hs, size_t kv_dim, size_t seq_len,
+                                  float scale, float* scratch) {
+    if (!attention_split_ok(max_count, kv_mul, hs) || n_heads % kv_mul != 0 || max_count > seq_len)
+        return hipErrorInvalidValue;
+    const size_t n_kv = n_heads / kv_mul, nchunks = (max_count + 63) / 64, loff = layer * seq_len * kv_dim;
+    const size_t scs = (max_count + 3) & ~(size_t)3;
+    float* sc = scratch;
+    const uint32_t ss = (uint32_t)((seq_len + 3) & ~(size_t)3);  // scratch row stride
+    const size_t lds = (kv_mul * scs + max_count * kAttnSplitDW) * 4;
+    const dim3 g1((unsigned)n_kv, (unsigned)nchunks), g2((unsigned)(n_kv * (hs / kAttnSplitDW)));
+#define KR_SPLIT(G, H)                                                                                              \
+    do {                                                                                                            \
+        hipLaunchKernelGGL((k_attn_scores<G, H>), g1, dim3(64), 0, st, q, k, v, kc, vc, loff, window, pos, table,   \
+                           interleaved, (uint32_t)kv_dim, scale, sc, ss);                                           \
+        hipLaunchKernelGGL((k_attn_softmax_v<G, H, kAttnSplitDW>), g2, dim3(1024), lds, st, sc, ss, vc, loff, window, \
+                           (uint32_t)kv_dim, (uint32_t)seq_len, (uint32_t)scs, att, out);                           \
+    } while (0)
+#define KR_SPLIT_H(G)              \
+    if (hs == 32)                  \
+        KR_SPLIT(G, 32);           \
+    else if (hs == 64)             \
+        KR_SPLIT(G, 64);           \
+    else                           \
+        KR_SPLIT(G, 128);
+    switch (kv_mul) {
+        case 8: KR_SPLIT_H(8) break;
+        case 4: KR_SPLIT_H(4) break;
+        case 3: KR_SPLIT_H(3) break;
+        case 2: KR_SPLIT_H(2) break;
+        default: KR_SPLIT_H(1) break;
+    }
+#undef KR_SPLIT_H
+#undef KR_SPLIT
+    return hipGetLastError();
 }
 
 // LDS budget of the latency-first attention and its shape for one call:

@@ -56,7 +56,8 @@ hipError_t launch_rope_kv(hipStream_t st, float* q, float* k, const float* v, si
 // y[m*ldy + n] for m < rows. Uses the GEMV path (rows <= 4) or the MFMA GEMM.
 // One decode row (M = 1) of 1-3 projections with the producer of their input
 // fused in front: pro_kind 1 = x (+= add) -> rms_norm(w, eps) -> Q8 (the
-// updated x row goes to x_out when non-null), 2 = silu(a) * b -> Q8.
+// updated x row goes to x_out when non-null), 2 = silu(a) * b -> Q8,
+// 3 = Q8 of the f32 row a.
 hipError_t launch_project_pro(hipStream_t st, int sem, const DevMatrix* const* w, float* const* y, int count,
                               int pro_kind, const float* a, const float* b, const float* norm_w, float* x_out,
                               float eps);
@@ -79,6 +80,16 @@ hipError_t launch_attention(hipStream_t st, const float* q, float* out, float* a
                             size_t max_count, size_t n_heads, size_t kv_mul, size_t head_size,
                             size_t kv_dim, size_t seq_len, float scale, int8_t* qo = nullptr,
                             float* so = nullptr, uint16_t* ho = nullptr);
+// Decode attention of one row in two launches (scores by 64-row chunks with
+// RoPE and the kv_write of k/v folded in, then softmax + V by 16-wide head
+// slices); `scratch` holds attention_split_scratch(n_heads, seq_len) floats.
+bool attention_split_ok(size_t max_count, size_t kv_mul, size_t hs);
+size_t attention_split_scratch(size_t n_heads, size_t seq_len);
+hipError_t launch_attention_split(hipStream_t st, const float* q, const float* k, const float* v, float* out,
+                                  float* att, float* kc, float* vc, size_t layer, const DevWindow* window,
+                                  const uint32_t* pos, const float2* table, int interleaved, size_t max_count,
+                                  size_t n_heads, size_t kv_mul, size_t hs, size_t kv_dim, size_t seq_len,
+                                  float scale, float* scratch);
 hipError_t launch_add(hipStream_t st, float* dst, const float* src, size_t n);
 hipError_t launch_mul(hipStream_t st, float* out, const float* a, const float* b, size_t n,
                       int sequential);

@@ -179,7 +179,8 @@ int decode_step_fused(krl_model* m, size_t token, size_t pos, bool dev) {
     kr_ctx* b = m->b;
     Geometry g = geometry(m->c);
     const uint32_t* s = m->step;
-    const bool pro = kri::pro_fusable(g.dim);
+    const bool pro = kri::pro_fusable(g.dim) && kri::pro_fusable(g.q_dim);
+    const bool split = kri::split_attention_ok(b, &g.as);
     kr_buf X[2] = {m->x, m->x2};
     int cur = 0;
     if (dev)
@@ -208,20 +209,27 @@ int decode_step_fused(krl_model* m, size_t token, size_t pos, bool dev) {
             TRY(norm_then(pending, n.att, l, qkv, ys, 3));
             if (n.has_q) KRC(m, kr_qk_norm(b, m->q, 1, g.q_dim, g.hs, n.q, g.eps));
             if (n.has_k) KRC(m, kr_qk_norm(b, m->k, 1, g.kv_dim, g.hs, n.k, g.eps));
-            KRC(m, kri::rope_kv(b, m->q, m->k, m->v, g.q_dim, g.kv_dim, 1, dev ? nullptr : positions,
-                                dev ? nullptr : positions, dev ? s + 2 : nullptr, l, &g.rs));
-            if (g.hs % 32 == 0) {
-                KRC(m, kri::attention_quant(b, m->q, m->attn, m->att, l, dev ? nullptr : &win, 1,
-                                            dev ? s + 1 : nullptr, &g.as));
-            } else {  // head outputs are not whole Q8 blocks: quantize the row after
-                if (dev)
-                    KRC(m, kri::attention_dev(b, m->q, m->attn, m->att, l, s + 1, &g.as));
-                else
-                    KRC(m, kr_attention(b, m->q, m->attn, m->att, l, &win, 1, &g.as));
-                KRC(m, kr_quantize_rows(b, m->attn, 1, g.q_dim));
+            if (split && pro) {
+                // rope + kv_write + attention in two launches; O quantizes its input
+                KRC(m, kri::rope_attention(b, m->q, m->k, m->v, m->attn, m->att, l, pos, dev ? s : nullptr, &g.as,
+                                           &g.rs));
+                KRC(m, kri::quant_project(b, l, KR_PROJ_O, m->attn, m->o, g.q_dim));
+            } else {
+                KRC(m, kri::rope_kv(b, m->q, m->k, m->v, g.q_dim, g.kv_dim, 1, dev ? nullptr : positions,
+                                    dev ? nullptr : positions, dev ? s + 2 : nullptr, l, &g.rs));
+                if (g.hs % 32 == 0) {
+                    KRC(m, kri::attention_quant(b, m->q, m->attn, m->att, l, dev ? nullptr : &win, 1,
+                                                dev ? s + 1 : nullptr, &g.as));
+                } else {  // head outputs are not whole Q8 blocks: quantize the row after
+                    if (dev)
+                        KRC(m, kri::attention_dev(b, m->q, m->attn, m->att, l, s + 1, &g.as));
+                    else
+                        KRC(m, kr_attention(b, m->q, m->attn, m->att, l, &win, 1, &g.as));
+                    KRC(m, kr_quantize_rows(b, m->attn, 1, g.q_dim));
+                }
+                int o[1] = {KR_PROJ_O};
+                KRC(m, kri::project_q(b, l, o, &m->o, 1, 1));
             }
-            int o[1] = {KR_PROJ_O};
-            KRC(m, kri::project_q(b, l, o, &m->o, 1, 1));
         } else {
             int ci[1] = {KR_PROJ_CONV_IN};
             TRY(norm_then(pending, n.att, l, ci, &m->bcx, 1));

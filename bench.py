@@ -43,26 +43,43 @@ CFG2 = dict(dim=960, hidden_dim=2560, n_layers=32, n_heads=15, n_kv_heads=5, voc
 CFG3 = dict(dim=2048, hidden_dim=8192, n_layers=24, n_heads=32, n_kv_heads=32, vocab_size=49152, seq_len=256,
             rms_eps=1e-5, rope_theta=130_000.0, rope_interleaved=False, head_dim=64)
 PREFILL_POS = 512
+# LFM2-700M shape (conv layers and 6 GQA attention layers)
+CFG4 = dict(dim=1536, hidden_dim=4608, n_layers=16, n_heads=24, n_kv_heads=8, vocab_size=65536, seq_len=8192,
+            rms_eps=1e-5, rope_theta=1_000_000.0, rope_interleaved=False, head_dim=64)
+CFG4_ATTENTION = (2, 5, 8, 10, 12, 14)
+# Qwen3-0.6B shape (head_dim 128, QK-norm)
+CFG5 = dict(dim=1024, hidden_dim=3072, n_layers=28, n_heads=16, n_kv_heads=8, vocab_size=151936, seq_len=2048,
+            rms_eps=1e-6, rope_theta=1_000_000.0, rope_interleaved=False, head_dim=128)
 
 
-def synthetic_model(K, cfg: dict, storage: str, seed: int):
-    """Device-generated N(0, 0.02) Q8 weights (tied classifier), unit norms."""
+def synthetic_model(K, cfg: dict, storage: str, seed: int, qk_norm: bool = False, lfm2_attention=None):
+    """Device-generated N(0, 0.02) Q8 weights (tied classifier), unit norms.
+    With `lfm2_attention` (the attention layer indices) an LFM2 hybrid: the
+    other layers are short convolutions (kernel 3, weights N(0, 0.02))."""
     hip = K.open("hip")
     c = K.Config(**cfg)
     layers, handles = [], []
     s = seed
+    rng = np.random.default_rng(seed)
+    ones = np.ones(c.dim, np.float32)
     for l in range(c.n_layers):
-        shapes = {"q": (c.q_dim, c.dim), "k": (c.kv_dim, c.dim), "v": (c.kv_dim, c.dim), "o": (c.dim, c.q_dim),
-                  "gate": (c.hidden_dim, c.dim), "up": (c.hidden_dim, c.dim), "down": (c.dim, c.hidden_dim)}
+        attention = lfm2_attention is None or l in lfm2_attention
+        if attention:
+            shapes = {"q": (c.q_dim, c.dim), "k": (c.kv_dim, c.dim), "v": (c.kv_dim, c.dim), "o": (c.dim, c.q_dim)}
+        else:
+            shapes = {"conv_in": (3 * c.dim, c.dim), "conv_out": (c.dim, c.dim)}
+        shapes.update({"gate": (c.hidden_dim, c.dim), "up": (c.hidden_dim, c.dim), "down": (c.dim, c.hidden_dim)})
         h = {}
         for name, (n, k) in shapes.items():
             s += 1
             h[name] = hip.synthetic_matrix(storage, n, k, s)
         handles.append(h)
-        layers.append(K.LayerWeights(np.ones(c.dim, np.float32), np.ones(c.dim, np.float32)))
+        qk = np.ones(c.head_dim, np.float32) if (qk_norm and attention) else None
+        conv = None if attention else (rng.standard_normal((c.dim, 3), dtype=np.float32) * np.float32(0.02))
+        layers.append(K.LayerWeights(ones, ones, rms_q=qk, rms_k=qk, conv_kernel=conv, is_attention=attention))
     emb = hip.synthetic_matrix(storage, c.vocab_size, c.dim, seed + 100_000)
     hip.bind_handles(emb, 0xFFFFFFFF, handles)
-    model = K.Model(c, hip, None, layers=layers, rms_final=np.ones(c.dim, np.float32))
+    model = K.Model(c, hip, None, lfm2=lfm2_attention is not None, layers=layers, rms_final=ones)
     return hip, model, c
 
 
@@ -332,6 +349,77 @@ def bench_prefill_model(K, n_tokens: int = 128, reps: int = 5):
     return dict(tokens=n_tokens, tok_s=n_tokens / best, best_ms=best * 1e3, first_call_ms=first * 1e3)
 
 
+def bench_cfg4(K, n_prompt: int = 128, n_decode: int = 256):
+    """`configs[3]`: the LFM2-700M-shaped hybrid with Q8_0x4 weights, a
+    128-token prefill of seeded random ids, then 256 greedy decode tokens
+    (context cap 8192), the decode replaying the captured step graph."""
+    log("cfg4: building the LFM2-700M-shaped Q8_0x4 hybrid on the device")
+    hip, model, c = synthetic_model(K, CFG4, "q8_0x4", seed=11, qk_norm=True, lfm2_attention=CFG4_ATTENTION)
+    toks = [int(t) for t in np.random.default_rng(12).integers(0, c.vocab_size, size=n_prompt)]
+    logits = model.prefill(toks, 0)
+    hip.synchronize()
+    t0 = time.perf_counter()
+    logits = model.prefill(toks, 0)
+    prefill_s = time.perf_counter() - t0
+    first = int(np.argmax(logits))
+    model.generate_greedy(first, n_prompt, 8)
+    hip.synchronize()
+    t0 = time.perf_counter()
+    model.generate_greedy(first, n_prompt, n_decode)
+    hip.synchronize()
+    decode_s = time.perf_counter() - t0
+    model.close()
+    hip.close()
+    return dict(prefill_tokens=n_prompt, prefill_tok_s=n_prompt / prefill_s, decode_tokens=n_decode,
+                decode_tok_s=n_decode / decode_s)
+
+
+def bench_cfg5(K, n_prompt: int = 2048, n_seq: int = 64, ctx: int = 1024, steps: int = 8):
+    """`configs[4]`: the Qwen3-0.6B-shaped Llama (head_dim 128, QK-norm) with
+    Q8_0 weights. (i) a 2048-token prefill of seeded random ids (best of 3
+    after a timed first call); (ii) batched decode of 64 sequences, each with
+    a 1024-position KV cache of its own (N(0, 1), 64 x 1024 slots in one
+    cache): every step is one row per sequence, so every projection and the
+    151936x1024 lm_head run as M = 64 int8 GEMMs; logits stay on the device."""
+    log("cfg5: building the Qwen3-0.6B-shaped Q8_0 model (prefill)")
+    hip, model, c = synthetic_model(K, CFG5, "q8_0", seed=21, qk_norm=True)
+    toks = [int(t) for t in np.random.default_rng(22).integers(0, c.vocab_size, size=n_prompt)]
+    t0 = time.perf_counter()
+    model.prefill(toks, 0)
+    first = time.perf_counter() - t0
+    best = None
+    for _ in range(3):
+        t0 = time.perf_counter()
+        model.prefill(toks, 0)
+        dt = time.perf_counter() - t0
+        best = dt if best is None else min(best, dt)
+    model.close()
+    hip.close()
+    log("cfg5: batched decode, 64 sequences x 1024-position caches")
+    cfg = dict(CFG5, seq_len=n_seq * ctx)
+    hip, model, c = synthetic_model(K, cfg, "q8_0", seed=23, qk_norm=True)
+    hip.kv_synthetic(n_seq * ctx, seed=24)
+    rng = np.random.default_rng(25)
+    tok = [int(t) for t in rng.integers(0, c.vocab_size, size=n_seq)]
+    pos = [ctx - 1] * n_seq
+    slots = [s * ctx + ctx - 1 for s in range(n_seq)]
+    starts = [s * ctx for s in range(n_seq)]
+    model.decode_batch(tok, pos, slots, starts, read=False)
+    hip.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        model.decode_batch(tok, pos, slots, starts, read=False)
+    hip.synchronize()
+    dt = time.perf_counter() - t0
+    kv_bytes = 2 * c.n_layers * n_seq * ctx * c.kv_dim * 4
+    model.close()
+    hip.close()
+    return dict(prefill_tokens=n_prompt, prefill_tok_s=n_prompt / best, prefill_best_ms=best * 1e3,
+                prefill_first_ms=first * 1e3, batch_sequences=n_seq, batch_ctx=ctx,
+                batch_step_ms=dt * 1e3 / steps, batch_tok_s=n_seq * steps / dt,
+                batch_kv_gbs=kv_bytes * steps / dt / 1e9)
+
+
 def bench_cpu_baseline(seconds_budget: float = 20.0):
     """The oracle's cpu backend (the reference's x86 Q8_0x4 path) on 1 core:
     cfg2 decode steps from a cache pre-filled to 512 positions."""
@@ -398,7 +486,7 @@ def main():
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--skip-cpu", action="store_true")
-    ap.add_argument("--only", choices=["decode", "gemv", "prefill"], default=None)
+    ap.add_argument("--only", choices=["decode", "gemv", "prefill", "cfg4", "cfg5"], default=None)
     ap.add_argument("--no-graph", action="store_true",
                     help="launch the decode step's and the GEMV passes' kernels directly instead of replaying "
                          "captured HIP graphs (same kernels; for profilers that cannot trace graph launches)")
@@ -421,6 +509,13 @@ def main():
         log(f"prefill: {res['prefill']['int8_tops']:.1f} TOPS in the GEMM kernels")
         res["prefill"]["model"] = bench_prefill_model(K)
         log(f"prefill model: {res['prefill']['model']['tok_s']:.0f} tok/s")
+    if args.only in (None, "cfg4"):
+        res["cfg4"] = bench_cfg4(K)
+        log(f"cfg4: prefill {res['cfg4']['prefill_tok_s']:.0f} tok/s, decode {res['cfg4']['decode_tok_s']:.1f} tok/s")
+    if args.only in (None, "cfg5"):
+        res["cfg5"] = bench_cfg5(K)
+        log(f"cfg5: prefill {res['cfg5']['prefill_tok_s']:.0f} tok/s, batched decode "
+            f"{res['cfg5']['batch_tok_s']:.0f} tok/s")
     cpu = None if args.skip_cpu or args.only else bench_cpu_baseline()
 
     d, g, p = res.get("decode"), res.get("gemv"), res.get("prefill")
@@ -458,6 +553,9 @@ def main():
         line["prefill"] = p
     if d:
         line["decode"] = d
+    for key in ("cfg4", "cfg5"):
+        if key in res:
+            line[key] = res[key]
     if cpu:
         line["cpu_baseline"] = cpu
     print(json.dumps(line), flush=True)

@@ -70,6 +70,18 @@ int krl_prefill_multi(krl_model* m, const size_t* tokens, const size_t* lens, si
 int krl_prefill_shared(krl_model* m, const size_t* prefix, size_t n_prefix, const size_t* tokens,
                        const size_t* lens, size_t n_seq, float* hiddens);
 
+/* One decode step for n_seq independent sequences that share the model and
+ * the cache, the batched shape of forward() (no counterpart in the
+ * reference, whose forward and logits take one row; the rows are laid out as
+ * prefill_multi lays out its sequences, llama.rs:552-580): row s feeds
+ * tokens[s] at RoPE position rope_pos[s] into cache slot slots[s] and
+ * attends over slots att_start[s] ..= slots[s]. Writes logits
+ * [n_seq][vocab_size] (unless `logits` is null: they then stay on the
+ * device); row s equals what forward() gives for that sequence alone. Llama
+ * models only. */
+int krl_decode_batch(krl_model* m, const size_t* tokens, const size_t* rope_pos, const size_t* slots,
+                     const size_t* att_start, size_t n_seq, float* logits);
+
 /* Greedy decoding of `n_steps` tokens after `token` at position `pos`, with
  * the argmax (generate.rs:70-77 tie rule) on the device. Each step is the
  * forward pass with its token and position read from device memory; with

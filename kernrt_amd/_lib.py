@@ -106,6 +106,7 @@ _SIGS = {
     "krl_prefill": (i32, [vp, vp, sz, sz, vp]),
     "krl_prefill_multi": (i32, [vp, vp, vp, sz, vp]),
     "krl_prefill_shared": (i32, [vp, vp, sz, vp, vp, sz, vp]),
+    "krl_decode_batch": (i32, [vp, vp, vp, vp, vp, sz, vp]),
     "krl_generate_greedy": (i32, [vp, sz, sz, sz, vp, i32]),
 }
 

@@ -1339,6 +1339,20 @@ int quant_project(kr_ctx* c, size_t layer, int proj, kr_buf x, kr_buf y, size_t 
     return KR_OK;
 }
 
+int logits_rows(kr_ctx* c, kr_buf y, size_t rows) {
+    CHECK(c, c->prepared, "prepare() runs before any compute");
+    Mat* mt = mat_of(c, c->classifier != KR_NO_MAT ? c->classifier : c->embedding);
+    CHECK(c, mt != nullptr, "no classifier bound");
+    const DevMatrix* m;
+    int sem;
+    int rc = classifier_matrix(c, mt, &m, &sem);
+    if (rc) return rc;
+    CHECK(c, c->q_rows >= rows && c->q_width == m->k, "the workspace does not hold the classifier input");
+    BUF(yb, y, rows * m->n);
+    HIPCHK(c, kr::launch_project(c->stream, sem, *m, act(c), rows, yb->p, m->n, nullptr));
+    return KR_OK;
+}
+
 int greedy_step(kr_ctx* c, kr_buf logits, size_t len, uint32_t* step) {
     BUF(l, logits, len);
     CHECK(c, len > 0, "argmax of an empty buffer");

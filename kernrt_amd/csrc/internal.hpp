@@ -55,6 +55,8 @@ int attention_quant(kr_ctx* c, kr_buf q, kr_buf out, kr_buf att, size_t layer, c
                     size_t n, const uint32_t* window_dev, const kr_attn_spec* spec);
 // the classifier over the quantized workspace row
 int logits_q(kr_ctx* c, kr_buf y);
+// the classifier over the first `rows` quantized workspace rows -> y [rows][vocab]
+int logits_rows(kr_ctx* c, kr_buf y, size_t rows);
 
 // One decode row with the producer of the projection input fused into the
 // projection launch (results identical to the separate steps above):

@@ -42,6 +42,8 @@ struct krl_model {
     std::vector<long> conv_kernels, conv_state;
     kr_buf rms_final = 0;
     kr_buf x, x2, xb, q, k, v, attn, o, bcx, h, co, cy, gate, up, mlp, hidden, att, logits;
+    kr_buf batch_logits = 0;  // [rows][vocab] for decode_batch
+    size_t batch_logits_rows = 0;
     std::vector<float> logits_host;
     bool has_prefill = false;
     PrefillBuffers pb;
@@ -557,6 +559,28 @@ int krl_prefill(krl_model* m, const size_t* tokens, size_t n, size_t start, floa
     KRC(m, kr_logits(m->b, m->xb, m->logits));
     KRC(m, kr_read(m->b, m->logits, m->logits_host.data(), m->c.vocab_size));
     memcpy(logits, m->logits_host.data(), m->c.vocab_size * sizeof(float));
+    return KR_OK;
+}
+
+int krl_decode_batch(krl_model* m, const size_t* tokens, const size_t* rope_pos, const size_t* slots,
+                     const size_t* att_start, size_t n_seq, float* logits) {
+    if (m->lfm2) return fail(m, "decode_batch is a Llama entry point");
+    if (n_seq == 0) return KR_OK;
+    std::vector<Row> rows;
+    for (size_t s = 0; s < n_seq; s++) {
+        if (slots[s] >= m->c.seq_len || att_start[s] > slots[s]) return fail(m, "decode_batch row out of range");
+        rows.push_back(Row{tokens[s], rope_pos[s], slots[s], att_start[s], 0, 0});
+    }
+    TRY(prefill_rows(m, rows));
+    // the final norm and the classifier over every row (cpu.rs:501-514 per row)
+    const size_t vocab = m->c.vocab_size, dim = m->c.dim;
+    if (m->batch_logits_rows < n_seq) {
+        TRY(alloc(m, n_seq * vocab, &m->batch_logits));
+        m->batch_logits_rows = n_seq;
+    }
+    KRC(m, kri::norm_quant(m->b, m->pb.x, kri::KR_NO_BUF, m->rms_final, m->pb.xb, n_seq, dim, m->c.rms_eps));
+    KRC(m, kri::logits_rows(m->b, m->batch_logits, n_seq));
+    if (logits) KRC(m, kr_read(m->b, m->batch_logits, logits, n_seq * vocab));
     return KR_OK;
 }
 

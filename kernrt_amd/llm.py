@@ -134,6 +134,18 @@ class Model:
         self._ck(self.L.krl_prefill_multi(self.h, _p(flat), _p(lens), len(seqs), _p(out)))
         return out
 
+    def decode_batch(self, tokens, rope_pos, slots, att_start, read: bool = True) -> Optional[np.ndarray]:
+        """One decode step for independent sequences sharing the cache: row s
+        feeds tokens[s] at RoPE position rope_pos[s] into slot slots[s] and
+        attends over slots att_start[s]..=slots[s]. Returns logits [n][vocab]
+        (with read=False they stay on the device and None is returned)."""
+        cols = [np.ascontiguousarray(a, np.uint64) for a in (tokens, rope_pos, slots, att_start)]
+        n = len(cols[0])
+        assert all(len(c) == n for c in cols)
+        out = np.zeros((n, self.config.vocab_size), np.float32) if read else None
+        self._ck(self.L.krl_decode_batch(self.h, *(_p(c) for c in cols), n, _p(out)))
+        return out
+
     def prefill_shared(self, prefix, suffixes) -> np.ndarray:
         p = np.ascontiguousarray(prefix, np.uint64)
         flat = np.ascontiguousarray([t for s in suffixes for t in s], np.uint64)

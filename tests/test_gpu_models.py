@@ -93,6 +93,30 @@ def test_shared_prefix_and_multi_sequence(storage):
                       "prefill_multi")
 
 
+@pytest.mark.parametrize("storage", ["q8_0", "q8_0x4"])
+@pytest.mark.parametrize("n_seq", [3, 9])
+def test_decode_batch_matches_per_sequence_forward(storage, n_seq):
+    # the batched decode step (krl_decode_batch): sequence s owns cache slots
+    # [s * room, (s + 1) * room) and is decoded token by token, every step a
+    # batch over the sequences still running; each row's logits must equal
+    # forward() of that sequence run alone. Batches of 3 or fewer rows take
+    # the GEMV path, 8 or more the int8 MFMA GEMM path.
+    c = O.backends_config()
+    ow = O.backends_weights(c, storage)
+    rng = np.random.default_rng(n_seq)
+    room = c.seq_len // n_seq
+    seqs = [[int(t) for t in rng.integers(0, c.vocab_size, size=int(n))]
+            for n in rng.integers(2, min(room, 7), size=n_seq)]
+    g = gpu_model(c, ow)
+    cpus = [O.Model(c, ow, "cpu") for _ in seqs]
+    for t in range(max(len(s) for s in seqs)):
+        live = [i for i, s in enumerate(seqs) if t < len(s)]
+        got = g.decode_batch([seqs[i][t] for i in live], [t] * len(live), [i * room + t for i in live],
+                             [i * room for i in live])
+        for r, i in enumerate(live):
+            assert_bits_equal(got[r], cpus[i].forward(seqs[i][t], t), f"decode_batch step {t} sequence {i}")
+
+
 def test_multi_tile_shapes():
     # tests/backends.rs:436-481: a 70-row prompt against 256-wide projections
     c = O.Config(dim=128, hidden_dim=256, n_layers=2, n_heads=4, n_kv_heads=2, vocab_size=128, seq_len=128,

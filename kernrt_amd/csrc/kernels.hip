@@ -889,6 +889,115 @@ __global__ __launch_bounds__(256, 2) void k_gemm_four(MatSet ms, QuantAct x, uin
     }
 }
 
+// Q8_0 GEMM for few rows (the 128-row prefill): the same four partial sums
+// as k_gemm_four, on 16x16x32 int8 MFMA. A 32x32 output tile is four 16x16
+// sub-tiles; 16 waves take (sub-tile, partial sum j) each, so a tile keeps 16
+// independent chains in flight (4 waves per SIMD) where 32x32 MFMAs leave one
+// chain per SIMD with every LDS and MFMA latency on its critical path. The
+// operand staging (A and B chunks of KC blocks through double-buffered,
+// padded LDS) and the global traffic are those of k_gemm_four.
+//
+// 16x16x32 operand map: lane l feeds row (col) l % 16 of the A (B) tile with
+// bytes 8 * (l / 16) .. +8 of the block, the same byte map for both; its
+// accumulator v is output (row 4 * (l / 16) + v, col l % 16).
+template <int SEM, bool DBG>
+__global__ __launch_bounds__(1024) void k_gemm_four16(MatSet ms, QuantAct x, uint32_t M, uint32_t K,
+                                                      uint32_t mtiles, int32_t* __restrict__ dbg) {
+    constexpr int KC = 8, ROW = KC * 32 + 16, NS = kGemmStages;
+    __shared__ __align__(16) int8_t sA[2][32 * ROW];
+    __shared__ __align__(16) int8_t sB[2][32 * ROW];
+    __shared__ __align__(16) float sX[2][KC * 32];  // [block][row]
+    __shared__ __align__(16) float sW[2][KC * 32];  // [block][col]
+    const uint32_t nb = K >> 5, nchunks = (nb + KC - 1) / KC;
+    const GemmPos p = gemm_pos(ms, mtiles, 32);
+    const int8_t* __restrict__ W = ms.q[p.mi];
+    const void* __restrict__ WS = ms.s[p.mi];
+    const uint32_t N = ms.n[p.mi];
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t chain = wave & 3, sub = wave >> 2, sm = sub >> 1, sn = sub & 1;
+    const uint32_t r = lane & 15, quad = lane >> 4;
+    constexpr bool WF16 = SEM == SEM_FOUR_PARTIALS_F16;
+
+    // loader map: threads 0..511 one 16-byte A piece (row t/16, column 16 (t%16)),
+    // 512..1023 the same for B; threads 0..255 one activation scale (row t/8,
+    // block t%8), 256..511 one weight scale. Rows past M or N read the last row.
+    const uint32_t lt = tid & 511, lr = lt >> 4, lc = (lt & 15) * 16;
+    const bool isB = tid >= 512;
+    const int8_t* g = isB ? W + (size_t)min(p.n0 + lr, N - 1) * K : x.q + (size_t)min(p.m0 + lr, M - 1) * K;
+    const uint32_t st_ = tid & 255, sr = st_ >> 3, sb = st_ & 7;
+    const bool isW = tid >= 256 && tid < 512, isS = tid < 512;
+    const float* gx = x.s + (size_t)min(p.m0 + sr, M - 1) * nb;
+    const size_t gw = (size_t)min(p.n0 + sr, N - 1) * nb;
+
+    struct Stage {
+        v4i v;
+        uint32_t sc;
+    };
+    auto gload = [&](Stage& st, uint32_t c) {
+        c = c < nchunks ? c : nchunks - 1;
+        const uint32_t col = min(c * KC * 32 + lc, K - 16);  // past the row end: a piece no block uses
+        st.v = *(const v4i*)(g + col);
+        const uint32_t blk = min(c * KC + sb, nb - 1);
+        st.sc = isS ? (isW ? scale_bits(WF16, WS, gw + blk) : f2u(gx[blk])) : 0u;
+    };
+    auto lstore = [&](const Stage& st, int buf) {
+        *(v4i*)((isB ? sB[buf] : sA[buf]) + lr * ROW + lc) = st.v;
+        if (isS) {
+            if (isW)
+                sW[buf][sb * 32 + sr] = scale_value(WF16, st.sc);
+            else
+                sX[buf][sb * 32 + sr] = u2f(st.sc);
+        }
+    };
+
+    float t[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    const v4i zero = {0, 0, 0, 0};
+    // wave (sub, chain j): blocks j and j + 4 of each chunk, chain t[j] in order
+    auto compute = [&](int buf, uint32_t c) {
+#pragma unroll
+        for (int i = 0; i < KC / 4; i++) {
+            const uint32_t blk = chain + 4 * i, b = c * KC + blk;
+            if (b >= nb) break;
+            const long a = *(const long*)(sA[buf] + (sm * 16 + r) * ROW + blk * 32 + 8 * quad);
+            const long bq = *(const long*)(sB[buf] + (sn * 16 + r) * ROW + blk * 32 + 8 * quad);
+            const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, bq, zero, 0, 0, 0);
+            const float w = sW[buf][blk * 32 + sn * 16 + r];
+            const float4 xs = *(const float4*)(sX[buf] + blk * 32 + sm * 16 + 4 * quad);
+            if (DBG && p.n0 + sn * 16 + r < N) {
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    const uint32_t m = p.m0 + sm * 16 + 4 * quad + v;
+                    if (m < M) dbg[((size_t)m * N + p.n0 + sn * 16 + r) * nb + b] = d[v];
+                }
+            }
+            // dot.rs: t[b & 3] += (sa * sb) * (isum as f32), with sa the weight scale
+            t[0] += (w * xs.x) * (float)d[0];
+            t[1] += (w * xs.y) * (float)d[1];
+            t[2] += (w * xs.z) * (float)d[2];
+            t[3] += (w * xs.w) * (float)d[3];
+        }
+    };
+
+    gemm_pipeline<NS, Stage>(nchunks, gload, lstore, compute);
+
+    float* part = (float*)&sA[0][0];  // [sub][chain][v][lane], after the last barrier
+#pragma unroll
+    for (int v = 0; v < 4; v++) part[((sub * 4 + chain) * 4 + v) * 64 + lane] = t[v];
+    __syncthreads();
+    float* Y = ms.y[p.mi];
+    const uint32_t ld = ms.ld[p.mi];
+    {
+        const uint32_t o = tid;  // (sub, v, lane): 4 * 4 * 64 = 1024 outputs
+        const uint32_t s2 = o >> 8, v = (o >> 6) & 3, l = o & 63;
+        const uint32_t m = p.m0 + (s2 >> 1) * 16 + 4 * (l >> 4) + v, n = p.n0 + (s2 & 1) * 16 + (l & 15);
+        if (m < M && n < N) {
+            auto at = [&](uint32_t j) { return part[((s2 * 4 + j) * 4 + v) * 64 + l]; };
+            Y[(size_t)m * ld + n] = ((at(0) + at(1)) + at(2)) + at(3);
+        }
+    }
+}
+
 template <bool DBG>
 __global__ __launch_bounds__(256, 2) void k_gemm_chain(MatSet ms, QuantAct x, uint32_t M, uint32_t K,
                                                        uint32_t mtiles, int32_t* __restrict__ dbg) {
@@ -1001,9 +1110,9 @@ static hipError_t gemm_launch(hipStream_t st, MatSet ms, size_t k, QuantAct x, s
             hipLaunchKernelGGL(k_gemm_chain<false>, grid, dim3(256), 0, st, ms, x, m, kk, mtiles, dbg);
     } else {
         if (dbg)
-            hipLaunchKernelGGL((k_gemm_four<SEM, true>), grid, dim3(256), 0, st, ms, x, m, kk, mtiles, dbg);
+            hipLaunchKernelGGL((k_gemm_four16<SEM, true>), grid, dim3(1024), 0, st, ms, x, m, kk, mtiles, dbg);
         else
-            hipLaunchKernelGGL((k_gemm_four<SEM, false>), grid, dim3(256), 0, st, ms, x, m, kk, mtiles, dbg);
+            hipLaunchKernelGGL((k_gemm_four16<SEM, false>), grid, dim3(1024), 0, st, ms, x, m, kk, mtiles, dbg);
     }
     return hipGetLastError();
 }

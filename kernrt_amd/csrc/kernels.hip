@@ -1958,6 +1958,7 @@ static AttnFastShape attn_fast_shape(size_t max_count, size_t G, size_t hs) {
     const size_t work = kAttnFastLds / 4 - fixed;
     size_t kcap = work / hs;
     if (kcap > kAttnFastThreads) kcap = kAttnFastThreads;
+    if (kcap > max_count) kcap = max_count;  // LDS sized to the longest window: more workgroups per CU
     // the widest slice whose V window fits in one chunk; else 32 wide, chunked
     size_t dw = 32, vcap = work / 32;
     if (hs >= 64 && work / 64 >= max_count && G * 64 <= kAttnFastThreads) dw = 64, vcap = work / 64;

@@ -261,6 +261,107 @@ __device__ __forceinline__ float lds_sum(const float* e, uint32_t n) {
     return t;
 }
 
+// Workgroup barrier that waits only for this wave's LDS operations
+// (lgkmcnt(0)), not for its outstanding global loads or stores: for phases
+// that communicate through LDS while other global traffic is in flight. The
+// asm statements keep the compiler from moving memory accesses across it.
+__device__ __forceinline__ void lds_barrier() {
+    __asm__ __volatile__("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // vmcnt(63) expcnt(7) lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    __asm__ __volatile__("" ::: "memory");
+}
+
+// Serial f32 sum s += e[i], i = 0..n-1 in order, over 16-byte aligned LDS:
+// 32 values per batch (8 x b128), the next batch's loads issued before the
+// current batch's adds, so the LDS round trip overlaps the dependent adds
+// and the chain runs at the add latency. Every batch load is unconditional
+// (the last one re-reads a valid batch), which keeps the compiler's wait
+// before each batch at lgkmcnt(8) instead of 0.
+__device__ __forceinline__ float chain_sum(const float* __restrict__ e, uint32_t n, float s = 0.0f) {
+    const uint32_t nb = n / 32;
+    float4 A[8], B[8];
+    auto ld = [&](float4(&r)[8], uint32_t b) {
+#pragma unroll
+        for (int u = 0; u < 8; u++) r[u] = *(const float4*)(e + 32 * b + 4 * u);
+    };
+    auto add = [&](const float4(&r)[8]) {
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            s += r[u].x;
+            s += r[u].y;
+            s += r[u].z;
+            s += r[u].w;
+        }
+    };
+    uint32_t b = 0;
+    if (nb > 0) ld(A, 0);
+    for (; b + 2 <= nb; b += 2) {
+        ld(B, b + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        add(A);
+        ld(A, b + 2 < nb ? b + 2 : b);
+        __builtin_amdgcn_sched_barrier(0);
+        add(B);
+    }
+    if (b < nb) add(A);
+    for (uint32_t i = 32 * nb; i < n; i++) s += e[i];
+    return s;
+}
+
+// Serial f32 dot o += p[i] * v[i] (a rounded product, then a rounded add),
+// i = 0..n-1 in order, both operands 16-byte aligned LDS rows. 16 steps per
+// batch. While the dependent adds of batch b run, each add is paired with
+// one product of batch b + 1 (pinned in that order, so the products fill the
+// add latency instead of preceding it), and the operands of batch b + 2 are
+// already being loaded into the other operand registers.
+__device__ __forceinline__ float chain_dot(const float* __restrict__ p, const float* __restrict__ v, uint32_t n) {
+    const uint32_t nb = n / 16;
+    float o = 0.0f;
+    float4 P0[4], V0[4], P1[4], V1[4];
+    float pa[16], pb[16];
+    auto ld = [&](float4(&pr)[4], float4(&vr)[4], uint32_t b) {
+        b = b < nb ? b : nb - 1;  // past the end: re-read a valid batch (its products are not used)
+#pragma unroll
+        for (int u = 0; u < 4; u++) pr[u] = *(const float4*)(p + 16 * b + 4 * u), vr[u] = *(const float4*)(v + 16 * b + 4 * u);
+    };
+    auto mul = [&](const float4(&pr)[4], const float4(&vr)[4], int k) {
+        const float4 a = pr[k / 4], c = vr[k / 4];
+        return (k & 3) == 0 ? a.x * c.x : (k & 3) == 1 ? a.y * c.y : (k & 3) == 2 ? a.z * c.z : a.w * c.w;
+    };
+    // o += cur[k] for k = 0..15, each followed by nxt[k] = product k of (pr, vr)
+    auto step = [&](const float(&cur)[16], float(&nxt)[16], const float4(&pr)[4], const float4(&vr)[4]) {
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            o += cur[k];
+            nxt[k] = mul(pr, vr, k);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    uint32_t b = 0;
+    if (nb > 0) {
+        ld(P0, V0, 0);
+#pragma unroll
+        for (int k = 0; k < 16; k++) pa[k] = mul(P0, V0, k);
+        ld(P0, V0, 1);
+        ld(P1, V1, 2);
+        for (; b + 2 <= nb; b += 2) {
+            __builtin_amdgcn_sched_barrier(0);
+            step(pa, pb, P0, V0);  // adds of batch b, products of batch b + 1
+            ld(P0, V0, b + 3);
+            __builtin_amdgcn_sched_barrier(0);
+            step(pb, pa, P1, V1);  // adds of batch b + 1, products of batch b + 2
+            ld(P1, V1, b + 4);
+        }
+        if (b < nb) {
+#pragma unroll
+            for (int k = 0; k < 16; k++) o += pa[k];
+        }
+    }
+    for (uint32_t i = 16 * nb; i < n; i++) o += p[i] * v[i];
+    return o;
+}
+
 // Lane k (0..3) of each quad, to every lane of the quad (DPP quad_perm).
 template <int K>
 __device__ __forceinline__ float quad_bcast(float v) {
@@ -523,21 +624,7 @@ __global__ __launch_bounds__(256) void k_gemv_pro(MatSet ms, GemvPro pro, uint32
         }
         __syncthreads();
         if (tid == 0) {  // rms_norm_row (cpu.rs:635-641)
-            float ss = 0.0f;
-            uint32_t i = 0;
-            for (; i + 64 <= K; i += 64) {
-                float4 r[16];
-#pragma unroll
-                for (int u = 0; u < 16; u++) r[u] = *(const float4*)(scratch + i + 4 * u);
-#pragma unroll
-                for (int u = 0; u < 16; u++) {
-                    ss += r[u].x;
-                    ss += r[u].y;
-                    ss += r[u].z;
-                    ss += r[u].w;
-                }
-            }
-            for (; i < K; i++) ss += scratch[i];
+            float ss = chain_sum(scratch, K);
             ss = div_rn(ss, (float)K);
             ss += pro.eps;
             s_scale = div_rn(1.0f, sqrt_rn(ss));
@@ -1613,26 +1700,7 @@ __global__ __launch_bounds__(512) void k_attention_fast(
     };
     if (wave > 0) v_dma(0, count < vcap ? count : vcap, 1);
     // softmax sums, left to right: lane j of wave 0 for head j
-    if (tid < G) {
-        const float* e = sc + tid * scs;
-        float s = 0.0f;
-        uint32_t i = 0;
-        for (; i + 64 <= count; i += 64) {
-            float4 r[16];
-#pragma unroll
-            for (int u = 0; u < 16; u++) r[u] = *(const float4*)(e + i + 4 * u);
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int u = 0; u < 16; u++) {
-                s += r[u].x;
-                s += r[u].y;
-                s += r[u].z;
-                s += r[u].w;
-            }
-        }
-        for (; i < count; i++) s += e[i];
-        s_sum[tid] = s;
-    }
+    if (tid < G) s_sum[tid] = chain_sum(sc + tid * scs, count);
     __syncthreads();
     for (uint32_t t = tid; t < G * count; t += T) {
         const uint32_t j = t / count, i = t - j * count;
@@ -1696,7 +1764,8 @@ __global__ __launch_bounds__(512) void k_attention_fast(
 // query heads and of the new key (cpu.rs:274-302, the host-built cos/sin
 // table), the kv_write of the new key and value (cpu.rs:238-246, by the
 // chunk-0 workgroup), then one lane per cache row runs the four-chain dot for
-// every query head; the scores go to a scratch row per head.
+// every query head; the scores go to a scratch row per head, and each
+// chunk's maximum per head to a second scratch array.
 // The new position's key is taken from LDS, not from the cache being written.
 template <int G, int HS>
 __global__ __launch_bounds__(64) void k_attn_scores(const float* __restrict__ q, const float* __restrict__ kin,
@@ -1704,7 +1773,8 @@ __global__ __launch_bounds__(64) void k_attn_scores(const float* __restrict__ q,
                                                     float* __restrict__ vc, size_t loff,
                                                     const DevWindow* __restrict__ win, const uint32_t* __restrict__ pos,
                                                     const float2* __restrict__ tab, int interleaved, uint32_t kv_dim,
-                                                    float scale, float* __restrict__ sc, uint32_t ss) {
+                                                    float scale, float* __restrict__ sc, uint32_t ss,
+                                                    float* __restrict__ mxp, uint32_t ms) {
     constexpr uint32_t F = HS / 4, HALF = HS / 2;
     __shared__ __align__(16) float qs[G * HS];
     __shared__ __align__(16) float kn[HS];
@@ -1760,23 +1830,38 @@ __global__ __launch_bounds__(64) void k_attn_scores(const float* __restrict__ q,
         // dot.rs:360: (acc0 + acc1) + (acc2 + acc3), then * scale (cpu.rs:609)
         const float sv = ((a0 + a1) + (a2 + a3)) * scale;
         if (live) sc[(size_t)(hk * G + j) * ss + i] = sv;
+        // the chunk's maximum (order-free), so the softmax launch need not scan the scores for it
+        const float m = wave_max(live ? sv : -INFINITY);
+        if (lane == 0) mxp[(size_t)(hk * G + j) * ms + chunk] = m;
     }
 }
 
-// k_attn_softmax_v, workgroup = (KV head, DW of its HS output dims): the V
-// slice of the whole window goes HBM -> LDS by DMA first, and lands while the
-// maxima, exp and the serial softmax sums (one lane per head) run; then one
-// lane per (query head, dim) runs the weighted V sum in position order. The
+// k_attn_softmax_v, workgroup = (KV head, DW of its HS output dims), 16
+// waves. Every wave reduces the per-chunk maxima of the G heads (written by
+// k_attn_scores) while the scores arrive by LDS DMA; then waves 8-15 issue
+// the loads of the V slice into registers (they land while the rest runs);
+// all waves run the exp; one lane per head runs the serial softmax sum while
+// waves 8-15 store the V slice transposed ([dim][position]); all waves
+// divide; then one lane per (query head, dim) runs the weighted V sum in
+// position order, reading both operands 4 positions per LDS load. The
 // probabilities are left in `att` (slice 0), as the reference leaves them.
+// LDS: probabilities [G][scs] | V slice [DW][vst], vst = round64(scs) + 4
+// (the 16 rows of a transposed read start 16 bytes apart, on distinct banks).
+static constexpr uint32_t kAttnVRegs = 8;  // V float4 per thread held in registers (1024 positions)
+__host__ __device__ inline size_t attn_split_vst(size_t scs) { return ((scs + 63) & ~(size_t)63) + 4; }
+__host__ __device__ inline size_t attn_split_lds(size_t scs, size_t G, size_t DW) {
+    return (G * scs + DW * attn_split_vst(scs)) * sizeof(float);
+}
+__host__ __device__ inline size_t attn_split_ms(size_t seq_len) { return ((seq_len + 63) / 64 + 3) & ~(size_t)3; }
 template <int G, int HS, int DW>
 __global__ __launch_bounds__(1024) void k_attn_softmax_v(const float* __restrict__ sc_in, uint32_t ss,
+                                                         const float* __restrict__ mxp, uint32_t ms,
                                                          const float* __restrict__ vc, size_t loff,
                                                          const DevWindow* __restrict__ win, uint32_t kv_dim,
                                                          uint32_t seq_len, uint32_t scs, float* __restrict__ att,
                                                          float* __restrict__ out) {
-    constexpr uint32_t S = HS / DW, FV = DW / 4, T = 1024;
-    extern __shared__ __align__(16) float sm[];  // probabilities [G][scs] | V slice [count][DW]
-    __shared__ float red[T / 64][G];
+    constexpr uint32_t S = HS / DW, FV = DW / 4, T = 1024, TV = 512;
+    extern __shared__ __align__(16) float sm[];
     __shared__ float s_sum[G];
     __shared__ uint64_t etab[32];
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1784,109 +1869,81 @@ __global__ __launch_bounds__(1024) void k_attn_softmax_v(const float* __restrict
     const DevWindow w = win[0];
     const uint32_t n_shared = w.shared_end - w.shared_start;
     const uint32_t count = n_shared + w.slot - w.att_start + 1;  // <= scs
+    const uint32_t vst = (uint32_t)attn_split_vst(scs), nch = (count + 63) / 64;
     float* ps = sm;
     float* vt = sm + G * scs;
-    // the G score rows go to LDS by DMA (16-byte units; rows padded to a
-    // multiple of 4 floats in both places) and are waited for at once ...
+    // 1. the chunk maxima of the G heads (every wave; nch <= 64), the exp
+    // table, ...
+    float pm[G];
+#pragma unroll
+    for (int j = 0; j < G; j++) pm[j] = lane < nch ? mxp[(size_t)(hk * G + j) * ms + lane] : -INFINITY;
+    const uint64_t et = kExp2Tab[tid & 31];
+    __asm__ __volatile__("" ::: "memory");
+    // ... and the G score rows by LDS DMA (16-byte units; rows padded to a multiple of 4 floats in both places)
     const uint32_t c4 = (count + 3) / 4, srow = scs / 4;
     for (uint32_t base = wave * 64; base < G * srow; base += T) {
         const uint32_t f = base + lane, j = f / srow, u = f - j * srow;
         if (f < G * srow && u < c4)
             __builtin_amdgcn_global_load_lds(sc_in + (size_t)(hk * G + j) * ss + 4 * u, ps + 4 * base, 16, 0, 0);
     }
-    if (tid < 32) etab[tid] = kExp2Tab[tid];
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    // ... the V slice likewise, but its wait is just before the V sums: it
-    // lands while the max, exp, serial sums and divisions run
-    const float* vbase = vc + loff + (size_t)hk * HS + d0;
-    const uint32_t units = count * FV;
-    for (uint32_t base = wave * 64; base < units; base += T) {
-        const uint32_t f = base + lane;
-        if (f < units) {
-            const uint32_t r = f / FV, col = f - r * FV;
-            __builtin_amdgcn_global_load_lds(vbase + (size_t)win_slot(w, n_shared, r) * kv_dim + 4 * col,
-                                             vt + 4 * base, 16, 0, 0);
-        }
-    }
-    // per-head max (order-free), then exp with it
-#pragma unroll
-    for (int j = 0; j < G; j++) {
-        float m = -INFINITY;
-        for (uint32_t i = tid; i < count; i += T) m = fmaxf(m, ps[j * scs + i]);
-        m = wave_max(m);
-        if (lane == 0) red[wave][j] = m;
-    }
-    __syncthreads();
+    __builtin_amdgcn_s_waitcnt(0x70);  // vmcnt(0) lgkmcnt(0): maxima, scores, exp table
+    if (tid < 32) etab[tid] = et;
     float mx[G];
 #pragma unroll
-    for (int j = 0; j < G; j++) {
-        float m = red[0][j];
+    for (int j = 0; j < G; j++) mx[j] = wave_max(pm[j]);
+    lds_barrier();  // the scores and the exp table are in LDS
+    // waves 8-15: the V slice into registers (unit f = position f / FV,
+    // float4 f % FV); it lands while the exp and the softmax sum run
+    const float* vbase = vc + loff + (size_t)hk * HS + d0;
+    const uint32_t units = count * FV, tv = tid - TV;
+    float4 vr[kAttnVRegs];
+    if (wave >= 8) {
 #pragma unroll
-        for (uint32_t wv = 1; wv < T / 64; wv++) m = fmaxf(m, red[wv][j]);
-        mx[j] = m;
-    }
-    for (uint32_t t = tid; t < G * count; t += T) {
-        const uint32_t j = t / count, i = t - j * count;
-        float m = mx[0];
-#pragma unroll
-        for (int jj = 1; jj < G; jj++)
-            if ((uint32_t)jj == j) m = mx[jj];
-        ps[j * scs + i] = glibc_expf(ps[j * scs + i] - m, etab);
-    }
-    __syncthreads();
-    if (tid < G) {  // softmax sum, left to right (elementwise.rs:81-91)
-        const float* e = ps + tid * scs;
-        float s = 0.0f;
-        uint32_t i = 0;
-        for (; i + 64 <= count; i += 64) {
-            float4 r[16];
-#pragma unroll
-            for (int u = 0; u < 16; u++) r[u] = *(const float4*)(e + i + 4 * u);
-#pragma unroll
-            for (int u = 0; u < 16; u++) {
-                s += r[u].x;
-                s += r[u].y;
-                s += r[u].z;
-                s += r[u].w;
+        for (int u = 0; u < (int)kAttnVRegs; u++) {
+            const uint32_t f = tv + TV * u;
+            if (f < units) {
+                const uint32_t r = f / FV, col = f - r * FV;
+                vr[u] = *(const float4*)(vbase + (size_t)win_slot(w, n_shared, r) * kv_dim + 4 * col);
             }
         }
-        for (; i < count; i++) s += e[i];
-        s_sum[tid] = s;
+    }
+    // 2. exp with the head's max
+#pragma unroll
+    for (int j = 0; j < G; j++)
+        for (uint32_t i = tid; i < count; i += T) ps[j * scs + i] = glibc_expf(ps[j * scs + i] - mx[j], etab);
+    lds_barrier();
+    // 3. softmax sum, left to right (elementwise.rs:81-91), one lane per head,
+    // while waves 8-15 store the V slice transposed
+    if (tid < G) s_sum[tid] = chain_sum(ps + tid * scs, count);
+    if (wave >= 8) {
+        auto put = [&](uint32_t f, float4 v) {
+            const uint32_t r = f / FV, c = 4 * (f - r * FV);
+            vt[c * vst + r] = v.x, vt[(c + 1) * vst + r] = v.y, vt[(c + 2) * vst + r] = v.z, vt[(c + 3) * vst + r] = v.w;
+        };
+#pragma unroll
+        for (int u = 0; u < (int)kAttnVRegs; u++)
+            if (tv + TV * u < units) put(tv + TV * u, vr[u]);
+        for (uint32_t f = tv + TV * kAttnVRegs; f < units; f += TV) {  // windows past the register capacity
+            const uint32_t r = f / FV, col = f - r * FV;
+            put(f, *(const float4*)(vbase + (size_t)win_slot(w, n_shared, r) * kv_dim + 4 * col));
+        }
     }
     __syncthreads();
-    for (uint32_t t = tid; t < G * count; t += T) {
-        const uint32_t j = t / count, i = t - j * count;
-        const float pv = div_rn(ps[j * scs + i], s_sum[j]);
-        ps[j * scs + i] = pv;
-        if (sidx == 0) att[(size_t)(hk * G + j) * seq_len + i] = pv;
+    // 4. probabilities
+#pragma unroll
+    for (int j = 0; j < G; j++) {
+        const float sj = s_sum[j];
+        for (uint32_t i = tid; i < count; i += T) {
+            const float pv = div_rn(ps[j * scs + i], sj);
+            ps[j * scs + i] = pv;
+            if (sidx == 0) att[(size_t)(hk * G + j) * seq_len + i] = pv;
+        }
     }
-    __builtin_amdgcn_s_waitcnt(0);  // this lane's V DMA has landed
-    __syncthreads();
+    lds_barrier();  // the `att` stores need not complete first
+    // 5. out[h][d0 + e] = sum_i p_i * v_i[e], lane (j, e), i in order
     if (tid < G * DW) {
         const uint32_t j = tid / DW, e = tid % DW;
-        const float* pp = ps + j * scs;
-        const float* vv = vt + e;
-        float o = 0.0f;
-        uint32_t i = 0;
-        for (; i + 32 <= count; i += 32) {
-            float4 p4[8];
-            float v[32];
-#pragma unroll
-            for (int u = 0; u < 8; u++) p4[u] = *(const float4*)(pp + i + 4 * u);
-#pragma unroll
-            for (int u = 0; u < 32; u++) v[u] = vv[(i + u) * DW];
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int u = 0; u < 8; u++) {
-                o += p4[u].x * v[4 * u];
-                o += p4[u].y * v[4 * u + 1];
-                o += p4[u].z * v[4 * u + 2];
-                o += p4[u].w * v[4 * u + 3];
-            }
-        }
-        for (; i < count; i++) o += pp[i] * vv[i * DW];
-        out[(size_t)(hk * G + j) * HS + d0 + e] = o;
+        out[(size_t)(hk * G + j) * HS + d0 + e] = chain_dot(ps + j * scs, vt + e * vst, count);
     }
 }
 
@@ -1897,10 +1954,14 @@ bool attention_split_ok(size_t max_count, size_t kv_mul, size_t hs) {
     if (kv_mul != 1 && kv_mul != 2 && kv_mul != 3 && kv_mul != 4 && kv_mul != 8) return false;
     if (hs != 32 && hs != 64 && hs != 128) return false;
     const size_t scs = (max_count + 3) & ~(size_t)3;
-    return max_count >= 1 && (kv_mul * scs + max_count * kAttnSplitDW) * 4 <= kAttnSplitLds;
+    // max_count <= 4096: one chunk maximum per lane of a wave in k_attn_softmax_v
+    return max_count >= 1 && max_count <= 64 * 64 && attn_split_lds(scs, kv_mul, kAttnSplitDW) <= kAttnSplitLds;
 }
 
-size_t attention_split_scratch(size_t n_heads, size_t seq_len) { return n_heads * ((seq_len + 3) & ~(size_t)3); }
+// scores [n_heads][round4(seq_len)] | chunk maxima [n_heads][attn_split_ms(seq_len)]
+size_t attention_split_scratch(size_t n_heads, size_t seq_len) {
+    return n_heads * (((seq_len + 3) & ~(size_t)3) + attn_split_ms(seq_len));
+}
 
 hipError_t launch_attention_split(hipStream_t st, const float* q, const float* k, const float* v, float* out,
                                   float* att, float* kc, float* vc, size_t layer, const DevWindow* window,
@@ -1913,13 +1974,16 @@ hipError_t launch_attention_split(hipStream_t st, const float* q, const float* k
     const size_t scs = (max_count + 3) & ~(size_t)3;
     float* sc = scratch;
     const uint32_t ss = (uint32_t)((seq_len + 3) & ~(size_t)3);  // scratch row stride
-    const size_t lds = (kv_mul * scs + max_count * kAttnSplitDW) * 4;
+    const uint32_t ms = (uint32_t)attn_split_ms(seq_len);
+    float* mxp = scratch + n_heads * ss;
+    const size_t lds = attn_split_lds(scs, kv_mul, kAttnSplitDW);
     const dim3 g1((unsigned)n_kv, (unsigned)nchunks), g2((unsigned)(n_kv * (hs / kAttnSplitDW)));
 #define KR_SPLIT(G, H)                                                                                              \
     do {                                                                                                            \
         hipLaunchKernelGGL((k_attn_scores<G, H>), g1, dim3(64), 0, st, q, k, v, kc, vc, loff, window, pos, table,   \
-                           interleaved, (uint32_t)kv_dim, scale, sc, ss);                                           \
-        hipLaunchKernelGGL((k_attn_softmax_v<G, H, kAttnSplitDW>), g2, dim3(1024), lds, st, sc, ss, vc, loff, window, \
+                           interleaved, (uint32_t)kv_dim, scale, sc, ss, mxp, ms);                                  \
+        hipLaunchKernelGGL((k_attn_softmax_v<G, H, kAttnSplitDW>), g2, dim3(1024), lds, st, sc, ss, mxp, ms, vc, loff, \
+                           window,                                                                                  \
                            (uint32_t)kv_dim, (uint32_t)seq_len, (uint32_t)scs, att, out);                           \
     } while (0)
 #define KR_SPLIT_H(G)              \
@@ -2088,21 +2152,7 @@ __global__ __launch_bounds__(256) void k_add_rms_quant(float* __restrict__ x, co
     if (tid == 0) {
         // rms_norm_row (cpu.rs:635-641): ss = sum of squares left to right,
         // ss /= dim, ss += eps, scale = 1 / sqrt(ss)
-        float ss = 0.0f;
-        uint32_t i = 0;
-        for (; i + 64 <= dim; i += 64) {
-            float4 r[16];
-#pragma unroll
-            for (int u = 0; u < 16; u++) r[u] = *(const float4*)(sq + i + 4 * u);
-#pragma unroll
-            for (int u = 0; u < 16; u++) {
-                ss += r[u].x;
-                ss += r[u].y;
-                ss += r[u].z;
-                ss += r[u].w;
-            }
-        }
-        for (; i < dim; i++) ss += sq[i];
+        float ss = chain_sum(sq, dim);
         ss = div_rn(ss, (float)dim);
         ss += eps;
         s_scale = div_rn(1.0f, sqrt_rn(ss));

@@ -172,6 +172,23 @@ def test_greedy_decode_matches_the_oracle(use_graph):
     assert list(got) == _oracle_greedy(cpu, 7, len(PROMPT), 40)
 
 
+@pytest.mark.parametrize("n_heads,n_kv,hs,ctx", [(2, 1, 64, 1100), (8, 8, 32, 300), (8, 2, 128, 300),
+                                                 (8, 1, 64, 200), (16, 4, 64, 150)])
+def test_split_decode_attention_windows(n_heads, n_kv, hs, ctx):
+    # The fused decode step's two-launch attention (k_attn_scores +
+    # k_attn_softmax_v) for head groups 2, 1, 4, 8 and 4 and head sizes 32-128,
+    # after a long prefill; the first case's window (1101+ positions) runs
+    # past the 1024 positions whose V the softmax launch keeps in registers.
+    c = O.Config(dim=n_heads * hs, hidden_dim=128, n_layers=1, n_heads=n_heads, n_kv_heads=n_kv, vocab_size=64,
+                 seq_len=ctx + 4, rms_eps=1e-5, rope_theta=10_000.0, rope_interleaved=False, head_dim=hs)
+    ow = gaussian_weights(c, "q8_0", seed=ctx + hs)
+    prompt = [(i * 7 + 3) % c.vocab_size for i in range(ctx)]
+    gpu, cpu = gpu_model(c, ow), O.Model(c, ow, "cpu")
+    assert_bits_equal(gpu.prefill(prompt, 0), cpu.prefill(prompt, 0), "prefill")
+    for t in range(3):
+        assert_bits_equal(gpu.forward(5 + t, ctx + t), cpu.forward(5 + t, ctx + t), f"decode at {ctx + t}")
+
+
 def test_greedy_256_tokens_at_360m_width():
     # SmolLM2-360M widths (dim 960, 15/5 heads, hd 64, hidden 2560, theta 1e5)
     # with 2 layers and an 8192-token vocabulary so the oracle finishes fast:

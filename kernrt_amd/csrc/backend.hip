@@ -735,7 +735,8 @@ int kr_attention(kr_ctx* c, kr_buf q, kr_buf out, kr_buf att, size_t layer, cons
     if (rc) return rc;
     float scale = 1.0f / sqrtf((float)sp->head_size);  // cpu.rs:591
     HIPCHK(c, kr::launch_attention(c->stream, qb->p, ob->p, ab->p, c->kc, c->vc, layer, (const kr::DevWindow*)wd, n,
-                                   max_count, sp->n_heads, sp->kv_mul, sp->head_size, sp->kv_dim, sp->seq_len, scale));
+                                   max_count, sp->n_heads, sp->kv_mul, sp->head_size, sp->kv_dim, sp->seq_len, scale,
+                                   nullptr, nullptr, nullptr, (const kr::DevWindow*)w.data()));
     return KR_OK;
 }
 
@@ -1155,12 +1156,13 @@ int attention_quant(kr_ctx* c, kr_buf q, kr_buf out, kr_buf att, size_t layer, c
     if (n == 0) return KR_OK;
     const uint32_t* wd;
     size_t max_count;
+    std::vector<uint32_t> w;  // host copy of the windows, read by launch_attention
     if (window_dev) {
         CHECK(c, n == 1, "a device window is for one row");
         wd = window_dev;
         max_count = c->seq_len;
     } else {
-        std::vector<uint32_t> w(4 * n);
+        w.resize(4 * n);
         max_count = 0;
         for (size_t i = 0; i < n; i++) {
             const kr_window& x = windows[i];
@@ -1183,7 +1185,7 @@ int attention_quant(kr_ctx* c, kr_buf q, kr_buf out, kr_buf att, size_t layer, c
     float scale = 1.0f / sqrtf((float)sp->head_size);
     HIPCHK(c, kr::launch_attention(c->stream, qb->p, ob->p, ab->p, c->kc, c->vc, layer, (const kr::DevWindow*)wd, n,
                                    max_count, sp->n_heads, sp->kv_mul, sp->head_size, sp->kv_dim, sp->seq_len, scale,
-                                   c->wq, c->ws, c->wh));
+                                   c->wq, c->ws, c->wh, w.empty() ? nullptr : (const kr::DevWindow*)w.data()));
     c->q_rows = n;
     c->q_width = width;
     return KR_OK;

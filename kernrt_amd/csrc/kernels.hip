@@ -2005,6 +2005,198 @@ hipError_t launch_attention_split(hipStream_t st, const float* q, const float* k
     return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// Attention for many rows whose windows map positions to the same cache slots
+// (prefill: every row of a sequence attends to a prefix of the same slots).
+// Same arithmetic as k_attention (cpu.rs:585-632): per (row, head) the 4-chain
+// scores, the softmax with its serial sum, the probabilities (left in `att`),
+// and per output dim the serial sum over positions of p * v.
+//
+// Workgroup = (G query heads of one KV head, block of R rows), 4 waves; a (row, head) pair is
+// "rg" = r * G + j. Each K tile (64 positions) goes to LDS once and serves
+// every pair of the block: lane = position, and each wave computes the
+// scores of its RPW pairs, reading q by broadcast. The scores stay in LDS;
+// each wave runs the max, exp, serial sum (one lane per pair) and division
+// of its own pairs. Then each V tile goes to LDS once and lane (pair, 4 dims)
+// runs four independent position-order chains. Row r of the block attends to
+// its first count_r positions (its window); the block's windows must agree
+// on att_start and the shared range (checked on the host), so window index i
+// is the same cache slot for every row.
+// LDS: q [4 RPW][HS] | scores [RG][scs] | tile [64][HS + 4].
+template <int HS>
+struct AttnRowsShape {
+    static constexpr uint32_t LPR = HS / 4;    // lanes per pair in the V phase (4 dims each)
+    static constexpr uint32_t RPW = 64 / LPR;  // pairs per wave
+    static constexpr uint32_t T = 64, KS = HS + 4;
+};
+template <int G, int HS>
+__global__ __launch_bounds__(256) void k_attn_rows(const float* __restrict__ q, float* __restrict__ out,
+                                                   float* __restrict__ att, const float* __restrict__ kc,
+                                                   const float* __restrict__ vc, size_t loff,
+                                                   const DevWindow* __restrict__ windows, uint32_t n_rows,
+                                                   uint32_t n_heads, uint32_t kv_mul, uint32_t kv_dim,
+                                                   uint32_t seq_len, float scale, uint32_t scs,
+                                                   int8_t* __restrict__ qo, float* __restrict__ so,
+                                                   uint16_t* __restrict__ ho) {
+    using Sh = AttnRowsShape<HS>;
+    constexpr uint32_t LPR = Sh::LPR, RPW = Sh::RPW, T = Sh::T, KS = Sh::KS, F = HS / 4;
+    constexpr uint32_t R = 4 * RPW / G, RG = R * G;
+    extern __shared__ __align__(16) float sm[];
+    float* qs = sm;                  // [4 RPW][HS]
+    float* sc = qs + 4 * RPW * HS;   // [RG][scs]
+    float* kt = sc + RG * scs;       // [T][KS]
+    __shared__ uint32_t s_cnt[4 * RPW];
+    __shared__ float s_sum[4 * RPW];
+    __shared__ uint64_t etab[32];
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t r0 = blockIdx.y * R;
+    const uint32_t nr = min(R, n_rows - r0);
+    // query heads h0 .. h0 + G - 1 of KV head h0 / kv_mul (G divides kv_mul)
+    const uint32_t width = n_heads * HS, h0 = blockIdx.x * G, kvo = (h0 / kv_mul) * HS;
+    const DevWindow w0 = windows[r0];
+    const uint32_t n_shared = w0.shared_end - w0.shared_start;
+
+    // the q rows of the block's pairs (rows past the block's end: zeros), the
+    // window lengths, the exp table
+    for (uint32_t t = tid; t < 4 * RPW * F; t += 256) {
+        const uint32_t rg = t / F, u = t - rg * F, r = rg / G, j = rg - r * G;
+        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (rg < RG && r < nr) v = *(const float4*)(q + (size_t)(r0 + r) * width + (size_t)(h0 + j) * HS + 4 * u);
+        *(float4*)(qs + rg * HS + 4 * u) = v;
+    }
+    if (tid < 4 * RPW) {
+        const uint32_t r = tid / G;
+        s_cnt[tid] = tid < RG && r < nr ? n_shared + windows[r0 + r].slot - w0.att_start + 1 : 0;
+    }
+    if (tid < 32) etab[tid] = kExp2Tab[tid];
+    __syncthreads();
+    uint32_t cmax = 0;
+    for (uint32_t rg = 0; rg < RG; rg++) cmax = max(cmax, s_cnt[rg]);
+    const float* kbase = kc + loff + kvo;
+    const float* vbase = vc + loff + kvo;
+    auto load_tile = [&](const float* base, uint32_t i0, uint32_t nt) {
+        for (uint32_t f = tid; f < nt * F; f += 256) {
+            const uint32_t rr = f / F, u = f - rr * F;
+            *(float4*)(kt + rr * KS + 4 * u) =
+                *(const float4*)(base + (size_t)win_slot(w0, n_shared, i0 + rr) * kv_dim + 4 * u);
+        }
+    };
+
+    // 1. scores: lane = position of the tile, wave = its RPW pairs
+    for (uint32_t i0 = 0; i0 < cmax; i0 += T) {
+        const uint32_t nt = min(T, cmax - i0);
+        load_tile(kbase, i0, nt);
+        __syncthreads();
+        if (lane < nt) {
+            float a[RPW][4];
+#pragma unroll
+            for (uint32_t k = 0; k < RPW; k++) a[k][0] = a[k][1] = a[k][2] = a[k][3] = 0.0f;
+            const float* kr = kt + lane * KS;
+#pragma unroll 4
+            for (uint32_t u = 0; u < F; u++) {
+                const float4 kk = *(const float4*)(kr + 4 * u);
+#pragma unroll
+                for (uint32_t k = 0; k < RPW; k++) {
+                    const float4 qq = *(const float4*)(qs + (wave * RPW + k) * HS + 4 * u);
+                    a[k][0] = __builtin_fmaf(qq.x, kk.x, a[k][0]);
+                    a[k][1] = __builtin_fmaf(qq.y, kk.y, a[k][1]);
+                    a[k][2] = __builtin_fmaf(qq.z, kk.z, a[k][2]);
+                    a[k][3] = __builtin_fmaf(qq.w, kk.w, a[k][3]);
+                }
+            }
+#pragma unroll
+            for (uint32_t k = 0; k < RPW; k++) {
+                const uint32_t rg = wave * RPW + k;
+                // dot.rs:360: (acc0 + acc1) + (acc2 + acc3), then * scale (cpu.rs:609)
+                if (rg < RG && i0 + lane < s_cnt[rg]) sc[rg * scs + i0 + lane] = ((a[k][0] + a[k][1]) + (a[k][2] + a[k][3])) * scale;
+            }
+        }
+        __syncthreads();
+    }
+
+    // 2. softmax of each pair, by the wave that computed its scores
+#pragma unroll
+    for (uint32_t k = 0; k < RPW; k++) {
+        const uint32_t rg = wave * RPW + k, n = rg < RG ? s_cnt[rg] : 0;
+        float* e = sc + rg * scs;
+        float m = -INFINITY;
+        for (uint32_t i = lane; i < n; i += 64) m = fmaxf(m, e[i]);
+        m = wave_max(m);
+        for (uint32_t i = lane; i < n; i += 64) e[i] = glibc_expf(e[i] - m, etab);
+    }
+    __builtin_amdgcn_wave_barrier();
+    if (lane < RPW) {  // sum left to right (elementwise.rs:81-91), one lane per pair
+        const uint32_t rg = wave * RPW + lane;
+        if (rg < RG) s_sum[rg] = chain_sum(sc + rg * scs, s_cnt[rg]);
+    }
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (uint32_t k = 0; k < RPW; k++) {
+        const uint32_t rg = wave * RPW + k;
+        if (rg >= RG) continue;
+        const uint32_t n = s_cnt[rg], r = rg / G, j = rg - r * G;
+        const float sj = s_sum[rg];
+        float* e = sc + rg * scs;
+        float* arow = att + (size_t)(r0 + r) * n_heads * seq_len + (size_t)(h0 + j) * seq_len;
+        for (uint32_t i = lane; i < n; i += 64) {
+            const float pv = div_rn(e[i], sj);
+            e[i] = pv;
+            arow[i] = pv;  // the probabilities stay in `att`, as the reference leaves them
+        }
+    }
+
+    // 3. out[pair][e] = sum_i p_i * v_i[e] in position order; lane = (pair, 4 dims)
+    const uint32_t rgv = wave * RPW + lane / LPR, e0 = 4 * (lane % LPR);
+    const uint32_t nv = rgv < RG ? s_cnt[rgv] : 0;
+    const float* pp = sc + rgv * scs;
+    float o0 = 0.0f, o1 = 0.0f, o2 = 0.0f, o3 = 0.0f;
+    for (uint32_t i0 = 0; i0 < cmax; i0 += T) {
+        const uint32_t nt = min(T, cmax - i0);
+        __syncthreads();  // the previous tile (K or V) is consumed
+        load_tile(vbase, i0, nt);
+        __syncthreads();
+        const uint32_t lim = nv > i0 ? min(nt, nv - i0) : 0;
+#pragma unroll 4
+        for (uint32_t ii = 0; ii < lim; ii++) {
+            const float p = pp[i0 + ii];
+            const float4 vv = *(const float4*)(kt + ii * KS + e0);
+            o0 += p * vv.x;
+            o1 += p * vv.y;
+            o2 += p * vv.z;
+            o3 += p * vv.w;
+        }
+    }
+    const uint32_t r = rgv / G, j = rgv - r * G;
+    const bool live = rgv < RG && r < nr;
+    const size_t o = (size_t)(r0 + r) * width + (size_t)(h0 + j) * HS + e0;
+    if (live) *(float4*)(out + o) = make_float4(o0, o1, o2, o3);
+    if (qo) {  // head outputs are whole Q8 blocks (HS % 32 == 0): quantize for o_proj (quant.rs:864-873)
+        float m = fmaxf(fmaxf(fmaxf(fmaxf(0.0f, fabsf(o0)), fabsf(o1)), fabsf(o2)), fabsf(o3));
+#pragma unroll
+        for (int off = 4; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 8));
+        const float d = div_rn(m, 127.0f);
+        const float inv = d > 0.0f ? div_rn(1.0f, d) : 0.0f;
+        if (live) {
+            char4 qq;
+            qq.x = q8_round(o0 * inv);
+            qq.y = q8_round(o1 * inv);
+            qq.z = q8_round(o2 * inv);
+            qq.w = q8_round(o3 * inv);
+            *(char4*)(qo + o) = qq;
+            if ((lane & 7) == 0) {
+                so[o / 32] = d;
+                ho[o / 32] = f32_to_f16_bits(d);
+            }
+        }
+    }
+}
+
+// LDS bytes of k_attn_rows for windows of up to max_count positions
+static size_t attn_rows_lds(size_t G, size_t hs, size_t max_count) {
+    const size_t lpr = hs / 4, rpw = 64 / lpr, rg = (4 * rpw / G) * G, scs = (max_count + 3) & ~(size_t)3;
+    return (4 * rpw * hs + rg * scs + 64 * (hs + 4)) * sizeof(float);
+}
+
 // LDS budget of the latency-first attention and its shape for one call:
 // slice width DW (32 or 64), K chunk and V chunk capacities.
 static constexpr size_t kAttnFastLds = 150 * 1024;
@@ -2043,11 +2235,54 @@ static AttnFastShape attn_fast_shape(size_t max_count, size_t G, size_t hs) {
 hipError_t launch_attention(hipStream_t st, const float* q, float* out, float* att, const float* kc,
                             const float* vc, size_t layer, const DevWindow* windows, size_t n_rows,
                             size_t max_count, size_t n_heads, size_t kv_mul, size_t hs, size_t kv_dim,
-                            size_t seq_len, float scale, int8_t* qo, float* so, uint16_t* ho) {
+                            size_t seq_len, float scale, int8_t* qo, float* so, uint16_t* ho,
+                            const DevWindow* host_windows) {
     if (n_rows == 0) return hipSuccess;
     if (hs == 0 || hs > 256 || hs % 4 != 0 || kv_mul == 0 || n_heads % kv_mul != 0) return hipErrorInvalidValue;
     if (qo && hs % 32 != 0) return hipErrorInvalidValue;
     if (max_count > seq_len) max_count = seq_len;
+    if (host_windows && n_rows >= 2 && (hs == 32 || hs == 64 || hs == 128)) {
+        // many rows: k_attn_rows, when every block of R rows shares its window layout
+        size_t G = 1;
+        for (size_t g : {8, 4, 3, 2})
+            if (kv_mul % g == 0) {
+                G = g;
+                break;
+            }
+        const size_t R = (4 * (256 / hs)) / G;
+        bool uniform = R >= 1 && attn_rows_lds(G, hs, max_count) <= kAttnLds;
+        for (size_t r = 0; uniform && r < n_rows; r++) {
+            const DevWindow& a = host_windows[r - r % R];
+            const DevWindow& b = host_windows[r];
+            uniform = a.att_start == b.att_start && a.shared_start == b.shared_start && a.shared_end == b.shared_end;
+        }
+        if (uniform) {
+            const size_t lds = attn_rows_lds(G, hs, max_count);
+            const uint32_t scs = (uint32_t)((max_count + 3) & ~(size_t)3);
+            const dim3 grid((unsigned)(n_heads / G), (unsigned)((n_rows + R - 1) / R));
+#define KR_ATTN_ROWS(g, h)                                                                                    \
+    hipLaunchKernelGGL((k_attn_rows<g, h>), grid, dim3(256), lds, st, q, out, att, kc, vc,                    \
+                       layer * seq_len * kv_dim, windows, (uint32_t)n_rows, (uint32_t)n_heads, (uint32_t)kv_mul, \
+                       (uint32_t)kv_dim, (uint32_t)seq_len, scale, scs, qo, so, ho)
+#define KR_ATTN_ROWS_G(g)          \
+    if (hs == 32)                  \
+        KR_ATTN_ROWS(g, 32);       \
+    else if (hs == 64)             \
+        KR_ATTN_ROWS(g, 64);       \
+    else                           \
+        KR_ATTN_ROWS(g, 128);
+            switch (G) {
+                case 8: KR_ATTN_ROWS_G(8) break;
+                case 4: KR_ATTN_ROWS_G(4) break;
+                case 3: KR_ATTN_ROWS_G(3) break;
+                case 2: KR_ATTN_ROWS_G(2) break;
+                default: KR_ATTN_ROWS_G(1) break;
+            }
+#undef KR_ATTN_ROWS_G
+#undef KR_ATTN_ROWS
+            return hipGetLastError();
+        }
+    }
     {
         // heads per workgroup: the largest of 8, 4, 3, 2, 1 dividing kv_mul
         size_t G = 1;

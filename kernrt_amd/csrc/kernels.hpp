@@ -79,7 +79,7 @@ hipError_t launch_attention(hipStream_t st, const float* q, float* out, float* a
                             const float* vc, size_t layer, const DevWindow* windows, size_t n_rows,
                             size_t max_count, size_t n_heads, size_t kv_mul, size_t head_size,
                             size_t kv_dim, size_t seq_len, float scale, int8_t* qo = nullptr,
-                            float* so = nullptr, uint16_t* ho = nullptr);
+                            float* so = nullptr, uint16_t* ho = nullptr, const DevWindow* host_windows = nullptr);
 // Decode attention of one row in two launches (scores by 64-row chunks with
 // RoPE and the kv_write of k/v folded in, then softmax + V by 16-wide head
 // slices); `scratch` holds attention_split_scratch(n_heads, seq_len) floats.

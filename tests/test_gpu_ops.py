@@ -245,6 +245,15 @@ def test_attention_shared_and_multi_windows():
     _attention_case(64, 4, 2, 8, [(0, 2, 0, 0), (3, 4, 0, 3), (5, 8, 0, 3), (9, 9, 0, 3), (10, 20, 0, 0)], 16)
 
 
+@pytest.mark.parametrize("n_heads,n_kv,hs", [(4, 4, 64), (8, 4, 128), (6, 2, 64), (16, 2, 32), (8, 1, 128)])
+def test_attention_prefill_rows(n_heads, n_kv, hs):
+    # prefill windows (row i attends to slots 0..=i, or a shared prefix plus
+    # its own suffix): blocks of rows that share one window layout, 70 rows =
+    # several blocks and a partial one, windows across 64-position tiles
+    _attention_case(160, n_heads, n_kv, hs, [(0, i, 0, 0) for i in range(70)], 40 + hs)
+    _attention_case(160, n_heads, n_kv, hs, [(90, 90 + i, 3, 71) for i in range(45)], 41 + hs)
+
+
 def test_attention_long_context_uses_global_scores():
     # more scores than fit in LDS: the kernel keeps them in `att`
     _attention_case(16384, 2, 1, 128, [(0, 13000, 0, 0), (100, 16383, 0, 0)], 17)

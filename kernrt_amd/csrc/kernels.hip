@@ -2012,25 +2012,26 @@ hipError_t launch_attention_split(hipStream_t st, const float* q, const float* k
 // scores, the softmax with its serial sum, the probabilities (left in `att`),
 // and per output dim the serial sum over positions of p * v.
 //
-// Workgroup = (G query heads of one KV head, block of R rows), 4 waves; a (row, head) pair is
-// "rg" = r * G + j. Each K tile (64 positions) goes to LDS once and serves
+// Workgroup = (G query heads of one KV head, block of R rows), 8 waves; a
+// (row, head) pair is "rg" = r * G + j. Each K tile (64 positions) goes to LDS once and serves
 // every pair of the block: lane = position, and each wave computes the
 // scores of its RPW pairs, reading q by broadcast. The scores stay in LDS;
 // each wave runs the max, exp, serial sum (one lane per pair) and division
-// of its own pairs. Then each V tile goes to LDS once and lane (pair, 4 dims)
-// runs four independent position-order chains. Row r of the block attends to
+// of its own pairs. Then each V tile goes to LDS once and lane (pair, 2 dims)
+// runs two independent position-order chains. Row r of the block attends to
 // its first count_r positions (its window); the block's windows must agree
 // on att_start and the shared range (checked on the host), so window index i
 // is the same cache slot for every row.
-// LDS: q [4 RPW][HS] | scores [RG][scs] | tile [64][HS + 4].
+// LDS: q [8 RPW][HS] | scores [RG][scs] | tile [64][HS + 4].
 template <int HS>
 struct AttnRowsShape {
-    static constexpr uint32_t LPR = HS / 4;    // lanes per pair in the V phase (4 dims each)
-    static constexpr uint32_t RPW = 64 / LPR;  // pairs per wave
+    static constexpr uint32_t NW = 8, NT = 64 * NW;  // waves, threads
+    static constexpr uint32_t LPR = HS / 2;          // lanes per pair in the V phase (2 dims each)
+    static constexpr uint32_t RPW = 64 / LPR;        // pairs per wave
     static constexpr uint32_t T = 64, KS = HS + 4;
 };
 template <int G, int HS>
-__global__ __launch_bounds__(256) void k_attn_rows(const float* __restrict__ q, float* __restrict__ out,
+__global__ __launch_bounds__(512) void k_attn_rows(const float* __restrict__ q, float* __restrict__ out,
                                                    float* __restrict__ att, const float* __restrict__ kc,
                                                    const float* __restrict__ vc, size_t loff,
                                                    const DevWindow* __restrict__ windows, uint32_t n_rows,
@@ -2039,14 +2040,14 @@ __global__ __launch_bounds__(256) void k_attn_rows(const float* __restrict__ q, 
                                                    int8_t* __restrict__ qo, float* __restrict__ so,
                                                    uint16_t* __restrict__ ho) {
     using Sh = AttnRowsShape<HS>;
-    constexpr uint32_t LPR = Sh::LPR, RPW = Sh::RPW, T = Sh::T, KS = Sh::KS, F = HS / 4;
-    constexpr uint32_t R = 4 * RPW / G, RG = R * G;
+    constexpr uint32_t NW = Sh::NW, NT = Sh::NT, LPR = Sh::LPR, RPW = Sh::RPW, T = Sh::T, KS = Sh::KS, F = HS / 4;
+    constexpr uint32_t R = NW * RPW / G, RG = R * G;
     extern __shared__ __align__(16) float sm[];
-    float* qs = sm;                  // [4 RPW][HS]
-    float* sc = qs + 4 * RPW * HS;   // [RG][scs]
-    float* kt = sc + RG * scs;       // [T][KS]
-    __shared__ uint32_t s_cnt[4 * RPW];
-    __shared__ float s_sum[4 * RPW];
+    float* qs = sm;                   // [NW RPW][HS]
+    float* sc = qs + NW * RPW * HS;   // [RG][scs]
+    float* kt = sc + RG * scs;        // [T][KS]
+    __shared__ uint32_t s_cnt[NW * RPW];
+    __shared__ float s_sum[NW * RPW];
     __shared__ uint64_t etab[32];
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t r0 = blockIdx.y * R;
@@ -2058,13 +2059,13 @@ __global__ __launch_bounds__(256) void k_attn_rows(const float* __restrict__ q, 
 
     // the q rows of the block's pairs (rows past the block's end: zeros), the
     // window lengths, the exp table
-    for (uint32_t t = tid; t < 4 * RPW * F; t += 256) {
+    for (uint32_t t = tid; t < NW * RPW * F; t += NT) {
         const uint32_t rg = t / F, u = t - rg * F, r = rg / G, j = rg - r * G;
         float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         if (rg < RG && r < nr) v = *(const float4*)(q + (size_t)(r0 + r) * width + (size_t)(h0 + j) * HS + 4 * u);
         *(float4*)(qs + rg * HS + 4 * u) = v;
     }
-    if (tid < 4 * RPW) {
+    if (tid < NW * RPW) {
         const uint32_t r = tid / G;
         s_cnt[tid] = tid < RG && r < nr ? n_shared + windows[r0 + r].slot - w0.att_start + 1 : 0;
     }
@@ -2074,19 +2075,44 @@ __global__ __launch_bounds__(256) void k_attn_rows(const float* __restrict__ q, 
     for (uint32_t rg = 0; rg < RG; rg++) cmax = max(cmax, s_cnt[rg]);
     const float* kbase = kc + loff + kvo;
     const float* vbase = vc + loff + kvo;
-    auto load_tile = [&](const float* base, uint32_t i0, uint32_t nt) {
-        for (uint32_t f = tid; f < nt * F; f += 256) {
-            const uint32_t rr = f / F, u = f - rr * F;
-            *(float4*)(kt + rr * KS + 4 * u) =
-                *(const float4*)(base + (size_t)win_slot(w0, n_shared, i0 + rr) * kv_dim + 4 * u);
-        }
-    };
+    // Tiles are fetched into registers one tile ahead (PT float4 per thread)
+    // and stored to LDS after the current tile is consumed, so the global
+    // latency overlaps the compute; the barrier after the compute waits for
+    // LDS only, leaving the fetch in flight.
+    constexpr uint32_t PT = T * F / NT;
+    typedef float v4f __attribute__((ext_vector_type(4)));  // a native vector: stays in registers
+    v4f pre[PT];
+    // every fetch loads all PT pieces (rows past the tile re-read its last
+    // row), so the registers are always defined and stay registers
+    auto tile_len = [&](uint32_t i0) { return i0 < cmax ? min(T, cmax - i0) : 0u; };
 
     // 1. scores: lane = position of the tile, wave = its RPW pairs
+    #pragma unroll
+    for (uint32_t k = 0; k < PT; k++) {
+        const uint32_t f = tid + NT * k, rr = f / F, u = f - rr * F, rc = rr < (tile_len(0)) ? rr : (tile_len(0)) - 1;
+        pre[k] = *(const v4f*)(kbase + (size_t)win_slot(w0, n_shared, (0) + rc) * kv_dim + 4 * u);
+    }
+    #pragma unroll
+    for (uint32_t k = 0; k < PT; k++) {
+        const uint32_t f = tid + NT * k, rr = f / F, u = f - rr * F;
+        if (rr < (tile_len(0))) *(v4f*)(kt + rr * KS + 4 * u) = pre[k];
+    }
+    __syncthreads();
     for (uint32_t i0 = 0; i0 < cmax; i0 += T) {
-        const uint32_t nt = min(T, cmax - i0);
-        load_tile(kbase, i0, nt);
-        __syncthreads();
+        const uint32_t nt = tile_len(i0), ntn = tile_len(i0 + T);
+        if (ntn) {
+            #pragma unroll
+            for (uint32_t k = 0; k < PT; k++) {
+                const uint32_t f = tid + NT * k, rr = f / F, u = f - rr * F, rc = rr < (ntn) ? rr : (ntn) - 1;
+                pre[k] = *(const v4f*)(kbase + (size_t)win_slot(w0, n_shared, (i0 + T) + rc) * kv_dim + 4 * u);
+            }
+        } else {  // the first V tile, for phase 3
+            #pragma unroll
+            for (uint32_t k = 0; k < PT; k++) {
+                const uint32_t f = tid + NT * k, rr = f / F, u = f - rr * F, rc = rr < (tile_len(0)) ? rr : (tile_len(0)) - 1;
+                pre[k] = *(const v4f*)(vbase + (size_t)win_slot(w0, n_shared, (0) + rc) * kv_dim + 4 * u);
+            }
+        }
         if (lane < nt) {
             float a[RPW][4];
 #pragma unroll
@@ -2111,7 +2137,15 @@ __global__ __launch_bounds__(256) void k_attn_rows(const float* __restrict__ q, 
                 if (rg < RG && i0 + lane < s_cnt[rg]) sc[rg * scs + i0 + lane] = ((a[k][0] + a[k][1]) + (a[k][2] + a[k][3])) * scale;
             }
         }
-        __syncthreads();
+        lds_barrier();  // the tile is consumed
+        if (ntn) {
+            #pragma unroll
+            for (uint32_t k = 0; k < PT; k++) {
+                const uint32_t f = tid + NT * k, rr = f / F, u = f - rr * F;
+                if (rr < (ntn)) *(v4f*)(kt + rr * KS + 4 * u) = pre[k];
+            }
+            lds_barrier();
+        }
     }
 
     // 2. softmax of each pair, by the wave that computed its scores
@@ -2145,45 +2179,62 @@ __global__ __launch_bounds__(256) void k_attn_rows(const float* __restrict__ q, 
         }
     }
 
-    // 3. out[pair][e] = sum_i p_i * v_i[e] in position order; lane = (pair, 4 dims)
-    const uint32_t rgv = wave * RPW + lane / LPR, e0 = 4 * (lane % LPR);
+    // 3. out[pair][e] = sum_i p_i * v_i[e] in position order; lane = (pair, 2 dims)
+    typedef float v2f __attribute__((ext_vector_type(2)));
+    const uint32_t rgv = wave * RPW + lane / LPR, e0 = 2 * (lane % LPR);
     const uint32_t nv = rgv < RG ? s_cnt[rgv] : 0;
     const float* pp = sc + rgv * scs;
-    float o0 = 0.0f, o1 = 0.0f, o2 = 0.0f, o3 = 0.0f;
+    float o0 = 0.0f, o1 = 0.0f;
+    // the first V tile (every wave is past the last K tile)
+    #pragma unroll
+    for (uint32_t k = 0; k < PT; k++) {
+        const uint32_t f = tid + NT * k, rr = f / F, u = f - rr * F;
+        if (rr < (tile_len(0))) *(v4f*)(kt + rr * KS + 4 * u) = pre[k];
+    }
+    __syncthreads();
     for (uint32_t i0 = 0; i0 < cmax; i0 += T) {
-        const uint32_t nt = min(T, cmax - i0);
-        __syncthreads();  // the previous tile (K or V) is consumed
-        load_tile(vbase, i0, nt);
-        __syncthreads();
+        const uint32_t nt = tile_len(i0), ntn = tile_len(i0 + T);
+        if (ntn) {
+            #pragma unroll
+            for (uint32_t k = 0; k < PT; k++) {
+                const uint32_t f = tid + NT * k, rr = f / F, u = f - rr * F, rc = rr < (ntn) ? rr : (ntn) - 1;
+                pre[k] = *(const v4f*)(vbase + (size_t)win_slot(w0, n_shared, (i0 + T) + rc) * kv_dim + 4 * u);
+            }
+        }
         const uint32_t lim = nv > i0 ? min(nt, nv - i0) : 0;
 #pragma unroll 4
         for (uint32_t ii = 0; ii < lim; ii++) {
             const float p = pp[i0 + ii];
-            const float4 vv = *(const float4*)(kt + ii * KS + e0);
+            const v2f vv = *(const v2f*)(kt + ii * KS + e0);
             o0 += p * vv.x;
             o1 += p * vv.y;
-            o2 += p * vv.z;
-            o3 += p * vv.w;
+        }
+        lds_barrier();
+        if (ntn) {
+            #pragma unroll
+            for (uint32_t k = 0; k < PT; k++) {
+                const uint32_t f = tid + NT * k, rr = f / F, u = f - rr * F;
+                if (rr < (ntn)) *(v4f*)(kt + rr * KS + 4 * u) = pre[k];
+            }
+            lds_barrier();
         }
     }
     const uint32_t r = rgv / G, j = rgv - r * G;
     const bool live = rgv < RG && r < nr;
     const size_t o = (size_t)(r0 + r) * width + (size_t)(h0 + j) * HS + e0;
-    if (live) *(float4*)(out + o) = make_float4(o0, o1, o2, o3);
+    if (live) *(v2f*)(out + o) = v2f{o0, o1};
     if (qo) {  // head outputs are whole Q8 blocks (HS % 32 == 0): quantize for o_proj (quant.rs:864-873)
-        float m = fmaxf(fmaxf(fmaxf(fmaxf(0.0f, fabsf(o0)), fabsf(o1)), fabsf(o2)), fabsf(o3));
+        float m = fmaxf(fmaxf(0.0f, fabsf(o0)), fabsf(o1));
 #pragma unroll
-        for (int off = 4; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 8));
+        for (int off = 8; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 16));
         const float d = div_rn(m, 127.0f);
         const float inv = d > 0.0f ? div_rn(1.0f, d) : 0.0f;
         if (live) {
-            char4 qq;
+            char2 qq;
             qq.x = q8_round(o0 * inv);
             qq.y = q8_round(o1 * inv);
-            qq.z = q8_round(o2 * inv);
-            qq.w = q8_round(o3 * inv);
-            *(char4*)(qo + o) = qq;
-            if ((lane & 7) == 0) {
+            *(char2*)(qo + o) = qq;
+            if ((lane & 15) == 0) {
                 so[o / 32] = d;
                 ho[o / 32] = f32_to_f16_bits(d);
             }
@@ -2193,8 +2244,8 @@ __global__ __launch_bounds__(256) void k_attn_rows(const float* __restrict__ q, 
 
 // LDS bytes of k_attn_rows for windows of up to max_count positions
 static size_t attn_rows_lds(size_t G, size_t hs, size_t max_count) {
-    const size_t lpr = hs / 4, rpw = 64 / lpr, rg = (4 * rpw / G) * G, scs = (max_count + 3) & ~(size_t)3;
-    return (4 * rpw * hs + rg * scs + 64 * (hs + 4)) * sizeof(float);
+    const size_t rpw = 128 / hs, rg = (8 * rpw / G) * G, scs = (max_count + 3) & ~(size_t)3;
+    return (8 * rpw * hs + rg * scs + 64 * (hs + 4)) * sizeof(float);
 }
 
 // LDS budget of the latency-first attention and its shape for one call:
@@ -2249,7 +2300,7 @@ hipError_t launch_attention(hipStream_t st, const float* q, float* out, float* a
                 G = g;
                 break;
             }
-        const size_t R = (4 * (256 / hs)) / G;
+        const size_t R = (8 * (128 / hs)) / G;  // rows per block: AttnRowsShape
         bool uniform = R >= 1 && attn_rows_lds(G, hs, max_count) <= kAttnLds;
         for (size_t r = 0; uniform && r < n_rows; r++) {
             const DevWindow& a = host_windows[r - r % R];
@@ -2261,7 +2312,7 @@ hipError_t launch_attention(hipStream_t st, const float* q, float* out, float* a
             const uint32_t scs = (uint32_t)((max_count + 3) & ~(size_t)3);
             const dim3 grid((unsigned)(n_heads / G), (unsigned)((n_rows + R - 1) / R));
 #define KR_ATTN_ROWS(g, h)                                                                                    \
-    hipLaunchKernelGGL((k_attn_rows<g, h>), grid, dim3(256), lds, st, q, out, att, kc, vc,                    \
+    hipLaunchKernelGGL((k_attn_rows<g, h>), grid, dim3(512), lds, st, q, out, att, kc, vc,                    \
                        layer * seq_len * kv_dim, windows, (uint32_t)n_rows, (uint32_t)n_heads, (uint32_t)kv_mul, \
                        (uint32_t)kv_dim, (uint32_t)seq_len, scale, scs, qo, so, ho)
 #define KR_ATTN_ROWS_G(g)          \

@@ -82,7 +82,7 @@ struct kr_ctx {
     size_t cap_q = 0, cap_s = 0;
     float* tmp = nullptr;
     size_t cap_tmp = 0;
-    IdxStage st_pos, st_slots, st_win;
+    IdxStage st_pos, st_slots, st_win, st_tok;
     std::map<std::pair<uint32_t, size_t>, RopeTable> rope;
     uint32_t* tokens = nullptr;
     static constexpr size_t kTokens = 1 << 16;
@@ -445,6 +445,7 @@ void kr_close(kr_ctx* c) {
     free_stage(c->st_pos);
     free_stage(c->st_slots);
     free_stage(c->st_win);
+    free_stage(c->st_tok);
     void* ptrs[] = {c->kc, c->vc, c->wq, c->ws, c->wh, c->tmp, c->tokens, c->counter, c->attn_scratch};
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
@@ -642,7 +643,7 @@ int kr_rms_norm(kr_ctx* c, kr_buf out, kr_buf x, kr_buf w, size_t rows, size_t d
 }
 
 int kr_qk_norm(kr_ctx* c, kr_buf v, size_t rows, size_t width, size_t head, kr_buf w, float eps) {
-    CHECK(c, head > 0, "head_size must be positive");
+    CHECK(c, head > 0 && head <= 256, "head_size must be in 1..=256");
     BUF(vb, v, rows * width);
     BUF(wb, w, head);
     HIPCHK(c, kr::launch_qk_norm(c->stream, vb->p, rows, width, head, wb->p, eps));
@@ -1000,6 +1001,22 @@ void device_free(void* p) {
 uint32_t* token_ring(kr_ctx* c) { return c->tokens; }
 uint64_t epoch(kr_ctx* c) { return c->epoch; }
 size_t token_ring_len() { return kr_ctx::kTokens; }
+
+int embed_rows(kr_ctx* c, const size_t* tokens, size_t n, kr_buf out) {
+    Mat* e = mat_of(c, c->embedding);
+    CHECK(c, c->prepared && e != nullptr, "prepare() runs before any compute");
+    BUF(o, out, n * e->m.k);
+    std::vector<uint32_t> t(n);
+    for (size_t i = 0; i < n; i++) {
+        CHECK(c, tokens[i] < e->m.n, "token %zu out of range (vocab %zu)", tokens[i], e->m.n);
+        t[i] = (uint32_t)tokens[i];
+    }
+    const uint32_t* td;
+    int rc = stage(c, c->st_tok, t.data(), n, &td);
+    if (rc) return rc;
+    HIPCHK(c, kr::launch_embed_rows(c->stream, e->m, td, n, o->p));
+    return KR_OK;
+}
 
 int embed_dev(kr_ctx* c, const uint32_t* token_dev, kr_buf out, size_t offset) {
     Mat* e = mat_of(c, c->embedding);

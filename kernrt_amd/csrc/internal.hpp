@@ -28,6 +28,8 @@ uint64_t epoch(kr_ctx* c);
 size_t token_ring_len();
 
 int embed_dev(kr_ctx* c, const uint32_t* token_dev, kr_buf out, size_t offset);
+// rows 0..n-1 of out get the embeddings of tokens[0..n-1] (one launch)
+int embed_rows(kr_ctx* c, const size_t* tokens, size_t n, kr_buf out);
 int rope_dev(kr_ctx* c, kr_buf q, kr_buf k, size_t qw, size_t kvw, const uint32_t* pos_dev,
              const kr_rope_spec* spec);
 int kv_write_dev(kr_ctx* c, size_t layer, const uint32_t* slot_dev, kr_buf k, kr_buf v);

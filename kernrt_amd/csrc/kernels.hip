@@ -1295,30 +1295,52 @@ hipError_t launch_rms_norm(hipStream_t st, float* out, const float* x, const flo
     return hipGetLastError();
 }
 
-// Per-head RMSNorm (cpu.rs:647-661): one lane per (row, head), in order.
-__global__ __launch_bounds__(256) void k_qk_norm(float* __restrict__ v, uint32_t rows, uint32_t width,
+// Per-head RMSNorm (cpu.rs:647-661), 16 lanes per (row, head): the squares
+// of the head's values are formed in parallel into LDS, one lane runs the
+// serial sum (the reference order), and the 16 lanes apply the scale to the
+// values they hold in registers.
+__global__ __launch_bounds__(256) void k_qk_norm(float* __restrict__ v, uint32_t items, uint32_t width,
                                                  uint32_t head, const float* __restrict__ w, float eps) {
-    uint32_t heads = width / head;
-    uint32_t id = blockIdx.x * 256 + threadIdx.x;
-    if (id >= rows * heads) return;
-    float* hd = v + (size_t)(id / heads) * width + (size_t)(id % heads) * head;
-    float ss = 0.0f;
-    for (uint32_t i = 0; i < head; i++) {
-        float a = hd[i];
-        ss += a * a;
+    constexpr uint32_t MAXV = 16;  // values per lane: head <= 256
+    extern __shared__ __align__(16) float sq[];  // [16 items][round4(head) + 4]
+    __shared__ float s_scale[16];
+    const uint32_t heads = width / head, slot = threadIdx.x >> 4, l16 = threadIdx.x & 15;
+    const uint32_t stride = ((head + 3) & ~3u) + 4;
+    const uint32_t item = blockIdx.x * 16 + slot;
+    const bool live = item < items;
+    float* hd = v + (size_t)(live ? item / heads : 0) * width + (size_t)(live ? item % heads : 0) * head;
+    float* row = sq + slot * stride;
+    float a[MAXV];
+#pragma unroll
+    for (uint32_t k = 0; k < MAXV; k++) {
+        const uint32_t i = l16 + 16 * k;
+        a[k] = live && i < head ? hd[i] : 0.0f;
+        if (i < head) row[i] = a[k] * a[k];
     }
-    ss = div_rn(ss, (float)head);
-    ss += eps;
-    float scale = div_rn(1.0f, sqrt_rn(ss));
-    for (uint32_t i = 0; i < head; i++) hd[i] = w[i] * (scale * hd[i]);
+    __builtin_amdgcn_wave_barrier();  // a row's 16 lanes are in one wave: LDS order within the wave suffices
+    if (l16 == 0) {  // rms of the head (cpu.rs:635-641 on one head)
+        float ss = chain_sum(row, head);
+        ss = div_rn(ss, (float)head);
+        ss += eps;
+        s_scale[slot] = div_rn(1.0f, sqrt_rn(ss));
+    }
+    __builtin_amdgcn_wave_barrier();
+    const float scale = s_scale[slot];
+#pragma unroll
+    for (uint32_t k = 0; k < MAXV; k++) {
+        const uint32_t i = l16 + 16 * k;
+        if (live && i < head) hd[i] = w[i] * (scale * a[k]);
+    }
 }
 
 hipError_t launch_qk_norm(hipStream_t st, float* v, size_t rows, size_t width, size_t head, const float* w,
                           float eps) {
     size_t n = rows * (width / head);
     if (n == 0) return hipSuccess;
-    hipLaunchKernelGGL(k_qk_norm, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, v, (uint32_t)rows,
-                       (uint32_t)width, (uint32_t)head, w, eps);
+    if (head > 256) return hipErrorInvalidValue;
+    const size_t stride = ((head + 3) & ~(size_t)3) + 4;
+    hipLaunchKernelGGL(k_qk_norm, dim3((unsigned)((n + 15) / 16)), dim3(256), 16 * stride * sizeof(float), st, v,
+                       (uint32_t)n, (uint32_t)width, (uint32_t)head, w, eps);
     return hipGetLastError();
 }
 
@@ -2729,6 +2751,21 @@ __global__ void k_embed(const int8_t* __restrict__ q, const void* __restrict__ s
     size_t si = t * (k / 32) + i / 32;
     float scale = f16 ? f16w(((const uint16_t*)s)[si]) : ((const float*)s)[si];
     out[i] = (float)q[t * k + i] * scale;
+}
+// Many rows at once: row blockIdx.y gets the embedding of tokens[blockIdx.y].
+__global__ void k_embed_rows(const int8_t* __restrict__ q, const void* __restrict__ s, int f16, uint32_t k,
+                             const uint32_t* __restrict__ tokens, float* __restrict__ out) {
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= k) return;
+    const size_t t = tokens[blockIdx.y], si = t * (k / 32) + i / 32;
+    const float scale = f16 ? f16w(((const uint16_t*)s)[si]) : ((const float*)s)[si];
+    out[(size_t)blockIdx.y * k + i] = (float)q[t * k + i] * scale;
+}
+hipError_t launch_embed_rows(hipStream_t st, const DevMatrix& e, const uint32_t* tokens_dev, size_t n, float* out) {
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_embed_rows, dim3((unsigned)((e.k + 255) / 256), (unsigned)n), dim3(256), 0, st, e.q, e.s,
+                       e.storage == kStorageQ8_0 ? 0 : 1, (uint32_t)e.k, tokens_dev, out);
+    return hipGetLastError();
 }
 hipError_t launch_embed(hipStream_t st, const DevMatrix& e, size_t token, const uint32_t* token_dev, float* out) {
     hipLaunchKernelGGL(k_embed, dim3((unsigned)((e.k + 255) / 256)), dim3(256), 0, st, e.q, e.s,

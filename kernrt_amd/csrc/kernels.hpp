@@ -102,6 +102,8 @@ hipError_t launch_conv_prefill(hipStream_t st, float* out, const float* x, const
 hipError_t launch_conv_decode(hipStream_t st, float* out, const float* x, const float* kernel,
                               float* state, size_t dim, size_t k);
 // token from `token_dev` when non-null, else `token`
+// rows 0..n-1 of out (row stride e.k) get the embeddings of tokens_dev[0..n-1]
+hipError_t launch_embed_rows(hipStream_t st, const DevMatrix& e, const uint32_t* tokens_dev, size_t n, float* out);
 hipError_t launch_embed(hipStream_t st, const DevMatrix& e, size_t token, const uint32_t* token_dev,
                         float* out);
 hipError_t launch_argmax(hipStream_t st, const float* x, size_t n, uint32_t* out);

@@ -351,7 +351,13 @@ int prefill_rows(krl_model* m, const std::vector<Row>& rows) {
     }
     TRY(ensure_prefill(m, n_tok));
     PrefillBuffers& p = m->pb;
-    for (size_t r = 0; r < n_tok; r++) KRC(m, kr_embed(b, rows[r].token, p.x, r * g.dim));
+    if (m->fused) {
+        std::vector<size_t> toks(n_tok);
+        for (size_t r = 0; r < n_tok; r++) toks[r] = rows[r].token;
+        KRC(m, kri::embed_rows(b, toks.data(), n_tok, p.x));  // one launch for every row
+    } else {
+        for (size_t r = 0; r < n_tok; r++) KRC(m, kr_embed(b, rows[r].token, p.x, r * g.dim));
+    }
     if (m->fused) {
         // prefill_rows with the fused kernels (see decode_step_fused); the
         // last residual add is applied here because the final norm reads one row

@@ -170,7 +170,8 @@ def test_rms_norm_and_qk_norm(hip):
             hip.rms_norm(go, gx, gw, rows, dim, eps)
             ob.rms_norm(oo, ox, ow, rows, dim, eps)
             assert_bits_equal(hip.read(go, rows * dim), ob.read(oo, rows * dim), f"rms_norm {rows}x{dim}")
-    for rows, width, head in [(1, 2048, 128), (4, 1024, 64), (3, 32, 8), (300, 2048, 128), (500, 960, 64)]:
+    for rows, width, head in [(1, 2048, 128), (4, 1024, 64), (3, 32, 8), (300, 2048, 128), (500, 960, 64),
+                              (2, 99, 33), (3, 512, 256)]:
         v = rng.normal(size=rows * width).astype(np.float32)
         w = rng.normal(size=head).astype(np.float32)
         gv, ov = hip.upload(v), ob.upload(v)

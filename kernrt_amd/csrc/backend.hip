@@ -701,6 +701,43 @@ int kr_kv_write(kr_ctx* c, size_t layer, const size_t* slots, kr_buf k, kr_buf v
     return KR_OK;
 }
 
+// The split-attention scratch (scores and chunk maxima), grown on demand.
+int ensure_attn_scratch(kr_ctx* c, size_t need) {
+    if (need > c->cap_attn_scratch) {
+        if (c->attn_scratch) HIPCHK(c, hipFree(c->attn_scratch));  // hipFree waits for the device
+        c->attn_scratch = nullptr;
+        HIPCHK(c, hipMalloc(&c->attn_scratch, need * sizeof(float)));
+        c->cap_attn_scratch = need;
+        c->epoch++;
+    }
+    return KR_OK;
+}
+
+// Attention over n >= 1 rows with host windows `w` (staged at `wd`): rows
+// whose windows differ (batched decode of separate sequences) take the
+// two-launch split form, everything else launch_attention.
+int attention_many(kr_ctx* c, const float* q, float* out, float* att, size_t layer, const uint32_t* wd,
+                   const std::vector<uint32_t>& w, size_t n, size_t max_count, const kr_attn_spec* sp,
+                   int8_t* qo, float* so, uint16_t* ho) {
+    const kr::DevWindow* hw = (const kr::DevWindow*)w.data();
+    const float scale = 1.0f / sqrtf((float)sp->head_size);  // cpu.rs:591
+    if (n >= 2 && !kr::attention_rows_uniform(hw, n, sp->kv_mul, sp->head_size) &&
+        kr::attention_split_ok(max_count, sp->kv_mul, sp->head_size)) {
+        int rc = ensure_attn_scratch(c, n * kr::attention_split_scratch(sp->n_heads, c->seq_len));
+        if (rc) return rc;
+        HIPCHK(c, kr::launch_attention_split_rows(c->stream, q, out, att, c->kc, c->vc, layer, (const kr::DevWindow*)wd,
+                                                  n, max_count, sp->n_heads, sp->kv_mul, sp->head_size, sp->kv_dim,
+                                                  sp->seq_len, scale, c->attn_scratch));
+        const size_t width = sp->n_heads * sp->head_size;
+        if (qo) HIPCHK(c, kr::launch_quantize(c->stream, out, n, width, width, qo, so, ho));
+        return KR_OK;
+    }
+    HIPCHK(c, kr::launch_attention(c->stream, q, out, att, c->kc, c->vc, layer, (const kr::DevWindow*)wd, n, max_count,
+                                   sp->n_heads, sp->kv_mul, sp->head_size, sp->kv_dim, sp->seq_len, scale, qo, so, ho,
+                                   hw));
+    return KR_OK;
+}
+
 int kr_attention(kr_ctx* c, kr_buf q, kr_buf out, kr_buf att, size_t layer, const kr_window* windows,
                  size_t n, const kr_attn_spec* sp) {
     CHECK(c, c->prepared, "prepare() runs before any compute");
@@ -734,11 +771,7 @@ int kr_attention(kr_ctx* c, kr_buf q, kr_buf out, kr_buf att, size_t layer, cons
     const uint32_t* wd;
     int rc = stage(c, c->st_win, w.data(), 4 * n, &wd);
     if (rc) return rc;
-    float scale = 1.0f / sqrtf((float)sp->head_size);  // cpu.rs:591
-    HIPCHK(c, kr::launch_attention(c->stream, qb->p, ob->p, ab->p, c->kc, c->vc, layer, (const kr::DevWindow*)wd, n,
-                                   max_count, sp->n_heads, sp->kv_mul, sp->head_size, sp->kv_dim, sp->seq_len, scale,
-                                   nullptr, nullptr, nullptr, (const kr::DevWindow*)w.data()));
-    return KR_OK;
+    return attention_many(c, qb->p, ob->p, ab->p, layer, wd, w, n, max_count, sp, nullptr, nullptr, nullptr);
 }
 
 int kr_add_in_place(kr_ctx* c, kr_buf dst, kr_buf src, size_t len) {
@@ -1199,10 +1232,15 @@ int attention_quant(kr_ctx* c, kr_buf q, kr_buf out, kr_buf att, size_t layer, c
     }
     int rc = ensure_workspace(c, n, width);
     if (rc) return rc;
-    float scale = 1.0f / sqrtf((float)sp->head_size);
-    HIPCHK(c, kr::launch_attention(c->stream, qb->p, ob->p, ab->p, c->kc, c->vc, layer, (const kr::DevWindow*)wd, n,
-                                   max_count, sp->n_heads, sp->kv_mul, sp->head_size, sp->kv_dim, sp->seq_len, scale,
-                                   c->wq, c->ws, c->wh, w.empty() ? nullptr : (const kr::DevWindow*)w.data()));
+    if (w.empty()) {  // one device window
+        float scale = 1.0f / sqrtf((float)sp->head_size);
+        HIPCHK(c, kr::launch_attention(c->stream, qb->p, ob->p, ab->p, c->kc, c->vc, layer, (const kr::DevWindow*)wd,
+                                       n, max_count, sp->n_heads, sp->kv_mul, sp->head_size, sp->kv_dim, sp->seq_len,
+                                       scale, c->wq, c->ws, c->wh));
+    } else {
+        rc = attention_many(c, qb->p, ob->p, ab->p, layer, wd, w, n, max_count, sp, c->wq, c->ws, c->wh);
+        if (rc) return rc;
+    }
     c->q_rows = n;
     c->q_width = width;
     return KR_OK;
@@ -1306,14 +1344,8 @@ int rope_attention(kr_ctx* c, kr_buf q, kr_buf k, kr_buf v, kr_buf out, kr_buf a
     BUF(vb, v, c->kv_dim);
     BUF(ob, out, width);
     BUF(ab, att, sp->n_heads * sp->seq_len);
-    const size_t need = kr::attention_split_scratch(sp->n_heads, c->seq_len);
-    if (need > c->cap_attn_scratch) {
-        if (c->attn_scratch) HIPCHK(c, hipFree(c->attn_scratch));
-        c->attn_scratch = nullptr;
-        HIPCHK(c, hipMalloc(&c->attn_scratch, need * sizeof(float)));
-        c->cap_attn_scratch = need;
-        c->epoch++;
-    }
+    int rc0 = ensure_attn_scratch(c, kr::attention_split_scratch(sp->n_heads, c->seq_len));
+    if (rc0) return rc0;
     const float2* tab;
     const uint32_t* wd;
     const uint32_t* pd;

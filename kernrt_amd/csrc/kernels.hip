@@ -1789,26 +1789,32 @@ __global__ __launch_bounds__(512) void k_attention_fast(
 // every query head; the scores go to a scratch row per head, and each
 // chunk's maximum per head to a second scratch array.
 // The new position's key is taken from LDS, not from the cache being written.
-template <int G, int HS>
+template <int G, int HS, bool ROPE>
 __global__ __launch_bounds__(64) void k_attn_scores(const float* __restrict__ q, const float* __restrict__ kin,
                                                     const float* __restrict__ vin, float* __restrict__ kc,
                                                     float* __restrict__ vc, size_t loff,
                                                     const DevWindow* __restrict__ win, const uint32_t* __restrict__ pos,
                                                     const float2* __restrict__ tab, int interleaved, uint32_t kv_dim,
                                                     float scale, float* __restrict__ sc, uint32_t ss,
-                                                    float* __restrict__ mxp, uint32_t ms) {
+                                                    float* __restrict__ mxp, uint32_t ms, uint32_t width) {
     constexpr uint32_t F = HS / 4, HALF = HS / 2;
     __shared__ __align__(16) float qs[G * HS];
     __shared__ __align__(16) float kn[HS];
-    const uint32_t lane = threadIdx.x, hk = blockIdx.x, chunk = blockIdx.y;
-    const DevWindow w = win[0];
+    const uint32_t lane = threadIdx.x, hk = blockIdx.x, chunk = blockIdx.y, row = blockIdx.z;
+    const uint32_t n_heads = width / HS;
+    const DevWindow w = win[row];
+    sc += (size_t)row * n_heads * ss;
+    mxp += (size_t)row * n_heads * ms;
     const uint32_t n_shared = w.shared_end - w.shared_start;
     const uint32_t count = n_shared + w.slot - w.att_start + 1;
     const uint32_t r0 = chunk * 64;
-    if (r0 >= count && chunk != 0) return;
-    const float2* tr = tab + (size_t)pos[0] * HALF;
-    const float* qh = q + (size_t)hk * G * HS;
-    for (uint32_t t = lane; t < (G + 1) * HALF; t += 64) {
+    if (r0 >= count && (chunk != 0 || !ROPE)) return;
+    const float* qh = q + (size_t)row * width + (size_t)hk * G * HS;
+    if (!ROPE) {  // q is already rotated, and every key is in the cache
+        for (uint32_t t = lane; t < G * F; t += 64) ((float4*)qs)[t] = ((const float4*)qh)[t];
+    }
+    const float2* tr = ROPE ? tab + (size_t)pos[0] * HALF : tab;
+    for (uint32_t t = lane; ROPE && t < (G + 1) * HALF; t += 64) {
         const uint32_t hh = t / HALF, i = t - hh * HALF;
         const float* src = hh < G ? qh + hh * HS : kin + (size_t)hk * HS;
         float* dst = hh < G ? qs + hh * HS : kn;
@@ -1819,7 +1825,7 @@ __global__ __launch_bounds__(64) void k_attn_scores(const float* __restrict__ q,
         dst[i1] = a * cs.y + b * cs.x;
     }
     __syncthreads();
-    if (chunk == 0) {
+    if (ROPE && chunk == 0) {
         const size_t at = loff + (size_t)w.slot * kv_dim + (size_t)hk * HS;
         for (uint32_t e = lane; e < HS; e += 64) {
             kc[at + e] = kn[e];
@@ -1834,7 +1840,7 @@ __global__ __launch_bounds__(64) void k_attn_scores(const float* __restrict__ q,
     const float4* krow = (const float4*)(kc + loff + (size_t)win_slot(w, n_shared, ic) * kv_dim + (size_t)hk * HS);
 #pragma unroll
     for (uint32_t u = 0; u < F; u++) kk[u] = krow[u];
-    if (ic == count - 1) {  // the new position: its key is the one just rotated
+    if (ROPE && ic == count - 1) {  // the new position: its key is the one just rotated
 #pragma unroll
         for (uint32_t u = 0; u < F; u++) kk[u] = ((const float4*)kn)[u];
     }
@@ -1887,8 +1893,13 @@ __global__ __launch_bounds__(1024) void k_attn_softmax_v(const float* __restrict
     __shared__ float s_sum[G];
     __shared__ uint64_t etab[32];
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t hk = blockIdx.x / S, sidx = blockIdx.x % S, d0 = sidx * DW;
-    const DevWindow w = win[0];
+    const uint32_t hk = blockIdx.x / S, sidx = blockIdx.x % S, d0 = sidx * DW, row = blockIdx.y;
+    const uint32_t n_heads = gridDim.x / S * G;
+    const DevWindow w = win[row];
+    sc_in += (size_t)row * n_heads * ss;
+    mxp += (size_t)row * n_heads * ms;
+    att += (size_t)row * n_heads * seq_len;
+    out += (size_t)row * n_heads * HS;
     const uint32_t n_shared = w.shared_end - w.shared_start;
     const uint32_t count = n_shared + w.slot - w.att_start + 1;  // <= scs
     const uint32_t vst = (uint32_t)attn_split_vst(scs), nch = (count + 63) / 64;
@@ -2002,8 +2013,8 @@ hipError_t launch_attention_split(hipStream_t st, const float* q, const float* k
     const dim3 g1((unsigned)n_kv, (unsigned)nchunks), g2((unsigned)(n_kv * (hs / kAttnSplitDW)));
 #define KR_SPLIT(G, H)                                                                                              \
     do {                                                                                                            \
-        hipLaunchKernelGGL((k_attn_scores<G, H>), g1, dim3(64), 0, st, q, k, v, kc, vc, loff, window, pos, table,   \
-                           interleaved, (uint32_t)kv_dim, scale, sc, ss, mxp, ms);                                  \
+        hipLaunchKernelGGL((k_attn_scores<G, H, true>), g1, dim3(64), 0, st, q, k, v, kc, vc, loff, window, pos,    \
+                           table, interleaved, (uint32_t)kv_dim, scale, sc, ss, mxp, ms, (uint32_t)(n_heads * hs)); \
         hipLaunchKernelGGL((k_attn_softmax_v<G, H, kAttnSplitDW>), g2, dim3(1024), lds, st, sc, ss, mxp, ms, vc, loff, \
                            window,                                                                                  \
                            (uint32_t)kv_dim, (uint32_t)seq_len, (uint32_t)scs, att, out);                           \
@@ -2268,6 +2279,73 @@ __global__ __launch_bounds__(512) void k_attn_rows(const float* __restrict__ q, 
 static size_t attn_rows_lds(size_t G, size_t hs, size_t max_count) {
     const size_t rpw = 128 / hs, rg = (8 * rpw / G) * G, scs = (max_count + 3) & ~(size_t)3;
     return (8 * rpw * hs + rg * scs + 64 * (hs + 4)) * sizeof(float);
+}
+
+// Many rows with windows of their own (batched decode of independent
+// sequences): the same two launches, without RoPE and kv_write (q rows are
+// already rotated and every key is in the cache), one row per grid z (scores)
+// or y (softmax and V). `scratch` holds n_rows * attention_split_scratch floats.
+hipError_t launch_attention_split_rows(hipStream_t st, const float* q, float* out, float* att, const float* kc,
+                                       const float* vc, size_t layer, const DevWindow* windows, size_t n_rows,
+                                       size_t max_count, size_t n_heads, size_t kv_mul, size_t hs, size_t kv_dim,
+                                       size_t seq_len, float scale, float* scratch) {
+    if (n_rows == 0) return hipSuccess;
+    if (!attention_split_ok(max_count, kv_mul, hs) || n_heads % kv_mul != 0 || max_count > seq_len)
+        return hipErrorInvalidValue;
+    const size_t n_kv = n_heads / kv_mul, nchunks = (max_count + 63) / 64, loff = layer * seq_len * kv_dim;
+    const size_t scs = (max_count + 3) & ~(size_t)3;
+    const uint32_t ss = (uint32_t)((seq_len + 3) & ~(size_t)3), ms = (uint32_t)attn_split_ms(seq_len);
+    float* sc = scratch;
+    float* mxp = scratch + n_rows * n_heads * ss;
+    const size_t lds = attn_split_lds(scs, kv_mul, kAttnSplitDW);
+    const dim3 g1((unsigned)n_kv, (unsigned)nchunks, (unsigned)n_rows),
+        g2((unsigned)(n_kv * (hs / kAttnSplitDW)), (unsigned)n_rows);
+    float* kcw = const_cast<float*>(kc);  // written only by the RoPE form
+    float* vcw = const_cast<float*>(vc);
+#define KR_SPLIT_ROWS(G, H)                                                                                          \
+    do {                                                                                                             \
+        hipLaunchKernelGGL((k_attn_scores<G, H, false>), g1, dim3(64), 0, st, q, nullptr, nullptr, kcw, vcw, loff,   \
+                           windows, nullptr, nullptr, 0, (uint32_t)kv_dim, scale, sc, ss, mxp, ms,                   \
+                           (uint32_t)(n_heads * hs));                                                                \
+        hipLaunchKernelGGL((k_attn_softmax_v<G, H, kAttnSplitDW>), g2, dim3(1024), lds, st, sc, ss, mxp, ms, vc,     \
+                           loff, windows, (uint32_t)kv_dim, (uint32_t)seq_len, (uint32_t)scs, att, out);            \
+    } while (0)
+#define KR_SPLIT_ROWS_H(G)       \
+    if (hs == 32)                \
+        KR_SPLIT_ROWS(G, 32);    \
+    else if (hs == 64)           \
+        KR_SPLIT_ROWS(G, 64);    \
+    else                         \
+        KR_SPLIT_ROWS(G, 128);
+    switch (kv_mul) {
+        case 8: KR_SPLIT_ROWS_H(8) break;
+        case 4: KR_SPLIT_ROWS_H(4) break;
+        case 3: KR_SPLIT_ROWS_H(3) break;
+        case 2: KR_SPLIT_ROWS_H(2) break;
+        default: KR_SPLIT_ROWS_H(1) break;
+    }
+#undef KR_SPLIT_ROWS_H
+#undef KR_SPLIT_ROWS
+    return hipGetLastError();
+}
+
+// Whether a block of rows can run k_attn_rows: its windows share att_start
+// and the shared range (prefill), checked per block of the kernel's R rows.
+bool attention_rows_uniform(const DevWindow* w, size_t n_rows, size_t kv_mul, size_t hs) {
+    if (n_rows < 2 || (hs != 32 && hs != 64 && hs != 128)) return false;
+    size_t G = 1;
+    for (size_t g : {8, 4, 3, 2})
+        if (kv_mul % g == 0) {
+            G = g;
+            break;
+        }
+    const size_t R = (8 * (128 / hs)) / G;
+    for (size_t r = 0; r < n_rows; r++) {
+        const DevWindow& a = w[r - r % R];
+        if (a.att_start != w[r].att_start || a.shared_start != w[r].shared_start || a.shared_end != w[r].shared_end)
+            return false;
+    }
+    return true;
 }
 
 // LDS budget of the latency-first attention and its shape for one call:

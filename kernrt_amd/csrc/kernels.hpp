@@ -90,6 +90,16 @@ hipError_t launch_attention_split(hipStream_t st, const float* q, const float* k
                                   const uint32_t* pos, const float2* table, int interleaved, size_t max_count,
                                   size_t n_heads, size_t kv_mul, size_t hs, size_t kv_dim, size_t seq_len,
                                   float scale, float* scratch);
+// The same two launches for many rows with windows of their own (batched
+// decode): q rows already rotated, keys already in the cache; `scratch`
+// holds n_rows * attention_split_scratch(n_heads, seq_len) floats.
+hipError_t launch_attention_split_rows(hipStream_t st, const float* q, float* out, float* att, const float* kc,
+                                       const float* vc, size_t layer, const DevWindow* windows, size_t n_rows,
+                                       size_t max_count, size_t n_heads, size_t kv_mul, size_t hs, size_t kv_dim,
+                                       size_t seq_len, float scale, float* scratch);
+// whether the rows' windows let launch_attention use its block-of-rows
+// (prefill) kernel: each block of rows shares att_start and the shared range
+bool attention_rows_uniform(const DevWindow* host_windows, size_t n_rows, size_t kv_mul, size_t hs);
 hipError_t launch_add(hipStream_t st, float* dst, const float* src, size_t n);
 hipError_t launch_mul(hipStream_t st, float* out, const float* a, const float* b, size_t n,
                       int sequential);

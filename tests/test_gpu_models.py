@@ -117,6 +117,31 @@ def test_decode_batch_matches_per_sequence_forward(storage, n_seq):
             assert_bits_equal(got[r], cpus[i].forward(seqs[i][t], t), f"decode_batch step {t} sequence {i}")
 
 
+@pytest.mark.parametrize("n_seq", [3, 9])
+def test_decode_batch_split_attention(n_seq):
+    # batched decode with head_dim 64: rows whose windows belong to different
+    # sequences take the two-launch split attention over many rows
+    c = O.Config(dim=128, hidden_dim=128, n_layers=1, n_heads=2, n_kv_heads=1, vocab_size=64, seq_len=96 * n_seq,
+                 rms_eps=1e-5, rope_theta=10_000.0, rope_interleaved=False, head_dim=64)
+    ow = gaussian_weights(c, "q8_0", seed=n_seq + 5)
+    rng = np.random.default_rng(n_seq + 1)
+    room = c.seq_len // n_seq
+    seqs = [[int(t) for t in rng.integers(0, c.vocab_size, size=int(n))] for n in rng.integers(70, 90, size=n_seq)]
+    g = gpu_model(c, ow)
+    cpus = [O.Model(c, ow, "cpu") for _ in seqs]
+    for t in range(max(len(s) for s in seqs)):
+        live = [i for i, s in enumerate(seqs) if t < len(s)]
+        got = g.decode_batch([seqs[i][t] for i in live], [t] * len(live), [i * room + t for i in live],
+                             [i * room for i in live])
+        if t % 16 == 15 or t + 1 == max(len(s) for s in seqs):
+            for r, i in enumerate(live):
+                want = cpus[i].forward(seqs[i][t], t)
+                assert_bits_equal(got[r], want, f"decode_batch step {t} sequence {i}")
+        else:
+            for i in live:
+                cpus[i].forward(seqs[i][t], t)
+
+
 def test_multi_tile_shapes():
     # tests/backends.rs:436-481: a 70-row prompt against 256-wide projections
     c = O.Config(dim=128, hidden_dim=256, n_layers=2, n_heads=4, n_kv_heads=2, vocab_size=128, seq_len=128,

@@ -2281,6 +2281,99 @@ static size_t attn_rows_lds(size_t G, size_t hs, size_t max_count) {
     return (8 * rpw * hs + rg * scs + 64 * (hs + 4)) * sizeof(float);
 }
 
+// Softmax and V sums of the many-row split attention: workgroup = (KV head,
+// row), G * HS threads, lane (j, e) = one output value. The G score rows and
+// their chunk maxima come from k_attn_scores; the max, exp, serial sum (one
+// lane per head) and division are as in k_attn_softmax_v; then V streams
+// through LDS in tiles of 64 positions (fetched into registers one tile
+// ahead) and every lane runs its own position-order chain. All lanes carry a
+// chain, which suits many rows in flight (k_attn_softmax_v instead spreads
+// one row over many CUs).
+template <int G, int HS>
+__global__ __launch_bounds__(G * HS < 64 ? 64 : G * HS) void k_attn_softmax_v_rows(
+    const float* __restrict__ sc_in, uint32_t ss, const float* __restrict__ mxp, uint32_t ms,
+    const float* __restrict__ vc, size_t loff, const DevWindow* __restrict__ win, uint32_t kv_dim, uint32_t seq_len,
+    uint32_t scs, uint32_t n_heads, float* __restrict__ att, float* __restrict__ out) {
+    constexpr uint32_t NT = G * HS < 64 ? 64 : G * HS, T = 64, F = HS / 4, PT = (T * F + NT - 1) / NT;
+    typedef float v4f __attribute__((ext_vector_type(4)));
+    extern __shared__ __align__(16) float sm[];  // probabilities [G][scs] | V tile [T][HS]
+    __shared__ float s_sum[G];
+    __shared__ float s_max[G];
+    __shared__ uint64_t etab[32];
+    const uint32_t tid = threadIdx.x, lane = tid & 63, hk = blockIdx.x, row = blockIdx.y;
+    const DevWindow w = win[row];
+    const uint32_t n_shared = w.shared_end - w.shared_start;
+    const uint32_t count = n_shared + w.slot - w.att_start + 1, nch = (count + 63) / 64;
+    sc_in += (size_t)row * n_heads * ss + (size_t)hk * G * ss;
+    mxp += (size_t)row * n_heads * ms + (size_t)hk * G * ms;
+    att += (size_t)row * n_heads * seq_len + (size_t)hk * G * seq_len;
+    out += (size_t)row * n_heads * HS + (size_t)hk * G * HS;
+    float* ps = sm;
+    float* vt = sm + G * scs;
+    const float* vbase = vc + loff + (size_t)hk * HS;
+    // scores, maxima, exp table
+    for (uint32_t t = tid; t < G * count; t += NT) {
+        const uint32_t j = t / count, i = t - j * count;
+        ps[j * scs + i] = sc_in[(size_t)j * ss + i];
+    }
+    if (tid < G) {
+        float m = -INFINITY;
+        for (uint32_t c = 0; c < nch; c++) m = fmaxf(m, mxp[(size_t)tid * ms + c]);
+        s_max[tid] = m;
+    }
+    if (tid < 32) etab[tid] = kExp2Tab[tid];
+    __syncthreads();
+    for (uint32_t t = tid; t < G * count; t += NT) {
+        const uint32_t j = t / count, i = t - j * count;
+        ps[j * scs + i] = glibc_expf(ps[j * scs + i] - s_max[j], etab);
+    }
+    __syncthreads();
+    if (tid < G) s_sum[tid] = chain_sum(ps + tid * scs, count);  // elementwise.rs:81-91
+    __syncthreads();
+    for (uint32_t t = tid; t < G * count; t += NT) {
+        const uint32_t j = t / count, i = t - j * count;
+        const float pv = div_rn(ps[j * scs + i], s_sum[j]);
+        ps[j * scs + i] = pv;
+        att[(size_t)j * seq_len + i] = pv;  // the probabilities stay in `att`, as the reference leaves them
+    }
+    // V tiles: piece f = (position f / F, float4 f % F)
+    v4f pre[PT];
+    auto tile_len = [&](uint32_t i0) { return i0 < count ? min(T, count - i0) : 0u; };
+#define KR_VROWS_FETCH(i0, nt)                                                                             \
+    _Pragma("unroll") for (uint32_t k = 0; k < PT; k++) {                                                  \
+        const uint32_t f = min(tid + NT * k, (nt) * F - 1), rr = f / F, u = f - rr * F;                   \
+        pre[k] = *(const v4f*)(vbase + (size_t)win_slot(w, n_shared, (i0) + rr) * kv_dim + 4 * u);       \
+    }
+#define KR_VROWS_PUT(nt)                                                                                   \
+    _Pragma("unroll") for (uint32_t k = 0; k < PT; k++) {                                                  \
+        const uint32_t f = tid + NT * k, rr = f / F, u = f - rr * F;                                       \
+        if (f < (nt) * F) *(v4f*)(vt + rr * HS + 4 * u) = pre[k];                                          \
+    }
+    KR_VROWS_FETCH(0, tile_len(0))
+    __syncthreads();  // the probabilities are in LDS
+    KR_VROWS_PUT(tile_len(0))
+    __syncthreads();
+    const uint32_t j = tid / HS, e = tid - j * HS;
+    const float* pp = ps + (j < G ? j : 0) * scs;
+    float o = 0.0f;
+    for (uint32_t i0 = 0; i0 < count; i0 += T) {
+        const uint32_t nt = tile_len(i0), ntn = tile_len(i0 + T);
+        if (ntn) {
+            KR_VROWS_FETCH(i0 + T, ntn)
+        }
+#pragma unroll 8
+        for (uint32_t ii = 0; ii < nt; ii++) o += pp[i0 + ii] * vt[ii * HS + e];
+        lds_barrier();  // the tile is consumed; the next fetch stays in flight
+        if (ntn) {
+            KR_VROWS_PUT(ntn)
+            lds_barrier();
+        }
+    }
+#undef KR_VROWS_FETCH
+#undef KR_VROWS_PUT
+    if (tid < G * HS) out[tid] = o;
+}
+
 // Many rows with windows of their own (batched decode of independent
 // sequences): the same two launches, without RoPE and kv_write (q rows are
 // already rotated and every key is in the cache), one row per grid z (scores)
@@ -2297,9 +2390,8 @@ hipError_t launch_attention_split_rows(hipStream_t st, const float* q, float* ou
     const uint32_t ss = (uint32_t)((seq_len + 3) & ~(size_t)3), ms = (uint32_t)attn_split_ms(seq_len);
     float* sc = scratch;
     float* mxp = scratch + n_rows * n_heads * ss;
-    const size_t lds = attn_split_lds(scs, kv_mul, kAttnSplitDW);
-    const dim3 g1((unsigned)n_kv, (unsigned)nchunks, (unsigned)n_rows),
-        g2((unsigned)(n_kv * (hs / kAttnSplitDW)), (unsigned)n_rows);
+    const size_t lds = (kv_mul * scs + 64 * hs) * sizeof(float);
+    const dim3 g1((unsigned)n_kv, (unsigned)nchunks, (unsigned)n_rows), g2((unsigned)n_kv, (unsigned)n_rows);
     float* kcw = const_cast<float*>(kc);  // written only by the RoPE form
     float* vcw = const_cast<float*>(vc);
 #define KR_SPLIT_ROWS(G, H)                                                                                          \
@@ -2307,8 +2399,9 @@ hipError_t launch_attention_split_rows(hipStream_t st, const float* q, float* ou
         hipLaunchKernelGGL((k_attn_scores<G, H, false>), g1, dim3(64), 0, st, q, nullptr, nullptr, kcw, vcw, loff,   \
                            windows, nullptr, nullptr, 0, (uint32_t)kv_dim, scale, sc, ss, mxp, ms,                   \
                            (uint32_t)(n_heads * hs));                                                                \
-        hipLaunchKernelGGL((k_attn_softmax_v<G, H, kAttnSplitDW>), g2, dim3(1024), lds, st, sc, ss, mxp, ms, vc,     \
-                           loff, windows, (uint32_t)kv_dim, (uint32_t)seq_len, (uint32_t)scs, att, out);            \
+        hipLaunchKernelGGL((k_attn_softmax_v_rows<G, H>), g2, dim3(G * H < 64 ? 64 : G * H), lds, st, sc, ss, mxp, ms, \
+                           vc, loff, windows, (uint32_t)kv_dim, (uint32_t)seq_len, (uint32_t)scs, (uint32_t)n_heads,  \
+                           att, out);                                                                               \
     } while (0)
 #define KR_SPLIT_ROWS_H(G)       \
     if (hs == 32)                \

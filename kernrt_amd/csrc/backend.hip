@@ -721,7 +721,7 @@ int attention_many(kr_ctx* c, const float* q, float* out, float* att, size_t lay
                    int8_t* qo, float* so, uint16_t* ho) {
     const kr::DevWindow* hw = (const kr::DevWindow*)w.data();
     const float scale = 1.0f / sqrtf((float)sp->head_size);  // cpu.rs:591
-    if (n >= 2 && !kr::attention_rows_uniform(hw, n, sp->kv_mul, sp->head_size) &&
+    if (n >= 2 && !kr::attention_rows_uniform(hw, n, max_count, sp->kv_mul, sp->head_size) &&
         kr::attention_split_ok(max_count, sp->kv_mul, sp->head_size)) {
         int rc = ensure_attn_scratch(c, n * kr::attention_split_scratch(sp->n_heads, c->seq_len));
         if (rc) return rc;
@@ -1287,43 +1287,6 @@ int norm_project(kr_ctx* c, size_t layer, const int* projs, const kr_buf* ys, in
         ap = ab->p;
     }
     HIPCHK(c, kr::launch_project_pro(c->stream, sem_for_project(*ms[0]), ms, yp, n, 1, xb->p, ap, wb->p, ob->p, eps));
-    return KR_OK;
-}
-
-int norm_logits(kr_ctx* c, kr_buf x, kr_buf add, kr_buf w, kr_buf y, size_t dim, float eps) {
-    CHECK(c, c->prepared, "prepare() runs before any compute");
-    Mat* mt = mat_of(c, c->classifier != KR_NO_MAT ? c->classifier : c->embedding);
-    CHECK(c, mt != nullptr, "no classifier bound");
-    CHECK(c, pro_fusable(dim) && mt->m.k == dim, "fused norm + logits: dim %zu", dim);
-    const DevMatrix* m;
-    int sem;
-    int rc = classifier_matrix(c, mt, &m, &sem);
-    if (rc) return rc;
-    BUF(yb, y, m->n);
-    BUF(xb, x, dim);
-    BUF(wb, w, dim);
-    const float* ap = nullptr;
-    if (add != KR_NO_BUF) {
-        BUF(ab, add, dim);
-        ap = ab->p;
-    }
-    float* yp = yb->p;
-    HIPCHK(c, kr::launch_project_pro(c->stream, sem, &m, &yp, 1, 1, xb->p, ap, wb->p, nullptr, eps));
-    return KR_OK;
-}
-
-int silu_project(kr_ctx* c, size_t layer, int proj, kr_buf gate, kr_buf up, kr_buf y, size_t width) {
-    CHECK(c, c->prepared && layer < c->n_layers, "layer %zu out of range", layer);
-    CHECK(c, pro_fusable(width), "fused silu + projection: width %zu", width);
-    const Mat* m = proj_mat(c, layer, proj);
-    CHECK(c, m != nullptr && m->m.k == width, "projection %d is not live on layer %zu", proj, layer);
-    BUF(g, gate, width);
-    BUF(u, up, width);
-    BUF(yb, y, m->m.n);
-    const DevMatrix* ms = &m->m;
-    float* yp = yb->p;
-    HIPCHK(c, kr::launch_project_pro(c->stream, sem_for_project(m->m), &ms, &yp, 1, 2, g->p, u->p, nullptr, nullptr,
-                                     0.0f));
     return KR_OK;
 }
 

@@ -68,10 +68,6 @@ bool pro_fusable(size_t k);
 // Q8(rms_norm(x_out, w)); x_out must not be x
 int norm_project(kr_ctx* c, size_t layer, const int* projs, const kr_buf* ys, int n, kr_buf x, kr_buf add, kr_buf w,
                  kr_buf x_out, size_t dim, float eps);
-// the classifier of Q8(rms_norm(x + add, w)) (the updated x is not kept)
-int norm_logits(kr_ctx* c, kr_buf x, kr_buf add, kr_buf w, kr_buf y, size_t dim, float eps);
-// the projection of Q8(silu(gate) * up)
-int silu_project(kr_ctx* c, size_t layer, int proj, kr_buf gate, kr_buf up, kr_buf y, size_t width);
 // the projection of Q8(x) (x one f32 row of `width`)
 int quant_project(kr_ctx* c, size_t layer, int proj, kr_buf x, kr_buf y, size_t width);
 

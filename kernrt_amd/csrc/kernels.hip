@@ -107,31 +107,6 @@ __device__ __forceinline__ float seq_fma(const float2* __restrict__ e, uint32_t 
     return slot;
 }
 
-// t[b & 3] += e[b] for b in order, then ((t0 + t1) + t2) + t3 (dot.rs:35-44)
-__device__ __forceinline__ float seq_four(const float* __restrict__ e, uint32_t n) {
-    float t[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    uint32_t full = n & ~(uint32_t)(kPipe - 1), i = 0;
-    if (full) {
-        float cur[kPipe];
-#pragma unroll
-        for (int j = 0; j < kPipe; j++) cur[j] = e[j];
-        for (i = kPipe; i < full; i += kPipe) {
-            float nxt[kPipe];
-#pragma unroll
-            for (int j = 0; j < kPipe; j++) nxt[j] = e[i + j];
-#pragma unroll
-            for (int j = 0; j < kPipe; j++) t[j & 3] += cur[j];
-#pragma unroll
-            for (int j = 0; j < kPipe; j++) cur[j] = nxt[j];
-        }
-#pragma unroll
-        for (int j = 0; j < kPipe; j++) t[j & 3] += cur[j];
-        i = full;
-    }
-    for (; i < n; i++) t[i & 3] += e[i];
-    return ((t[0] + t[1]) + t[2]) + t[3];
-}
-
 // Quantize one f32 value per lane as part of a 32-lane Q8 block (lanes
 // 32k..32k+31 hold one block), exactly as Q8Vec::quantize_into does
 // (quant.rs:864-873). Every lane of the half-wave must call this.
@@ -538,25 +513,25 @@ static hipError_t gemv_launch(hipStream_t st, MatSet ms, size_t k, QuantAct x, i
 // Decode GEMV with the producer of its activation fused in front (M = 1).
 //
 // A decode step alternates a short serial producer (the residual add +
-// RMSNorm + quantization, or SiLU(gate) * up + quantization) with a GEMV that
+// RMSNorm + quantization, or the quantization of an f32 row) with a GEMV that
 // must wait for it. Run as two launches, the GEMV's weight fetch cannot start
 // until the producer ends. Here every workgroup issues the producer's loads
 // (L2-resident, a few KiB), then its weight loads, and computes the producer
 // while the weights are in flight: the serial RMS sum (dim dependent adds,
 // the reference order) overlaps the HBM round trip instead of preceding it.
 // The quantized row is built in LDS with the exact arithmetic of the
-// standalone kernels (k_add_rms_quant, k_silu_quant), so the results are
+// standalone kernels (k_add_rms_quant, k_quantize), so the results are
 // bit-identical to running those and then k_gemv. Workgroup 0 writes the
 // updated residual row to a second buffer (the other workgroups still read
 // the old one).
 struct GemvPro {
-    const float* a;  // PRO_NORM: residual row x; PRO_SILU: gate row
-    const float* b;  // PRO_NORM: the add into x (may be null); PRO_SILU: up row
+    const float* a;  // PRO_NORM: residual row x; PRO_QUANT: the f32 row
+    const float* b;  // PRO_NORM: the add into x (may be null)
     const float* w;  // PRO_NORM: norm weight
     float* x_out;    // PRO_NORM: x + add, written by workgroup 0 (may be null)
     float eps;
 };
-static constexpr int PRO_NORM = 1, PRO_SILU = 2, PRO_QUANT = 3;
+static constexpr int PRO_NORM = 1, PRO_QUANT = 3;
 
 template <int SEM, int PRO, int VPT>
 __global__ __launch_bounds__(256) void k_gemv_pro(MatSet ms, GemvPro pro, uint32_t K, uint32_t R,
@@ -610,7 +585,7 @@ __global__ __launch_bounds__(256) void k_gemv_pro(MatSet ms, GemvPro pro, uint32
 
     // 3. the producer, while the weights are in flight
     float4 o[VPT];
-    if (PRO == PRO_NORM) {
+    if constexpr (PRO == PRO_NORM) {
 #pragma unroll
         for (int u = 0; u < VPT; u++) {
             const uint32_t f = tid + 256 * u;
@@ -636,16 +611,10 @@ __global__ __launch_bounds__(256) void k_gemv_pro(MatSet ms, GemvPro pro, uint32
             const float4 v = va[u], wq = vw[u];
             o[u] = make_float4(wq.x * (scale * v.x), wq.y * (scale * v.y), wq.z * (scale * v.z), wq.w * (scale * v.w));
         }
-    } else if (PRO == PRO_QUANT) {
+    } else {
+        static_assert(PRO == PRO_QUANT, "producer kind");
 #pragma unroll
         for (int u = 0; u < VPT; u++) o[u] = va[u];
-    } else {
-#pragma unroll
-        for (int u = 0; u < VPT; u++) {  // silu (cpu.rs:708-710), then * up (cpu.rs:494-499)
-            const float4 g = va[u], up = vb[u];
-            o[u] = make_float4(div_rn(g.x, 1.0f + glibc_expf(-g.x)) * up.x, div_rn(g.y, 1.0f + glibc_expf(-g.y)) * up.y,
-                               div_rn(g.z, 1.0f + glibc_expf(-g.z)) * up.z, div_rn(g.w, 1.0f + glibc_expf(-g.w)) * up.w);
-        }
     }
     // Q8Vec::quantize_into (quant.rs:864-873) into LDS; a block is 8 threads
 #pragma unroll
@@ -745,7 +714,7 @@ static hipError_t gemv_pro_go(hipStream_t st, MatSet ms, size_t k, const GemvPro
 hipError_t launch_project_pro(hipStream_t st, int sem, const DevMatrix* const* w, float* const* y, int count,
                               int pro_kind, const float* a, const float* b, const float* norm_w, float* x_out,
                               float eps) {
-    if (count < 1 || count > 3 || pro_kind < PRO_NORM || pro_kind > PRO_QUANT) return hipErrorInvalidValue;
+    if (count < 1 || count > 3 || (pro_kind != PRO_NORM && pro_kind != PRO_QUANT)) return hipErrorInvalidValue;
     const size_t k = w[0]->k;
     if (k % 32 != 0 || k > 8192) return hipErrorInvalidValue;
     MatSet ms{};
@@ -767,10 +736,8 @@ hipError_t launch_project_pro(hipStream_t st, int sem, const DevMatrix* const* w
     }
     if (pro_kind == PRO_NORM) {
         KR_PRO_SEM(PRO_NORM)
-    } else if (pro_kind == PRO_QUANT) {
-        KR_PRO_SEM(PRO_QUANT)
     } else {
-        KR_PRO_SEM(PRO_SILU)
+        KR_PRO_SEM(PRO_QUANT)
     }
 #undef KR_PRO_SEM
     return hipErrorInvalidValue;
@@ -797,15 +764,17 @@ hipError_t launch_project_pro(hipStream_t st, int sem, const DevMatrix* const* w
 // rows are padded by 16 bytes so that the fragment reads of 32 consecutive
 // rows spread over all banks. One barrier per chunk.
 //
-// Two workgroup shapes, both 4 waves:
-//  * four partial sums (Q8_0, dot.rs:35-44): t[b & 3] are independent chains,
-//    so the 4 waves share one 32x32 output tile and wave j runs chain j over
-//    the blocks b = j, j+4, ...; the chains meet in LDS and are summed in the
-//    reference order ((t0 + t1) + t2) + t3. This is a 4-way split of K that
-//    changes no rounding. KC = 8.
-//  * one FMA chain (Q8_0x4, quant.rs:276-288): the chain is serial, so each
-//    wave owns its own 32x32 tile over all of K; the workgroup tile is 32x128
-//    and the 4 waves share the activation chunk. KC = 4.
+// Two workgroup shapes:
+//  * four partial sums (Q8_0, dot.rs:35-44, k_gemm_four16): t[b & 3] are
+//    independent chains, so they may run on different waves: a 32x32 output
+//    tile is split over 16 waves (four 16x16 sub-tiles x four chains); the
+//    chains meet in LDS and are summed in the reference order
+//    ((t0 + t1) + t2) + t3. This is a 4-way split of K that changes no
+//    rounding. KC = 8.
+//  * one FMA chain (Q8_0x4, quant.rs:276-288, k_gemm_chain, 4 waves): the
+//    chain is serial, so each wave owns its own 32x32 tile over all of K; the
+//    workgroup tile is 32x128 and the 4 waves share the activation chunk.
+//    KC = 4.
 //
 // Workgroups are numbered XCD-aware: the row tiles that share a column tile
 // of weights run on one XCD and share its L2.
@@ -877,112 +846,12 @@ __device__ __forceinline__ void gemm_pipeline(uint32_t nchunks, Load&& gload, St
     }
 }
 
-template <int SEM, bool DBG>
-__global__ __launch_bounds__(256, 2) void k_gemm_four(MatSet ms, QuantAct x, uint32_t M, uint32_t K,
-                                                      uint32_t mtiles, int32_t* __restrict__ dbg) {
-    constexpr int KC = 8, ROW = KC * 32 + 16, NS = kGemmStages;
-    __shared__ __align__(16) int8_t sA[2][32 * ROW];
-    __shared__ __align__(16) int8_t sB[2][32 * ROW];
-    __shared__ __align__(16) float sX[2][KC * 32];  // [block][row]
-    __shared__ __align__(16) float sW[2][KC * 32];  // [block][col]
-    const uint32_t nb = K >> 5, nchunks = (nb + KC - 1) / KC;
-    const GemmPos p = gemm_pos(ms, mtiles, 32);
-    const int8_t* __restrict__ W = ms.q[p.mi];
-    const void* __restrict__ WS = ms.s[p.mi];
-    const uint32_t N = ms.n[p.mi];
-    const uint32_t tid = threadIdx.x, lane = tid & 63;
-    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: block checks branch on SGPRs
-    const uint32_t r = lane & 31, half = lane >> 5;
-
-    // loader map: operand pieces (row tid/16 and tid/16 + 16, 16-byte column
-    // tid%16), scale entries (row or column tid/8, block tid%8). Rows past M
-    // or N read the last row; their outputs are never stored.
-    const uint32_t lr = tid >> 4, lc = (tid & 15) * 16, sr = tid >> 3, sb = tid & 7;
-    const int8_t* ga0 = x.q + (size_t)min(p.m0 + lr, M - 1) * K;
-    const int8_t* ga1 = x.q + (size_t)min(p.m0 + lr + 16, M - 1) * K;
-    const int8_t* gb0 = W + (size_t)min(p.n0 + lr, N - 1) * K;
-    const int8_t* gb1 = W + (size_t)min(p.n0 + lr + 16, N - 1) * K;
-    const float* gx = x.s + (size_t)min(p.m0 + sr, M - 1) * nb;
-    const size_t gw = (size_t)min(p.n0 + sr, N - 1) * nb;
-    constexpr bool WF16 = SEM == SEM_FOUR_PARTIALS_F16;
-
-    struct Stage {
-        v4i a0, a1, b0, b1;
-        float xs;
-        uint32_t ws;
-    };
-    auto gload = [&](Stage& st, uint32_t c) {
-        c = c < nchunks ? c : nchunks - 1;
-        const uint32_t col = min(c * KC * 32 + lc, K - 16);  // past the row end: a piece no block uses
-        st.a0 = *(const v4i*)(ga0 + col), st.a1 = *(const v4i*)(ga1 + col);
-        st.b0 = *(const v4i*)(gb0 + col), st.b1 = *(const v4i*)(gb1 + col);
-        const uint32_t blk = min(c * KC + sb, nb - 1);
-        st.xs = gx[blk];
-        st.ws = scale_bits(WF16, WS, gw + blk);
-    };
-    auto lstore = [&](const Stage& st, int buf) {
-        *(v4i*)(sA[buf] + lr * ROW + lc) = st.a0, *(v4i*)(sA[buf] + (lr + 16) * ROW + lc) = st.a1;
-        *(v4i*)(sB[buf] + lr * ROW + lc) = st.b0, *(v4i*)(sB[buf] + (lr + 16) * ROW + lc) = st.b1;
-        sX[buf][sb * 32 + sr] = st.xs;
-        sW[buf][sb * 32 + sr] = scale_value(WF16, st.ws);
-    };
-
-    const v16i zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-    float t[16];
-#pragma unroll
-    for (int v = 0; v < 16; v++) t[v] = 0.0f;
-    // wave j: blocks j and j + 4 of each chunk, i.e. chain t[j] in order
-    auto compute = [&](int buf, uint32_t c) {
-#pragma unroll
-        for (int i = 0; i < KC / 4; i++) {
-            const uint32_t blk = wave + 4 * i, b = c * KC + blk;
-            if (b >= nb) break;
-            const v4i a = *(const v4i*)(sA[buf] + r * ROW + blk * 32 + 16 * half);
-            const v4i bq = *(const v4i*)(sB[buf] + r * ROW + blk * 32 + 16 * half);
-            const v16i d = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bq, zero, 0, 0, 0);
-            const float w = sW[buf][blk * 32 + r];
-            float xs[16];
-            gemm_row_scales(xs, sX[buf] + blk * 32 + 4 * half);
-            if (DBG && p.n0 + r < N) {
-#pragma unroll
-                for (int v = 0; v < 16; v++) {
-                    const uint32_t m = p.m0 + 8 * (v >> 2) + 4 * half + (v & 3);
-                    if (m < M) dbg[((size_t)m * N + p.n0 + r) * nb + b] = d[v];
-                }
-            }
-            // dot.rs: t[b & 3] += (sa * sb) * (isum as f32), with sa the weight scale
-#pragma unroll
-            for (int v = 0; v < 16; v++) t[v] += (w * xs[v]) * (float)d[v];
-        }
-    };
-
-    gemm_pipeline<NS, Stage>(nchunks, gload, lstore, compute);
-
-    float* part = (float*)&sA[0][0];  // [4 waves][16][64], after the last barrier
-#pragma unroll
-    for (int v = 0; v < 16; v++) part[(wave * 16 + v) * 64 + lane] = t[v];
-    __syncthreads();
-    float* Y = ms.y[p.mi];
-    const uint32_t ld = ms.ld[p.mi];
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const uint32_t o = tid + 256 * i;  // (v, lane)
-        const uint32_t v = o >> 6, l = o & 63;
-        const uint32_t m = p.m0 + 8 * (v >> 2) + 4 * (l >> 5) + (v & 3), n = p.n0 + (l & 31);
-        if (m >= M || n >= N) continue;
-        const float sum = ((part[(0 * 16 + v) * 64 + l] + part[(1 * 16 + v) * 64 + l]) + part[(2 * 16 + v) * 64 + l]) +
-                          part[(3 * 16 + v) * 64 + l];
-        Y[(size_t)m * ld + n] = sum;
-    }
-}
-
-// Q8_0 GEMM for few rows (the 128-row prefill): the same four partial sums
-// as k_gemm_four, on 16x16x32 int8 MFMA. A 32x32 output tile is four 16x16
-// sub-tiles; 16 waves take (sub-tile, partial sum j) each, so a tile keeps 16
-// independent chains in flight (4 waves per SIMD) where 32x32 MFMAs leave one
-// chain per SIMD with every LDS and MFMA latency on its critical path. The
-// operand staging (A and B chunks of KC blocks through double-buffered,
-// padded LDS) and the global traffic are those of k_gemm_four.
+// Q8_0 GEMM: the four partial sums on 16x16x32 int8 MFMA. A 32x32 output
+// tile is four 16x16 sub-tiles; 16 waves take (sub-tile, partial sum j)
+// each, so a tile keeps 16 independent chains in flight (4 waves per SIMD)
+// where 32x32 MFMAs with one wave per chain would leave one chain per SIMD
+// with every LDS and MFMA latency on its critical path. Operands are staged
+// as A and B chunks of KC blocks through double-buffered, padded LDS.
 //
 // 16x16x32 operand map: lane l feeds row (col) l % 16 of the A (B) tile with
 // bytes 8 * (l / 16) .. +8 of the block, the same byte map for both; its
@@ -2046,25 +1915,26 @@ hipError_t launch_attention_split(hipStream_t st, const float* q, const float* k
 // and per output dim the serial sum over positions of p * v.
 //
 // Workgroup = (G query heads of one KV head, block of R rows), 8 waves; a
-// (row, head) pair is "rg" = r * G + j. Each K tile (64 positions) goes to LDS once and serves
-// every pair of the block: lane = position, and each wave computes the
-// scores of its RPW pairs, reading q by broadcast. The scores stay in LDS;
-// each wave runs the max, exp, serial sum (one lane per pair) and division
-// of its own pairs. Then each V tile goes to LDS once and lane (pair, 2 dims)
+// (row, head) pair is "rg" = r * G + j. Each K tile (64 positions) goes to
+// LDS once and serves every pair of the block: lane = (pair, a few
+// positions), so a wave's K and q reads hit a few addresses each (LDS
+// broadcasts). The scores stay in LDS; after the last tile each wave runs the
+// max, exp, serial sum (one lane per pair) and division of its RPW pairs.
+// Then each V tile goes to LDS once and lane (pair, 2 dims)
 // runs two independent position-order chains. Row r of the block attends to
 // its first count_r positions (its window); the block's windows must agree
 // on att_start and the shared range (checked on the host), so window index i
 // is the same cache slot for every row.
-// LDS: q [8 RPW][HS] | scores [RG][scs] | tile [64][HS + 4].
-template <int HS>
+// LDS: q [8 RPW][HS + 4] | scores [RG][scs] | tile [64][HS + 4].
+template <int HS, int NWAVES>
 struct AttnRowsShape {
-    static constexpr uint32_t NW = 8, NT = 64 * NW;  // waves, threads
+    static constexpr uint32_t NW = NWAVES, NT = 64 * NW;  // waves, threads
     static constexpr uint32_t LPR = HS / 2;          // lanes per pair in the V phase (2 dims each)
     static constexpr uint32_t RPW = 64 / LPR;        // pairs per wave
     static constexpr uint32_t T = 64, KS = HS + 4;
 };
-template <int G, int HS>
-__global__ __launch_bounds__(512) void k_attn_rows(const float* __restrict__ q, float* __restrict__ out,
+template <int G, int HS, int NWAVES>
+__global__ __launch_bounds__(64 * NWAVES) void k_attn_rows(const float* __restrict__ q, float* __restrict__ out,
                                                    float* __restrict__ att, const float* __restrict__ kc,
                                                    const float* __restrict__ vc, size_t loff,
                                                    const DevWindow* __restrict__ windows, uint32_t n_rows,
@@ -2072,12 +1942,12 @@ __global__ __launch_bounds__(512) void k_attn_rows(const float* __restrict__ q, 
                                                    uint32_t seq_len, float scale, uint32_t scs,
                                                    int8_t* __restrict__ qo, float* __restrict__ so,
                                                    uint16_t* __restrict__ ho) {
-    using Sh = AttnRowsShape<HS>;
+    using Sh = AttnRowsShape<HS, NWAVES>;
     constexpr uint32_t NW = Sh::NW, NT = Sh::NT, LPR = Sh::LPR, RPW = Sh::RPW, T = Sh::T, KS = Sh::KS, F = HS / 4;
-    constexpr uint32_t R = NW * RPW / G, RG = R * G;
+    constexpr uint32_t R = NW * RPW / G, RG = R * G, QS = HS + 4;
     extern __shared__ __align__(16) float sm[];
-    float* qs = sm;                   // [NW RPW][HS]
-    float* sc = qs + NW * RPW * HS;   // [RG][scs]
+    float* qs = sm;                   // [NW RPW][QS]
+    float* sc = qs + NW * RPW * QS;   // [RG][scs]
     float* kt = sc + RG * scs;        // [T][KS]
     __shared__ uint32_t s_cnt[NW * RPW];
     __shared__ float s_sum[NW * RPW];
@@ -2096,7 +1966,7 @@ __global__ __launch_bounds__(512) void k_attn_rows(const float* __restrict__ q, 
         const uint32_t rg = t / F, u = t - rg * F, r = rg / G, j = rg - r * G;
         float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         if (rg < RG && r < nr) v = *(const float4*)(q + (size_t)(r0 + r) * width + (size_t)(h0 + j) * HS + 4 * u);
-        *(float4*)(qs + rg * HS + 4 * u) = v;
+        *(float4*)(qs + rg * QS + 4 * u) = v;
     }
     if (tid < NW * RPW) {
         const uint32_t r = tid / G;
@@ -2119,7 +1989,7 @@ __global__ __launch_bounds__(512) void k_attn_rows(const float* __restrict__ q, 
     // row), so the registers are always defined and stay registers
     auto tile_len = [&](uint32_t i0) { return i0 < cmax ? min(T, cmax - i0) : 0u; };
 
-    // 1. scores: lane = position of the tile, wave = its RPW pairs
+    // 1. scores of every (pair, position) of each K tile
     #pragma unroll
     for (uint32_t k = 0; k < PT; k++) {
         const uint32_t f = tid + NT * k, rr = f / F, u = f - rr * F, rc = rr < (tile_len(0)) ? rr : (tile_len(0)) - 1;
@@ -2146,17 +2016,19 @@ __global__ __launch_bounds__(512) void k_attn_rows(const float* __restrict__ q, 
                 pre[k] = *(const v4f*)(vbase + (size_t)win_slot(w0, n_shared, (0) + rc) * kv_dim + 4 * u);
             }
         }
-        if (lane < nt) {
-            float a[RPW][4];
+        {  // lane (pair r, positions p0, p0 + PP, ...): K and q reads are few-address broadcasts
+            constexpr uint32_t RGP = NW * RPW, PP = NT / RGP, SPL = T / PP;
+            const uint32_t r = tid % RGP, p0 = tid / RGP;
+            const float* qr = qs + r * QS;
+            float a[SPL][4];
 #pragma unroll
-            for (uint32_t k = 0; k < RPW; k++) a[k][0] = a[k][1] = a[k][2] = a[k][3] = 0.0f;
-            const float* kr = kt + lane * KS;
+            for (uint32_t k = 0; k < SPL; k++) a[k][0] = a[k][1] = a[k][2] = a[k][3] = 0.0f;
 #pragma unroll 4
             for (uint32_t u = 0; u < F; u++) {
-                const float4 kk = *(const float4*)(kr + 4 * u);
+                const float4 qq = *(const float4*)(qr + 4 * u);
 #pragma unroll
-                for (uint32_t k = 0; k < RPW; k++) {
-                    const float4 qq = *(const float4*)(qs + (wave * RPW + k) * HS + 4 * u);
+                for (uint32_t k = 0; k < SPL; k++) {
+                    const float4 kk = *(const float4*)(kt + (p0 + k * PP) * KS + 4 * u);
                     a[k][0] = __builtin_fmaf(qq.x, kk.x, a[k][0]);
                     a[k][1] = __builtin_fmaf(qq.y, kk.y, a[k][1]);
                     a[k][2] = __builtin_fmaf(qq.z, kk.z, a[k][2]);
@@ -2164,10 +2036,11 @@ __global__ __launch_bounds__(512) void k_attn_rows(const float* __restrict__ q, 
                 }
             }
 #pragma unroll
-            for (uint32_t k = 0; k < RPW; k++) {
-                const uint32_t rg = wave * RPW + k;
+            for (uint32_t k = 0; k < SPL; k++) {
+                const uint32_t pos = p0 + k * PP;
                 // dot.rs:360: (acc0 + acc1) + (acc2 + acc3), then * scale (cpu.rs:609)
-                if (rg < RG && i0 + lane < s_cnt[rg]) sc[rg * scs + i0 + lane] = ((a[k][0] + a[k][1]) + (a[k][2] + a[k][3])) * scale;
+                if (r < RG && pos < nt && i0 + pos < s_cnt[r])
+                    sc[r * scs + i0 + pos] = ((a[k][0] + a[k][1]) + (a[k][2] + a[k][3])) * scale;
             }
         }
         lds_barrier();  // the tile is consumed
@@ -2276,9 +2149,26 @@ __global__ __launch_bounds__(512) void k_attn_rows(const float* __restrict__ q, 
 }
 
 // LDS bytes of k_attn_rows for windows of up to max_count positions
-static size_t attn_rows_lds(size_t G, size_t hs, size_t max_count) {
-    const size_t rpw = 128 / hs, rg = (8 * rpw / G) * G, scs = (max_count + 3) & ~(size_t)3;
-    return (8 * rpw * hs + rg * scs + 64 * (hs + 4)) * sizeof(float);
+static size_t attn_rows_lds(size_t G, size_t hs, size_t max_count, size_t nw) {
+    const size_t rpw = 128 / hs, rg = (nw * rpw / G) * G, scs = (max_count + 3) & ~(size_t)3;
+    return (nw * rpw * (hs + 4) + rg * scs + 64 * (hs + 4)) * sizeof(float);
+}
+// Waves per k_attn_rows workgroup: 8 while two workgroups fit a CU's LDS,
+// else 4 (half the rows per block) if that lets two fit, else whichever fits
+// at all (8 first), else 0 (the kernel does not apply).
+static size_t attn_rows_waves(size_t G, size_t hs, size_t max_count) {
+    if (hs != 32 && hs != 64 && hs != 128) return 0;
+    const bool four = 4 * (128 / hs) / G >= 1;  // at least one row per block
+    if (attn_rows_lds(G, hs, max_count, 8) <= 80 * 1024) return 8;
+    if (four && attn_rows_lds(G, hs, max_count, 4) <= 80 * 1024) return 4;
+    if (attn_rows_lds(G, hs, max_count, 8) <= kAttnLds) return 8;
+    if (four && attn_rows_lds(G, hs, max_count, 4) <= kAttnLds) return 4;
+    return 0;
+}
+static size_t attn_rows_group(size_t kv_mul) {  // query heads per workgroup
+    for (size_t g : {8, 4, 3, 2})
+        if (kv_mul % g == 0) return g;
+    return 1;
 }
 
 // Softmax and V sums of the many-row split attention: workgroup = (KV head,
@@ -2300,7 +2190,7 @@ __global__ __launch_bounds__(G * HS < 64 ? 64 : G * HS) void k_attn_softmax_v_ro
     __shared__ float s_sum[G];
     __shared__ float s_max[G];
     __shared__ uint64_t etab[32];
-    const uint32_t tid = threadIdx.x, lane = tid & 63, hk = blockIdx.x, row = blockIdx.y;
+    const uint32_t tid = threadIdx.x, hk = blockIdx.x, row = blockIdx.y;
     const DevWindow w = win[row];
     const uint32_t n_shared = w.shared_end - w.shared_start;
     const uint32_t count = n_shared + w.slot - w.att_start + 1, nch = (count + 63) / 64;
@@ -2424,15 +2314,10 @@ hipError_t launch_attention_split_rows(hipStream_t st, const float* q, float* ou
 
 // Whether a block of rows can run k_attn_rows: its windows share att_start
 // and the shared range (prefill), checked per block of the kernel's R rows.
-bool attention_rows_uniform(const DevWindow* w, size_t n_rows, size_t kv_mul, size_t hs) {
-    if (n_rows < 2 || (hs != 32 && hs != 64 && hs != 128)) return false;
-    size_t G = 1;
-    for (size_t g : {8, 4, 3, 2})
-        if (kv_mul % g == 0) {
-            G = g;
-            break;
-        }
-    const size_t R = (8 * (128 / hs)) / G;
+bool attention_rows_uniform(const DevWindow* w, size_t n_rows, size_t max_count, size_t kv_mul, size_t hs) {
+    const size_t G = attn_rows_group(kv_mul), nw = attn_rows_waves(G, hs, max_count);
+    if (n_rows < 2 || nw == 0) return false;
+    const size_t R = (nw * (128 / hs)) / G;
     for (size_t r = 0; r < n_rows; r++) {
         const DevWindow& a = w[r - r % R];
         if (a.att_start != w[r].att_start || a.shared_start != w[r].shared_start || a.shared_end != w[r].shared_end)
@@ -2485,47 +2370,40 @@ hipError_t launch_attention(hipStream_t st, const float* q, float* out, float* a
     if (hs == 0 || hs > 256 || hs % 4 != 0 || kv_mul == 0 || n_heads % kv_mul != 0) return hipErrorInvalidValue;
     if (qo && hs % 32 != 0) return hipErrorInvalidValue;
     if (max_count > seq_len) max_count = seq_len;
-    if (host_windows && n_rows >= 2 && (hs == 32 || hs == 64 || hs == 128)) {
-        // many rows: k_attn_rows, when every block of R rows shares its window layout
-        size_t G = 1;
-        for (size_t g : {8, 4, 3, 2})
-            if (kv_mul % g == 0) {
-                G = g;
-                break;
-            }
-        const size_t R = (8 * (128 / hs)) / G;  // rows per block: AttnRowsShape
-        bool uniform = R >= 1 && attn_rows_lds(G, hs, max_count) <= kAttnLds;
-        for (size_t r = 0; uniform && r < n_rows; r++) {
-            const DevWindow& a = host_windows[r - r % R];
-            const DevWindow& b = host_windows[r];
-            uniform = a.att_start == b.att_start && a.shared_start == b.shared_start && a.shared_end == b.shared_end;
-        }
-        if (uniform) {
-            const size_t lds = attn_rows_lds(G, hs, max_count);
-            const uint32_t scs = (uint32_t)((max_count + 3) & ~(size_t)3);
-            const dim3 grid((unsigned)(n_heads / G), (unsigned)((n_rows + R - 1) / R));
-#define KR_ATTN_ROWS(g, h)                                                                                    \
-    hipLaunchKernelGGL((k_attn_rows<g, h>), grid, dim3(512), lds, st, q, out, att, kc, vc,                    \
+    if (host_windows && attention_rows_uniform(host_windows, n_rows, max_count, kv_mul, hs)) {
+        // many rows whose blocks share a window layout: k_attn_rows
+        const size_t G = attn_rows_group(kv_mul), nw = attn_rows_waves(G, hs, max_count);
+        const size_t R = (nw * (128 / hs)) / G;  // rows per block: AttnRowsShape
+        const size_t lds = attn_rows_lds(G, hs, max_count, nw);
+        const uint32_t scs = (uint32_t)((max_count + 3) & ~(size_t)3);
+        const dim3 grid((unsigned)(n_heads / G), (unsigned)((n_rows + R - 1) / R));
+#define KR_ATTN_ROWS(g, h, w)                                                                                 \
+    hipLaunchKernelGGL((k_attn_rows<g, h, w>), grid, dim3(64 * w), lds, st, q, out, att, kc, vc,              \
                        layer * seq_len * kv_dim, windows, (uint32_t)n_rows, (uint32_t)n_heads, (uint32_t)kv_mul, \
                        (uint32_t)kv_dim, (uint32_t)seq_len, scale, scs, qo, so, ho)
+#define KR_ATTN_ROWS_W(g, h)         \
+    if (nw == 8)                     \
+        KR_ATTN_ROWS(g, h, 8);       \
+    else                             \
+        KR_ATTN_ROWS(g, h, 4);
 #define KR_ATTN_ROWS_G(g)          \
     if (hs == 32)                  \
-        KR_ATTN_ROWS(g, 32);       \
+        KR_ATTN_ROWS_W(g, 32)      \
     else if (hs == 64)             \
-        KR_ATTN_ROWS(g, 64);       \
+        KR_ATTN_ROWS_W(g, 64)      \
     else                           \
-        KR_ATTN_ROWS(g, 128);
-            switch (G) {
-                case 8: KR_ATTN_ROWS_G(8) break;
-                case 4: KR_ATTN_ROWS_G(4) break;
-                case 3: KR_ATTN_ROWS_G(3) break;
-                case 2: KR_ATTN_ROWS_G(2) break;
-                default: KR_ATTN_ROWS_G(1) break;
-            }
-#undef KR_ATTN_ROWS_G
-#undef KR_ATTN_ROWS
-            return hipGetLastError();
+        KR_ATTN_ROWS_W(g, 128)
+        switch (G) {
+            case 8: KR_ATTN_ROWS_G(8) break;
+            case 4: KR_ATTN_ROWS_G(4) break;
+            case 3: KR_ATTN_ROWS_G(3) break;
+            case 2: KR_ATTN_ROWS_G(2) break;
+            default: KR_ATTN_ROWS_G(1) break;
         }
+#undef KR_ATTN_ROWS_G
+#undef KR_ATTN_ROWS_W
+#undef KR_ATTN_ROWS
+        return hipGetLastError();
     }
     {
         // heads per workgroup: the largest of 8, 4, 3, 2, 1 dividing kv_mul

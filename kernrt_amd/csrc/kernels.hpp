@@ -56,8 +56,7 @@ hipError_t launch_rope_kv(hipStream_t st, float* q, float* k, const float* v, si
 // y[m*ldy + n] for m < rows. Uses the GEMV path (rows <= 4) or the MFMA GEMM.
 // One decode row (M = 1) of 1-3 projections with the producer of their input
 // fused in front: pro_kind 1 = x (+= add) -> rms_norm(w, eps) -> Q8 (the
-// updated x row goes to x_out when non-null), 2 = silu(a) * b -> Q8,
-// 3 = Q8 of the f32 row a.
+// updated x row goes to x_out when non-null), 3 = Q8 of the f32 row a.
 hipError_t launch_project_pro(hipStream_t st, int sem, const DevMatrix* const* w, float* const* y, int count,
                               int pro_kind, const float* a, const float* b, const float* norm_w, float* x_out,
                               float eps);
@@ -99,7 +98,8 @@ hipError_t launch_attention_split_rows(hipStream_t st, const float* q, float* ou
                                        size_t seq_len, float scale, float* scratch);
 // whether the rows' windows let launch_attention use its block-of-rows
 // (prefill) kernel: each block of rows shares att_start and the shared range
-bool attention_rows_uniform(const DevWindow* host_windows, size_t n_rows, size_t kv_mul, size_t hs);
+bool attention_rows_uniform(const DevWindow* host_windows, size_t n_rows, size_t max_count, size_t kv_mul,
+                            size_t hs);
 hipError_t launch_add(hipStream_t st, float* dst, const float* src, size_t n);
 hipError_t launch_mul(hipStream_t st, float* out, const float* a, const float* b, size_t n,
                       int sequential);

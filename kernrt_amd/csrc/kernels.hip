@@ -107,13 +107,34 @@ __device__ __forceinline__ float seq_fma(const float2* __restrict__ e, uint32_t 
     return slot;
 }
 
+// NaN-ignoring max across lanes with DPP (a few cycles per step, no LDS
+// round trip as with __shfl_xor). Max is order-free, so every grouping gives
+// the same result.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float dpp_max_step(float v) {
+    return fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, ROWS, 0xf,
+                                                               false)));
+}
+// max over each aligned group of 8 / 16 / 32 lanes, in every lane of the group
+__device__ __forceinline__ float group_max8(float v) {
+    v = dpp_max_step<0xB1, 0xf>(v);      // quad_perm [1,0,3,2]
+    v = dpp_max_step<0x4E, 0xf>(v);      // quad_perm [2,3,0,1]
+    return dpp_max_step<0x141, 0xf>(v);  // row_half_mirror
+}
+__device__ __forceinline__ float group_max16(float v) { return dpp_max_step<0x140, 0xf>(group_max8(v)); }  // row_mirror
+__device__ __forceinline__ float group_max32(float v) {
+    v = group_max16(v);  // then lane ^ 16 within the 32-lane group (ds_swizzle bit mode)
+    return fmaxf(v, __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F)));
+}
+// a + (a of the neighbouring lane l ^ 1): exact integer sum of a lane pair
+__device__ __forceinline__ int lane_pair_sum(int a) { return a + __builtin_amdgcn_mov_dpp(a, 0xB1, 0xf, 0xf, false); }
+
 // Quantize one f32 value per lane as part of a 32-lane Q8 block (lanes
 // 32k..32k+31 hold one block), exactly as Q8Vec::quantize_into does
 // (quant.rs:864-873). Every lane of the half-wave must call this.
 __device__ __forceinline__ void quant_lane(float v, bool valid, int8_t* q, float* s, uint16_t* h) {
     float m = fmaxf(0.0f, fabsf(v));
-#pragma unroll
-    for (int off = 16; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 32));
+    m = group_max32(m);
     float d = div_rn(m, 127.0f);
     float inv = d > 0.0f ? div_rn(1.0f, d) : 0.0f;
     if (valid) {
@@ -141,8 +162,7 @@ __global__ __launch_bounds__(256) void k_quantize(const float* __restrict__ x, s
     size_t row = valid ? blk / nb : 0, b = valid ? blk % nb : 0;
     float v = valid ? x[row * x_stride + b * 32 + lane] : 0.0f;
     float m = fmaxf(0.0f, fabsf(v));  // fold(0.0, max(|v|)), NaN-ignoring
-#pragma unroll
-    for (int off = 16; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 32));
+    m = group_max32(m);
     float d = div_rn(m, 127.0f);
     float inv = d > 0.0f ? div_rn(1.0f, d) : 0.0f;
     if (valid) {
@@ -346,11 +366,6 @@ __device__ __forceinline__ float quad_bcast(float v) {
 // NaN-ignoring max over the 64 lanes of a wave, returned to every lane: DPP
 // swaps within quads, half-rows and rows, then row broadcasts 15 and 31 into
 // lane 63 (a few cycles each, no LDS round trip). Max is order-free.
-template <int CTRL, int ROWS>
-__device__ __forceinline__ float dpp_max_step(float v) {
-    return fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, ROWS, 0xf,
-                                                               false)));
-}
 __device__ __forceinline__ float wave_max(float v) {
     v = dpp_max_step<0xB1, 0xf>(v);   // quad_perm [1,0,3,2]
     v = dpp_max_step<0x4E, 0xf>(v);   // quad_perm [2,3,0,1]
@@ -417,7 +432,7 @@ __global__ __launch_bounds__(256) void k_gemv(MatSet ms, QuantAct x, uint32_t K,
             acc = __builtin_amdgcn_sdot4(wv[u].y, xv[u][m].y, acc, false);
             acc = __builtin_amdgcn_sdot4(wv[u].z, xv[u][m].z, acc, false);
             acc = __builtin_amdgcn_sdot4(wv[u].w, xv[u][m].w, acc, false);
-            const int isum = acc + __shfl_xor(acc, 1);
+            const int isum = lane_pair_sum(acc);
             // every lane forms the operand and stores it (lanes that own no
             // block to a dummy slot): with no branch around the use, the
             // scale loads stay at the top of the kernel
@@ -623,8 +638,7 @@ __global__ __launch_bounds__(256) void k_gemv_pro(MatSet ms, GemvPro pro, uint32
         if (f < n4) {  // K % 32 == 0: the 8 threads of a block are all in range or all out
             const float4 v = o[u];
             float m = fmaxf(fmaxf(fmaxf(fmaxf(0.0f, fabsf(v.x)), fabsf(v.y)), fabsf(v.z)), fabsf(v.w));
-#pragma unroll
-            for (int off = 4; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 8));
+            m = group_max8(m);
             const float d = div_rn(m, 127.0f);
             const float inv = d > 0.0f ? div_rn(1.0f, d) : 0.0f;
             char4 qq;
@@ -655,7 +669,7 @@ __global__ __launch_bounds__(256) void k_gemv_pro(MatSet ms, GemvPro pro, uint32
         acc = __builtin_amdgcn_sdot4(wv[u].y, xv.y, acc, false);
         acc = __builtin_amdgcn_sdot4(wv[u].z, xv.z, acc, false);
         acc = __builtin_amdgcn_sdot4(wv[u].w, xv.w, acc, false);
-        const int isum = acc + __shfl_xor(acc, 1);
+        const int isum = lane_pair_sum(acc);
         const bool own = valid && even;
         const uint32_t base = r * per;
         if (SEM == SEM_FMA_CHAIN) {
@@ -2131,8 +2145,7 @@ __global__ __launch_bounds__(64 * NWAVES) void k_attn_rows(const float* __restri
     if (live) *(v2f*)(out + o) = v2f{o0, o1};
     if (qo) {  // head outputs are whole Q8 blocks (HS % 32 == 0): quantize for o_proj (quant.rs:864-873)
         float m = fmaxf(fmaxf(0.0f, fabsf(o0)), fabsf(o1));
-#pragma unroll
-        for (int off = 8; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 16));
+        m = group_max16(m);
         const float d = div_rn(m, 127.0f);
         const float inv = d > 0.0f ? div_rn(1.0f, d) : 0.0f;
         if (live) {
@@ -2528,8 +2541,7 @@ __global__ __launch_bounds__(256) void k_add_rms_quant(float* __restrict__ x, co
             ((float4*)(out + row * dim))[f] = o;
             // Q8Vec::quantize_into (quant.rs:864-873) on the block of 8 threads
             float m = fmaxf(fmaxf(fmaxf(fmaxf(0.0f, fabsf(o.x)), fabsf(o.y)), fabsf(o.z)), fabsf(o.w));
-#pragma unroll
-            for (int off = 4; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 8));
+            m = group_max8(m);
             const float d = div_rn(m, 127.0f);
             const float inv = d > 0.0f ? div_rn(1.0f, d) : 0.0f;
             char4 qq;

@@ -27,84 +27,56 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ float div_rn(float a, float b) { return (float)((double)a / (double)b); }
 __device__ __forceinline__ float sqrt_rn(float a) { return (float)__builtin_sqrt((double)a); }
 
-// Serial f32 chains, software-pipelined: operands are fetched kPipe elements
-// ahead into registers so each dependent add waits only on the previous add,
-// never on a memory read. The accumulation order is exactly left to right.
+// Serial f32 chains, software-pipelined: operands are fetched in batches of
+// kPipe elements, the next batch's loads issued before the current batch's
+// dependent operations, so each step waits only on the previous one, never
+// on a memory read. The last batch may be partial: its loads are clamped to
+// the last element (n is uniform across the lanes that call these) and only
+// its first n % kPipe steps are applied. The accumulation order is exactly
+// left to right.
 static constexpr int kPipe = 16;
+
+template <typename T, typename Load, typename Op>
+__device__ __forceinline__ float seq_chain(float acc, uint32_t n, Load&& load, Op&& op) {
+    if (n == 0) return acc;
+    const uint32_t nbt = (n + kPipe - 1) / kPipe;
+    auto fetch = [&](T(&r)[kPipe], uint32_t b) {
+#pragma unroll
+        for (int j = 0; j < kPipe; j++) r[j] = load(min(b * kPipe + j, n - 1));
+    };
+    T cur[kPipe];
+    fetch(cur, 0);
+    for (uint32_t b = 1; b < nbt; b++) {
+        T nxt[kPipe];
+        fetch(nxt, b);
+#pragma unroll
+        for (int j = 0; j < kPipe; j++) acc = op(acc, cur[j]);
+#pragma unroll
+        for (int j = 0; j < kPipe; j++) cur[j] = nxt[j];
+    }
+    const uint32_t last = n - (nbt - 1) * kPipe;  // 1..kPipe
+#pragma unroll
+    for (int j = 0; j < kPipe; j++)
+        if ((uint32_t)j < last) acc = op(acc, cur[j]);
+    return acc;
+}
 
 // ((0 + a[0]) + a[1]) + ... + a[n-1]
 __device__ __forceinline__ float seq_sum(const float* __restrict__ a, uint32_t n) {
-    float s = 0.0f;
-    uint32_t full = n & ~(uint32_t)(kPipe - 1), i = 0;
-    if (full) {
-        float cur[kPipe];
-#pragma unroll
-        for (int j = 0; j < kPipe; j++) cur[j] = a[j];
-        for (i = kPipe; i < full; i += kPipe) {
-            float nxt[kPipe];
-#pragma unroll
-            for (int j = 0; j < kPipe; j++) nxt[j] = a[i + j];
-#pragma unroll
-            for (int j = 0; j < kPipe; j++) s += cur[j];
-#pragma unroll
-            for (int j = 0; j < kPipe; j++) cur[j] = nxt[j];
-        }
-#pragma unroll
-        for (int j = 0; j < kPipe; j++) s += cur[j];
-        i = full;
-    }
-    for (; i < n; i++) s += a[i];
-    return s;
+    return seq_chain<float>(0.0f, n, [&](uint32_t i) { return a[i]; }, [](float s, float v) { return s + v; });
 }
 
 // acc += p[j] * t[j * stride] for j in order (mul then add, unfused)
 __device__ __forceinline__ float seq_dot(float acc, const float* __restrict__ p, const float* __restrict__ t,
                                          uint32_t stride, uint32_t n) {
-    uint32_t full = n & ~(uint32_t)(kPipe - 1), i = 0;
-    if (full) {
-        float cur[kPipe];
-#pragma unroll
-        for (int j = 0; j < kPipe; j++) cur[j] = p[j] * t[j * stride];
-        for (i = kPipe; i < full; i += kPipe) {
-            float nxt[kPipe];
-#pragma unroll
-            for (int j = 0; j < kPipe; j++) nxt[j] = p[i + j] * t[(i + j) * stride];
-#pragma unroll
-            for (int j = 0; j < kPipe; j++) acc += cur[j];
-#pragma unroll
-            for (int j = 0; j < kPipe; j++) cur[j] = nxt[j];
-        }
-#pragma unroll
-        for (int j = 0; j < kPipe; j++) acc += cur[j];
-        i = full;
-    }
-    for (; i < n; i++) acc += p[i] * t[i * stride];
-    return acc;
+    return seq_chain<float>(acc, n, [&](uint32_t i) { return p[i] * t[i * stride]; },
+                            [](float s, float v) { return s + v; });
 }
 
 // slot = fma(e[b].x, e[b].y, slot) for b in order (quant.rs:287)
 __device__ __forceinline__ float seq_fma(const float2* __restrict__ e, uint32_t n) {
-    float slot = 0.0f;
-    uint32_t full = n & ~(uint32_t)(kPipe - 1), i = 0;
-    if (full) {
-        float2 cur[kPipe];
-#pragma unroll
-        for (int j = 0; j < kPipe; j++) cur[j] = e[j];
-        for (i = kPipe; i < full; i += kPipe) {
-            float2 nxt[kPipe];
-#pragma unroll
-            for (int j = 0; j < kPipe; j++) nxt[j] = e[i + j];
-#pragma unroll
-            for (int j = 0; j < kPipe; j++) slot = __builtin_fmaf(cur[j].x, cur[j].y, slot);
-#pragma unroll
-            for (int j = 0; j < kPipe; j++) cur[j] = nxt[j];
-        }
-#pragma unroll
-        for (int j = 0; j < kPipe; j++) slot = __builtin_fmaf(cur[j].x, cur[j].y, slot);
-        i = full;
-    }
-    for (; i < n; i++) slot = __builtin_fmaf(e[i].x, e[i].y, slot);
-    return slot;
+    return seq_chain<float2>(0.0f, n, [&](uint32_t i) { return e[i]; },
+                             [](float s, float2 v) { return __builtin_fmaf(v.x, v.y, s); });
 }
 
 // NaN-ignoring max across lanes with DPP (a few cycles per step, no LDS

@@ -40,17 +40,34 @@ template <typename T, typename Load, typename Op>
 __device__ __forceinline__ float seq_chain(float acc, uint32_t n, Load&& load, Op&& op) {
     if (n == 0) return acc;
     const uint32_t nbt = (n + kPipe - 1) / kPipe;
-    auto fetch = [&](T(&r)[kPipe], uint32_t b) {
+    auto fetch = [&](T(&r)[kPipe], uint32_t b) {  // a whole batch: contiguous loads
+#pragma unroll
+        for (int j = 0; j < kPipe; j++) r[j] = load(b * kPipe + j);
+    };
+    auto fetch_last = [&](T(&r)[kPipe], uint32_t b) {
 #pragma unroll
         for (int j = 0; j < kPipe; j++) r[j] = load(min(b * kPipe + j, n - 1));
     };
+    auto apply = [&](const T(&r)[kPipe]) {
+#pragma unroll
+        for (int j = 0; j < kPipe; j++) acc = op(acc, r[j]);
+    };
     T cur[kPipe];
-    fetch(cur, 0);
-    for (uint32_t b = 1; b < nbt; b++) {
+    if (nbt == 1)
+        fetch_last(cur, 0);
+    else
+        fetch(cur, 0);
+    for (uint32_t b = 1; b + 1 < nbt; b++) {
         T nxt[kPipe];
         fetch(nxt, b);
+        apply(cur);
 #pragma unroll
-        for (int j = 0; j < kPipe; j++) acc = op(acc, cur[j]);
+        for (int j = 0; j < kPipe; j++) cur[j] = nxt[j];
+    }
+    if (nbt > 1) {
+        T nxt[kPipe];
+        fetch_last(nxt, nbt - 1);
+        apply(cur);
 #pragma unroll
         for (int j = 0; j < kPipe; j++) cur[j] = nxt[j];
     }
@@ -1122,7 +1139,7 @@ hipError_t launch_project(hipStream_t st, int sem, const DevMatrix& w, QuantAct 
 // are formed in parallel and one lane adds them in order.
 __global__ __launch_bounds__(256) void k_rms_norm(float* __restrict__ out, const float* __restrict__ x,
                                                   const float* __restrict__ w, uint32_t dim, float eps) {
-    extern __shared__ float sq[];
+    extern __shared__ __align__(16) float sq[];
     __shared__ float s_scale;
     const float* xr = x + (size_t)blockIdx.x * dim;
     float* orow = out + (size_t)blockIdx.x * dim;
@@ -1132,7 +1149,7 @@ __global__ __launch_bounds__(256) void k_rms_norm(float* __restrict__ out, const
     }
     __syncthreads();
     if (threadIdx.x == 0) {
-        float ss = seq_sum(sq, dim);
+        float ss = chain_sum(sq, dim);
         ss = div_rn(ss, (float)dim);
         ss += eps;
         s_scale = div_rn(1.0f, sqrt_rn(ss));

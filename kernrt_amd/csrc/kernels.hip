@@ -1910,6 +1910,55 @@ hipError_t launch_attention_split(hipStream_t st, const float* q, const float* k
     return hipGetLastError();
 }
 
+// o0 += p[i] * v[i * KS], o1 += p[i] * v[i * KS + 1] for i < n in position
+// order (each a rounded product, then a rounded add): p is a 16-byte aligned
+// LDS row, v an LDS tile with row stride KS. Batches of 8 positions, the
+// next batch's reads issued before the current batch's adds, so the chains
+// wait on the previous add rather than on LDS; the last n % 8 positions run
+// one at a time.
+template <uint32_t KS>
+__device__ __forceinline__ void attn_v_chain(const float* __restrict__ p, const float* __restrict__ v, uint32_t n,
+                                             float& o0, float& o1) {
+    typedef float v2f __attribute__((ext_vector_type(2)));
+    typedef float v4f __attribute__((ext_vector_type(4)));
+    struct Batch {
+        v4f pa, pb;
+        v2f vv[8];
+    };
+    auto ld = [&](Batch& b, uint32_t i) {
+        b.pa = *(const v4f*)(p + i), b.pb = *(const v4f*)(p + i + 4);
+#pragma unroll
+        for (int k = 0; k < 8; k++) b.vv[k] = *(const v2f*)(v + (i + k) * KS);
+    };
+    auto apply = [&](const Batch& b) {
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const float pk = k < 4 ? b.pa[k] : b.pb[k - 4];
+            o0 += pk * b.vv[k].x;
+            o1 += pk * b.vv[k].y;
+        }
+    };
+    uint32_t i = 0;
+    if (n >= 8) {
+        Batch cur;
+        ld(cur, 0);
+        for (; i + 16 <= n; i += 8) {
+            Batch nxt;
+            ld(nxt, i + 8);
+            apply(cur);
+            cur = nxt;
+        }
+        apply(cur);
+        i += 8;
+    }
+    for (; i < n; i++) {
+        const float pk = p[i];
+        const v2f vk = *(const v2f*)(v + i * KS);
+        o0 += pk * vk.x;
+        o1 += pk * vk.y;
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Attention for many rows whose windows map positions to the same cache slots
 // (prefill: every row of a sequence attends to a prefix of the same slots).
@@ -1917,18 +1966,19 @@ hipError_t launch_attention_split(hipStream_t st, const float* q, const float* k
 // scores, the softmax with its serial sum, the probabilities (left in `att`),
 // and per output dim the serial sum over positions of p * v.
 //
-// Workgroup = (G query heads of one KV head, block of R rows), 8 waves; a
-// (row, head) pair is "rg" = r * G + j. Each K tile (64 positions) goes to
-// LDS once and serves every pair of the block: lane = (pair, a few
-// positions), so a wave's K and q reads hit a few addresses each (LDS
-// broadcasts). The scores stay in LDS; after the last tile each wave runs the
-// max, exp, serial sum (one lane per pair) and division of its RPW pairs.
+// Workgroup = (G query heads of one KV head, block of R rows), 8 or 4 waves;
+// a (row, head) pair is "rg" = r * G + j, and wave w owns pairs
+// w RPW .. w RPW + RPW - 1. Each K tile (64 positions) goes to LDS once and
+// serves every pair of the block: lane = position, and the wave's q rows are
+// wave-uniform (scalar loads), so one LDS read of 4 K values feeds 4 FMAs per
+// pair. The scores stay in LDS; after the last tile each wave runs the max,
+// exp, serial sum (one lane per pair) and division of its RPW pairs.
 // Then each V tile goes to LDS once and lane (pair, 2 dims)
 // runs two independent position-order chains. Row r of the block attends to
 // its first count_r positions (its window); the block's windows must agree
 // on att_start and the shared range (checked on the host), so window index i
 // is the same cache slot for every row.
-// LDS: q [8 RPW][HS + 4] | scores [RG][scs] | tile [64][HS + 4].
+// LDS: scores [RG][scs] | tile [64][HS + 4].
 template <int HS, int NWAVES>
 struct AttnRowsShape {
     static constexpr uint32_t NW = NWAVES, NT = 64 * NW;  // waves, threads
@@ -1947,11 +1997,10 @@ __global__ __launch_bounds__(64 * NWAVES) void k_attn_rows(const float* __restri
                                                    uint16_t* __restrict__ ho) {
     using Sh = AttnRowsShape<HS, NWAVES>;
     constexpr uint32_t NW = Sh::NW, NT = Sh::NT, LPR = Sh::LPR, RPW = Sh::RPW, T = Sh::T, KS = Sh::KS, F = HS / 4;
-    constexpr uint32_t R = NW * RPW / G, RG = R * G, QS = HS + 4;
+    constexpr uint32_t R = NW * RPW / G, RG = R * G;
     extern __shared__ __align__(16) float sm[];
-    float* qs = sm;                   // [NW RPW][QS]
-    float* sc = qs + NW * RPW * QS;   // [RG][scs]
-    float* kt = sc + RG * scs;        // [T][KS]
+    float* sc = sm;             // [RG][scs]
+    float* kt = sc + RG * scs;  // [T][KS]
     __shared__ uint32_t s_cnt[NW * RPW];
     __shared__ float s_sum[NW * RPW];
     __shared__ uint64_t etab[32];
@@ -1963,13 +2012,15 @@ __global__ __launch_bounds__(64 * NWAVES) void k_attn_rows(const float* __restri
     const DevWindow w0 = windows[r0];
     const uint32_t n_shared = w0.shared_end - w0.shared_start;
 
-    // the q rows of the block's pairs (rows past the block's end: zeros), the
-    // window lengths, the exp table
-    for (uint32_t t = tid; t < NW * RPW * F; t += NT) {
-        const uint32_t rg = t / F, u = t - rg * F, r = rg / G, j = rg - r * G;
-        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (rg < RG && r < nr) v = *(const float4*)(q + (size_t)(r0 + r) * width + (size_t)(h0 + j) * HS + 4 * u);
-        *(float4*)(qs + rg * QS + 4 * u) = v;
+    // the q rows of this wave's pairs (wave-uniform addresses: scalar loads;
+    // pairs past the block's end read the last valid pair), the window
+    // lengths, the exp table
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(wave);
+    const float* qrow[RPW];
+#pragma unroll
+    for (uint32_t k = 0; k < RPW; k++) {
+        const uint32_t rg = min(wv * RPW + k, min(RG, nr * G) - 1), r = rg / G, j = rg - r * G;
+        qrow[k] = q + (size_t)(r0 + r) * width + (size_t)(h0 + j) * HS;
     }
     if (tid < NW * RPW) {
         const uint32_t r = tid / G;
@@ -1989,70 +2040,101 @@ __global__ __launch_bounds__(64 * NWAVES) void k_attn_rows(const float* __restri
     typedef float v4f __attribute__((ext_vector_type(4)));  // a native vector: stays in registers
     v4f pre[PT];
     // every fetch loads all PT pieces (rows past the tile re-read its last
-    // row), so the registers are always defined and stay registers
+    // row), so the registers are always defined and stay registers. Piece k
+    // of a thread is tile row tid / F + k RS, 16-byte column tid % F. A whole
+    // tile inside one linear run of the window (the shared prefix or the own
+    // range) takes one slot lookup and a 32-bit byte offset per piece.
     auto tile_len = [&](uint32_t i0) { return i0 < cmax ? min(T, cmax - i0) : 0u; };
+    constexpr uint32_t RS = NT / F;
+    static_assert(NT % F == 0 && PT * RS == T, "tile pieces");
+    const uint32_t prow = tid / F, pcol = tid - prow * F;
+    const bool off32 = (uint64_t)seq_len * kv_dim * 4 <= 0xFFFFFFFFull;  // every slot's byte offset fits 32 bits
+    auto fetch = [&](const float* base, uint32_t i0, uint32_t n) {
+        if (off32 && n == T && (i0 + T <= n_shared || i0 >= n_shared)) {
+            const char* b = (const char*)base;
+            const uint32_t off = (win_slot(w0, n_shared, i0 + prow) * kv_dim + 4 * pcol) * 4;
+#pragma unroll
+            for (uint32_t k = 0; k < PT; k++) pre[k] = *(const v4f*)(b + off + k * RS * kv_dim * 4);
+        } else {
+#pragma unroll
+            for (uint32_t k = 0; k < PT; k++) {
+                const uint32_t rr = prow + k * RS, rc = rr < n ? rr : n - 1;
+                pre[k] = *(const v4f*)(base + (size_t)win_slot(w0, n_shared, i0 + rc) * kv_dim + 4 * pcol);
+            }
+        }
+    };
+    auto put = [&](uint32_t n) {  // the fetched tile into LDS
+        if (n == T) {
+#pragma unroll
+            for (uint32_t k = 0; k < PT; k++) *(v4f*)(kt + (prow + k * RS) * KS + 4 * pcol) = pre[k];
+        } else {
+#pragma unroll
+            for (uint32_t k = 0; k < PT; k++)
+                if (prow + k * RS < n) *(v4f*)(kt + (prow + k * RS) * KS + 4 * pcol) = pre[k];
+        }
+    };
 
     // 1. scores of every (pair, position) of each K tile
-    #pragma unroll
-    for (uint32_t k = 0; k < PT; k++) {
-        const uint32_t f = tid + NT * k, rr = f / F, u = f - rr * F, rc = rr < (tile_len(0)) ? rr : (tile_len(0)) - 1;
-        pre[k] = *(const v4f*)(kbase + (size_t)win_slot(w0, n_shared, (0) + rc) * kv_dim + 4 * u);
-    }
-    #pragma unroll
-    for (uint32_t k = 0; k < PT; k++) {
-        const uint32_t f = tid + NT * k, rr = f / F, u = f - rr * F;
-        if (rr < (tile_len(0))) *(v4f*)(kt + rr * KS + 4 * u) = pre[k];
-    }
+    fetch(kbase, 0, tile_len(0));
+    put(tile_len(0));
     __syncthreads();
     for (uint32_t i0 = 0; i0 < cmax; i0 += T) {
         const uint32_t nt = tile_len(i0), ntn = tile_len(i0 + T);
         if (ntn) {
-            #pragma unroll
-            for (uint32_t k = 0; k < PT; k++) {
-                const uint32_t f = tid + NT * k, rr = f / F, u = f - rr * F, rc = rr < (ntn) ? rr : (ntn) - 1;
-                pre[k] = *(const v4f*)(kbase + (size_t)win_slot(w0, n_shared, (i0 + T) + rc) * kv_dim + 4 * u);
-            }
+            fetch(kbase, i0 + T, ntn);
         } else {  // the first V tile, for phase 3
-            #pragma unroll
-            for (uint32_t k = 0; k < PT; k++) {
-                const uint32_t f = tid + NT * k, rr = f / F, u = f - rr * F, rc = rr < (tile_len(0)) ? rr : (tile_len(0)) - 1;
-                pre[k] = *(const v4f*)(vbase + (size_t)win_slot(w0, n_shared, (0) + rc) * kv_dim + 4 * u);
-            }
+            fetch(vbase, 0, tile_len(0));
         }
-        {  // lane (pair r, positions p0, p0 + PP, ...): K and q reads are few-address broadcasts
-            constexpr uint32_t RGP = NW * RPW, PP = NT / RGP, SPL = T / PP;
-            const uint32_t r = tid % RGP, p0 = tid / RGP;
-            const float* qr = qs + r * QS;
-            float a[SPL][4];
+        {  // lane = position, wave = its RPW pairs; the pairs' q rows are wave-uniform
+           // (scalar loads), so each 4 FMAs per pair cost one LDS read of K
+            // q in blocks of UB float4 per pair, the next block loaded during this
+            // one (2 RPW UB 4 = 64 scalar registers)
+            constexpr uint32_t UB = 8 / RPW;
+            static_assert(F % UB == 0, "q blocks");
+            const uint32_t pos = lane;
+            float a[RPW][4];
 #pragma unroll
-            for (uint32_t k = 0; k < SPL; k++) a[k][0] = a[k][1] = a[k][2] = a[k][3] = 0.0f;
-#pragma unroll 4
-            for (uint32_t u = 0; u < F; u++) {
-                const float4 qq = *(const float4*)(qr + 4 * u);
+            for (uint32_t k = 0; k < RPW; k++) a[k][0] = a[k][1] = a[k][2] = a[k][3] = 0.0f;
+            float4 qc[RPW][UB];
+            auto load_q = [&](float4(&qv)[RPW][UB], uint32_t u0) {
 #pragma unroll
-                for (uint32_t k = 0; k < SPL; k++) {
-                    const float4 kk = *(const float4*)(kt + (p0 + k * PP) * KS + 4 * u);
-                    a[k][0] = __builtin_fmaf(qq.x, kk.x, a[k][0]);
-                    a[k][1] = __builtin_fmaf(qq.y, kk.y, a[k][1]);
-                    a[k][2] = __builtin_fmaf(qq.z, kk.z, a[k][2]);
-                    a[k][3] = __builtin_fmaf(qq.w, kk.w, a[k][3]);
+                for (uint32_t k = 0; k < RPW; k++)
+#pragma unroll
+                    for (uint32_t u = 0; u < UB; u++) qv[k][u] = *(const float4*)(qrow[k] + 4 * (u0 + u));
+            };
+            load_q(qc, 0);
+#pragma unroll 1
+            for (uint32_t u0 = 0; u0 < F; u0 += UB) {
+                float4 qn[RPW][UB];
+                load_q(qn, u0 + UB < F ? u0 + UB : u0);
+#pragma unroll
+                for (uint32_t u = 0; u < UB; u++) {
+                    const float4 kk = *(const float4*)(kt + pos * KS + 4 * (u0 + u));
+#pragma unroll
+                    for (uint32_t k = 0; k < RPW; k++) {
+                        const float4 qq = qc[k][u];
+                        a[k][0] = __builtin_fmaf(qq.x, kk.x, a[k][0]);
+                        a[k][1] = __builtin_fmaf(qq.y, kk.y, a[k][1]);
+                        a[k][2] = __builtin_fmaf(qq.z, kk.z, a[k][2]);
+                        a[k][3] = __builtin_fmaf(qq.w, kk.w, a[k][3]);
+                    }
                 }
+#pragma unroll
+                for (uint32_t k = 0; k < RPW; k++)
+#pragma unroll
+                    for (uint32_t u = 0; u < UB; u++) qc[k][u] = qn[k][u];
             }
 #pragma unroll
-            for (uint32_t k = 0; k < SPL; k++) {
-                const uint32_t pos = p0 + k * PP;
+            for (uint32_t k = 0; k < RPW; k++) {
+                const uint32_t rg = wv * RPW + k;
                 // dot.rs:360: (acc0 + acc1) + (acc2 + acc3), then * scale (cpu.rs:609)
-                if (r < RG && pos < nt && i0 + pos < s_cnt[r])
-                    sc[r * scs + i0 + pos] = ((a[k][0] + a[k][1]) + (a[k][2] + a[k][3])) * scale;
+                if (rg < RG && pos < nt && i0 + pos < s_cnt[rg])
+                    sc[rg * scs + i0 + pos] = ((a[k][0] + a[k][1]) + (a[k][2] + a[k][3])) * scale;
             }
         }
         lds_barrier();  // the tile is consumed
         if (ntn) {
-            #pragma unroll
-            for (uint32_t k = 0; k < PT; k++) {
-                const uint32_t f = tid + NT * k, rr = f / F, u = f - rr * F;
-                if (rr < (ntn)) *(v4f*)(kt + rr * KS + 4 * u) = pre[k];
-            }
+            put(ntn);
             lds_barrier();
         }
     }
@@ -2095,36 +2177,18 @@ __global__ __launch_bounds__(64 * NWAVES) void k_attn_rows(const float* __restri
     const float* pp = sc + rgv * scs;
     float o0 = 0.0f, o1 = 0.0f;
     // the first V tile (every wave is past the last K tile)
-    #pragma unroll
-    for (uint32_t k = 0; k < PT; k++) {
-        const uint32_t f = tid + NT * k, rr = f / F, u = f - rr * F;
-        if (rr < (tile_len(0))) *(v4f*)(kt + rr * KS + 4 * u) = pre[k];
-    }
+    put(tile_len(0));
     __syncthreads();
     for (uint32_t i0 = 0; i0 < cmax; i0 += T) {
         const uint32_t nt = tile_len(i0), ntn = tile_len(i0 + T);
         if (ntn) {
-            #pragma unroll
-            for (uint32_t k = 0; k < PT; k++) {
-                const uint32_t f = tid + NT * k, rr = f / F, u = f - rr * F, rc = rr < (ntn) ? rr : (ntn) - 1;
-                pre[k] = *(const v4f*)(vbase + (size_t)win_slot(w0, n_shared, (i0 + T) + rc) * kv_dim + 4 * u);
-            }
+            fetch(vbase, i0 + T, ntn);
         }
         const uint32_t lim = nv > i0 ? min(nt, nv - i0) : 0;
-#pragma unroll 4
-        for (uint32_t ii = 0; ii < lim; ii++) {
-            const float p = pp[i0 + ii];
-            const v2f vv = *(const v2f*)(kt + ii * KS + e0);
-            o0 += p * vv.x;
-            o1 += p * vv.y;
-        }
+        attn_v_chain<KS>(pp + i0, kt + e0, lim, o0, o1);
         lds_barrier();
         if (ntn) {
-            #pragma unroll
-            for (uint32_t k = 0; k < PT; k++) {
-                const uint32_t f = tid + NT * k, rr = f / F, u = f - rr * F;
-                if (rr < (ntn)) *(v4f*)(kt + rr * KS + 4 * u) = pre[k];
-            }
+            put(ntn);
             lds_barrier();
         }
     }
@@ -2153,7 +2217,7 @@ __global__ __launch_bounds__(64 * NWAVES) void k_attn_rows(const float* __restri
 // LDS bytes of k_attn_rows for windows of up to max_count positions
 static size_t attn_rows_lds(size_t G, size_t hs, size_t max_count, size_t nw) {
     const size_t rpw = 128 / hs, rg = (nw * rpw / G) * G, scs = (max_count + 3) & ~(size_t)3;
-    return (nw * rpw * (hs + 4) + rg * scs + 64 * (hs + 4)) * sizeof(float);
+    return (rg * scs + 64 * (hs + 4)) * sizeof(float);
 }
 // Waves per k_attn_rows workgroup: 8 while two workgroups fit a CU's LDS,
 // else 4 (half the rows per block) if that lets two fit, else whichever fits

@@ -1912,44 +1912,47 @@ hipError_t launch_attention_split(hipStream_t st, const float* q, const float* k
 
 // o0 += p[i] * v[i * KS], o1 += p[i] * v[i * KS + 1] for i < n in position
 // order (each a rounded product, then a rounded add): p is a 16-byte aligned
-// LDS row, v an LDS tile with row stride KS. Batches of 8 positions, the
-// next batch's reads issued before the current batch's adds, so the chains
-// wait on the previous add rather than on LDS; the last n % 8 positions run
-// one at a time.
+// LDS row, v an LDS tile with row stride KS. Batches of kAttnVBatch
+// positions, the next batch's reads issued before the current batch's adds,
+// so the chains wait on the previous add rather than on LDS; the last
+// n % kAttnVBatch positions run one at a time.
+static constexpr uint32_t kAttnVBatch = 8;
 template <uint32_t KS>
 __device__ __forceinline__ void attn_v_chain(const float* __restrict__ p, const float* __restrict__ v, uint32_t n,
                                              float& o0, float& o1) {
     typedef float v2f __attribute__((ext_vector_type(2)));
     typedef float v4f __attribute__((ext_vector_type(4)));
+    constexpr uint32_t B = kAttnVBatch;
     struct Batch {
-        v4f pa, pb;
-        v2f vv[8];
+        v4f pq[B / 4];
+        v2f vv[B];
     };
     auto ld = [&](Batch& b, uint32_t i) {
-        b.pa = *(const v4f*)(p + i), b.pb = *(const v4f*)(p + i + 4);
 #pragma unroll
-        for (int k = 0; k < 8; k++) b.vv[k] = *(const v2f*)(v + (i + k) * KS);
+        for (uint32_t k = 0; k < B / 4; k++) b.pq[k] = *(const v4f*)(p + i + 4 * k);
+#pragma unroll
+        for (uint32_t k = 0; k < B; k++) b.vv[k] = *(const v2f*)(v + (i + k) * KS);
     };
     auto apply = [&](const Batch& b) {
 #pragma unroll
-        for (int k = 0; k < 8; k++) {
-            const float pk = k < 4 ? b.pa[k] : b.pb[k - 4];
+        for (uint32_t k = 0; k < B; k++) {
+            const float pk = b.pq[k / 4][k % 4];
             o0 += pk * b.vv[k].x;
             o1 += pk * b.vv[k].y;
         }
     };
     uint32_t i = 0;
-    if (n >= 8) {
+    if (n >= B) {
         Batch cur;
         ld(cur, 0);
-        for (; i + 16 <= n; i += 8) {
+        for (; i + 2 * B <= n; i += B) {
             Batch nxt;
-            ld(nxt, i + 8);
+            ld(nxt, i + B);
             apply(cur);
             cur = nxt;
         }
         apply(cur);
-        i += 8;
+        i += B;
     }
     for (; i < n; i++) {
         const float pk = p[i];
@@ -1978,14 +1981,64 @@ __device__ __forceinline__ void attn_v_chain(const float* __restrict__ p, const 
 // its first count_r positions (its window); the block's windows must agree
 // on att_start and the shared range (checked on the host), so window index i
 // is the same cache slot for every row.
-// LDS: scores [RG][scs] | tile [64][HS + 4].
+// LDS: scores [RG][scs] | the current K or V stage (AttnRowsShape::TILE floats).
 template <int HS, int NWAVES>
 struct AttnRowsShape {
     static constexpr uint32_t NW = NWAVES, NT = 64 * NW;  // waves, threads
     static constexpr uint32_t LPR = HS / 2;          // lanes per pair in the V phase (2 dims each)
     static constexpr uint32_t RPW = 64 / LPR;        // pairs per wave
-    static constexpr uint32_t T = 64, KS = HS + 4;
+    static constexpr uint32_t T = 64;                // positions per K tile
+    // head_dim 128 stages each tile in two halves (K: half the dims, V: half
+    // the positions), which halves the tile's LDS and lets a third
+    // workgroup share the CU
+    static constexpr uint32_t NH = HS == 128 ? 2 : 1;
+    static constexpr uint32_t FK = HS / 4 / NH, KSK = HS / NH + 4;  // K stage: 16-byte columns, row stride
+    static constexpr uint32_t TV = T / NH, KSV = HS + 4;           // V stage: positions, row stride
+    static constexpr uint32_t TILE = T * KSK > TV * KSV ? T * KSK : TV * KSV;  // floats
 };
+typedef float attn_v4f __attribute__((ext_vector_type(4)));  // a native vector: stays in registers
+
+// One tile stage of a window into registers: ROWS window positions from i0
+// (n of them valid; rows past n re-read row n - 1), C 16-byte columns from
+// column c0 of each cache row; thread t holds row t / C + k (NT / C), column
+// t % C, for k < PT. Every piece is loaded, so the registers are always
+// defined. A whole stage inside one linear run of the window (the shared
+// prefix or the own range) takes one slot lookup and a 32-bit byte offset
+// per piece.
+template <uint32_t C, uint32_t PT, uint32_t NT, uint32_t ROWS>
+__device__ __forceinline__ void attn_tile_fetch(attn_v4f (&pre)[PT], const float* base, const DevWindow& w0,
+                                                uint32_t n_shared, uint32_t kv_dim, bool off32, uint32_t i0,
+                                                uint32_t n, uint32_t c0) {
+    constexpr uint32_t RS = NT / C;
+    static_assert(NT % C == 0 && PT * RS == ROWS, "tile pieces");
+    const uint32_t prow = threadIdx.x / C, pcol = threadIdx.x % C + c0;
+    if (off32 && n == ROWS && (i0 + ROWS <= n_shared || i0 >= n_shared)) {
+        const char* b = (const char*)base;
+        const uint32_t off = (win_slot(w0, n_shared, i0 + prow) * kv_dim + 4 * pcol) * 4;
+#pragma unroll
+        for (uint32_t k = 0; k < PT; k++) pre[k] = *(const attn_v4f*)(b + off + k * RS * kv_dim * 4);
+    } else {
+#pragma unroll
+        for (uint32_t k = 0; k < PT; k++) {
+            const uint32_t rr = prow + k * RS, rc = rr < n ? rr : n - 1;
+            pre[k] = *(const attn_v4f*)(base + (size_t)win_slot(w0, n_shared, i0 + rc) * kv_dim + 4 * pcol);
+        }
+    }
+}
+// The fetched stage into the LDS tile (row stride STRIDE floats), rows < n.
+template <uint32_t C, uint32_t PT, uint32_t NT, uint32_t ROWS, uint32_t STRIDE>
+__device__ __forceinline__ void attn_tile_put(const attn_v4f (&pre)[PT], float* kt, uint32_t n) {
+    constexpr uint32_t RS = NT / C;
+    const uint32_t prow = threadIdx.x / C, pcol = threadIdx.x % C;
+    if (n == ROWS) {
+#pragma unroll
+        for (uint32_t k = 0; k < PT; k++) *(attn_v4f*)(kt + (prow + k * RS) * STRIDE + 4 * pcol) = pre[k];
+    } else {
+#pragma unroll
+        for (uint32_t k = 0; k < PT; k++)
+            if (prow + k * RS < n) *(attn_v4f*)(kt + (prow + k * RS) * STRIDE + 4 * pcol) = pre[k];
+    }
+}
 template <int G, int HS, int NWAVES>
 __global__ __launch_bounds__(64 * NWAVES) void k_attn_rows(const float* __restrict__ q, float* __restrict__ out,
                                                    float* __restrict__ att, const float* __restrict__ kc,
@@ -1996,11 +2049,12 @@ __global__ __launch_bounds__(64 * NWAVES) void k_attn_rows(const float* __restri
                                                    int8_t* __restrict__ qo, float* __restrict__ so,
                                                    uint16_t* __restrict__ ho) {
     using Sh = AttnRowsShape<HS, NWAVES>;
-    constexpr uint32_t NW = Sh::NW, NT = Sh::NT, LPR = Sh::LPR, RPW = Sh::RPW, T = Sh::T, KS = Sh::KS, F = HS / 4;
+    constexpr uint32_t NW = Sh::NW, NT = Sh::NT, LPR = Sh::LPR, RPW = Sh::RPW, T = Sh::T, F = HS / 4;
+    constexpr uint32_t NH = Sh::NH, FK = Sh::FK, KSK = Sh::KSK, TV = Sh::TV, KSV = Sh::KSV;
     constexpr uint32_t R = NW * RPW / G, RG = R * G;
     extern __shared__ __align__(16) float sm[];
     float* sc = sm;             // [RG][scs]
-    float* kt = sc + RG * scs;  // [T][KS]
+    float* kt = sc + RG * scs;  // K stage [T][KSK] or V stage [TV][KSV]
     __shared__ uint32_t s_cnt[NW * RPW];
     __shared__ float s_sum[NW * RPW];
     __shared__ uint64_t etab[32];
@@ -2032,84 +2086,73 @@ __global__ __launch_bounds__(64 * NWAVES) void k_attn_rows(const float* __restri
     for (uint32_t rg = 0; rg < RG; rg++) cmax = max(cmax, s_cnt[rg]);
     const float* kbase = kc + loff + kvo;
     const float* vbase = vc + loff + kvo;
-    // Tiles are fetched into registers one tile ahead (PT float4 per thread)
-    // and stored to LDS after the current tile is consumed, so the global
-    // latency overlaps the compute; the barrier after the compute waits for
-    // LDS only, leaving the fetch in flight.
-    constexpr uint32_t PT = T * F / NT;
-    typedef float v4f __attribute__((ext_vector_type(4)));  // a native vector: stays in registers
-    v4f pre[PT];
-    // every fetch loads all PT pieces (rows past the tile re-read its last
-    // row), so the registers are always defined and stay registers. Piece k
-    // of a thread is tile row tid / F + k RS, 16-byte column tid % F. A whole
-    // tile inside one linear run of the window (the shared prefix or the own
-    // range) takes one slot lookup and a 32-bit byte offset per piece.
-    auto tile_len = [&](uint32_t i0) { return i0 < cmax ? min(T, cmax - i0) : 0u; };
-    constexpr uint32_t RS = NT / F;
-    static_assert(NT % F == 0 && PT * RS == T, "tile pieces");
-    const uint32_t prow = tid / F, pcol = tid - prow * F;
+    // Stages are fetched into registers one stage ahead (PT float4 per
+    // thread) and stored to LDS after the current stage is consumed, so the
+    // global latency overlaps the compute; the barrier after the compute
+    // waits for LDS only, leaving the fetch in flight.
+    constexpr uint32_t PT = T * FK / NT;
+    static_assert(PT * NT == TV * F, "K and V stages hold the same pieces");
+    attn_v4f pre[PT];
     const bool off32 = (uint64_t)seq_len * kv_dim * 4 <= 0xFFFFFFFFull;  // every slot's byte offset fits 32 bits
-    auto fetch = [&](const float* base, uint32_t i0, uint32_t n) {
-        if (off32 && n == T && (i0 + T <= n_shared || i0 >= n_shared)) {
-            const char* b = (const char*)base;
-            const uint32_t off = (win_slot(w0, n_shared, i0 + prow) * kv_dim + 4 * pcol) * 4;
-#pragma unroll
-            for (uint32_t k = 0; k < PT; k++) pre[k] = *(const v4f*)(b + off + k * RS * kv_dim * 4);
-        } else {
-#pragma unroll
-            for (uint32_t k = 0; k < PT; k++) {
-                const uint32_t rr = prow + k * RS, rc = rr < n ? rr : n - 1;
-                pre[k] = *(const v4f*)(base + (size_t)win_slot(w0, n_shared, i0 + rc) * kv_dim + 4 * pcol);
-            }
-        }
+    auto tile_len = [&](uint32_t i0) { return i0 < cmax ? min(T, cmax - i0) : 0u; };
+    auto vlen = [&](uint32_t i0) { return i0 < cmax ? min(TV, cmax - i0) : 0u; };
+    // K stage s: positions of tile s / NH, dims half s % NH; V stage s: positions s TV ..
+    auto kfetch = [&](uint32_t st) {
+        const uint32_t i0 = st / NH * T;
+        attn_tile_fetch<FK, PT, NT, T>(pre, kbase, w0, n_shared, kv_dim, off32, i0, tile_len(i0), st % NH * FK);
     };
-    auto put = [&](uint32_t n) {  // the fetched tile into LDS
-        if (n == T) {
-#pragma unroll
-            for (uint32_t k = 0; k < PT; k++) *(v4f*)(kt + (prow + k * RS) * KS + 4 * pcol) = pre[k];
-        } else {
-#pragma unroll
-            for (uint32_t k = 0; k < PT; k++)
-                if (prow + k * RS < n) *(v4f*)(kt + (prow + k * RS) * KS + 4 * pcol) = pre[k];
-        }
+    auto vfetch = [&](uint32_t st) {
+        attn_tile_fetch<F, PT, NT, TV>(pre, vbase, w0, n_shared, kv_dim, off32, st * TV, vlen(st * TV), 0);
     };
 
     // 1. scores of every (pair, position) of each K tile
-    fetch(kbase, 0, tile_len(0));
-    put(tile_len(0));
+    const uint32_t nks = (cmax + T - 1) / T * NH;
+    kfetch(0);
+    attn_tile_put<FK, PT, NT, T, KSK>(pre, kt, tile_len(0));
     __syncthreads();
-    for (uint32_t i0 = 0; i0 < cmax; i0 += T) {
-        const uint32_t nt = tile_len(i0), ntn = tile_len(i0 + T);
-        if (ntn) {
-            fetch(kbase, i0 + T, ntn);
-        } else {  // the first V tile, for phase 3
-            fetch(vbase, 0, tile_len(0));
-        }
+    float a[RPW][4];
+    for (uint32_t st = 0; st < nks; st++) {
+        const uint32_t i0 = st / NH * T, h = st % NH, nt = tile_len(i0);
+        if (st + 1 < nks)
+            kfetch(st + 1);
+        else  // the first V stage, for phase 3
+            vfetch(0);
         {  // lane = position, wave = its RPW pairs; the pairs' q rows are wave-uniform
            // (scalar loads), so each 4 FMAs per pair cost one LDS read of K
             // q in blocks of UB float4 per pair, the next block loaded during this
             // one (2 RPW UB 4 = 64 scalar registers)
             constexpr uint32_t UB = 8 / RPW;
-            static_assert(F % UB == 0, "q blocks");
+            static_assert(FK % UB == 0, "q blocks");
+            const uint32_t ug = h * FK;  // first dim block of this stage
             const uint32_t pos = lane;
-            float a[RPW][4];
+            if (h == 0) {
 #pragma unroll
-            for (uint32_t k = 0; k < RPW; k++) a[k][0] = a[k][1] = a[k][2] = a[k][3] = 0.0f;
+                for (uint32_t k = 0; k < RPW; k++) a[k][0] = a[k][1] = a[k][2] = a[k][3] = 0.0f;
+            }
             float4 qc[RPW][UB];
             auto load_q = [&](float4(&qv)[RPW][UB], uint32_t u0) {
 #pragma unroll
                 for (uint32_t k = 0; k < RPW; k++)
 #pragma unroll
-                    for (uint32_t u = 0; u < UB; u++) qv[k][u] = *(const float4*)(qrow[k] + 4 * (u0 + u));
+                    for (uint32_t u = 0; u < UB; u++) qv[k][u] = *(const float4*)(qrow[k] + 4 * (ug + u0 + u));
+            };
+            // the K values of block u0 + UB are read before block u0's FMAs
+            float4 kc[UB];
+            auto load_k = [&](float4(&kv)[UB], uint32_t u0) {
+#pragma unroll
+                for (uint32_t u = 0; u < UB; u++) kv[u] = *(const float4*)(kt + pos * KSK + 4 * (u0 + u));
             };
             load_q(qc, 0);
+            load_k(kc, 0);
 #pragma unroll 1
-            for (uint32_t u0 = 0; u0 < F; u0 += UB) {
-                float4 qn[RPW][UB];
-                load_q(qn, u0 + UB < F ? u0 + UB : u0);
+            for (uint32_t u0 = 0; u0 < FK; u0 += UB) {
+                const uint32_t un = u0 + UB < FK ? u0 + UB : u0;
+                float4 qn[RPW][UB], kn[UB];
+                load_q(qn, un);
+                load_k(kn, un);
 #pragma unroll
                 for (uint32_t u = 0; u < UB; u++) {
-                    const float4 kk = *(const float4*)(kt + pos * KS + 4 * (u0 + u));
+                    const float4 kk = kc[u];
 #pragma unroll
                     for (uint32_t k = 0; k < RPW; k++) {
                         const float4 qq = qc[k][u];
@@ -2120,21 +2163,23 @@ __global__ __launch_bounds__(64 * NWAVES) void k_attn_rows(const float* __restri
                     }
                 }
 #pragma unroll
-                for (uint32_t k = 0; k < RPW; k++)
+                for (uint32_t u = 0; u < UB; u++) {
+                    kc[u] = kn[u];
 #pragma unroll
-                    for (uint32_t u = 0; u < UB; u++) qc[k][u] = qn[k][u];
+                    for (uint32_t k = 0; k < RPW; k++) qc[k][u] = qn[k][u];
+                }
             }
 #pragma unroll
             for (uint32_t k = 0; k < RPW; k++) {
                 const uint32_t rg = wv * RPW + k;
                 // dot.rs:360: (acc0 + acc1) + (acc2 + acc3), then * scale (cpu.rs:609)
-                if (rg < RG && pos < nt && i0 + pos < s_cnt[rg])
+                if (h == NH - 1 && rg < RG && pos < nt && i0 + pos < s_cnt[rg])
                     sc[rg * scs + i0 + pos] = ((a[k][0] + a[k][1]) + (a[k][2] + a[k][3])) * scale;
             }
         }
-        lds_barrier();  // the tile is consumed
-        if (ntn) {
-            put(ntn);
+        lds_barrier();  // the stage is consumed
+        if (st + 1 < nks) {
+            attn_tile_put<FK, PT, NT, T, KSK>(pre, kt, tile_len((st + 1) / NH * T));
             lds_barrier();
         }
     }
@@ -2176,19 +2221,18 @@ __global__ __launch_bounds__(64 * NWAVES) void k_attn_rows(const float* __restri
     const uint32_t nv = rgv < RG ? s_cnt[rgv] : 0;
     const float* pp = sc + rgv * scs;
     float o0 = 0.0f, o1 = 0.0f;
-    // the first V tile (every wave is past the last K tile)
-    put(tile_len(0));
+    // the first V stage (every wave is past the last K stage)
+    const uint32_t nvs = (cmax + TV - 1) / TV;
+    attn_tile_put<F, PT, NT, TV, KSV>(pre, kt, vlen(0));
     __syncthreads();
-    for (uint32_t i0 = 0; i0 < cmax; i0 += T) {
-        const uint32_t nt = tile_len(i0), ntn = tile_len(i0 + T);
-        if (ntn) {
-            fetch(vbase, i0 + T, ntn);
-        }
+    for (uint32_t st = 0; st < nvs; st++) {
+        const uint32_t i0 = st * TV, nt = vlen(i0);
+        if (st + 1 < nvs) vfetch(st + 1);
         const uint32_t lim = nv > i0 ? min(nt, nv - i0) : 0;
-        attn_v_chain<KS>(pp + i0, kt + e0, lim, o0, o1);
+        attn_v_chain<KSV>(pp + i0, kt + e0, lim, o0, o1);
         lds_barrier();
-        if (ntn) {
-            put(ntn);
+        if (st + 1 < nvs) {
+            attn_tile_put<F, PT, NT, TV, KSV>(pre, kt, vlen(i0 + TV));
             lds_barrier();
         }
     }
@@ -2217,7 +2261,8 @@ __global__ __launch_bounds__(64 * NWAVES) void k_attn_rows(const float* __restri
 // LDS bytes of k_attn_rows for windows of up to max_count positions
 static size_t attn_rows_lds(size_t G, size_t hs, size_t max_count, size_t nw) {
     const size_t rpw = 128 / hs, rg = (nw * rpw / G) * G, scs = (max_count + 3) & ~(size_t)3;
-    return (rg * scs + 64 * (hs + 4)) * sizeof(float);
+    const size_t tile = hs == 128 ? std::max(64 * (hs / 2 + 4), 32 * (hs + 4)) : 64 * (hs + 4);  // AttnRowsShape::TILE
+    return (rg * scs + tile) * sizeof(float);
 }
 // Waves per k_attn_rows workgroup: 8 while two workgroups fit a CU's LDS,
 // else 4 (half the rows per block) if that lets two fit, else whichever fits

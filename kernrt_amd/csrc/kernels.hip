@@ -1328,6 +1328,8 @@ __global__ __launch_bounds__(512) void k_attention(const float* __restrict__ q, 
     extern __shared__ float sm[];
     __shared__ float red[16][8];
     __shared__ float s_sum[8];
+    __shared__ uint64_t etab[32];
+    if (threadIdx.x < 32) etab[threadIdx.x] = kExp2Tab[threadIdx.x];  // read after the barriers below
     // this workgroup: query heads [h0, h0 + G), G | kv_mul, all on one KV head
     const uint32_t row = blockIdx.y, T = kAttnThreads;
     const DevWindow w = windows[row];
@@ -1411,7 +1413,7 @@ __global__ __launch_bounds__(512) void k_attention(const float* __restrict__ q, 
         float m = red[0][j];
         for (uint32_t wv = 1; wv < T / 64; wv++) m = fmaxf(m, red[wv][j]);
         float* sc = sc_base + j * sc_stride;
-        sc[i] = glibc_expf(sc[i] - m);
+        sc[i] = glibc_expf(sc[i] - m, etab);
     }
     __syncthreads();
     // 3. per-head sums, lanes 0..kv_mul-1 of wave 0 in lockstep
@@ -2688,12 +2690,15 @@ hipError_t launch_add_rms_quant(hipStream_t st, float* x, const float* add, cons
 __global__ __launch_bounds__(256) void k_silu_quant(float* __restrict__ g, const float* __restrict__ u, size_t n,
                                                     int8_t* __restrict__ q, float* __restrict__ s,
                                                     uint16_t* __restrict__ h) {
+    __shared__ uint64_t etab[32];  // the exp table in LDS: per-lane lookups without a global round trip
     size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
     bool valid = i < n;  // n % 32 == 0
+    const float xv = valid ? g[i] : 0.0f, uv = valid ? u[i] : 0.0f;
+    if (threadIdx.x < 32) etab[threadIdx.x] = kExp2Tab[threadIdx.x];
+    __syncthreads();
     float r = 0.0f;
     if (valid) {
-        float xv = g[i];
-        r = div_rn(xv, 1.0f + glibc_expf(-xv)) * u[i];
+        r = div_rn(xv, 1.0f + glibc_expf(-xv, etab)) * uv;
         g[i] = r;
     }
     quant_lane(r, valid, q + i, s + i / 32, h + i / 32);
@@ -2837,11 +2842,14 @@ hipError_t launch_stream_read(hipStream_t st, const float* p, size_t n, int* sin
 }
 
 // silu (cpu.rs:708-710): x / (1 + exp(-x)), then * up.
-__global__ void k_silu_mul(float* __restrict__ g, const float* __restrict__ u, size_t n) {
+__global__ __launch_bounds__(256) void k_silu_mul(float* __restrict__ g, const float* __restrict__ u, size_t n) {
+    __shared__ uint64_t etab[32];
     size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    const float x = i < n ? g[i] : 0.0f;
+    if (threadIdx.x < 32) etab[threadIdx.x] = kExp2Tab[threadIdx.x];
+    __syncthreads();
     if (i < n) {
-        float x = g[i];
-        float s = div_rn(x, 1.0f + glibc_expf(-x));
+        float s = div_rn(x, 1.0f + glibc_expf(-x, etab));
         g[i] = s * u[i];
     }
 }

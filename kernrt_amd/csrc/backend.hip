@@ -1290,6 +1290,41 @@ int norm_project(kr_ctx* c, size_t layer, const int* projs, const kr_buf* ys, in
     return KR_OK;
 }
 
+// Decode gate/up of one row with the norm in front and SiLU(gate) * up + Q8
+// behind (k_gemv_swiglu): the down projection's input lands in the
+// activation workspace; h (f32) goes to `h`.
+bool swiglu_ok(kr_ctx* c, size_t layer, size_t dim) {
+    if (!c->prepared || layer >= c->n_layers) return false;
+    const Mat* g = proj_mat(c, layer, KR_PROJ_GATE);
+    const Mat* u = proj_mat(c, layer, KR_PROJ_UP);
+    return g && u && g->m.k == dim && kr::swiglu_fusable(g->m, u->m);
+}
+
+int norm_swiglu(kr_ctx* c, size_t layer, kr_buf x, kr_buf add, kr_buf w, kr_buf x_out, kr_buf h, size_t dim,
+                float eps) {
+    CHECK(c, swiglu_ok(c, layer, dim), "fused gate/up + SwiGLU does not apply to layer %zu", layer);
+    const Mat* g = proj_mat(c, layer, KR_PROJ_GATE);
+    const Mat* u = proj_mat(c, layer, KR_PROJ_UP);
+    const size_t hidden = g->m.n;
+    BUF(xb, x, dim);
+    BUF(wb, w, dim);
+    BUF(ob, x_out, dim);
+    BUF(hb, h, hidden);
+    CHECK(c, x_out != x, "the updated residual goes to a second buffer");
+    const float* ap = nullptr;
+    if (add != KR_NO_BUF) {
+        BUF(ab, add, dim);
+        ap = ab->p;
+    }
+    int rc = ensure_workspace(c, 1, hidden);
+    if (rc) return rc;
+    HIPCHK(c, kr::launch_gate_up_swiglu(c->stream, sem_for_project(g->m), g->m, u->m, xb->p, ap, wb->p, ob->p, eps,
+                                        c->wq, c->ws, c->wh, hb->p));
+    c->q_rows = 1;
+    c->q_width = hidden;
+    return KR_OK;
+}
+
 bool split_attention_ok(kr_ctx* c, const kr_attn_spec* sp) {
     return sp && c->prepared && sp->seq_len == c->seq_len &&
            kr::attention_split_ok(c->seq_len, sp->kv_mul, sp->head_size);

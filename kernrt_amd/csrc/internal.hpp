@@ -68,6 +68,11 @@ bool pro_fusable(size_t k);
 // Q8(rms_norm(x_out, w)); x_out must not be x
 int norm_project(kr_ctx* c, size_t layer, const int* projs, const kr_buf* ys, int n, kr_buf x, kr_buf add, kr_buf w,
                  kr_buf x_out, size_t dim, float eps);
+// gate/up of Q8(rms_norm(x + add, w)) with Q8(silu(gate) * up) into the
+// activation workspace (h = silu(gate) * up to `h`); x_out must not be x
+bool swiglu_ok(kr_ctx* c, size_t layer, size_t dim);
+int norm_swiglu(kr_ctx* c, size_t layer, kr_buf x, kr_buf add, kr_buf w, kr_buf x_out, kr_buf h, size_t dim,
+                float eps);
 // the projection of Q8(x) (x one f32 row of `width`)
 int quant_project(kr_ctx* c, size_t layer, int proj, kr_buf x, kr_buf y, size_t width);
 

@@ -537,6 +537,74 @@ struct GemvPro {
 };
 static constexpr int PRO_NORM = 1, PRO_QUANT = 3;
 
+// The producer of k_gemv_pro / k_gemv_swiglu, after its inputs were loaded
+// into registers (va: the residual row or the f32 row, vb: the add, vw: the
+// norm weight): with PRO_NORM the residual add, the serial RMS sum on one
+// lane (rms_norm_row, cpu.rs:635-641) and out = w * (scale * x) (cpu.rs:643);
+// then Q8Vec::quantize_into (quant.rs:864-873) of the row into LDS (xq, and
+// the scale bits xsb: f16 for the FMA-chain format, else f32), a block per 8
+// threads. Every thread of the workgroup calls this; the row is spread over
+// threads 0..255 (VPT float4 each), further threads only join the barriers.
+template <int SEM, int PRO, int VPT>
+__device__ __forceinline__ void gemv_produce(const GemvPro& pro, uint32_t K, float4 (&va)[VPT], const float4 (&vb)[VPT],
+                                             const float4 (&vw)[VPT], int8_t* xq, uint32_t* xsb, float* scratch,
+                                             float* s_scale_p) {
+    constexpr bool XF16 = SEM == SEM_FMA_CHAIN;
+    const uint32_t tid = threadIdx.x, n4 = K >> 2;
+    float4 o[VPT];
+    if constexpr (PRO == PRO_NORM) {
+#pragma unroll
+        for (int u = 0; u < VPT; u++) {
+            const uint32_t f = tid + 256 * u;
+            if (f < n4) {
+                float4 v = va[u];
+                if (pro.b) v = make_float4(v.x + vb[u].x, v.y + vb[u].y, v.z + vb[u].z, v.w + vb[u].w);
+                va[u] = v;
+                if (blockIdx.x == 0 && pro.x_out) ((float4*)pro.x_out)[f] = v;
+                ((float4*)scratch)[f] = make_float4(v.x * v.x, v.y * v.y, v.z * v.z, v.w * v.w);
+            }
+        }
+        __syncthreads();
+        if (tid == 0) {  // rms_norm_row (cpu.rs:635-641)
+            float ss = chain_sum(scratch, K);
+            ss = div_rn(ss, (float)K);
+            ss += pro.eps;
+            *s_scale_p = div_rn(1.0f, sqrt_rn(ss));
+        }
+        __syncthreads();
+        const float scale = *s_scale_p;
+#pragma unroll
+        for (int u = 0; u < VPT; u++) {
+            const float4 v = va[u], wq = vw[u];
+            o[u] = make_float4(wq.x * (scale * v.x), wq.y * (scale * v.y), wq.z * (scale * v.z), wq.w * (scale * v.w));
+        }
+    } else {
+        static_assert(PRO == PRO_QUANT, "producer kind");
+#pragma unroll
+        for (int u = 0; u < VPT; u++) o[u] = va[u];
+    }
+    // Q8Vec::quantize_into (quant.rs:864-873) into LDS; a block is 8 threads
+#pragma unroll
+    for (int u = 0; u < VPT; u++) {
+        const uint32_t f = tid + 256 * u;
+        if (f < n4) {  // K % 32 == 0: the 8 threads of a block are all in range or all out
+            const float4 v = o[u];
+            float m = fmaxf(fmaxf(fmaxf(fmaxf(0.0f, fabsf(v.x)), fabsf(v.y)), fabsf(v.z)), fabsf(v.w));
+            m = group_max8(m);
+            const float d = div_rn(m, 127.0f);
+            const float inv = d > 0.0f ? div_rn(1.0f, d) : 0.0f;
+            char4 qq;
+            qq.x = q8_round(v.x * inv);
+            qq.y = q8_round(v.y * inv);
+            qq.z = q8_round(v.z * inv);
+            qq.w = q8_round(v.w * inv);
+            ((char4*)xq)[f] = qq;
+            if ((f & 7) == 0) xsb[f / 8] = XF16 ? (uint32_t)f32_to_f16_bits(d) : f2u(d);
+        }
+    }
+    __syncthreads();
+}
+
 template <int SEM, int PRO, int VPT>
 __global__ __launch_bounds__(256) void k_gemv_pro(MatSet ms, GemvPro pro, uint32_t K, uint32_t R,
                                                   uint32_t step_rows, uint32_t step_cols) {
@@ -588,58 +656,7 @@ __global__ __launch_bounds__(256) void k_gemv_pro(MatSet ms, GemvPro pro, uint32
     }
 
     // 3. the producer, while the weights are in flight
-    float4 o[VPT];
-    if constexpr (PRO == PRO_NORM) {
-#pragma unroll
-        for (int u = 0; u < VPT; u++) {
-            const uint32_t f = tid + 256 * u;
-            if (f < n4) {
-                float4 v = va[u];
-                if (pro.b) v = make_float4(v.x + vb[u].x, v.y + vb[u].y, v.z + vb[u].z, v.w + vb[u].w);
-                va[u] = v;
-                if (blockIdx.x == 0 && pro.x_out) ((float4*)pro.x_out)[f] = v;
-                ((float4*)scratch)[f] = make_float4(v.x * v.x, v.y * v.y, v.z * v.z, v.w * v.w);
-            }
-        }
-        __syncthreads();
-        if (tid == 0) {  // rms_norm_row (cpu.rs:635-641)
-            float ss = chain_sum(scratch, K);
-            ss = div_rn(ss, (float)K);
-            ss += pro.eps;
-            s_scale = div_rn(1.0f, sqrt_rn(ss));
-        }
-        __syncthreads();
-        const float scale = s_scale;
-#pragma unroll
-        for (int u = 0; u < VPT; u++) {
-            const float4 v = va[u], wq = vw[u];
-            o[u] = make_float4(wq.x * (scale * v.x), wq.y * (scale * v.y), wq.z * (scale * v.z), wq.w * (scale * v.w));
-        }
-    } else {
-        static_assert(PRO == PRO_QUANT, "producer kind");
-#pragma unroll
-        for (int u = 0; u < VPT; u++) o[u] = va[u];
-    }
-    // Q8Vec::quantize_into (quant.rs:864-873) into LDS; a block is 8 threads
-#pragma unroll
-    for (int u = 0; u < VPT; u++) {
-        const uint32_t f = tid + 256 * u;
-        if (f < n4) {  // K % 32 == 0: the 8 threads of a block are all in range or all out
-            const float4 v = o[u];
-            float m = fmaxf(fmaxf(fmaxf(fmaxf(0.0f, fabsf(v.x)), fabsf(v.y)), fabsf(v.z)), fabsf(v.w));
-            m = group_max8(m);
-            const float d = div_rn(m, 127.0f);
-            const float inv = d > 0.0f ? div_rn(1.0f, d) : 0.0f;
-            char4 qq;
-            qq.x = q8_round(v.x * inv);
-            qq.y = q8_round(v.y * inv);
-            qq.z = q8_round(v.z * inv);
-            qq.w = q8_round(v.w * inv);
-            ((char4*)xq)[f] = qq;
-            if ((f & 7) == 0) xsb[f / 8] = XF16 ? (uint32_t)f32_to_f16_bits(d) : f2u(d);
-        }
-    }
-    __syncthreads();
+    gemv_produce<SEM, PRO, VPT>(pro, K, va, vb, vw, xq, xsb, scratch, &s_scale);
 
     // 4. block dots against the LDS row, then the epilogue of k_gemv
     const uint32_t per = gemv_out_floats(SEM, nb), q4p = gemv_q4p(nb);
@@ -744,6 +761,159 @@ hipError_t launch_project_pro(hipStream_t st, int sem, const DevMatrix* const* w
     }
 #undef KR_PRO_SEM
     return hipErrorInvalidValue;
+}
+
+// Decode gate/up with the SwiGLU product and its quantization fused behind
+// (M = 1, K <= 1024). Workgroup t computes rows 32 t .. 32 t + 31 of both the
+// gate and the up matrix, with the residual add + RMSNorm + Q8 producer in
+// front exactly as k_gemv_pro<PRO_NORM>; then one half-wave forms
+// h = silu(gate) * up (cpu.rs:708-710, then cpu.rs:494-499) for those 32
+// rows and quantizes them as Q8 block t of h (quant.rs:864-873) — the input
+// of the down projection. The results are bit-identical to k_gemv_pro
+// followed by k_silu_quant, with one launch fewer per layer. Tile row r < 32
+// is gate row 32 t + r, r >= 32 up row 32 t + r - 32.
+static constexpr uint32_t kSwigluMaxK = 1024;
+static constexpr uint32_t kSwigluThreads = 512;  // the producer runs on the first 256 (K <= 1024)
+template <int SEM, int CPT>
+__global__ __launch_bounds__(kSwigluThreads) void k_gemv_swiglu(MatSet ms, GemvPro pro, uint32_t K, uint32_t step_rows,
+                                                     uint32_t step_cols, int8_t* __restrict__ hq,
+                                                     float* __restrict__ hsc, uint16_t* __restrict__ hh,
+                                                     float* __restrict__ hf) {
+    constexpr int VPT = 1;              // K <= 1024: one float4 of the row per thread
+    constexpr uint32_t RT = 64;         // tile rows: 32 gate + 32 up
+    extern __shared__ __align__(16) float sm[];  // x quants [K] | x scale bits [nb] | squares, then epilogue operands
+    __shared__ float s_scale;
+    __shared__ float s_out[RT];
+    __shared__ uint64_t etab[32];
+    constexpr uint32_t NT = kSwigluThreads;
+    const uint32_t t = blockIdx.x;
+    const uint32_t nb = K >> 5, kc = K >> 4, n4 = K >> 2, C = RT * kc;
+    const uint32_t tid = threadIdx.x;
+    constexpr bool WF16 = SEM != SEM_FOUR_PARTIALS_F32;
+    int8_t* xq = (int8_t*)sm;
+    uint32_t* xsb = (uint32_t*)(sm + n4);
+    float* scratch = sm + ((n4 + nb + 3) & ~3u);
+    if (tid < 32) etab[tid] = kExp2Tab[tid];
+
+    // 1. the producer's inputs first, so waiting for them never waits for the weights
+    float4 va[VPT], vb[VPT], vw[VPT];
+    if (tid < n4) {
+        va[0] = ((const float4*)pro.a)[tid];
+        vb[0] = pro.b ? ((const float4*)pro.b)[tid] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        vw[0] = ((const float4*)pro.w)[tid];
+    }
+    // 2. the weight tile: chunk tid + NT u is (tile row, 16-byte column)
+    v4i wv[CPT];
+    uint32_t wsb[CPT];
+    {
+        uint32_t row = tid / kc, col = tid - (tid / kc) * kc;
+#pragma unroll
+        for (int u = 0; u < CPT; u++) {
+            const bool in = tid + NT * u < C;
+            const uint32_t rr = in ? row : RT - 1, cc = in ? col : kc - 1;
+            const int mi = rr >= 32 ? 1 : 0;
+            const uint32_t grow = 32 * t + (rr & 31);
+            wv[u] = __builtin_nontemporal_load((const v4i*)(ms.q[mi] + (size_t)grow * K + cc * 16));
+            wsb[u] = scale_bits(WF16, ms.s[mi], (size_t)grow * nb + (cc >> 1));
+            col += step_cols;
+            row += step_rows;
+            if (col >= kc) col -= kc, row += 1;
+        }
+    }
+    // 3. the producer, while the weights are in flight
+    gemv_produce<SEM, PRO_NORM, VPT>(pro, K, va, vb, vw, xq, xsb, scratch, &s_scale);
+
+    // 4. block dots against the LDS row, the epilogue operands to LDS
+    const uint32_t per = gemv_out_floats(SEM, nb), q4p = gemv_q4p(nb);
+    float* res = scratch;
+    const uint32_t dummy = RT * per;
+    const bool even = (tid & 1) == 0;
+    {
+        uint32_t row = tid / kc, col = tid - (tid / kc) * kc;
+#pragma unroll
+        for (int u = 0; u < CPT; u++) {
+            const bool valid = tid + NT * u < C;
+            const uint32_t r = valid ? row : RT - 1, cc = valid ? col : kc - 1, b = cc >> 1;
+            const float ws = scale_value(WF16, wsb[u]);
+            const v4i xv = *(const v4i*)(xq + cc * 16);
+            const uint32_t xs = xsb[b];
+            int acc = 0;
+            acc = __builtin_amdgcn_sdot4(wv[u].x, xv.x, acc, false);
+            acc = __builtin_amdgcn_sdot4(wv[u].y, xv.y, acc, false);
+            acc = __builtin_amdgcn_sdot4(wv[u].z, xv.z, acc, false);
+            acc = __builtin_amdgcn_sdot4(wv[u].w, xv.w, acc, false);
+            const int isum = lane_pair_sum(acc);
+            const bool own = valid && even;
+            const uint32_t base = r * per;
+            if (SEM == SEM_FMA_CHAIN) {
+                float2* op = (float2*)(res + (own ? base + 2 * b : dummy));
+                *op = make_float2((float)isum, ws * f16w((uint16_t)xs));
+            } else {
+                res[own ? base + (b & 3) * q4p + (b >> 2) : dummy] = (ws * u2f(xs)) * (float)isum;
+            }
+            col += step_cols;
+            row += step_rows;
+            if (col >= kc) col -= kc, row += 1;
+        }
+    }
+    __syncthreads();
+    // 5. each row's chain in reference order (quant.rs:276-288 or dot.rs:35-44)
+    if (SEM == SEM_FMA_CHAIN) {
+        if (tid < RT) s_out[tid] = seq_fma((const float2*)(res + (size_t)tid * per), nb);
+    } else {
+        const uint32_t oi = tid >> 2, j = tid & 3;  // threads 0..255 = 64 rows x 4 partial sums
+        float v = 0.0f;
+        if (oi < RT && j < nb) v = lds_sum(res + (size_t)oi * per + j * q4p, (nb - j + 3) / 4);
+        const float t0 = quad_bcast<0>(v), t1 = quad_bcast<1>(v), t2 = quad_bcast<2>(v), t3 = quad_bcast<3>(v);
+        if (oi < RT && j == 0) s_out[oi] = ((t0 + t1) + t2) + t3;
+    }
+    __syncthreads();
+    // 6. h = silu(gate) * up and its Q8 block, on the first half-wave
+    if (tid < 32) {
+        const float g = s_out[tid], up = s_out[32 + tid];
+        const float h = div_rn(g, 1.0f + glibc_expf(-g, etab)) * up;
+        if (hf) hf[32 * t + tid] = h;
+        quant_lane(h, true, hq + 32 * t + tid, hsc + t, hh + t);
+    }
+}
+
+hipError_t launch_gate_up_swiglu(hipStream_t st, int sem, const DevMatrix& gate, const DevMatrix& up, const float* x,
+                                 const float* add, const float* norm_w, float* x_out, float eps, int8_t* hq,
+                                 float* hs, uint16_t* hh, float* hf) {
+    const size_t k = gate.k, n = gate.n;
+    if (!swiglu_fusable(gate, up)) return hipErrorInvalidValue;
+    MatSet ms{};
+    ms.count = 2;
+    ms.q[0] = gate.q, ms.s[0] = gate.s, ms.n[0] = (uint32_t)n;
+    ms.q[1] = up.q, ms.s[1] = up.s, ms.n[1] = (uint32_t)n;
+    GemvPro pro{x, add, norm_w, x_out, eps};
+    const size_t nb = k / 32, kc = k / 16, head = (k / 4 + nb + 3) & ~(size_t)3;
+    const size_t ops = 64 * gemv_out_floats(sem, (uint32_t)nb) + 2;
+    const size_t lds = (head + (ops > k ? ops : k)) * sizeof(float);
+    const size_t cpt = (64 * kc + kSwigluThreads - 1) / kSwigluThreads;
+    const dim3 grid((unsigned)(n / 32));
+#define KR_SWIGLU(SEMV, CPTV)                                                                                     \
+    hipLaunchKernelGGL((k_gemv_swiglu<SEMV, CPTV>), grid, dim3(kSwigluThreads), lds, st, ms, pro, (uint32_t)k,  \
+                       (uint32_t)(kSwigluThreads / kc), (uint32_t)(kSwigluThreads % kc), hq, hs, hh, hf)
+#define KR_SWIGLU_CPT(SEMV) \
+    if (cpt <= 4)           \
+        KR_SWIGLU(SEMV, 4); \
+    else                    \
+        KR_SWIGLU(SEMV, 8);
+    switch (sem) {
+        case SEM_FMA_CHAIN: KR_SWIGLU_CPT(SEM_FMA_CHAIN) break;
+        case SEM_FOUR_PARTIALS_F32: KR_SWIGLU_CPT(SEM_FOUR_PARTIALS_F32) break;
+        case SEM_FOUR_PARTIALS_F16: KR_SWIGLU_CPT(SEM_FOUR_PARTIALS_F16) break;
+        default: return hipErrorInvalidValue;
+    }
+#undef KR_SWIGLU_CPT
+#undef KR_SWIGLU
+    return hipGetLastError();
+}
+
+bool swiglu_fusable(const DevMatrix& gate, const DevMatrix& up) {
+    return gate.k == up.k && gate.n == up.n && gate.storage == up.storage && gate.k % 32 == 0 &&
+           gate.k >= 64 && gate.k <= kSwigluMaxK && gate.n % 32 == 0 && gate.n > 0;
 }
 
 // ---------------------------------------------------------------------------

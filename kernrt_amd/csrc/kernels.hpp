@@ -57,6 +57,14 @@ hipError_t launch_rope_kv(hipStream_t st, float* q, float* k, const float* v, si
 // One decode row (M = 1) of 1-3 projections with the producer of their input
 // fused in front: pro_kind 1 = x (+= add) -> rms_norm(w, eps) -> Q8 (the
 // updated x row goes to x_out when non-null), 3 = Q8 of the f32 row a.
+// One decode row of gate/up with the producer in front (x (+= add) ->
+// rms_norm(norm_w, eps) -> Q8, the updated x row to x_out when non-null) and
+// h = silu(gate) * up behind, quantized into (hq, hs, hh) for the down
+// projection; h itself goes to hf when non-null. Needs swiglu_fusable.
+bool swiglu_fusable(const DevMatrix& gate, const DevMatrix& up);
+hipError_t launch_gate_up_swiglu(hipStream_t st, int sem, const DevMatrix& gate, const DevMatrix& up, const float* x,
+                                 const float* add, const float* norm_w, float* x_out, float eps, int8_t* hq,
+                                 float* hs, uint16_t* hh, float* hf);
 hipError_t launch_project_pro(hipStream_t st, int sem, const DevMatrix* const* w, float* const* y, int count,
                               int pro_kind, const float* a, const float* b, const float* norm_w, float* x_out,
                               float eps);

@@ -243,12 +243,17 @@ int decode_step_fused(krl_model* m, size_t token, size_t pos, bool dev) {
         }
         int gu[2] = {KR_PROJ_GATE, KR_PROJ_UP};
         kr_buf gys[2] = {m->gate, m->up};
-        TRY(norm_then(m->o, n.ffn, l, gu, gys, 2));
-        // SiLU * up and the final norm stay separate launches: every workgroup
-        // of a fused launch would redo 'hidden' double-precision exp/divisions,
-        // or (classifier) 49k rows' worth of workgroups the serial norm sum;
-        // both measured slower than the two-launch form
-        KRC(m, kri::silu_quant(b, m->gate, m->up, 1, g.hidden));
+        if (pro && kri::swiglu_ok(b, l, g.dim)) {
+            // gate/up, SiLU * up and its Q8 in one launch (each workgroup owns
+            // 32 rows of both matrices, so no workgroup redoes another's work)
+            KRC(m, kri::norm_swiglu(b, l, X[cur], m->o, n.ffn, X[cur ^ 1], m->gate, g.dim, g.eps));
+            cur ^= 1;
+        } else {
+            TRY(norm_then(m->o, n.ffn, l, gu, gys, 2));
+            KRC(m, kri::silu_quant(b, m->gate, m->up, 1, g.hidden));
+        }
+        // the final norm stays a separate launch: folded into the classifier,
+        // 49k rows' worth of workgroups would each redo its serial sum
         int dn[1] = {KR_PROJ_DOWN};
         KRC(m, kri::project_q(b, l, dn, &m->mlp, 1, 1));
         pending = m->mlp;

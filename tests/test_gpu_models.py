@@ -142,6 +142,21 @@ def test_decode_batch_split_attention(n_seq):
                 cpus[i].forward(seqs[i][t], t)
 
 
+@pytest.mark.parametrize("storage", ["q8_0", "q8_0x4"])
+@pytest.mark.parametrize("dim,hidden", [(128, 256), (1024, 2048)])
+def test_decode_at_fused_swiglu_widths(storage, dim, hidden):
+    # widths where the fused decode step computes gate/up, SiLU * up and its
+    # Q8 in one launch (64 <= dim <= 1024, hidden % 32 == 0): logits bitwise
+    # against the cpu backend, both weight formats (FMA chain and the four
+    # partial sums in the kernel's epilogue)
+    c = O.Config(dim=dim, hidden_dim=hidden, n_layers=2, n_heads=dim // 64, n_kv_heads=dim // 128, vocab_size=128,
+                 seq_len=64, rms_eps=1e-5, rope_theta=10_000.0, rope_interleaved=False, head_dim=64)
+    ow = O.backends_weights(c, storage)
+    gpu, cpu = gpu_model(c, ow), O.Model(c, ow, "cpu")
+    for pos, tok in enumerate(PROMPT):
+        assert_bits_equal(gpu.forward(tok, pos), cpu.forward(tok, pos), f"{storage} {dim} pos {pos}")
+
+
 def test_multi_tile_shapes():
     # tests/backends.rs:436-481: a 70-row prompt against 256-wide projections
     c = O.Config(dim=128, hidden_dim=256, n_layers=2, n_heads=4, n_kv_heads=2, vocab_size=128, seq_len=128,

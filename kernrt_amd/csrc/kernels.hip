@@ -622,7 +622,6 @@ __global__ __launch_bounds__(256) void k_gemv_pro(MatSet ms, GemvPro pro, uint32
     const uint32_t C = rows * kc;
     const uint32_t tid = threadIdx.x;
     constexpr bool WF16 = SEM != SEM_FOUR_PARTIALS_F32;
-    constexpr bool XF16 = SEM == SEM_FMA_CHAIN;
     int8_t* xq = (int8_t*)sm;
     uint32_t* xsb = (uint32_t*)(sm + n4);
     float* scratch = sm + ((n4 + nb + 3) & ~3u);

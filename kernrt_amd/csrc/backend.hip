@@ -1290,6 +1290,18 @@ int norm_project(kr_ctx* c, size_t layer, const int* projs, const kr_buf* ys, in
     return KR_OK;
 }
 
+// y = C * conv(B * x) of one LFM2 decode row (k_conv_block_decode)
+int conv_block_decode(kr_ctx* c, kr_buf y, kr_buf bcx, kr_buf kernel, kr_buf state, size_t dim, size_t k) {
+    CHECK(c, k >= 1, "conv kernel width must be positive");
+    BUF(yb, y, dim);
+    BUF(xb, bcx, 3 * dim);
+    BUF(kb, kernel, dim * k);
+    BUF(sb, state, (k - 1) * dim);
+    CHECK(c, y != bcx, "the conv block writes a second buffer");
+    HIPCHK(c, kr::launch_conv_block_decode(c->stream, yb->p, xb->p, kb->p, sb->p, dim, k));
+    return KR_OK;
+}
+
 // Decode gate/up of one row with the norm in front and SiLU(gate) * up + Q8
 // behind (k_gemv_swiglu): the down projection's input lands in the
 // activation workspace; h (f32) goes to `h`.

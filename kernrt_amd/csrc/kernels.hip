@@ -3078,6 +3078,40 @@ hipError_t launch_conv_decode(hipStream_t st, float* out, const float* x, const 
     return hipGetLastError();
 }
 
+// The LFM2 short-conv block of one decode row (lfm2.rs:414-474) after
+// in_proj: with B, C, x the three dim-wide parts of bcx, h = B * x, then the
+// causal depthwise conv of h against the layer's kernel and k - 1 rows of
+// state (which shifts by one, h entering last), then y = C * conv. Per
+// element the same operations as k_mul, k_conv_decode and k_mul in sequence,
+// in one launch.
+__global__ void k_conv_block_decode(float* __restrict__ y, const float* __restrict__ bcx,
+                                    const float* __restrict__ kern, float* __restrict__ state, uint32_t dim,
+                                    uint32_t k) {
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= dim) return;
+    const uint32_t hist = k - 1;
+    const float bx = bcx[i], cx = bcx[dim + i], xx = bcx[2 * dim + i];
+    const float h = bx * xx;
+    float acc = 0.0f;
+    for (uint32_t j = 0; j < k; j++) {
+        const float hv = j < hist ? state[(size_t)j * dim + i] : h;
+        acc += kern[(size_t)i * k + j] * hv;
+    }
+    if (hist > 0) {
+        for (uint32_t j = 0; j + 1 < hist; j++) state[(size_t)j * dim + i] = state[(size_t)(j + 1) * dim + i];
+        state[(size_t)(hist - 1) * dim + i] = h;
+    }
+    y[i] = cx * acc;
+}
+hipError_t launch_conv_block_decode(hipStream_t st, float* y, const float* bcx, const float* kern, float* state,
+                                    size_t dim, size_t k) {
+    if (dim == 0) return hipSuccess;
+    if (k < 1) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_conv_block_decode, dim3((unsigned)((dim + 255) / 256)), dim3(256), 0, st, y, bcx, kern,
+                       state, (uint32_t)dim, (uint32_t)k);
+    return hipGetLastError();
+}
+
 // Embedding row (Matrix::decode_row, quant.rs:670-691): q * scale, exact.
 __global__ void k_embed(const int8_t* __restrict__ q, const void* __restrict__ s, int f16, uint32_t k,
                         size_t token, const uint32_t* __restrict__ token_dev, float* __restrict__ out) {

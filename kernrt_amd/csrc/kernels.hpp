@@ -117,6 +117,10 @@ hipError_t launch_stream_read(hipStream_t st, const float* p, size_t n, int* sin
 hipError_t launch_silu_mul(hipStream_t st, float* g, const float* u, size_t n);
 hipError_t launch_conv_prefill(hipStream_t st, float* out, const float* x, const float* kernel,
                                size_t rows, size_t dim, size_t k);
+// y = C * conv(B * x) for one decode row, bcx = [B | C | x] (3 * dim), the
+// conv state shifted in place
+hipError_t launch_conv_block_decode(hipStream_t st, float* y, const float* bcx, const float* kern, float* state,
+                                    size_t dim, size_t k);
 hipError_t launch_conv_decode(hipStream_t st, float* out, const float* x, const float* kernel,
                               float* state, size_t dim, size_t k);
 // token from `token_dev` when non-null, else `token`

@@ -235,11 +235,13 @@ int decode_step_fused(krl_model* m, size_t token, size_t pos, bool dev) {
         } else {
             int ci[1] = {KR_PROJ_CONV_IN};
             TRY(norm_then(pending, n.att, l, ci, &m->bcx, 1));
-            KRC(m, kr_mul(b, m->h, 0, m->bcx, 0, m->bcx, 2 * g.dim, g.dim));
-            KRC(m, kr_conv_decode(b, m->co, m->h, (kr_buf)m->conv_kernels[l], (kr_buf)m->conv_state[l], g.dim,
-                                  m->conv_k[l]));
-            KRC(m, kr_mul(b, m->cy, 0, m->bcx, g.dim, m->co, 0, g.dim));
-            KRC(m, kr_project(b, l, KR_PROJ_CONV_OUT, m->cy, m->o, 1));
+            // B * x, the conv and C * conv in one launch; out_proj quantizes its input
+            KRC(m, kri::conv_block_decode(b, m->cy, m->bcx, (kr_buf)m->conv_kernels[l], (kr_buf)m->conv_state[l],
+                                          g.dim, m->conv_k[l]));
+            if (pro)
+                KRC(m, kri::quant_project(b, l, KR_PROJ_CONV_OUT, m->cy, m->o, g.dim));
+            else
+                KRC(m, kr_project(b, l, KR_PROJ_CONV_OUT, m->cy, m->o, 1));
         }
         int gu[2] = {KR_PROJ_GATE, KR_PROJ_UP};
         kr_buf gys[2] = {m->gate, m->up};

@@ -1290,6 +1290,18 @@ int norm_project(kr_ctx* c, size_t layer, const int* projs, const kr_buf* ys, in
     return KR_OK;
 }
 
+// the per-head RMSNorms of q and k (qk-norm models) in one launch
+int qk_norm_pair(kr_ctx* c, kr_buf q, kr_buf k, size_t rows, size_t q_width, size_t k_width, size_t head,
+                 kr_buf wq, kr_buf wk, float eps) {
+    CHECK(c, head > 0 && head <= 256, "head_size must be in 1..=256");
+    BUF(qb, q, rows * q_width);
+    BUF(kb, k, rows * k_width);
+    BUF(wqb, wq, head);
+    BUF(wkb, wk, head);
+    HIPCHK(c, kr::launch_qk_norm(c->stream, qb->p, rows, q_width, head, wqb->p, eps, kb->p, k_width, wkb->p));
+    return KR_OK;
+}
+
 // y = C * conv(B * x) of one LFM2 decode row (k_conv_block_decode)
 int conv_block_decode(kr_ctx* c, kr_buf y, kr_buf bcx, kr_buf kernel, kr_buf state, size_t dim, size_t k) {
     CHECK(c, k >= 1, "conv kernel width must be positive");

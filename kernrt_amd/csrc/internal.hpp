@@ -73,6 +73,9 @@ int norm_project(kr_ctx* c, size_t layer, const int* projs, const kr_buf* ys, in
 bool swiglu_ok(kr_ctx* c, size_t layer, size_t dim);
 int norm_swiglu(kr_ctx* c, size_t layer, kr_buf x, kr_buf add, kr_buf w, kr_buf x_out, kr_buf h, size_t dim,
                 float eps);
+// kr_qk_norm of q and of k in one launch
+int qk_norm_pair(kr_ctx* c, kr_buf q, kr_buf k, size_t rows, size_t q_width, size_t k_width, size_t head,
+                 kr_buf wq, kr_buf wk, float eps);
 // y = C * conv(B * x) of one LFM2 decode row, bcx = [B | C | x]
 int conv_block_decode(kr_ctx* c, kr_buf y, kr_buf bcx, kr_buf kernel, kr_buf state, size_t dim, size_t k);
 // the projection of Q8(x) (x one f32 row of `width`)

@@ -1340,15 +1340,21 @@ hipError_t launch_rms_norm(hipStream_t st, float* out, const float* x, const flo
 // of the head's values are formed in parallel into LDS, one lane runs the
 // serial sum (the reference order), and the 16 lanes apply the scale to the
 // values they hold in registers.
+// Items 0 .. items1 - 1 are the heads of (v, width, w), the rest those of
+// (v2, width2, w2): q and k of a layer in one launch.
 __global__ __launch_bounds__(256) void k_qk_norm(float* __restrict__ v, uint32_t items, uint32_t width,
-                                                 uint32_t head, const float* __restrict__ w, float eps) {
+                                                 uint32_t head, const float* __restrict__ w, float eps,
+                                                 uint32_t items1, float* __restrict__ v2, uint32_t width2,
+                                                 const float* __restrict__ w2) {
     constexpr uint32_t MAXV = 16;  // values per lane: head <= 256
     extern __shared__ __align__(16) float sq[];  // [16 items][round4(head) + 4]
     __shared__ float s_scale[16];
-    const uint32_t heads = width / head, slot = threadIdx.x >> 4, l16 = threadIdx.x & 15;
+    const uint32_t slot = threadIdx.x >> 4, l16 = threadIdx.x & 15;
     const uint32_t stride = ((head + 3) & ~3u) + 4;
-    const uint32_t item = blockIdx.x * 16 + slot;
+    uint32_t item = blockIdx.x * 16 + slot;
     const bool live = item < items;
+    if (item >= items1) item -= items1, v = v2, width = width2, w = w2;
+    const uint32_t heads = width / head;
     float* hd = v + (size_t)(live ? item / heads : 0) * width + (size_t)(live ? item % heads : 0) * head;
     float* row = sq + slot * stride;
     float a[MAXV];
@@ -1375,13 +1381,14 @@ __global__ __launch_bounds__(256) void k_qk_norm(float* __restrict__ v, uint32_t
 }
 
 hipError_t launch_qk_norm(hipStream_t st, float* v, size_t rows, size_t width, size_t head, const float* w,
-                          float eps) {
-    size_t n = rows * (width / head);
+                          float eps, float* v2, size_t width2, const float* w2) {
+    const size_t n1 = rows * (width / head), n = n1 + (v2 ? rows * (width2 / head) : 0);
     if (n == 0) return hipSuccess;
     if (head > 256) return hipErrorInvalidValue;
     const size_t stride = ((head + 3) & ~(size_t)3) + 4;
     hipLaunchKernelGGL(k_qk_norm, dim3((unsigned)((n + 15) / 16)), dim3(256), 16 * stride * sizeof(float), st, v,
-                       (uint32_t)n, (uint32_t)width, (uint32_t)head, w, eps);
+                       (uint32_t)n, (uint32_t)width, (uint32_t)head, w, eps, (uint32_t)n1, v2 ? v2 : v,
+                       (uint32_t)(v2 ? width2 : width), v2 ? w2 : w);
     return hipGetLastError();
 }
 

@@ -73,8 +73,11 @@ hipError_t launch_project(hipStream_t st, int sem, const DevMatrix& w, QuantAct 
 
 hipError_t launch_rms_norm(hipStream_t st, float* out, const float* x, const float* w, size_t rows,
                            size_t dim, float eps);
+// per-head RMSNorm of the rows of v (width = heads * head); with v2 non-null
+// also those of v2 (width2, weight w2) in the same launch
 hipError_t launch_qk_norm(hipStream_t st, float* v, size_t rows, size_t width, size_t head,
-                          const float* w, float eps);
+                          const float* w, float eps, float* v2 = nullptr, size_t width2 = 0,
+                          const float* w2 = nullptr);
 // table: [n_pos][head_size/2] of (cos, sin)
 hipError_t launch_rope(hipStream_t st, float* q, float* k, size_t qw, size_t kvw, size_t rows,
                        const uint32_t* positions, const float2* table, size_t head_size, int interleaved);

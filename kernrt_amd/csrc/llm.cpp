@@ -209,8 +209,12 @@ int decode_step_fused(krl_model* m, size_t token, size_t pos, bool dev) {
             int qkv[3] = {KR_PROJ_Q, KR_PROJ_K, KR_PROJ_V};
             kr_buf ys[3] = {m->q, m->k, m->v};
             TRY(norm_then(pending, n.att, l, qkv, ys, 3));
-            if (n.has_q) KRC(m, kr_qk_norm(b, m->q, 1, g.q_dim, g.hs, n.q, g.eps));
-            if (n.has_k) KRC(m, kr_qk_norm(b, m->k, 1, g.kv_dim, g.hs, n.k, g.eps));
+            if (n.has_q && n.has_k) {
+                KRC(m, kri::qk_norm_pair(b, m->q, m->k, 1, g.q_dim, g.kv_dim, g.hs, n.q, n.k, g.eps));
+            } else {
+                if (n.has_q) KRC(m, kr_qk_norm(b, m->q, 1, g.q_dim, g.hs, n.q, g.eps));
+                if (n.has_k) KRC(m, kr_qk_norm(b, m->k, 1, g.kv_dim, g.hs, n.k, g.eps));
+            }
             if (split && pro) {
                 // rope + kv_write + attention in two launches; O quantizes its input
                 KRC(m, kri::rope_attention(b, m->q, m->k, m->v, m->attn, m->att, l, pos, dev ? s : nullptr, &g.as,
@@ -376,8 +380,12 @@ int prefill_rows(krl_model* m, const std::vector<Row>& rows) {
                 int qkv[3] = {KR_PROJ_Q, KR_PROJ_K, KR_PROJ_V};
                 kr_buf ys[3] = {p.q, p.k, p.v};
                 KRC(m, kri::project_q(b, l, qkv, ys, 3, n_tok));
-                if (n.has_q) KRC(m, kr_qk_norm(b, p.q, n_tok, g.q_dim, g.hs, n.q, g.eps));
-                if (n.has_k) KRC(m, kr_qk_norm(b, p.k, n_tok, g.kv_dim, g.hs, n.k, g.eps));
+                if (n.has_q && n.has_k) {
+                    KRC(m, kri::qk_norm_pair(b, p.q, p.k, n_tok, g.q_dim, g.kv_dim, g.hs, n.q, n.k, g.eps));
+                } else {
+                    if (n.has_q) KRC(m, kr_qk_norm(b, p.q, n_tok, g.q_dim, g.hs, n.q, g.eps));
+                    if (n.has_k) KRC(m, kr_qk_norm(b, p.k, n_tok, g.kv_dim, g.hs, n.k, g.eps));
+                }
                 KRC(m, kri::rope_kv(b, p.q, p.k, p.v, g.q_dim, g.kv_dim, n_tok, positions.data(), slots.data(), nullptr,
                                     l, &g.rs));
                 if (g.hs % 32 == 0) {

@@ -792,7 +792,7 @@ __global__ __launch_bounds__(kSwigluThreads) void k_gemv_swiglu(MatSet ms, GemvP
     int8_t* xq = (int8_t*)sm;
     uint32_t* xsb = (uint32_t*)(sm + n4);
     float* scratch = sm + ((n4 + nb + 3) & ~3u);
-    if (tid < 32) etab[tid] = kExp2Tab[tid];
+    const uint64_t etv = kExp2Tab[tid & 31];  // stored to LDS after every load is issued
 
     // 1. the producer's inputs first, so waiting for them never waits for the weights
     float4 va[VPT], vb[VPT], vw[VPT];
@@ -801,24 +801,31 @@ __global__ __launch_bounds__(kSwigluThreads) void k_gemv_swiglu(MatSet ms, GemvP
         vb[0] = pro.b ? ((const float4*)pro.b)[tid] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         vw[0] = ((const float4*)pro.w)[tid];
     }
-    // 2. the weight tile: chunk tid + NT u is (tile row, 16-byte column)
+    // 2. the weight tile: chunk tid + NT u is (tile row, 16-byte column). The
+    // two matrices' bases are read once (uniform) and selected per chunk: an
+    // argument array indexed per lane would be loaded from memory per lane.
     v4i wv[CPT];
     uint32_t wsb[CPT];
     {
+        const int8_t* const wq0 = ms.q[0];
+        const int8_t* const wq1 = ms.q[1];
+        const void* const ws0 = ms.s[0];
+        const void* const ws1 = ms.s[1];
         uint32_t row = tid / kc, col = tid - (tid / kc) * kc;
 #pragma unroll
         for (int u = 0; u < CPT; u++) {
             const bool in = tid + NT * u < C;
             const uint32_t rr = in ? row : RT - 1, cc = in ? col : kc - 1;
-            const int mi = rr >= 32 ? 1 : 0;
+            const bool up_row = rr >= 32;
             const uint32_t grow = 32 * t + (rr & 31);
-            wv[u] = __builtin_nontemporal_load((const v4i*)(ms.q[mi] + (size_t)grow * K + cc * 16));
-            wsb[u] = scale_bits(WF16, ms.s[mi], (size_t)grow * nb + (cc >> 1));
+            wv[u] = __builtin_nontemporal_load((const v4i*)((up_row ? wq1 : wq0) + (size_t)grow * K + cc * 16));
+            wsb[u] = scale_bits(WF16, up_row ? ws1 : ws0, (size_t)grow * nb + (cc >> 1));
             col += step_cols;
             row += step_rows;
             if (col >= kc) col -= kc, row += 1;
         }
     }
+    if (tid < 32) etab[tid] = etv;  // read after the producer's barriers
     // 3. the producer, while the weights are in flight
     gemv_produce<SEM, PRO_NORM, VPT>(pro, K, va, vb, vw, xq, xsb, scratch, &s_scale);
 

@@ -118,6 +118,17 @@ __device__ __forceinline__ float group_max32(float v) {
 // a + (a of the neighbouring lane l ^ 1): exact integer sum of a lane pair
 __device__ __forceinline__ int lane_pair_sum(int a) { return a + __builtin_amdgcn_mov_dpp(a, 0xB1, 0xf, 0xf, false); }
 
+// f32 -> IEEE binary16 bits, round to nearest even, as f32_to_f16_bits
+// (quant.rs:722-758): the hardware conversion gives the same bits for every
+// non-NaN input (all 2^32 inputs compared on gfx950); NaN keeps the software
+// routine's quiet-NaN pattern. A couple of instructions instead of a branchy
+// integer routine on the quantizers' critical path.
+__device__ __forceinline__ uint16_t f16_bits(float v) {
+    const uint32_t b = f2u(v);
+    const uint16_t hw = __builtin_bit_cast(uint16_t, (_Float16)v);
+    return (b & 0x7fffffffu) > 0x7f800000u ? (uint16_t)(((b >> 16) & 0x8000u) | 0x7e00u) : hw;
+}
+
 // Quantize one f32 value per lane as part of a 32-lane Q8 block (lanes
 // 32k..32k+31 hold one block), exactly as Q8Vec::quantize_into does
 // (quant.rs:864-873). Every lane of the half-wave must call this.
@@ -130,7 +141,7 @@ __device__ __forceinline__ void quant_lane(float v, bool valid, int8_t* q, float
         *q = q8_round(v * inv);
         if ((threadIdx.x & 31) == 0) {
             *s = d;
-            *h = f32_to_f16_bits(d);
+            *h = f16_bits(d);
         }
     }
 }
@@ -158,7 +169,7 @@ __global__ __launch_bounds__(256) void k_quantize(const float* __restrict__ x, s
         q[row * k + b * 32 + lane] = q8_round(v * inv);
         if (lane == 0) {
             s[blk] = d;
-            h[blk] = f32_to_f16_bits(d);
+            h[blk] = f16_bits(d);
         }
     }
 }
@@ -599,7 +610,7 @@ __device__ __forceinline__ void gemv_produce(const GemvPro& pro, uint32_t K, flo
             qq.z = q8_round(v.z * inv);
             qq.w = q8_round(v.w * inv);
             ((char4*)xq)[f] = qq;
-            if ((f & 7) == 0) xsb[f / 8] = XF16 ? (uint32_t)f32_to_f16_bits(d) : f2u(d);
+            if ((f & 7) == 0) xsb[f / 8] = XF16 ? (uint32_t)f16_bits(d) : f2u(d);
         }
     }
     __syncthreads();
@@ -2437,7 +2448,7 @@ __global__ __launch_bounds__(64 * NWAVES) void k_attn_rows(const float* __restri
             *(char2*)(qo + o) = qq;
             if ((lane & 15) == 0) {
                 so[o / 32] = d;
-                ho[o / 32] = f32_to_f16_bits(d);
+                ho[o / 32] = f16_bits(d);
             }
         }
     }
@@ -2835,7 +2846,7 @@ __global__ __launch_bounds__(256) void k_add_rms_quant(float* __restrict__ x, co
             ((char4*)(q + row * dim))[f] = qq;
             if ((f & 7) == 0) {
                 s[row * nb + f / 8] = d;
-                h[row * nb + f / 8] = f32_to_f16_bits(d);
+                h[row * nb + f / 8] = f16_bits(d);
             }
         }
     }
@@ -3263,7 +3274,7 @@ __global__ void k_synth_q8(int8_t* __restrict__ q, void* __restrict__ s, int f16
     float inv = d > 0.0f ? div_rn(1.0f, d) : 0.0f;
     for (int i = 0; i < 32; i++) q[b * 32 + i] = q8_round(v[i] * inv);
     if (f16)
-        ((uint16_t*)s)[b] = f32_to_f16_bits(d);
+        ((uint16_t*)s)[b] = f16_bits(d);
     else
         ((float*)s)[b] = d;
 }

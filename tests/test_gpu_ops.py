@@ -50,6 +50,21 @@ def test_quantize_is_bit_exact(hip, width):
         assert np.array_equal(h[r * nb:(r + 1) * nb], wh), f"row {r} f16 scales"
 
 
+def test_quantize_scales_across_the_f16_range(hip):
+    # block maxima from 2^-64 to 2^63 (random mantissas): the f16 scale bits
+    # cover zero, subnormal, normal and infinite results and their rounding
+    rng = np.random.default_rng(11)
+    nb = 128
+    m = 127.0 * np.exp2(np.arange(nb) - 64.0) * (1.0 + rng.uniform(0.0, 1.0, size=nb))
+    x = (np.repeat(m, 32) * rng.uniform(-1.0, 1.0, size=nb * 32)).astype(np.float32)
+    x[::32] = m.astype(np.float32)  # each block's max is its first element
+    q, s, h = hip.dbg_quantize(hip.upload(x), 1, nb * 32)
+    wq, ws, wh = O.quantize(x)
+    assert np.array_equal(q, wq)
+    assert_bits_equal(s, ws, "scales")
+    assert np.array_equal(h, wh), "f16 scales"
+
+
 SHAPES = [(1536, 576), (960, 960), (320, 960), (2560, 960), (960, 2560), (36, 8192), (100, 96)]
 
 

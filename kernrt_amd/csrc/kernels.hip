@@ -2008,10 +2008,15 @@ __global__ __launch_bounds__(1024) void k_attn_softmax_v(const float* __restrict
             }
         }
     }
-    // 2. exp with the head's max
+    // 2. exp with the head's max; the G heads of a position together, so a
+    // thread's exps are independent chains that overlap
+    for (uint32_t i = tid; i < count; i += T) {
+        float e[G];
 #pragma unroll
-    for (int j = 0; j < G; j++)
-        for (uint32_t i = tid; i < count; i += T) ps[j * scs + i] = glibc_expf(ps[j * scs + i] - mx[j], etab);
+        for (int j = 0; j < G; j++) e[j] = ps[j * scs + i];
+#pragma unroll
+        for (int j = 0; j < G; j++) ps[j * scs + i] = glibc_expf(e[j] - mx[j], etab);
+    }
     lds_barrier();
     // 3. softmax sum, left to right (elementwise.rs:81-91), one lane per head,
     // while waves 8-15 store the V slice transposed
@@ -2030,14 +2035,18 @@ __global__ __launch_bounds__(1024) void k_attn_softmax_v(const float* __restrict
         }
     }
     __syncthreads();
-    // 4. probabilities
+    // 4. probabilities, the G heads of a position together
+    float sj[G];
 #pragma unroll
-    for (int j = 0; j < G; j++) {
-        const float sj = s_sum[j];
-        for (uint32_t i = tid; i < count; i += T) {
-            const float pv = div_rn(ps[j * scs + i], sj);
-            ps[j * scs + i] = pv;
-            if (sidx == 0) att[(size_t)(hk * G + j) * seq_len + i] = pv;
+    for (int j = 0; j < G; j++) sj[j] = s_sum[j];
+    for (uint32_t i = tid; i < count; i += T) {
+        float pv[G];
+#pragma unroll
+        for (int j = 0; j < G; j++) pv[j] = div_rn(ps[j * scs + i], sj[j]);
+#pragma unroll
+        for (int j = 0; j < G; j++) {
+            ps[j * scs + i] = pv[j];
+            if (sidx == 0) att[(size_t)(hk * G + j) * seq_len + i] = pv[j];
         }
     }
     lds_barrier();  // the `att` stores need not complete first
@@ -2520,18 +2529,32 @@ __global__ __launch_bounds__(G * HS < 64 ? 64 : G * HS) void k_attn_softmax_v_ro
     }
     if (tid < 32) etab[tid] = kExp2Tab[tid];
     __syncthreads();
-    for (uint32_t t = tid; t < G * count; t += NT) {
-        const uint32_t j = t / count, i = t - j * count;
-        ps[j * scs + i] = glibc_expf(ps[j * scs + i] - s_max[j], etab);
+    // the G heads of a position together: independent exps (and divisions) per thread
+    float mj[G];
+#pragma unroll
+    for (int j = 0; j < G; j++) mj[j] = s_max[j];
+    for (uint32_t i = tid; i < count; i += NT) {
+        float e[G];
+#pragma unroll
+        for (int j = 0; j < G; j++) e[j] = ps[j * scs + i];
+#pragma unroll
+        for (int j = 0; j < G; j++) ps[j * scs + i] = glibc_expf(e[j] - mj[j], etab);
     }
     __syncthreads();
     if (tid < G) s_sum[tid] = chain_sum(ps + tid * scs, count);  // elementwise.rs:81-91
     __syncthreads();
-    for (uint32_t t = tid; t < G * count; t += NT) {
-        const uint32_t j = t / count, i = t - j * count;
-        const float pv = div_rn(ps[j * scs + i], s_sum[j]);
-        ps[j * scs + i] = pv;
-        att[(size_t)j * seq_len + i] = pv;  // the probabilities stay in `att`, as the reference leaves them
+    float sj[G];
+#pragma unroll
+    for (int j = 0; j < G; j++) sj[j] = s_sum[j];
+    for (uint32_t i = tid; i < count; i += NT) {
+        float pv[G];
+#pragma unroll
+        for (int j = 0; j < G; j++) pv[j] = div_rn(ps[j * scs + i], sj[j]);
+#pragma unroll
+        for (int j = 0; j < G; j++) {
+            ps[j * scs + i] = pv[j];
+            att[(size_t)j * seq_len + i] = pv[j];  // the probabilities stay in `att`, as the reference leaves them
+        }
     }
     // V tiles: piece f = (position f / F, float4 f % F)
     v4f pre[PT];

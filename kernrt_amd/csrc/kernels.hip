@@ -2397,7 +2397,8 @@ __global__ __launch_bounds__(64 * NWAVES) void k_attn_rows(const float* __restri
         float m = -INFINITY;
         for (uint32_t i = lane; i < n; i += 64) m = fmaxf(m, e[i]);
         m = wave_max(m);
-        for (uint32_t i = lane; i < n; i += 64) e[i] = glibc_expf(e[i] - m, etab);
+#pragma unroll 4
+        for (uint32_t i = lane; i < n; i += 64) e[i] = glibc_expf(e[i] - m, etab);  // independent: 4 in flight
     }
     __builtin_amdgcn_wave_barrier();
     if (lane < RPW) {  // sum left to right (elementwise.rs:81-91), one lane per pair
@@ -2413,6 +2414,7 @@ __global__ __launch_bounds__(64 * NWAVES) void k_attn_rows(const float* __restri
         const float sj = s_sum[rg];
         float* e = sc + rg * scs;
         float* arow = att + (size_t)(r0 + r) * n_heads * seq_len + (size_t)(h0 + j) * seq_len;
+#pragma unroll 4
         for (uint32_t i = lane; i < n; i += 64) {
             const float pv = div_rn(e[i], sj);
             e[i] = pv;

@@ -492,8 +492,9 @@ def main():
                          "captured HIP graphs (same kernels; for profilers that cannot trace graph launches)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (the design note in DESIGN.md "
-              "says how the projections would shard).", file=sys.stderr)
+        print("bench.py measures one GPU: this build has no multi-GPU path (every projection would "
+              "shard by output rows, with an all-gather of the f32 input rows in front of O and down, so that "
+              "each output's f32 chain stays on one GPU).", file=sys.stderr)
         sys.exit(2)
     import kernrt_amd as K
 

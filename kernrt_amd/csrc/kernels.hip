@@ -1877,6 +1877,16 @@ __global__ __launch_bounds__(64) void k_attn_scores(const float* __restrict__ q,
     const uint32_t count = n_shared + w.slot - w.att_start + 1;
     const uint32_t r0 = chunk * 64;
     if (r0 >= count && (chunk != 0 || !ROPE)) return;
+    // this lane's key row, issued first so that its latency overlaps the q
+    // and RoPE loads (the new position's key is replaced below by the one
+    // rotated here, so reading its cache slot before the write is harmless)
+    const uint32_t i = r0 + lane;
+    const bool live = i < count;
+    const uint32_t ic = live ? i : count - 1;
+    float4 kk[F];
+    const float4* krow = (const float4*)(kc + loff + (size_t)win_slot(w, n_shared, ic) * kv_dim + (size_t)hk * HS);
+#pragma unroll
+    for (uint32_t u = 0; u < F; u++) kk[u] = krow[u];
     const float* qh = q + (size_t)row * width + (size_t)hk * G * HS;
     if (!ROPE) {  // q is already rotated, and every key is in the cache
         for (uint32_t t = lane; t < G * F; t += 64) ((float4*)qs)[t] = ((const float4*)qh)[t];
@@ -1901,13 +1911,6 @@ __global__ __launch_bounds__(64) void k_attn_scores(const float* __restrict__ q,
         }
         if (r0 >= count) return;
     }
-    const uint32_t i = r0 + lane;
-    const bool live = i < count;
-    const uint32_t ic = live ? i : count - 1;
-    float4 kk[F];
-    const float4* krow = (const float4*)(kc + loff + (size_t)win_slot(w, n_shared, ic) * kv_dim + (size_t)hk * HS);
-#pragma unroll
-    for (uint32_t u = 0; u < F; u++) kk[u] = krow[u];
     if (ROPE && ic == count - 1) {  // the new position: its key is the one just rotated
 #pragma unroll
         for (uint32_t u = 0; u < F; u++) kk[u] = ((const float4*)kn)[u];

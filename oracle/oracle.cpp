@@ -521,7 +521,9 @@ static void rope_half(float* v, size_t len, size_t pos, size_t head_size, float 
 }
 
 // The buffer table, KV cache and the ops both scalar backends share verbatim
-// (copy, kv_write, add, mul, conv, silu_mul, rope, qk_norm, rms_norm).
+// (copy, kv_write, add, mul, conv, silu_mul); rms_norm, qk_norm and rope here
+// follow cpu.rs, and the Reference backend below overrides them with its own
+// transcription of reference.rs.
 class HostBackend : public Backend {
 protected:
     std::shared_ptr<const ModelWeights> w_;
@@ -570,13 +572,13 @@ public:
             std::memcpy(&vc_[at], &bufs_.at(v)[row * width], width * sizeof(float));
         }
     }
-    // cpu.rs:248-255 / reference.rs:161-178 (same arithmetic)
+    // cpu.rs:248-255 + rms_norm_row cpu.rs:633-644
     void rms_norm(Buf out, Buf x, Buf w, size_t rows, size_t dim, float eps) override {
         std::vector<float> wv = bufs_.at(w);
         for (size_t r = 0; r < rows; r++)
             rms_norm_row(&bufs_.at(out)[r * dim], &bufs_.at(x)[r * dim], wv.data(), dim, eps);
     }
-    // cpu.rs:647-661 / reference.rs:180-207
+    // cpu.rs:257-272 + qk_norm_row cpu.rs:647-661
     void qk_norm(Buf v, size_t rows, size_t width, size_t head, Buf w, float eps) override {
         std::vector<float> wv = bufs_.at(w);
         float* data = bufs_.at(v).data();
@@ -586,7 +588,7 @@ public:
                 rms_norm_row(hd, hd, wv.data(), head, eps);
             }
     }
-    // cpu.rs:274-302 / reference.rs:209-257
+    // cpu.rs:274-302 + rope_interleaved / rope_half cpu.rs:664-705
     void rope(Buf q, Buf k, size_t qw, size_t kvw, size_t rows, const size_t* positions,
               RopeSpec spec) override {
         for (size_t r = 0; r < rows; r++) {
@@ -751,6 +753,87 @@ public:
 class Reference : public HostBackend {
 public:
     const char* name() const override { return "reference"; }
+
+    // reference.rs:160-176, transcribed on its own (index arithmetic over the
+    // flat buffers) rather than through the cpu backend's rms_norm_row, so
+    // that cpu-vs-reference agreement checks one transcription against the other.
+    void rms_norm(Buf out, Buf x, Buf weight, size_t rows, size_t dim, float eps) override {
+        std::vector<float> w = bufs_.at(weight);
+        std::vector<float>& xi = bufs_.at(x);
+        for (size_t row = 0; row < rows; row++) {
+            size_t at = row * dim;
+            float ss = 0.0f;
+            for (size_t i = 0; i < dim; i++) ss += xi[at + i] * xi[at + i];
+            ss /= (float)dim;
+            ss += eps;
+            float scale = 1.0f / std::sqrt(ss);
+            std::vector<float>& o = bufs_.at(out);
+            for (size_t i = 0; i < dim; i++) o[at + i] = w[i] * (scale * xi[at + i]);
+        }
+    }
+
+    // reference.rs:178-207
+    void qk_norm(Buf v, size_t rows, size_t width, size_t head_size, Buf weight, float eps) override {
+        std::vector<float> w = bufs_.at(weight);
+        std::vector<float>& data = bufs_.at(v);
+        for (size_t row = 0; row < rows; row++) {
+            size_t base = row * width;
+            for (size_t head = 0; head < width / head_size; head++) {
+                size_t at = base + head * head_size;
+                float ss = 0.0f;
+                for (size_t i = 0; i < head_size; i++) ss += data[at + i] * data[at + i];
+                ss /= (float)head_size;
+                ss += eps;
+                float scale = 1.0f / std::sqrt(ss);
+                for (size_t i = 0; i < head_size; i++) data[at + i] = w[i] * (scale * data[at + i]);
+            }
+        }
+    }
+
+    // reference.rs:209-257
+    void rope(Buf q, Buf k, size_t q_width, size_t kv_width, size_t rows, const size_t* positions,
+              RopeSpec spec) override {
+        std::vector<float>& qv = bufs_.at(q);
+        std::vector<float>& kv = bufs_.at(k);
+        for (size_t row = 0; row < rows; row++) {
+            size_t pos = positions[row];
+            size_t qo = row * q_width, ko = row * kv_width;
+            if (spec.interleaved) {
+                for (size_t i = 0; i + 1 < q_width; i += 2) {
+                    size_t head_dim = i % spec.head_size;
+                    float freq = 1.0f / std::pow(spec.theta, (float)head_dim / (float)spec.head_size);
+                    float angle = (float)pos * freq;
+                    float sn = std::sin(angle), cs = std::cos(angle);
+                    float q0 = qv[qo + i], q1 = qv[qo + i + 1];
+                    qv[qo + i] = q0 * cs - q1 * sn;
+                    qv[qo + i + 1] = q0 * sn + q1 * cs;
+                    if (i < kv_width) {
+                        float k0 = kv[ko + i], k1 = kv[ko + i + 1];
+                        kv[ko + i] = k0 * cs - k1 * sn;
+                        kv[ko + i + 1] = k0 * sn + k1 * cs;
+                    }
+                }
+            } else {
+                size_t half = spec.head_size / 2;
+                std::vector<float>* vecs[2] = {&qv, &kv};
+                size_t bases[2] = {qo, ko}, widths[2] = {q_width, kv_width};
+                for (int s = 0; s < 2; s++) {
+                    std::vector<float>& vec = *vecs[s];
+                    for (size_t head = 0; head < widths[s] / spec.head_size; head++) {
+                        size_t at = bases[s] + head * spec.head_size;
+                        for (size_t i = 0; i < half; i++) {
+                            float freq = 1.0f / std::pow(spec.theta, (float)(2 * i) / (float)spec.head_size);
+                            float angle = (float)pos * freq;
+                            float sn = std::sin(angle), cs = std::cos(angle);
+                            float lo = vec[at + i], hi = vec[at + i + half];
+                            vec[at + i] = lo * cs - hi * sn;
+                            vec[at + i + half] = lo * sn + hi * cs;
+                        }
+                    }
+                }
+            }
+        }
+    }
 
     // reference.rs:259-274
     void project(size_t layer, Proj p, Buf x, Buf y, size_t rows) override {

@@ -60,9 +60,14 @@ const char* krl_last_error(const krl_model* m);
 /* forward(token, pos) -> logits (llama.rs:786-862, lfm2.rs:380-477). */
 int krl_forward(krl_model* m, size_t token, size_t pos, float* logits);
 /* prefill(tokens, start) -> logits of the last row (llama.rs:473-492,
- * lfm2.rs:481-498). Every storage runs batched here (the HIP kernels give
- * per-row results identical to the decode loop, so the reference's Q8_0
- * per-token fallback is not needed). */
+ * lfm2.rs:481-498). Every storage runs batched here. For a Q8_0 model the
+ * reference loops forward() token by token instead; the batch gives that
+ * loop's values: Llama rows are independent apart from causal attention
+ * over the same cache, and an LFM2's conv layers take their history from the
+ * conv ring and advance it as the token loop would (so a chunked prefill or
+ * a prefill after decoding continues the ring). For q8_0x4 the LFM2 conv is
+ * the reference's batched one: zero history before the first row, then the
+ * last k - 1 rows copied into the ring's tail (lfm2.rs:587-603). */
 int krl_prefill(krl_model* m, const size_t* tokens, size_t n, size_t start, float* logits);
 /* prefill_multi / prefill_shared (llama.rs:552-647): sequences flattened,
  * `lens[i]` tokens each; one final-normed hidden row [dim] per sequence. */

@@ -1314,6 +1314,21 @@ int conv_block_decode(kr_ctx* c, kr_buf y, kr_buf bcx, kr_buf kernel, kr_buf sta
     return KR_OK;
 }
 
+// The conv of `rows` rows of x as if they were fed one at a time through
+// conv_decode (the ring supplies the history, then advances by `rows`).
+int conv_prefill_stepped(kr_ctx* c, kr_buf out, kr_buf x, kr_buf kernel, kr_buf state, size_t rows, size_t dim,
+                         size_t k) {
+    CHECK(c, k >= 1 && k <= 16, "conv kernel width %zu outside 1..16", k);
+    BUF(o, out, rows * dim);
+    BUF(xb, x, rows * dim);
+    BUF(kb, kernel, dim * k);
+    BUF(sb, state, (k - 1) * dim);
+    CHECK(c, out != x && out != state && x != state, "conv_prefill_stepped buffers must be distinct");
+    HIPCHK(c, kr::launch_conv_prefill(c->stream, o->p, xb->p, kb->p, rows, dim, k, sb->p));
+    HIPCHK(c, kr::launch_conv_ring_advance(c->stream, sb->p, xb->p, rows, dim, k));
+    return KR_OK;
+}
+
 // Decode gate/up of one row with the norm in front and SiLU(gate) * up + Q8
 // behind (k_gemv_swiglu): the down projection's input lands in the
 // activation workspace; h (f32) goes to `h`.

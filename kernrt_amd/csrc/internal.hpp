@@ -78,6 +78,10 @@ int qk_norm_pair(kr_ctx* c, kr_buf q, kr_buf k, size_t rows, size_t q_width, siz
                  kr_buf wq, kr_buf wk, float eps);
 // y = C * conv(B * x) of one LFM2 decode row, bcx = [B | C | x]
 int conv_block_decode(kr_ctx* c, kr_buf y, kr_buf bcx, kr_buf kernel, kr_buf state, size_t dim, size_t k);
+// conv of `rows` rows of x with the ring as their history, then the ring
+// advanced past them: the values of `rows` conv_decode steps in one launch
+int conv_prefill_stepped(kr_ctx* c, kr_buf out, kr_buf x, kr_buf kernel, kr_buf state, size_t rows, size_t dim,
+                         size_t k);
 // the projection of Q8(x) (x one f32 row of `width`)
 int quant_project(kr_ctx* c, size_t layer, int proj, kr_buf x, kr_buf y, size_t width);
 

@@ -3081,24 +3081,61 @@ hipError_t launch_silu_mul(hipStream_t st, float* g, const float* u, size_t n) {
     return hipGetLastError();
 }
 
-// Causal depthwise conv (cpu.rs:557-571).
+// Causal depthwise conv (cpu.rs:557-571). With `state` null, history below
+// row 0 is zero padding and its terms are skipped, as conv_rows does. With a
+// ring `state` (k - 1 rows, oldest first), row r reads ring row r + j where
+// conv_rows would read row r - (k - 1) + j < 0, and adds that term: exactly
+// what k_conv_decode computes when the rows are fed one at a time through the
+// ring (cpu.rs:469-492), which is how the reference's per-token prefill of a
+// Q8_0 LFM2 (lfm2.rs:490-495) sees them. The ring itself is advanced
+// afterwards by k_conv_ring_advance.
 __global__ void k_conv_prefill(float* __restrict__ out, const float* __restrict__ x,
-                               const float* __restrict__ kern, uint32_t rows, uint32_t dim, uint32_t k) {
+                               const float* __restrict__ kern, const float* __restrict__ state, uint32_t rows,
+                               uint32_t dim, uint32_t k) {
     size_t id = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (id >= (size_t)rows * dim) return;
     uint32_t r = id / dim, i = id % dim;
     float acc = 0.0f;
     for (uint32_t j = 0; j < k; j++) {
         long h = (long)r - ((long)k - 1) + (long)j;
-        if (h >= 0) acc += kern[(size_t)i * k + j] * x[(size_t)h * dim + i];
+        if (h >= 0)
+            acc += kern[(size_t)i * k + j] * x[(size_t)h * dim + i];
+        else if (state)
+            acc += kern[(size_t)i * k + j] * state[((size_t)r + j) * dim + i];
     }
     out[id] = acc;
 }
 hipError_t launch_conv_prefill(hipStream_t st, float* out, const float* x, const float* kern, size_t rows,
-                               size_t dim, size_t k) {
+                               size_t dim, size_t k, const float* state) {
     size_t n = rows * dim;
     if (n == 0) return hipSuccess;
-    hipLaunchKernelGGL(k_conv_prefill, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, out, x, kern,
+    hipLaunchKernelGGL(k_conv_prefill, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, out, x, kern, state,
+                       (uint32_t)rows, (uint32_t)dim, (uint32_t)k);
+    return hipGetLastError();
+}
+
+// The ring after `rows` rows of x have passed through it one at a time:
+// ring row m holds the row at time rows - (k - 1) + m of the series
+// [old ring; x]. One thread per column reads everything it needs before it
+// writes, so columns never interfere.
+__global__ void k_conv_ring_advance(float* __restrict__ state, const float* __restrict__ x, uint32_t rows,
+                                    uint32_t dim, uint32_t k) {
+    uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= dim) return;
+    constexpr uint32_t kMaxHist = 15;
+    const uint32_t hist = k - 1;
+    float nv[kMaxHist];
+    for (uint32_t m = 0; m < hist; m++) {
+        long t = (long)rows - (long)hist + (long)m;
+        nv[m] = t >= 0 ? x[(size_t)t * dim + i] : state[(size_t)((long)hist + t) * dim + i];
+    }
+    for (uint32_t m = 0; m < hist; m++) state[(size_t)m * dim + i] = nv[m];
+}
+hipError_t launch_conv_ring_advance(hipStream_t st, float* state, const float* x, size_t rows, size_t dim,
+                                    size_t k) {
+    if (dim == 0 || rows == 0 || k < 2) return hipSuccess;
+    if (k > 16) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_conv_ring_advance, dim3((unsigned)((dim + 255) / 256)), dim3(256), 0, st, state, x,
                        (uint32_t)rows, (uint32_t)dim, (uint32_t)k);
     return hipGetLastError();
 }

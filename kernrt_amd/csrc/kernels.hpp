@@ -118,8 +118,13 @@ hipError_t launch_copy(hipStream_t st, float* dst, const float* src, size_t n);
 // reads n floats (n % 4 == 0) and discards them; `sink` is never written in practice
 hipError_t launch_stream_read(hipStream_t st, const float* p, size_t n, int* sink);
 hipError_t launch_silu_mul(hipStream_t st, float* g, const float* u, size_t n);
+// causal depthwise conv of rows of x; history before row 0 is zero padding
+// (state null) or the ring `state` of k - 1 rows, oldest first
 hipError_t launch_conv_prefill(hipStream_t st, float* out, const float* x, const float* kernel,
-                               size_t rows, size_t dim, size_t k);
+                               size_t rows, size_t dim, size_t k, const float* state = nullptr);
+// the ring after `rows` rows of x have entered it one at a time (k <= 16)
+hipError_t launch_conv_ring_advance(hipStream_t st, float* state, const float* x, size_t rows, size_t dim,
+                                    size_t k);
 // y = C * conv(B * x) for one decode row, bcx = [B | C | x] (3 * dim), the
 // conv state shifted in place
 hipError_t launch_conv_block_decode(hipStream_t st, float* y, const float* bcx, const float* kern, float* state,

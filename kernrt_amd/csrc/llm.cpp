@@ -348,8 +348,33 @@ int ensure_prefill(krl_model* m, size_t n_tok) {
     return KR_OK;
 }
 
+// The conv of an LFM2 prefill, h = p.h -> p.co, and the ring it leaves.
+// Batched (lfm2.rs:587-603): zero history below the first row, then the last
+// k - 1 rows of h copied into the tail of the ring. Stepped: the values the
+// reference's per-token prefill of a Q8_0 model (lfm2.rs:490-495) produces,
+// i.e. conv_decode row by row through the ring, in one launch plus the ring
+// advance.
+int prefill_conv(krl_model* m, size_t l, size_t n_tok, bool stepped) {
+    kr_ctx* b = m->b;
+    PrefillBuffers& p = m->pb;
+    size_t dim = m->c.dim, k = m->conv_k[l];
+    if (stepped) {
+        KRC(m, kri::conv_prefill_stepped(b, p.co, p.h, (kr_buf)m->conv_kernels[l], (kr_buf)m->conv_state[l], n_tok,
+                                         dim, k));
+        return KR_OK;
+    }
+    KRC(m, kr_conv_prefill(b, p.co, p.h, (kr_buf)m->conv_kernels[l], n_tok, dim, k));
+    if (m->conv_state[l] >= 0) {
+        size_t take = std::min(n_tok, k - 1);
+        KRC(m, kr_copy(b, p.h, (n_tok - take) * dim, (kr_buf)m->conv_state[l], (k - 1 - take) * dim, take * dim));
+    }
+    return KR_OK;
+}
+
 // llama.rs:690-771, generalised with the LFM2 conv branch of lfm2.rs:559-632.
-int prefill_rows(krl_model* m, const std::vector<Row>& rows) {
+// `stepped_conv`: the conv layers reproduce a token-by-token prefill
+// (prefill_conv).
+int prefill_rows(krl_model* m, const std::vector<Row>& rows, bool stepped_conv = false) {
     kr_ctx* b = m->b;
     Geometry g = geometry(m->c);
     size_t n_tok = rows.size();
@@ -402,13 +427,7 @@ int prefill_rows(krl_model* m, const std::vector<Row>& rows) {
                 KRC(m, kri::project_q(b, l, ci, &p.bcx, 1, n_tok));
                 for (size_t r = 0; r < n_tok; r++)
                     KRC(m, kr_mul(b, p.h, r * g.dim, p.bcx, r * 3 * g.dim, p.bcx, r * 3 * g.dim + 2 * g.dim, g.dim));
-                size_t k = m->conv_k[l];
-                KRC(m, kr_conv_prefill(b, p.co, p.h, (kr_buf)m->conv_kernels[l], n_tok, g.dim, k));
-                if (m->conv_state[l] >= 0) {
-                    size_t take = std::min(n_tok, k - 1);
-                    KRC(m, kr_copy(b, p.h, (n_tok - take) * g.dim, (kr_buf)m->conv_state[l], (k - 1 - take) * g.dim,
-                                   take * g.dim));
-                }
+                TRY(prefill_conv(m, l, n_tok, stepped_conv));
                 for (size_t r = 0; r < n_tok; r++)
                     KRC(m, kr_mul(b, p.cy, r * g.dim, p.bcx, r * 3 * g.dim + g.dim, p.co, r * g.dim, g.dim));
                 KRC(m, kr_project(b, l, KR_PROJ_CONV_OUT, p.cy, p.o, n_tok));
@@ -441,13 +460,7 @@ int prefill_rows(krl_model* m, const std::vector<Row>& rows) {
             KRC(m, kr_project(b, l, KR_PROJ_CONV_IN, p.xb, p.bcx, n_tok));
             for (size_t r = 0; r < n_tok; r++)
                 KRC(m, kr_mul(b, p.h, r * g.dim, p.bcx, r * 3 * g.dim, p.bcx, r * 3 * g.dim + 2 * g.dim, g.dim));
-            size_t k = m->conv_k[l];
-            KRC(m, kr_conv_prefill(b, p.co, p.h, (kr_buf)m->conv_kernels[l], n_tok, g.dim, k));
-            if (m->conv_state[l] >= 0) {
-                size_t take = std::min(n_tok, k - 1);
-                KRC(m, kr_copy(b, p.h, (n_tok - take) * g.dim, (kr_buf)m->conv_state[l], (k - 1 - take) * g.dim,
-                               take * g.dim));
-            }
+            TRY(prefill_conv(m, l, n_tok, stepped_conv));
             for (size_t r = 0; r < n_tok; r++)
                 KRC(m, kr_mul(b, p.cy, r * g.dim, p.bcx, r * 3 * g.dim + g.dim, p.co, r * g.dim, g.dim));
             KRC(m, kr_project(b, l, KR_PROJ_CONV_OUT, p.cy, p.o, n_tok));
@@ -564,7 +577,12 @@ int krl_forward(krl_model* m, size_t token, size_t pos, float* logits) {
     return KR_OK;
 }
 
-// llama.rs:473-536 / lfm2.rs:481-640 (batched for every storage)
+// llama.rs:473-536 / lfm2.rs:481-640. Every storage runs batched. Where the
+// reference loops forward() per token instead (storages other than f32, bf16
+// and q8_0x4: here q8_0), the batch reproduces that loop's values: for Llama
+// the rows are independent apart from causal attention, which reads the same
+// cache either way; for LFM2 the conv layers take their history from the ring
+// (prefill_conv's stepped form) instead of zero padding.
 int krl_prefill(krl_model* m, const size_t* tokens, size_t n, size_t start, float* logits) {
     if (start + n > m->c.seq_len) return fail(m, "prefill runs past the context length");
     if (n == 0) {
@@ -573,7 +591,10 @@ int krl_prefill(krl_model* m, const size_t* tokens, size_t n, size_t start, floa
     }
     std::vector<Row> rows;
     for (size_t i = 0; i < n; i++) rows.push_back(Row{tokens[i], start + i, start + i, 0, 0, 0});
-    TRY(prefill_rows(m, rows));
+    const char* storage = kr_storage(m->b);
+    bool batched_in_reference =
+        !strcmp(storage, "f32") || !strcmp(storage, "bf16") || !strcmp(storage, "q8_0x4");  // lfm2.rs:489
+    TRY(prefill_rows(m, rows, m->lfm2 && !batched_in_reference));
     size_t dim = m->c.dim;
     KRC(m, kr_copy(m->b, m->pb.x, (n - 1) * dim, m->hidden, 0, dim));
     KRC(m, kr_rms_norm(m->b, m->xb, m->hidden, m->rms_final, 1, dim, m->c.rms_eps));

@@ -103,6 +103,7 @@ def lib():
         L.or_lfm2_new.argtypes = [C.POINTER(OracleConfig), vp, vp, C.c_char_p, C.POINTER(vp)]
         L.or_model_free.argtypes = [vp]
         L.or_model_kv_fill.argtypes = [vp, sz, C.c_uint64]
+        L.or_model_kv_upload.argtypes = [vp, C.c_int, sz, vp, sz]
         L.or_model_forward.argtypes = [vp, sz, sz, vp, sz]
         L.or_model_prefill.argtypes = [vp, vp, sz, sz, vp, sz]
         L.or_llama_prefill_multi.argtypes = [vp, vp, vp, sz, vp, sz]
@@ -475,6 +476,12 @@ class Model:
     def kv_fill(self, slots: int, seed: int):
         """Benchmark set-up: N(0,1) into cache slots [0, slots) of every layer."""
         _check(lib().or_model_kv_fill(self.h, slots, seed))
+
+    def kv_upload(self, which: int, offset: int, data):
+        """Test set-up: values into the key (0) or value (1) cache at an element
+        offset of [n_layers, seq_len, kv_dim]."""
+        d = np.ascontiguousarray(data, np.float32)
+        _check(lib().or_model_kv_upload(self.h, which, offset, _ptr(d), d.size))
 
     def forward(self, token: int, pos: int) -> np.ndarray:
         out = np.empty(self.config.vocab_size, np.float32)

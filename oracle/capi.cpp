@@ -327,6 +327,13 @@ int or_model_kv_fill(void* mp, size_t slots, uint64_t seed) {
     });
 }
 
+int or_model_kv_upload(void* mp, int which, size_t offset, const float* data, size_t len) {
+    return guard([&] {
+        OModel* m = (OModel*)mp;
+        set_kv(m->llama ? m->llama->backend() : m->lfm2->backend(), which, offset, data, len);
+    });
+}
+
 int or_model_forward(void* mp, size_t token, size_t pos, float* logits, size_t n) {
     return guard([&] {
         OModel* m = (OModel*)mp;

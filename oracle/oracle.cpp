@@ -644,6 +644,13 @@ public:
                 vc_[at] = nd(rng);
             }
     }
+    // test set-up: data into the key (which 0) or value (1) cache at an
+    // element offset of [n_layers, seq_len, kv_dim]
+    void set_kv(int which, size_t offset, const float* data, size_t len) {
+        std::vector<float>& c = which == 0 ? kc_ : vc_;
+        if (offset + len > c.size()) throw std::runtime_error("kv upload past the cache");
+        std::memcpy(&c[offset], data, len * sizeof(float));
+    }
     void silu_mul(Buf gate, Buf up, size_t len) override {
         float* g = bufs_.at(gate).data();
         const float* u = bufs_.at(up).data();
@@ -909,6 +916,9 @@ public:
 
 std::unique_ptr<Backend> make_cpu() { return std::unique_ptr<Backend>(new Cpu()); }
 void fill_kv(Backend& b, size_t slots, uint64_t seed) { dynamic_cast<HostBackend&>(b).fill_kv(slots, seed); }
+void set_kv(Backend& b, int which, size_t offset, const float* data, size_t len) {
+    dynamic_cast<HostBackend&>(b).set_kv(which, offset, data, len);
+}
 std::unique_ptr<Backend> make_reference() { return std::unique_ptr<Backend>(new Reference()); }
 
 // ---------------------------------------------------------------------------

@@ -183,6 +183,8 @@ std::unique_ptr<Backend> make_reference();
 // Benchmark set-up only: fill cache slots [0, slots) of every layer with
 // N(0, 1) draws (the cpu baseline starts decoding from a pre-filled cache).
 void fill_kv(Backend& b, size_t slots, uint64_t seed);
+// test set-up: raw values into the key (0) or value (1) cache
+void set_kv(Backend& b, int which, size_t offset, const float* data, size_t len);
 
 // arch/llm/llama.rs:26-67
 struct Config {

@@ -43,13 +43,21 @@ def gpu_model(c: "O.Config", w: "O.Weights", lfm2: bool = False):
     return K.Model(product_config(c), hip, product_weights(w), lfm2=lfm2)
 
 
-def gaussian_weights(c: "O.Config", storage: str, seed: int, lfm2_mask=None, tied: bool = True):
-    """N(0, 0.02) weights (the benchmark recipe) with unit norm weights."""
+def gaussian_weights(c: "O.Config", storage: str, seed: int, lfm2_mask=None, tied: bool = True,
+                     qk_norm: bool = False, norms: str = "ones"):
+    """N(0, 0.02) weights (the benchmark recipe). Norm weights are 1.0
+    (norms="ones") or U(0.5, 1.5) (norms="uniform"); with qk_norm the
+    attention layers get per-head q and k norm weights (Qwen3, LFM2)."""
     rng = np.random.default_rng(seed)
     dim, hidden = c.dim, c.hidden_dim
 
     def mat(rows, cols):
         return O.Matrix(rng.normal(0.0, 0.02, size=(rows, cols)).astype(np.float32), storage)
+
+    def norm(n):
+        if norms == "ones":
+            return np.ones(n, np.float32)
+        return rng.uniform(0.5, 1.5, size=n).astype(np.float32)
 
     w = O.Weights(c.n_layers)
     mask = lfm2_mask or [True] * c.n_layers
@@ -59,17 +67,20 @@ def gaussian_weights(c: "O.Config", storage: str, seed: int, lfm2_mask=None, tie
             w.set_proj(l, "k", mat(c.kv_dim, dim))
             w.set_proj(l, "v", mat(c.kv_dim, dim))
             w.set_proj(l, "o", mat(dim, c.q_dim))
+            if qk_norm:
+                w.set_norm(l, "q", norm(c.head_dim))
+                w.set_norm(l, "k", norm(c.head_dim))
         else:
             w.set_proj(l, "conv_in", mat(3 * dim, dim))
             w.set_proj(l, "conv_out", mat(dim, dim))
             w.set_conv(l, rng.normal(0.0, 0.2, size=(dim, 3)).astype(np.float32))
-        w.set_norm(l, "att", np.ones(dim, np.float32))
-        w.set_norm(l, "ffn", np.ones(dim, np.float32))
+        w.set_norm(l, "att", norm(dim))
+        w.set_norm(l, "ffn", norm(dim))
         w.set_proj(l, "gate", mat(hidden, dim))
         w.set_proj(l, "down", mat(dim, hidden))
         w.set_proj(l, "up", mat(hidden, dim))
     w.set_embedding(mat(c.vocab_size, dim))
-    w.set_final_norm(np.ones(dim, np.float32))
+    w.set_final_norm(norm(dim))
     w.set_classifier(None if tied else mat(c.vocab_size, dim))
     return w
 

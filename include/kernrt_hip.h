@@ -139,6 +139,20 @@ int kr_matmul(kr_ctx* ctx, kr_mat w, kr_buf x, kr_buf y, size_t rows);
 /* Cpu::logits arithmetic (cpu.rs:501-514) with `w` as the classifier. */
 int kr_classify(kr_ctx* ctx, kr_mat w, kr_buf x, kr_buf y);
 
+/* kr_matmul for callers that cannot allocate device memory (code being
+ * captured into a HIP graph, tight serving loops, harnesses that forbid
+ * hipMalloc). No counterpart in the reference. Same arguments and the same
+ * results as kr_matmul, but the quantized activations go to a fixed device
+ * array of kr_matmul_noalloc_max_elems() elements (4 Mi: 4.75 MiB with the
+ * scales) that each device holds from the first kr_open on it until the
+ * process ends, so the call itself makes no allocating call. Fails with
+ * KR_ERR_INVALID when rows * in_dim exceeds that limit. All calls on one
+ * device share the array: calls that overlap in time on one device (two
+ * contexts' streams, or two threads) race; calls on one context's stream
+ * are ordered and safe. */
+int kr_matmul_noalloc(kr_ctx* ctx, kr_mat w, kr_buf x, kr_buf y, size_t rows);
+size_t kr_matmul_noalloc_max_elems(void);
+
 /* The two halves of kr_matmul, as Cpu::project runs them (quantize_rows,
  * cpu.rs:143-158, then the batched kernel): quantize rows of x into the
  * context's activation workspace, then run the projection kernel on it. */

@@ -81,6 +81,8 @@ _SIGS = {
     "kr_silu_mul": (i32, [vp, u32, u32, sz]),
     "kr_logits": (i32, [vp, u32, u32]),
     "kr_matmul": (i32, [vp, u32, u32, u32, sz]),
+    "kr_matmul_noalloc": (i32, [vp, u32, u32, u32, sz]),
+    "kr_matmul_noalloc_max_elems": (sz, []),
     "kr_classify": (i32, [vp, u32, u32, u32]),
     "kr_quantize_rows": (i32, [vp, u32, sz, sz]),
     "kr_matmul_quantized": (i32, [vp, u32, u32, sz]),

@@ -302,6 +302,14 @@ class Hip:
     def matmul(self, mat: int, x: Buf, y: Buf, rows: int):
         self._ck(self._L.kr_matmul(self.ctx, mat, x, y, rows))
 
+    def matmul_noalloc(self, mat: int, x: Buf, y: Buf, rows: int):
+        """`matmul` through the entry point that allocates nothing
+        (kr_matmul_noalloc): rows * in_dim <= matmul_noalloc_max_elems()."""
+        self._ck(self._L.kr_matmul_noalloc(self.ctx, mat, x, y, rows))
+
+    def matmul_noalloc_max_elems(self) -> int:
+        return int(self._L.kr_matmul_noalloc_max_elems())
+
     def quantize_rows(self, x: Buf, rows: int, width: int):
         self._ck(self._L.kr_quantize_rows(self.ctx, x, rows, width))
 

@@ -15,6 +15,7 @@
 
 #include <array>
 #include <map>
+#include <mutex>
 #include <string>
 #include <utility>
 #include <vector>
@@ -59,11 +60,50 @@ struct RopeTable {
     size_t n_pos = 0;
 };
 
+// The activation workspace of kr_matmul_noalloc: a fixed device array, so
+// that entry point never allocates. Each device holds its own copy from the
+// first kr_open on it until the process ends. Host code must not pass
+// `scratch` itself to a kernel (in host code the name is a stand-in, not a
+// device address): kr_open looks up each device's address once, with that
+// device current, and every use goes through that pointer.
+constexpr size_t kNoAllocMaxElems = (size_t)4 << 20;  // rows * in_dim per call
+constexpr size_t kScratchQuants = kNoAllocMaxElems;                        // int8 [rows][K]
+constexpr size_t kScratchScales = kNoAllocMaxElems / 32 * sizeof(float);   // f32 [rows][K/32]
+constexpr size_t kScratchBits = kNoAllocMaxElems / 32 * sizeof(uint16_t);  // f16 bits [rows][K/32]
+constexpr size_t kScratchBytes = kScratchQuants + kScratchScales + kScratchBits;
+static_assert(kScratchQuants % 256 == 0 && kScratchScales % 256 == 0, "sections stay 256-byte aligned");
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+uint8_t* g_scratch_dev[kMaxDevices] = {};
+
+}  // namespace
+
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+namespace {
+
+// The device address of `scratch` on `device` (current), looked up once.
+hipError_t scratch_address(int device, uint8_t** out) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+    if (!g_scratch_dev[device]) {
+        void* p = nullptr;
+        hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        if (!p) return hipErrorInvalidSymbol;
+        g_scratch_dev[device] = (uint8_t*)p;
+    }
+    *out = g_scratch_dev[device];
+    return hipSuccess;
+}
+
 }  // namespace
 
 struct kr_ctx {
     int device = 0;
     hipStream_t stream = nullptr;
+    uint8_t* scratch = nullptr;  // this device's `scratch` array (kr_matmul_noalloc)
     std::string err;
     std::string devname;
     const char* storage = "f32";
@@ -420,7 +460,8 @@ int kr_open(int device, kr_ctx** out, char* detail, size_t detail_len) {
     if (hipSetDevice(device) != hipSuccess || hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess ||
         hipMalloc(&c->tokens, kr_ctx::kTokens * sizeof(uint32_t)) != hipSuccess ||
         hipMalloc(&c->counter, sizeof(unsigned int)) != hipSuccess ||
-        hipMemset(c->tokens, 0, kr_ctx::kTokens * sizeof(uint32_t)) != hipSuccess) {
+        hipMemset(c->tokens, 0, kr_ctx::kTokens * sizeof(uint32_t)) != hipSuccess ||
+        scratch_address(device, &c->scratch) != hipSuccess) {
         say("HIP device present but failed to start");
         kr_close(c);
         return KR_ERR_HIP;
@@ -838,6 +879,29 @@ int kr_matmul(kr_ctx* c, kr_mat w, kr_buf x, kr_buf y, size_t rows) {
     HIPCHK(c, kr::launch_project(c->stream, sem_for_project(m->m), m->m, act(c), rows, yb->p, m->m.n, nullptr));
     return KR_OK;
 }
+
+// kr_matmul with the activation quantization in this device's `scratch`
+// array: no hipMalloc, hipFree or other allocating call. The context's own
+// workspace (what kr_matmul_quantized reads) is left untouched.
+int kr_matmul_noalloc(kr_ctx* c, kr_mat w, kr_buf x, kr_buf y, size_t rows) {
+    Mat* m = mat_of(c, w);
+    CHECK(c, m != nullptr, "unknown matrix %u", (unsigned)w);
+    BUF(xb, x, rows * m->m.k);
+    BUF(yb, y, rows * m->m.n);
+    CHECK(c, rows <= kNoAllocMaxElems / m->m.k, "rows * in_dim = %zu * %zu exceeds the no-allocation limit of %zu",
+          rows, m->m.k, kNoAllocMaxElems);
+    CHECK(c, c->scratch != nullptr, "no scratch array on this device");
+    if (rows == 0) return KR_OK;
+    int8_t* q = (int8_t*)c->scratch;
+    float* s = (float*)(c->scratch + kScratchQuants);
+    uint16_t* h = (uint16_t*)(c->scratch + kScratchQuants + kScratchScales);
+    HIPCHK(c, kr::launch_quantize(c->stream, xb->p, rows, m->m.k, m->m.k, q, s, h));
+    HIPCHK(c, kr::launch_project(c->stream, sem_for_project(m->m), m->m, kr::QuantAct{q, s, h}, rows, yb->p, m->m.n,
+                                 nullptr));
+    return KR_OK;
+}
+
+size_t kr_matmul_noalloc_max_elems(void) { return kNoAllocMaxElems; }
 
 int kr_quantize_rows(kr_ctx* c, kr_buf x, size_t rows, size_t width) {
     CHECK(c, width % 32 == 0 && width > 0, "width must be a positive multiple of 32");

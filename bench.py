@@ -29,6 +29,10 @@ import numpy as np  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0
+# non-packed f32 VALU lane operations per second: 256 CUs x 4 SIMDs x 16 lanes
+# x 2.4 GHz. Every (row, column, block) of an exact Q8_0 GEMM costs 4 of them
+# (cvt, two multiplies, add), which bounds the prefill GEMM below the MFMA peak.
+VALU_LANE_OPS_PER_S = 256 * 4 * 16 * 2.4e9
 METRIC = "decode tok/s + Q8_0 GEMV HBM GB/s (% peak); prefill int8 MFMA util, 1 GPU"
 
 
@@ -280,50 +284,62 @@ def bench_gemv(K, reps: int = 3, use_graph: bool = True):
 
 def bench_prefill(K, reps: int = 2):
     """128-token Q8_0 prefill at 1.7B projection shapes (`configs[2]`): the
-    int8 MFMA GEMM kernels alone (activations quantized beforehand), and the
-    projections with their activation quantization, over all 24 layers."""
+    int8 MFMA GEMM launches the model's prefill issues per layer -- fused
+    q/k/v (one launch over 6144 rows), o, fused gate/up (16384 rows), down --
+    alone (activations quantized beforehand), and the projections with their
+    activation quantization, over all 24 layers' distinct matrices."""
     log("prefill: 128-row Q8_0 projections at 1.7B shapes")
     hip = K.open("hip")
     c = K.Config(**CFG3)
     m_rows = 128
-    shapes = [(c.q_dim, c.dim), (c.kv_dim, c.dim), (c.kv_dim, c.dim), (c.dim, c.q_dim), (c.hidden_dim, c.dim),
-              (c.hidden_dim, c.dim), (c.dim, c.hidden_dim)]
-    mats = [[hip.synthetic_matrix("q8_0", n, k, 5000 * l + i) for i, (n, k) in enumerate(shapes)]
-            for l in range(c.n_layers)]
+    groups = [("qkv", [(c.q_dim, c.dim), (c.kv_dim, c.dim), (c.kv_dim, c.dim)]), ("o", [(c.dim, c.q_dim)]),
+              ("gate_up", [(c.hidden_dim, c.dim), (c.hidden_dim, c.dim)]), ("down", [(c.dim, c.hidden_dim)])]
+    mats = [[[hip.synthetic_matrix("q8_0", n, k, 5000 * l + 10 * g + i) for i, (n, k) in enumerate(shapes)]
+             for g, (_, shapes) in enumerate(groups)] for l in range(c.n_layers)]
     rng = np.random.default_rng(4)
-    xs = {k: hip.upload(rng.normal(size=m_rows * k).astype(np.float32)) for k in {k for _, k in shapes}}
-    ys = {n: hip.alloc(m_rows * n) for n in {n for n, _ in shapes}}
+    ks = {k for _, shapes in groups for _, k in shapes}
+    xs = {k: hip.upload(rng.normal(size=m_rows * k).astype(np.float32)) for k in ks}
+    ys = [[hip.alloc(m_rows * n) for n, _ in shapes] for _, shapes in groups]
 
     def run():
         for l in range(c.n_layers):
-            for i, (n, k) in enumerate(shapes):
-                hip.matmul(mats[l][i], xs[k], ys[n], m_rows)
+            for g, (_, shapes) in enumerate(groups):
+                k = shapes[0][1]
+                hip.quantize_rows(xs[k], m_rows, k)
+                hip.matmul_quantized_set(mats[l][g], ys[g], m_rows)
 
     run()
     hip.synchronize()
     hip.timer_start()
     run()
     proj_ms = hip.timer_stop()
-    # GEMM kernels only: one shape at a time over the 24 layers' matrices
+    # GEMM kernels only: one launch group at a time over the 24 layers' matrices
     gemm_ms, per_shape = 0.0, {}
-    for i, (n, k) in enumerate(shapes):
+    for g, (name, shapes) in enumerate(groups):
+        k = shapes[0][1]
+        n = sum(nn for nn, _ in shapes)
         hip.quantize_rows(xs[k], m_rows, k)
         for l in range(c.n_layers):
-            hip.matmul_quantized(mats[l][i], ys[n], m_rows)
+            hip.matmul_quantized_set(mats[l][g], ys[g], m_rows)
         hip.synchronize()
         hip.timer_start()
         for _ in range(reps):
             for l in range(c.n_layers):
-                hip.matmul_quantized(mats[l][i], ys[n], m_rows)
+                hip.matmul_quantized_set(mats[l][g], ys[g], m_rows)
         ms = hip.timer_stop() / reps
         gemm_ms += ms
         us = ms * 1e3 / c.n_layers
-        per_shape[f"{n}x{k}"] = dict(avg_us=us, tops=2 * m_rows * n * k / (us * 1e-6) / 1e12,
-                                     weight_gbs=n * k * (1 + 4 / 32) / (us * 1e-6) / 1e9)
-    ops = 2 * m_rows * sum(n * k for n, k in shapes) * c.n_layers
+        valu_floor_us = m_rows * n * (k // 32) * 4 / VALU_LANE_OPS_PER_S * 1e6
+        per_shape[f"{name} {n}x{k}"] = dict(avg_us=us, tops=2 * m_rows * n * k / (us * 1e-6) / 1e12,
+                                           weight_gbs=n * k * (1 + 4 / 32) / (us * 1e-6) / 1e9,
+                                           valu_floor_us=valu_floor_us, frac_of_valu_floor=valu_floor_us / us)
+    ops = 2 * m_rows * sum(n * k for _, shapes in groups for n, k in shapes) * c.n_layers
     tops = ops / (gemm_ms * 1e-3) / 1e12
+    triples = m_rows * sum(n * k // 32 for _, shapes in groups for n, k in shapes) * c.n_layers
+    valu_floor_ms = triples * 4 / VALU_LANE_OPS_PER_S * 1e3
     hip.close()
     return dict(rows=m_rows, gemm_ms=gemm_ms, int8_tops=tops, mfma_util=tops / INT8_PEAK_TOPS, ops=ops,
+                valu_floor_ms=valu_floor_ms, frac_of_valu_floor=valu_floor_ms / gemm_ms,
                 projection_ms_with_quantize=proj_ms, per_shape=per_shape)
 
 

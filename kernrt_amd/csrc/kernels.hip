@@ -954,13 +954,12 @@ bool swiglu_fusable(const DevMatrix& gate, const DevMatrix& up) {
 // rows are padded by 16 bytes so that the fragment reads of 32 consecutive
 // rows spread over all banks. One barrier per chunk.
 //
-// Two workgroup shapes:
-//  * four partial sums (Q8_0, dot.rs:35-44, k_gemm_four16): t[b & 3] are
-//    independent chains, so they may run on different waves: a 32x32 output
-//    tile is split over 16 waves (four 16x16 sub-tiles x four chains); the
-//    chains meet in LDS and are summed in the reference order
-//    ((t0 + t1) + t2) + t3. This is a 4-way split of K that changes no
-//    rounding. KC = 8.
+// Two kernels:
+//  * four partial sums (Q8_0, dot.rs:35-44, k_gemm_q8): t[b & 3] are
+//    independent chains, so they run on different waves, each over a
+//    sub-tile of the workgroup's tile; the chains meet in LDS and are summed
+//    in the reference order ((t0 + t1) + t2) + t3. This is a 4-way split of
+//    K that changes no rounding. Tiles 64x128, 64x64 or 32x32 by grid size.
 //  * one FMA chain (Q8_0x4, quant.rs:276-288, k_gemm_chain, 4 waves): the
 //    chain is serial, so each wave owns its own 32x32 tile over all of K; the
 //    workgroup tile is 32x128 and the 4 waves share the activation chunk.
@@ -970,6 +969,10 @@ bool swiglu_fusable(const DevMatrix& gate, const DevMatrix& up) {
 // of weights run on one XCD and share its L2.
 typedef int v16i __attribute__((ext_vector_type(16)));
 static constexpr size_t kGemmMinRows = 8;
+// workgroups a 64 x 128 (64 x 64) tiling must give before the four-partial
+// GEMM uses it rather than a narrower one (256 CUs)
+static constexpr uint32_t kGemmWideTiles = 200;
+static constexpr uint32_t kGemmMidTiles = 160;
 // chunks each thread keeps in flight in registers (even: LDS buffer parity)
 static constexpr int kGemmStages = 4;
 
@@ -1036,110 +1039,202 @@ __device__ __forceinline__ void gemm_pipeline(uint32_t nchunks, Load&& gload, St
     }
 }
 
-// Q8_0 GEMM: the four partial sums on 16x16x32 int8 MFMA. A 32x32 output
-// tile is four 16x16 sub-tiles; 16 waves take (sub-tile, partial sum j)
-// each, so a tile keeps 16 independent chains in flight (4 waves per SIMD)
-// where 32x32 MFMAs with one wave per chain would leave one chain per SIMD
-// with every LDS and MFMA latency on its critical path. Operands are staged
-// as A and B chunks of KC blocks through double-buffered, padded LDS.
-//
-// 16x16x32 operand map: lane l feeds row (col) l % 16 of the A (B) tile with
-// bytes 8 * (l / 16) .. +8 of the block, the same byte map for both; its
-// accumulator v is output (row 4 * (l / 16) + v, col l % 16).
-template <int SEM, bool DBG>
-__global__ __launch_bounds__(1024) void k_gemm_four16(MatSet ms, QuantAct x, uint32_t M, uint32_t K,
-                                                      uint32_t mtiles, int32_t* __restrict__ dbg) {
-    constexpr int KC = 8, ROW = KC * 32 + 16, NS = kGemmStages;
-    __shared__ __align__(16) int8_t sA[2][32 * ROW];
-    __shared__ __align__(16) int8_t sB[2][32 * ROW];
-    __shared__ __align__(16) float sX[2][KC * 32];  // [block][row]
-    __shared__ __align__(16) float sW[2][KC * 32];  // [block][col]
+// Q8_0 GEMM, four partial sums (dot.rs:34-45), on 16x16x32 int8 MFMA. The
+// reference's four partial sums t[j] (blocks b with b % 4 == j, in order) are
+// independent chains, so they are the unit of work: a workgroup owns a TM x TN
+// output tile, and each of its waves runs CPW of the four chains over a
+// WM x WN sub-tile. Per block a wave reads one A fragment and four activation
+// scales per 16-row slice and one B fragment and one weight scale per
+// 16-column slice from LDS and reuses them across the other dimension, so the
+// LDS read traffic per output falls with the sub-tile size and the per-block
+// f32 epilogue (cvt, two multiplies, add: 4 VALU operations per output)
+// dominates the instruction stream. Chunks of KC blocks of the A and B rows
+// and their scales are staged through a double-buffered, padded LDS tile, NS
+// chunks ahead in registers. At the end the chains of every output meet --
+// in registers when one wave holds all four, else in LDS -- and are summed as
+// ((t0 + t1) + t2) + t3.
+template <int SEM, int TM, int TN, int WM, int WN, int CPW, int KC, int NS, int WPE, bool DBG>
+__global__ __launch_bounds__(64 * (TM / WM) * (TN / WN) * (4 / CPW), WPE) void k_gemm_q8(MatSet ms, QuantAct x,
+                                                                                 uint32_t M, uint32_t K,
+                                                                                 uint32_t mtiles,
+                                                                                 int32_t* __restrict__ dbg) {
+    constexpr int ROW = KC * 32 + 16, PPR = KC * 2, MI = WM / 16, NI = WN / 16, CG = 4 / CPW;
+    constexpr int SM = TM / WM, NSUB = SM * (TN / WN), NT = 64 * NSUB * CG;
+    constexpr int A_BYTES = TM * ROW, B_BYTES = TN * ROW;
+    constexpr int BUF_BYTES = A_BYTES + B_BYTES + KC * (TM + TN) * 4;
+    constexpr int PART_BYTES = CPW == 4 ? 0 : 4 * TM * TN * 4;
+    constexpr int LDS_BYTES = 2 * BUF_BYTES > PART_BYTES ? 2 * BUF_BYTES : PART_BYTES;
+    constexpr int NQ = (TM + TN) * PPR, NP = (NQ + NT - 1) / NT;  // 16-byte pieces per chunk, per thread
+    constexpr int NSC = ((TM + TN) * KC + NT - 1) / NT;  // scales per thread per chunk
+    static_assert(WM % 16 == 0 && WN % 16 == 0 && TM % WM == 0 && TN % WN == 0 && KC % 4 == 0, "tile shape");
+    static_assert(CPW == 1 || CPW == 2 || CPW == 4, "chains per wave");
+    static_assert(NT % PPR == 0, "a thread's pieces share their column");
+    __shared__ __align__(16) int8_t lds[LDS_BYTES];
+    auto sA = [&](int buf) { return lds + buf * BUF_BYTES; };
+    auto sB = [&](int buf) { return lds + buf * BUF_BYTES + A_BYTES; };
+    auto sX = [&](int buf) { return (float*)(lds + buf * BUF_BYTES + A_BYTES + B_BYTES); };  // [block][row]
+    auto sW = [&](int buf) { return sX(buf) + KC * TM; };                                     // [block][col]
+
     const uint32_t nb = K >> 5, nchunks = (nb + KC - 1) / KC;
-    const GemmPos p = gemm_pos(ms, mtiles, 32);
-    const int8_t* __restrict__ W = ms.q[p.mi];
-    const void* __restrict__ WS = ms.s[p.mi];
-    const uint32_t N = ms.n[p.mi];
+    const uint32_t L = xcd_tile(blockIdx.x, gridDim.x);
+    const uint32_t mt = L % mtiles, nt = L / mtiles;
+    const int mi_ = nt < ms.tile_end[0] ? 0 : (nt < ms.tile_end[1] ? 1 : 2);
+    const uint32_t m0 = mt * TM, n0 = (nt - (mi_ == 0 ? 0 : ms.tile_end[mi_ - 1])) * TN;
+    const int8_t* __restrict__ W = ms.q[mi_];
+    const void* __restrict__ WS = ms.s[mi_];
+    const uint32_t N = ms.n[mi_];
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t chain = wave & 3, sub = wave >> 2, sm = sub >> 1, sn = sub & 1;
+    const uint32_t cg = wave % CG, sub = wave / CG;                // chains cg*CPW .. +CPW-1
+    const uint32_t wm0 = (sub % SM) * WM, wn0 = (sub / SM) * WN;  // the wave's sub-tile
     const uint32_t r = lane & 15, quad = lane >> 4;
     constexpr bool WF16 = SEM == SEM_FOUR_PARTIALS_F16;
 
-    // loader map: threads 0..511 one 16-byte A piece (row t/16, column 16 (t%16)),
-    // 512..1023 the same for B; threads 0..255 one activation scale (row t/8,
-    // block t%8), 256..511 one weight scale. Rows past M or N read the last row.
-    const uint32_t lt = tid & 511, lr = lt >> 4, lc = (lt & 15) * 16;
-    const bool isB = tid >= 512;
-    const int8_t* g = isB ? W + (size_t)min(p.n0 + lr, N - 1) * K : x.q + (size_t)min(p.m0 + lr, M - 1) * K;
-    const uint32_t st_ = tid & 255, sr = st_ >> 3, sb = st_ & 7;
-    const bool isW = tid >= 256 && tid < 512, isS = tid < 512;
-    const float* gx = x.s + (size_t)min(p.m0 + sr, M - 1) * nb;
-    const size_t gw = (size_t)min(p.n0 + sr, N - 1) * nb;
+    // loader map: piece q = tid + NT i is the 16-byte piece (row q / PPR,
+    // column 16 (q % PPR)) of the A chunk for q < PPR TM, else of the B
+    // chunk; scale s = tid + NT i is an activation scale (row s / KC, block
+    // s % KC) for s < KC TM, else a weight scale. Rows past M or N read the
+    // last row, blocks past the row end its last block.
+    const int8_t* gp[NP];
+    uint32_t lp[NP];
+#pragma unroll
+    for (int i = 0; i < NP; i++) {
+        const uint32_t q = min(tid + NT * i, (uint32_t)NQ - 1), isb = q >= PPR * TM;
+        const uint32_t row = (isb ? q - PPR * TM : q) / PPR;
+        gp[i] = isb ? W + (size_t)min(n0 + row, N - 1) * K : x.q + (size_t)min(m0 + row, M - 1) * K;
+        lp[i] = (isb ? A_BYTES : 0) + row * ROW + (q % PPR) * 16;
+    }
+    const uint32_t pc = (tid % PPR) * 16;
 
     struct Stage {
-        v4i v;
-        uint32_t sc;
+        v4i p[NP];
+        uint32_t sc[NSC];
     };
     auto gload = [&](Stage& st, uint32_t c) {
         c = c < nchunks ? c : nchunks - 1;
-        const uint32_t col = min(c * KC * 32 + lc, K - 16);  // past the row end: a piece no block uses
-        st.v = *(const v4i*)(g + col);
-        const uint32_t blk = min(c * KC + sb, nb - 1);
-        st.sc = isS ? (isW ? scale_bits(WF16, WS, gw + blk) : f2u(gx[blk])) : 0u;
+        const uint32_t col = min(c * KC * 32 + pc, K - 16);  // past the row end: a piece no block uses
+#pragma unroll
+        for (int i = 0; i < NP; i++) st.p[i] = *(const v4i*)(gp[i] + col);
+#pragma unroll
+        for (int i = 0; i < NSC; i++) {
+            const uint32_t sidx = tid + NT * i;
+            const uint32_t blk = min(c * KC + sidx % KC, nb - 1);
+            if (sidx < KC * TM) {
+                st.sc[i] = f2u(x.s[(size_t)min(m0 + sidx / KC, M - 1) * nb + blk]);
+            } else if (sidx < KC * (TM + TN)) {
+                const uint32_t col2 = (sidx - KC * TM) / KC;
+                st.sc[i] = scale_bits(WF16, WS, (size_t)min(n0 + col2, N - 1) * nb + blk);
+            }
+        }
     };
     auto lstore = [&](const Stage& st, int buf) {
-        *(v4i*)((isB ? sB[buf] : sA[buf]) + lr * ROW + lc) = st.v;
-        if (isS) {
-            if (isW)
-                sW[buf][sb * 32 + sr] = scale_value(WF16, st.sc);
-            else
-                sX[buf][sb * 32 + sr] = u2f(st.sc);
+#pragma unroll
+        for (int i = 0; i < NP; i++)
+            if (NQ % NT == 0 || i + 1 < NP || tid + NT * i < NQ) *(v4i*)(sA(buf) + lp[i]) = st.p[i];
+#pragma unroll
+        for (int i = 0; i < NSC; i++) {
+            const uint32_t sidx = tid + NT * i, blk = sidx % KC;
+            if (sidx < KC * TM)
+                sX(buf)[blk * TM + sidx / KC] = u2f(st.sc[i]);
+            else if (sidx < KC * (TM + TN))
+                sW(buf)[blk * TN + (sidx - KC * TM) / KC] = scale_value(WF16, st.sc[i]);
         }
     };
 
-    float t[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float t[CPW][MI][NI][4];
+#pragma unroll
+    for (int c2 = 0; c2 < CPW; c2++)
+#pragma unroll
+        for (int i = 0; i < MI; i++)
+#pragma unroll
+            for (int j = 0; j < NI; j++)
+#pragma unroll
+                for (int v = 0; v < 4; v++) t[c2][i][j][v] = 0.0f;
     const v4i zero = {0, 0, 0, 0};
-    // wave (sub, chain j): blocks j and j + 4 of each chunk, chain t[j] in order
     auto compute = [&](int buf, uint32_t c) {
 #pragma unroll
-        for (int i = 0; i < KC / 4; i++) {
-            const uint32_t blk = chain + 4 * i, b = c * KC + blk;
-            if (b >= nb) break;
-            const long a = *(const long*)(sA[buf] + (sm * 16 + r) * ROW + blk * 32 + 8 * quad);
-            const long bq = *(const long*)(sB[buf] + (sn * 16 + r) * ROW + blk * 32 + 8 * quad);
-            const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, bq, zero, 0, 0, 0);
-            const float w = sW[buf][blk * 32 + sn * 16 + r];
-            const float4 xs = *(const float4*)(sX[buf] + blk * 32 + sm * 16 + 4 * quad);
-            if (DBG && p.n0 + sn * 16 + r < N) {
+        for (int h = 0; h < KC / 4; h++)
 #pragma unroll
-                for (int v = 0; v < 4; v++) {
-                    const uint32_t m = p.m0 + sm * 16 + 4 * quad + v;
-                    if (m < M) dbg[((size_t)m * N + p.n0 + sn * 16 + r) * nb + b] = d[v];
+            for (int c2 = 0; c2 < CPW; c2++) {
+                const uint32_t blk = cg * CPW + c2 + 4 * h, b = c * KC + blk;
+                if (b >= nb) break;
+                long a[MI], bq[NI];
+                float w[NI];
+                float4 xs[MI];
+#pragma unroll
+                for (int i = 0; i < MI; i++) {
+                    a[i] = *(const long*)(sA(buf) + (wm0 + i * 16 + r) * ROW + blk * 32 + 8 * quad);
+                    xs[i] = *(const float4*)(sX(buf) + blk * TM + wm0 + i * 16 + 4 * quad);
                 }
+#pragma unroll
+                for (int j = 0; j < NI; j++) {
+                    bq[j] = *(const long*)(sB(buf) + (wn0 + j * 16 + r) * ROW + blk * 32 + 8 * quad);
+                    w[j] = sW(buf)[blk * TN + wn0 + j * 16 + r];
+                }
+#pragma unroll
+                for (int i = 0; i < MI; i++)
+#pragma unroll
+                    for (int j = 0; j < NI; j++) {
+                        const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[i], bq[j], zero, 0, 0, 0);
+                        if (DBG) {
+                            const uint32_t n = n0 + wn0 + j * 16 + r;
+#pragma unroll
+                            for (int v = 0; v < 4; v++) {
+                                const uint32_t m = m0 + wm0 + i * 16 + 4 * quad + v;
+                                if (m < M && n < N) dbg[((size_t)m * N + n) * nb + b] = d[v];
+                            }
+                        }
+                        // dot.rs: t[b & 3] += (sa * sb) * (isum as f32)
+                        t[c2][i][j][0] += (w[j] * xs[i].x) * (float)d[0];
+                        t[c2][i][j][1] += (w[j] * xs[i].y) * (float)d[1];
+                        t[c2][i][j][2] += (w[j] * xs[i].z) * (float)d[2];
+                        t[c2][i][j][3] += (w[j] * xs[i].w) * (float)d[3];
+                    }
             }
-            // dot.rs: t[b & 3] += (sa * sb) * (isum as f32), with sa the weight scale
-            t[0] += (w * xs.x) * (float)d[0];
-            t[1] += (w * xs.y) * (float)d[1];
-            t[2] += (w * xs.z) * (float)d[2];
-            t[3] += (w * xs.w) * (float)d[3];
-        }
     };
 
     gemm_pipeline<NS, Stage>(nchunks, gload, lstore, compute);
 
-    float* part = (float*)&sA[0][0];  // [sub][chain][v][lane], after the last barrier
+    float* Y = ms.y[mi_];
+    const uint32_t ld = ms.ld[mi_];
+    if constexpr (CPW == 4) {
+        // one wave holds all four chains of its outputs
 #pragma unroll
-    for (int v = 0; v < 4; v++) part[((sub * 4 + chain) * 4 + v) * 64 + lane] = t[v];
-    __syncthreads();
-    float* Y = ms.y[p.mi];
-    const uint32_t ld = ms.ld[p.mi];
-    {
-        const uint32_t o = tid;  // (sub, v, lane): 4 * 4 * 64 = 1024 outputs
-        const uint32_t s2 = o >> 8, v = (o >> 6) & 3, l = o & 63;
-        const uint32_t m = p.m0 + (s2 >> 1) * 16 + 4 * (l >> 4) + v, n = p.n0 + (s2 & 1) * 16 + (l & 15);
-        if (m < M && n < N) {
-            auto at = [&](uint32_t j) { return part[((s2 * 4 + j) * 4 + v) * 64 + l]; };
-            Y[(size_t)m * ld + n] = ((at(0) + at(1)) + at(2)) + at(3);
+        for (int i = 0; i < MI; i++)
+#pragma unroll
+            for (int j = 0; j < NI; j++)
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    const uint32_t m = m0 + wm0 + i * 16 + 4 * quad + v, n = n0 + wn0 + j * 16 + r;
+                    if (m < M && n < N)
+                        Y[(size_t)m * ld + n] = ((t[0][i][j][v] + t[1][i][j][v]) + t[2][i][j][v]) + t[3][i][j][v];
+                }
+    } else {
+        // the chains meet in LDS: part[chain][sub][((i * NI + j) * 4 + v) * 64 + lane]
+        constexpr int WOUT = WM * WN;
+        float* part = (float*)lds;
+#pragma unroll
+        for (int c2 = 0; c2 < CPW; c2++)
+#pragma unroll
+            for (int i = 0; i < MI; i++)
+#pragma unroll
+                for (int j = 0; j < NI; j++)
+#pragma unroll
+                    for (int v = 0; v < 4; v++)
+                        part[((cg * CPW + c2) * NSUB + sub) * WOUT + ((i * NI + j) * 4 + v) * 64 + lane] =
+                            t[c2][i][j][v];
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < TM * TN / NT; k++) {
+            const uint32_t o = tid + NT * k, sb = o / WOUT, oo = o % WOUT;
+            const uint32_t l = oo & 63, v = (oo >> 6) & 3, ij = oo >> 8, i = ij / NI, j = ij % NI;
+            const uint32_t m = m0 + (sb % SM) * WM + i * 16 + 4 * (l >> 4) + v;
+            const uint32_t n = n0 + (sb / SM) * WN + j * 16 + (l & 15);
+            if (m < M && n < N) {
+                const float p0 = part[o], p1 = part[TM * TN + o], p2 = part[2 * TM * TN + o];
+                const float p3 = part[3 * TM * TN + o];
+                Y[(size_t)m * ld + n] = ((p0 + p1) + p2) + p3;
+            }
         }
     }
 }
@@ -1238,6 +1333,23 @@ __global__ __launch_bounds__(256, 2) void k_gemm_chain(MatSet ms, QuantAct x, ui
     }
 }
 
+template <int SEM, int TM, int TN, int WM, int WN, int CPW, int KC, int NS, int WPE>
+static void launch_q8(hipStream_t st, MatSet ms, QuantAct x, size_t rows, size_t k, int32_t* dbg) {
+    uint32_t total = 0;
+    for (int i = 0; i < 3; i++) {
+        if (i < ms.count) total += (uint32_t)((ms.n[i] + TN - 1) / TN);
+        ms.tile_end[i] = total;
+    }
+    const uint32_t mtiles = (uint32_t)((rows + TM - 1) / TM);
+    const dim3 grid(total * mtiles), block(64 * (TM / WM) * (TN / WN) * (4 / CPW));
+    if (dbg)
+        hipLaunchKernelGGL((k_gemm_q8<SEM, TM, TN, WM, WN, CPW, KC, NS, WPE, true>), grid, block, 0, st, ms, x,
+                           (uint32_t)rows, (uint32_t)k, mtiles, dbg);
+    else
+        hipLaunchKernelGGL((k_gemm_q8<SEM, TM, TN, WM, WN, CPW, KC, NS, WPE, false>), grid, block, 0, st, ms, x,
+                           (uint32_t)rows, (uint32_t)k, mtiles, dbg);
+}
+
 template <int SEM>
 static hipError_t gemm_launch(hipStream_t st, MatSet ms, size_t k, QuantAct x, size_t rows, int32_t* dbg) {
     const uint32_t cols = SEM == SEM_FMA_CHAIN ? 128 : 32;
@@ -1255,10 +1367,21 @@ static hipError_t gemm_launch(hipStream_t st, MatSet ms, size_t k, QuantAct x, s
         else
             hipLaunchKernelGGL(k_gemm_chain<false>, grid, dim3(256), 0, st, ms, x, m, kk, mtiles, dbg);
     } else {
-        if (dbg)
-            hipLaunchKernelGGL((k_gemm_four16<SEM, true>), grid, dim3(1024), 0, st, ms, x, m, kk, mtiles, dbg);
+        // the widest tile that still gives the grid enough workgroups: wider
+        // tiles stage fewer bytes per output (A and B rows are shared by more
+        // outputs) but give fewer, longer workgroups
+        uint32_t n128 = 0, n64 = 0;
+        for (int i = 0; i < ms.count; i++) {
+            n128 += (uint32_t)((ms.n[i] + 127) / 128);
+            n64 += (uint32_t)((ms.n[i] + 63) / 64);
+        }
+        const size_t m64 = (rows + 63) / 64;
+        if (rows >= 64 && m64 * n128 >= kGemmWideTiles)
+            launch_q8<SEM, 64, 128, 32, 64, 1, 8, 2, 1>(st, ms, x, rows, k, dbg);
+        else if (rows >= 64 && m64 * n64 >= kGemmMidTiles)
+            launch_q8<SEM, 64, 64, 32, 32, 1, 4, 4, 1>(st, ms, x, rows, k, dbg);
         else
-            hipLaunchKernelGGL((k_gemm_four16<SEM, false>), grid, dim3(1024), 0, st, ms, x, m, kk, mtiles, dbg);
+            launch_q8<SEM, 32, 32, 16, 16, 1, 8, 4, 1>(st, ms, x, rows, k, dbg);
     }
     return hipGetLastError();
 }

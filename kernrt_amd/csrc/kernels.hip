@@ -304,6 +304,42 @@ __device__ __forceinline__ float chain_sum(const float* __restrict__ e, uint32_t
     return s;
 }
 
+// Serial f32 sum s += e[i], i = 0..n-1 in order, run by one whole wave
+// (all 64 lanes call it; every lane gets the sum): lane L first loads
+// e[64 L .. 64 L + 63] into registers (all lanes at once, so the LDS round
+// trip is paid once), then the chain passes from lane to lane: every lane
+// adds its values to its running sum in order -- only lane L's is the
+// chain -- and a DPP wave_shr:1 move hands lane L's sum to lane L + 1 as its
+// start. Register-fed dependent adds run at ~4.5 clocks each against ~8-9
+// for an LDS-fed one-lane chain; a hand-off costs ~25 clocks, once per 64
+// values. e is 16-byte aligned LDS readable up to round4(n) (values past n
+// are read but never added), n <= 4096.
+__device__ __forceinline__ float wave_chain_sum(const float* __restrict__ e, uint32_t n) {
+    constexpr int VPL = 64;
+    const uint32_t lane = threadIdx.x & 63, base = lane * VPL, n4 = (n + 3) & ~3u;
+    float v[VPL];
+#pragma unroll
+    for (int u = 0; u < VPL / 4; u++) {
+        const float4 f = base + 4 * u < n4 ? *(const float4*)(e + base + 4 * u) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        v[4 * u] = f.x, v[4 * u + 1] = f.y, v[4 * u + 2] = f.z, v[4 * u + 3] = f.w;
+    }
+    const uint32_t full = n / VPL, rest = n - full * VPL;
+    float acc = 0.0f;
+    for (uint32_t L = 0; L < full; L++) {
+#pragma unroll
+        for (int k = 0; k < VPL; k++) acc += v[k];
+        if (L + 1 < full || rest)  // wave_shr:1 -- lane L + 1 continues from lane L
+            acc = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(acc), 0x138, 0xf, 0xf, false));
+    }
+    if (rest) {
+#pragma unroll
+        for (int k = 0; k < VPL; k++)
+            if ((uint32_t)k < rest) acc += v[k];
+        return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), full));
+    }
+    return full ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), full - 1)) : 0.0f;
+}
+
 // Serial f32 dot o += p[i] * v[i] (a rounded product, then a rounded add),
 // i = 0..n-1 in order, both operands 16-byte aligned LDS rows. 16 steps per
 // batch. While the dependent adds of batch b run, each add is paired with
@@ -576,11 +612,11 @@ __device__ __forceinline__ void gemv_produce(const GemvPro& pro, uint32_t K, flo
             }
         }
         __syncthreads();
-        if (tid == 0) {  // rms_norm_row (cpu.rs:635-641)
-            float ss = chain_sum(scratch, K);
+        if (tid < 64) {  // rms_norm_row (cpu.rs:635-641): the serial sum on wave 0
+            float ss = K <= 4096 ? wave_chain_sum(scratch, K) : chain_sum(scratch, K);
             ss = div_rn(ss, (float)K);
             ss += pro.eps;
-            *s_scale_p = div_rn(1.0f, sqrt_rn(ss));
+            if (tid == 0) *s_scale_p = div_rn(1.0f, sqrt_rn(ss));
         }
         __syncthreads();
         const float scale = *s_scale_p;
@@ -2144,9 +2180,12 @@ __global__ __launch_bounds__(1024) void k_attn_softmax_v(const float* __restrict
         for (int j = 0; j < G; j++) ps[j * scs + i] = glibc_expf(e[j] - mx[j], etab);
     }
     lds_barrier();
-    // 3. softmax sum, left to right (elementwise.rs:81-91), one lane per head,
+    // 3. softmax sum, left to right (elementwise.rs:81-91), one wave per head,
     // while waves 8-15 store the V slice transposed
-    if (tid < G) s_sum[tid] = chain_sum(ps + tid * scs, count);
+    if (wave < G) {
+        const float sj = wave_chain_sum(ps + wave * scs, count);
+        if (lane == 0) s_sum[wave] = sj;
+    }
     if (wave >= 8) {
         auto put = [&](uint32_t f, float4 v) {
             const uint32_t r = f / FV, c = 4 * (f - r * FV);

@@ -84,6 +84,7 @@ def synthetic_model(K, cfg: dict, storage: str, seed: int, qk_norm: bool = False
     emb = hip.synthetic_matrix(storage, c.vocab_size, c.dim, seed + 100_000)
     hip.bind_handles(emb, 0xFFFFFFFF, handles)
     model = K.Model(c, hip, None, lfm2=lfm2_attention is not None, layers=layers, rms_final=ones)
+    model.weight_handles = (emb, handles)  # for checkers that read the device bytes back
     return hip, model, c
 
 
@@ -436,47 +437,123 @@ def bench_cfg5(K, n_prompt: int = 2048, n_seq: int = 64, ctx: int = 1024, steps:
                 batch_kv_gbs=kv_bytes * steps / dt / 1e9)
 
 
-def bench_cpu_baseline(seconds_budget: float = 20.0):
-    """The oracle's cpu backend (the reference's x86 Q8_0x4 path) on 1 core:
-    cfg2 decode steps from a cache pre-filled to 512 positions."""
+def host_cpu():
+    """The host CPU model name and the cores this process may use."""
+    name = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    name = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except AttributeError:
+        usable = os.cpu_count()
+    return name, os.cpu_count(), usable
+
+
+def bench_cpu_baseline(K, gpu_first_tokens=None, decode_budget: float = 20.0, prefill_budget: float = 15.0):
+    """The oracle's cpu backend -- a C++ restatement of the reference's x86
+    path (Q8_0x4: quantize_rows + gemm_q8_0x4_batched, re-quantizing logits;
+    Q8_0: per-row quantize + dot_q8_0_scalar), built -O2 -ffp-contract=off,
+    scalar, no autovectorization -- on 1 core, on the very bytes the GPU legs
+    use: the synthetic weights and the pre-filled cache are generated on the
+    device with the decode / prefill legs' seeds and read back.
+
+    decode: greedy steps from the decode leg's token at position
+    512, bounded by `decode_budget` seconds; p10 and median step as the
+    reference's decode_rate harness reports (examples/decode_rate.rs:62-79),
+    and the first tokens checked against the GPU decode's.
+    prefill: one layer's seven Q8_0 projections at 128 rows
+    (layer 0 of the prefill leg's weights), the first call timed apart and
+    the best of the repeats that fit `prefill_budget`
+    (examples/prefill_rate.rs:98-119), scaled to the 24-layer model."""
     import oracle as O
-    log("cpu baseline: building the 360M-shaped Q8_0x4 model on the host")
-    c = O.Config(**CFG2)
-    rng = np.random.default_rng(9)
+    cpu_name, n_cpu, usable = host_cpu()
+    log("cpu baseline: reading the decode leg's weights and cache back from the device")
+    hip, model, c = synthetic_model(K, CFG2, "q8_0x4", seed=2)
+    hip.kv_synthetic(PREFILL_POS, seed=5)
+    token0 = int(np.random.default_rng(2).integers(0, c.vocab_size))
+    emb, handles = model.weight_handles
+    oc = O.Config(**CFG2)
     w = O.Weights(c.n_layers)
 
-    def mat(n, k):
-        return O.Matrix(rng.standard_normal(size=(n, k), dtype=np.float32) * np.float32(0.02), "q8_0x4")
+    def omat(h, n, k):
+        q, sc = hip.read_matrix(h, "q8_0x4", n, k)
+        return O.Matrix.from_q8_0x4_blocks(K.backends.q8_0x4_records(q, sc), n, k)
 
+    shapes = {"q": (c.q_dim, c.dim), "k": (c.kv_dim, c.dim), "v": (c.kv_dim, c.dim), "o": (c.dim, c.q_dim),
+              "gate": (c.hidden_dim, c.dim), "up": (c.hidden_dim, c.dim), "down": (c.dim, c.hidden_dim)}
     for l in range(c.n_layers):
-        for name, (n, k) in {"q": (c.q_dim, c.dim), "k": (c.kv_dim, c.dim), "v": (c.kv_dim, c.dim),
-                             "o": (c.dim, c.q_dim), "gate": (c.hidden_dim, c.dim), "up": (c.hidden_dim, c.dim),
-                             "down": (c.dim, c.hidden_dim)}.items():
-            w.set_proj(l, name, mat(n, k))
+        for name, (n, k) in shapes.items():
+            w.set_proj(l, name, omat(handles[l][name], n, k))
         w.set_norm(l, "att", np.ones(c.dim, np.float32))
         w.set_norm(l, "ffn", np.ones(c.dim, np.float32))
-    w.set_embedding(mat(c.vocab_size, c.dim))
+    w.set_embedding(omat(emb, c.vocab_size, c.dim))
     w.set_final_norm(np.ones(c.dim, np.float32))
     w.set_classifier(None)
-    model = O.Model(c, w, "cpu")
-    model.kv_fill(PREFILL_POS, 5)
+    cpu = O.Model(oc, w, "cpu")
+    per = PREFILL_POS * c.kv_dim
+    for l in range(c.n_layers):
+        for which in (0, 1):
+            cpu.kv_upload(which, l * c.seq_len * c.kv_dim, hip.kv_read(which, l * c.seq_len * c.kv_dim, per))
+    model.close()
+    hip.close()
     log("cpu baseline: timing decode steps on one core")
-    tok, n, t0 = 1, 0, time.perf_counter()
-    times = []
-    while True:
-        s = time.perf_counter()
-        logits = model.forward(tok, PREFILL_POS + n)
-        times.append(time.perf_counter() - s)
+    tok, toks, times, t0 = token0, [], [], time.perf_counter()
+    while len(times) < 300 and time.perf_counter() - t0 < decode_budget:
+        s0 = time.perf_counter()
+        logits = cpu.forward(tok, PREFILL_POS + len(times))
+        times.append(time.perf_counter() - s0)
         tok = O.argmax(logits)
-        n += 1
-        if time.perf_counter() - t0 > seconds_budget or n >= 64:
-            break
-    times.sort()
-    median = times[len(times) // 2]
+        toks.append(tok)
+    del cpu, w
+    st = sorted(times)
+    median, p10 = st[len(st) // 2], st[len(st) // 10]
+    check = gpu_first_tokens[:len(toks)] if gpu_first_tokens else []
+    match = bool(check) and toks[:len(check)] == list(check)
+
+    log("cpu baseline: one 1.7B layer's prefill projections on one core")
+    hip, pm, c3 = synthetic_model(K, CFG3, "q8_0", seed=7)
+    _, handles3 = pm.weight_handles
+    shapes3 = {"q": (c3.q_dim, c3.dim), "k": (c3.kv_dim, c3.dim), "v": (c3.kv_dim, c3.dim),
+               "o": (c3.dim, c3.q_dim), "gate": (c3.hidden_dim, c3.dim), "up": (c3.hidden_dim, c3.dim),
+               "down": (c3.dim, c3.hidden_dim)}
+    mats = {}
+    for name, (n, k) in shapes3.items():
+        q, sc = hip.read_matrix(handles3[0][name], "q8_0", n, k)
+        mats[name] = O.Matrix.from_q8_0(q.ravel(), sc.ravel(), n, k)
+    pm.close()
+    hip.close()
+    rng = np.random.default_rng(12)
+    xs = {k: rng.normal(size=(128, k)).astype(np.float32) for k in (c3.dim, c3.hidden_dim)}
+
+    def layer():
+        s0 = time.perf_counter()
+        for name, (n, k) in shapes3.items():
+            mats[name].project_cpu(xs[k])
+        return time.perf_counter() - s0
+
+    first = layer()
+    reps, t1 = [], time.perf_counter()
+    while len(reps) < 20 and time.perf_counter() - t1 + first < prefill_budget:
+        reps.append(layer())
+    best = min(reps) if reps else first
+    ops = 2 * 128 * sum(n * k for n, k in shapes3.values())
+    prefill = dict(tokens=128, layer_first_s=first, layer_best_s=best, layer_repeats=len(reps),
+                   tok_s_24_layers=128 / (best * c3.n_layers), gops=ops / best / 1e9)
     return dict(value=1.0 / median, unit="tok/s", cores=1, kind="port",
-                sample=f"{n} greedy decode steps of the cfg2 360M-shaped Q8_0x4 model at positions "
-                       f"{PREFILL_POS}-{PREFILL_POS + n - 1} (cache pre-filled), oracle cpu backend, 1 thread, "
-                       f"median step {median * 1e3:.1f} ms")
+                sample=f"{len(times)} greedy decode steps of the cfg2 360M-shaped Q8_0x4 model (the decode leg's "
+                       f"device-generated weights and cache, read back) from position {PREFILL_POS}, oracle cpu "
+                       f"backend (scalar C++ port of the reference's x86 path, g++ -O2, no autovectorization), "
+                       f"1 thread on {cpu_name} ({usable} of {n_cpu} cores usable); median step "
+                       f"{median * 1e3:.1f} ms, p10 {p10 * 1e3:.1f} ms",
+                host_cpu=cpu_name, nproc=n_cpu, cores_usable=usable, p10_tok_s=1.0 / p10,
+                median_ms=median * 1e3, steps=len(times), first_tokens=toks[:8],
+                first_tokens_match_gpu=match, tokens_compared=len(check), prefill=prefill)
 
 
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "k_gemv_q8_0_1p7b_decode_pmc.md")
@@ -502,7 +579,7 @@ def main():
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--skip-cpu", action="store_true")
-    ap.add_argument("--only", choices=["decode", "gemv", "prefill", "cfg4", "cfg5"], default=None)
+    ap.add_argument("--only", choices=["decode", "gemv", "prefill", "cfg4", "cfg5", "cpu"], default=None)
     ap.add_argument("--no-graph", action="store_true",
                     help="launch the decode step's and the GEMV passes' kernels directly instead of replaying "
                          "captured HIP graphs (same kernels; for profilers that cannot trace graph launches)")
@@ -533,7 +610,12 @@ def main():
         res["cfg5"] = bench_cfg5(K)
         log(f"cfg5: prefill {res['cfg5']['prefill_tok_s']:.0f} tok/s, batched decode "
             f"{res['cfg5']['batch_tok_s']:.0f} tok/s")
-    cpu = None if args.skip_cpu or args.only else bench_cpu_baseline()
+    if args.skip_cpu or (args.only and args.only != "cpu"):
+        cpu = None
+    else:
+        cpu = bench_cpu_baseline(K, res["decode"]["first_tokens"] if "decode" in res else None)
+        log(f"cpu baseline: {cpu['value']:.2f} tok/s on one core (first tokens match the GPU: "
+            f"{cpu['first_tokens_match_gpu']})")
 
     d, g, p = res.get("decode"), res.get("gemv"), res.get("prefill")
     line = {

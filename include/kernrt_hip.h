@@ -90,6 +90,10 @@ int kr_matrix_q8_0x4(kr_ctx* ctx, size_t out_dim, size_t in_dim, const void* blo
  * Matrix::from_f32_q8_0 / Q8_0x4::from_f32 (quant.rs:544-557, 124-164). */
 int kr_matrix_synthetic(kr_ctx* ctx, int storage, size_t out_dim, size_t in_dim, uint64_t seed,
                         float stddev, kr_mat* out);
+/* The f32 values kr_matrix_synthetic quantizes for (seed, stddev): element i
+ * of the flattened [out_dim, in_dim] matrix into out[i], i < n -- so a checker
+ * can quantize them the reference's way and compare with kr_matrix_read. */
+int kr_synthetic_values(kr_ctx* ctx, kr_buf out, size_t n, uint64_t seed, float stddev);
 int kr_matrix_free(kr_ctx* ctx, kr_mat m);
 
 /* Bind matrices into the model layout, then `prepare` (mod.rs:272). */
@@ -191,9 +195,16 @@ int kr_dbg_quantize(kr_ctx* ctx, kr_buf x, size_t rows, size_t width, int8_t* qu
  * x: out [rows][out_dim][in_dim/32], through the same dot code as kr_matmul. */
 int kr_dbg_block_dots(kr_ctx* ctx, kr_mat w, kr_buf x, size_t rows, int32_t* out);
 
+/* A device matrix as stored: row-major int8 quants [out_dim][in_dim] and the
+ * block scales [out_dim][in_dim/32] (f32 for Q8_0, f16 bits for Q8_0x4) --
+ * so a host checker can rebuild the reference's Matrix from the very bytes a
+ * kernel reads (e.g. the device-generated synthetic weights). */
+int kr_matrix_read(kr_ctx* ctx, kr_mat m, int8_t* quants, void* scales);
+
 /* ---- key/value cache access, for benchmarks that start from a filled cache */
 /* which: 0 keys, 1 values; element offset into [n_layers, seq_len, kv_dim]. */
 int kr_kv_upload(kr_ctx* ctx, int which, size_t offset, const float* data, size_t len);
+int kr_kv_read(kr_ctx* ctx, int which, size_t offset, float* out, size_t len);
 int kr_kv_synthetic(kr_ctx* ctx, size_t slots, uint64_t seed); /* N(0,1) into slots [0,slots) */
 
 /* ---- device-side helpers for on-device greedy decoding */

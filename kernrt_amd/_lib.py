@@ -56,6 +56,7 @@ _SIGS = {
     "kr_matrix_q8_0": (i32, [vp, sz, sz, vp, vp, C.POINTER(u32)]),
     "kr_matrix_q8_0x4": (i32, [vp, sz, sz, vp, C.POINTER(u32)]),
     "kr_matrix_synthetic": (i32, [vp, i32, sz, sz, C.c_uint64, C.c_float, C.POINTER(u32)]),
+    "kr_synthetic_values": (i32, [vp, u32, sz, C.c_uint64, C.c_float]),
     "kr_matrix_free": (i32, [vp, u32]),
     "kr_bind_embedding": (i32, [vp, u32]),
     "kr_bind_classifier": (i32, [vp, u32]),
@@ -96,6 +97,8 @@ _SIGS = {
     "kr_dbg_quantize": (i32, [vp, u32, sz, sz, vp, vp, vp]),
     "kr_dbg_block_dots": (i32, [vp, u32, u32, sz, vp]),
     "kr_kv_upload": (i32, [vp, i32, sz, vp, sz]),
+    "kr_kv_read": (i32, [vp, i32, sz, vp, sz]),
+    "kr_matrix_read": (i32, [vp, u32, vp, vp]),
     "kr_kv_synthetic": (i32, [vp, sz, C.c_uint64]),
     "kr_argmax": (i32, [vp, u32, sz, sz]),
     "kr_read_tokens": (i32, [vp, vp, sz]),

@@ -131,6 +131,23 @@ def _f32(a) -> np.ndarray:
     return np.ascontiguousarray(a, dtype=np.float32)
 
 
+def q8_0x4_records(quants: np.ndarray, scales_f16: np.ndarray) -> np.ndarray:
+    """The reference's Q8_0x4 storage (`Q8Block4`, quant.rs:113-118) of a
+    row-major int8 matrix [out_dim, in_dim] and its f16 scale bits
+    [out_dim, in_dim / 32]: (out_dim / 4) x (in_dim / 32) records of 136
+    bytes, {u16 scales[4]; i8 quants[128]} with quants[seg * 16 + r * 4 + lane]
+    = row 4 g + r, column 32 b + 4 seg + lane -- the inverse of the
+    de-interleave kr_matrix_q8_0x4 does on upload."""
+    n, k = quants.shape
+    g, nb = n // 4, k // 32
+    q = np.ascontiguousarray(quants, np.int8).reshape(g, 4, nb, 8, 4).transpose(0, 2, 3, 1, 4).reshape(g, nb, 128)
+    s = np.ascontiguousarray(scales_f16, np.uint16).reshape(g, 4, nb).transpose(0, 2, 1)
+    rec = np.empty((g, nb, 136), np.uint8)
+    rec[:, :, :8] = np.ascontiguousarray(s).view(np.uint8).reshape(g, nb, 8)
+    rec[:, :, 8:] = q.view(np.uint8)
+    return rec.ravel()
+
+
 def _p(a: np.ndarray):
     return a.ctypes.data_as(C.c_void_p)
 
@@ -366,6 +383,25 @@ class Hip:
     def kv_upload(self, which: int, offset: int, data):
         d = _f32(data).ravel()
         self._ck(self._L.kr_kv_upload(self.ctx, which, offset, _p(d), d.size))
+
+    def kv_read(self, which: int, offset: int, n: int) -> np.ndarray:
+        out = np.empty(n, np.float32)
+        self._ck(self._L.kr_kv_read(self.ctx, which, offset, _p(out), n))
+        return out
+
+    def synthetic_values(self, n: int, seed: int, stddev: float = 0.02) -> np.ndarray:
+        """The f32 values synthetic_matrix(seed, stddev) quantizes, flattened."""
+        b = self.alloc(n)
+        self._ck(self._L.kr_synthetic_values(self.ctx, b, n, seed, stddev))
+        return self.read(b, n)
+
+    def read_matrix(self, mat: int, storage: str, out_dim: int, in_dim: int):
+        """The device bytes of a matrix: int8 quants [out_dim, in_dim] and the
+        block scales (f32 for q8_0, f16 bits as uint16 for q8_0x4)."""
+        q = np.empty((out_dim, in_dim), np.int8)
+        s = np.empty((out_dim, in_dim // 32), np.float32 if storage == "q8_0" else np.uint16)
+        self._ck(self._L.kr_matrix_read(self.ctx, mat, _p(q), _p(s)))
+        return q, s
 
     def kv_synthetic(self, slots: int, seed: int):
         self._ck(self._L.kr_kv_synthetic(self.ctx, slots, seed))

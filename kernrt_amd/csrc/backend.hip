@@ -554,6 +554,12 @@ int kr_matrix_synthetic(kr_ctx* c, int storage, size_t n, size_t k, uint64_t see
     return KR_OK;
 }
 
+int kr_synthetic_values(kr_ctx* c, kr_buf out, size_t n, uint64_t seed, float stddev) {
+    BUF(ob, out, n);
+    HIPCHK(c, kr::launch_synthetic_values(c->stream, ob->p, n, seed, stddev));
+    return KR_OK;
+}
+
 int kr_matrix_free(kr_ctx* c, kr_mat h) {
     Mat* m = mat_of(c, h);
     CHECK(c, m != nullptr, "unknown matrix %u", (unsigned)h);
@@ -1036,6 +1042,25 @@ int kr_kv_upload(kr_ctx* c, int which, size_t offset, const float* data, size_t 
     CHECK(c, offset + len <= c->n_layers * c->seq_len * c->kv_dim, "cache range out of bounds");
     float* base = which == 0 ? c->kc : c->vc;
     HIPCHK(c, hipMemcpyAsync(base + offset, data, len * sizeof(float), hipMemcpyHostToDevice, c->stream));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    return KR_OK;
+}
+
+int kr_kv_read(kr_ctx* c, int which, size_t offset, float* out, size_t len) {
+    CHECK(c, c->prepared, "prepare() runs before any compute");
+    CHECK(c, offset + len <= c->n_layers * c->seq_len * c->kv_dim, "cache range out of bounds");
+    const float* base = which == 0 ? c->kc : c->vc;
+    HIPCHK(c, hipMemcpyAsync(out, base + offset, len * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    return KR_OK;
+}
+
+int kr_matrix_read(kr_ctx* c, kr_mat w, int8_t* quants, void* scales) {
+    Mat* m = mat_of(c, w);
+    CHECK(c, m != nullptr, "unknown matrix %u", (unsigned)w);
+    const size_t nk = m->m.n * m->m.k, ns = m->m.n * (m->m.k / 32) * (m->m.storage == KR_STORAGE_Q8_0 ? 4 : 2);
+    HIPCHK(c, hipMemcpyAsync(quants, m->m.q, nk, hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(c, hipMemcpyAsync(scales, m->m.s, ns, hipMemcpyDeviceToHost, c->stream));
     HIPCHK(c, hipStreamSynchronize(c->stream));
     return KR_OK;
 }

@@ -3512,6 +3512,17 @@ hipError_t launch_synthetic_q8(hipStream_t st, const DevMatrix& m, uint64_t seed
     return hipGetLastError();
 }
 
+// The f32 values k_synth_q8 quantizes (element i of the flattened matrix).
+__global__ void k_synth_values(float* __restrict__ out, size_t n, uint64_t seed, float stddev) {
+    size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) out[i] = normal_at(seed, i) * stddev;
+}
+hipError_t launch_synthetic_values(hipStream_t st, float* out, size_t n, uint64_t seed, float stddev) {
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_synth_values, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, out, n, seed, stddev);
+    return hipGetLastError();
+}
+
 __global__ void k_synth_normal(float* __restrict__ out, size_t n, uint64_t seed) {
     size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (i < n) out[i] = normal_at(seed, i);

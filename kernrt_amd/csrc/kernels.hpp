@@ -141,6 +141,8 @@ hipError_t launch_greedy_step(hipStream_t st, const float* logits, size_t n, uin
                               size_t ring_len);
 hipError_t launch_synthetic_q8(hipStream_t st, const DevMatrix& m, uint64_t seed, float stddev);
 hipError_t launch_synthetic_normal(hipStream_t st, float* out, size_t n, uint64_t seed);
+// the f32 values launch_synthetic_q8 quantizes, element i of the flattened matrix
+hipError_t launch_synthetic_values(hipStream_t st, float* out, size_t n, uint64_t seed, float stddev);
 // counts Q8_0x4 blocks whose max |q| is neither 0 nor 127
 hipError_t launch_requant_check(hipStream_t st, const DevMatrix& m, unsigned int* counter);
 // x86 `gemv_q8_0x4` re-quantization of every row into a Q8_0 matrix (quant.rs:232-235)

@@ -59,3 +59,20 @@ def test_unknown_backend_is_an_error():
     assert e.value.requested == "cuda" and e.value.detail is None
     assert "available" in str(e.value) and "hip" in str(e.value)
     assert kernrt_amd.available() == ["hip"]
+
+
+def test_q8_0x4_records_invert_the_upload_deinterleave():
+    # the host repack that turns the device layout (row-major int8 + f16 scale
+    # bits) back into the reference's 136-byte records (quant.rs:113-164)
+    import numpy as np
+    import kernrt_amd as K
+    import oracle as O
+    rng = np.random.default_rng(4)
+    n, k = 64, 96
+    m = O.Matrix(rng.normal(0, 0.02, size=(n, k)).astype(np.float32), "q8_0x4")
+    rec = m.q8_0x4_blocks().reshape(n // 4, k // 32, 136)
+    q, s = m.to_row_major()  # int8 [n*k] and the widened f32 scales
+    bits = rec[:, :, :8].copy().view(np.uint16).reshape(n // 4, k // 32, 4).transpose(0, 2, 1).reshape(n, k // 32)
+    assert np.array_equal(np.array([O.f16_scale_to_f32(int(b)) for b in bits.ravel()], np.float32), s)
+    got = K.backends.q8_0x4_records(q.reshape(n, k), bits)
+    assert np.array_equal(got, rec.ravel())

@@ -339,3 +339,22 @@ def test_argmax_tie_rule(hip):
     b = hip.upload(big)
     hip.argmax(b, big.size, 3)
     assert int(hip.read_tokens(4)[3]) == O.argmax(big) == 150000
+
+
+@pytest.mark.parametrize("storage", ["q8_0", "q8_0x4"])
+@pytest.mark.parametrize("shape", [(96, 960), (2560, 960), (2048, 8192)])
+def test_synthetic_weights_quantize_as_the_oracle(hip, storage, shape):
+    # the benchmarks' device-generated weights (kr_matrix_synthetic): the
+    # stored bytes equal the reference quantization (quant.rs:544-557,
+    # 124-164) of the very f32 values the generator drew
+    n, k = shape
+    mat = hip.synthetic_matrix(storage, n, k, 41)
+    vals = hip.synthetic_values(n * k, 41, 0.02).reshape(n, k)
+    om = O.Matrix(vals, storage)
+    q, s = hip.read_matrix(mat, storage, n, k)
+    if storage == "q8_0":
+        oq, os_ = om.q8_0_data()
+        assert np.array_equal(q.ravel(), oq) and np.array_equal(s.ravel().view(np.uint32), os_.view(np.uint32))
+    else:
+        assert np.array_equal(K.backends.q8_0x4_records(q, s), om.q8_0x4_blocks())
+    hip.free_matrix(mat)

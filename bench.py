@@ -344,6 +344,24 @@ def bench_prefill(K, reps: int = 2):
                 projection_ms_with_quantize=proj_ms, per_shape=per_shape)
 
 
+def bench_mfma_peak(K, workgroups: int = 2048, iters: int = 20000):
+    """The chip's dense int8 MFMA rate measured with a probe kernel (four
+    independent MFMAs in flight per wave, 8 workgroups of 4 waves per CU),
+    for the 32x32x32 instruction and for the 16x16x32 one the Q8_0 GEMM
+    issues -- the measured counterpart of the vendor's 5.0 POPS."""
+    hip = K.open("hip")
+    out = {}
+    for kind, name in ((0, "i32_32x32x32_i8"), (1, "i32_16x16x32_i8")):
+        hip.mfma_rate(kind, workgroups, 100)
+        hip.synchronize()
+        hip.timer_start()
+        ops = hip.mfma_rate(kind, workgroups, iters)
+        ms = hip.timer_stop()
+        out[name] = dict(tops=ops / (ms * 1e-3) / 1e12, ms=ms)
+    hip.close()
+    return out
+
+
 def bench_prefill_model(K, n_tokens: int = 128, reps: int = 5):
     """`configs[2]` end to end: a 128-token prefill of the synthetic
     SmolLM2-1.7B-shaped Llama with Q8_0 weights, seeded random token ids.
@@ -601,6 +619,7 @@ def main():
     if args.only in (None, "prefill"):
         res["prefill"] = bench_prefill(K)
         log(f"prefill: {res['prefill']['int8_tops']:.1f} TOPS in the GEMM kernels")
+        res["prefill"]["mfma_peak_measured"] = bench_mfma_peak(K)
         res["prefill"]["model"] = bench_prefill_model(K)
         log(f"prefill model: {res['prefill']['model']['tok_s']:.0f} tok/s")
     if args.only in (None, "cfg4"):

@@ -172,6 +172,13 @@ int kr_matmul_quantized_set(kr_ctx* ctx, const kr_mat* w, const kr_buf* y, int n
  * benchmarks. No counterpart in the reference. */
 int kr_stream_read(kr_ctx* ctx, kr_buf src, size_t offset, size_t len);
 
+/* An int8 MFMA throughput probe for benchmarks (no counterpart in the
+ * reference): `workgroups` x 4 waves, each keeping four independent int8 MFMAs
+ * in flight for `iters` rounds (kind 0: v_mfma_i32_32x32x32_i8, kind 1:
+ * v_mfma_i32_16x16x32_i8); *ops gets the int8 operations issued. Time it with
+ * kr_timer_start / kr_timer_stop to measure the chip's dense int8 rate. */
+int kr_mfma_rate(kr_ctx* ctx, int kind, size_t workgroups, size_t iters, double* ops);
+
 /* Launch capture: the ops issued between kr_capture_begin and
  * kr_capture_end are recorded into one HIP graph instead of running (so
  * their inputs must stay alive and unchanged); kr_replay launches that

@@ -56,6 +56,7 @@ _SIGS = {
     "kr_matrix_q8_0": (i32, [vp, sz, sz, vp, vp, C.POINTER(u32)]),
     "kr_matrix_q8_0x4": (i32, [vp, sz, sz, vp, C.POINTER(u32)]),
     "kr_matrix_synthetic": (i32, [vp, i32, sz, sz, C.c_uint64, C.c_float, C.POINTER(u32)]),
+    "kr_mfma_rate": (i32, [vp, i32, sz, sz, C.POINTER(C.c_double)]),
     "kr_synthetic_values": (i32, [vp, u32, sz, C.c_uint64, C.c_float]),
     "kr_matrix_free": (i32, [vp, u32]),
     "kr_bind_embedding": (i32, [vp, u32]),

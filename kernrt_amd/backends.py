@@ -389,6 +389,12 @@ class Hip:
         self._ck(self._L.kr_kv_read(self.ctx, which, offset, _p(out), n))
         return out
 
+    def mfma_rate(self, kind: int, workgroups: int, iters: int) -> float:
+        """Launch the int8 MFMA probe (kr_mfma_rate); returns the ops issued."""
+        ops = C.c_double()
+        self._ck(self._L.kr_mfma_rate(self.ctx, kind, workgroups, iters, C.byref(ops)))
+        return ops.value
+
     def synthetic_values(self, n: int, seed: int, stddev: float = 0.02) -> np.ndarray:
         """The f32 values synthetic_matrix(seed, stddev) quantizes, flattened."""
         b = self.alloc(n)

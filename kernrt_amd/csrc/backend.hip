@@ -554,6 +554,15 @@ int kr_matrix_synthetic(kr_ctx* c, int storage, size_t n, size_t k, uint64_t see
     return KR_OK;
 }
 
+int kr_mfma_rate(kr_ctx* c, int kind, size_t workgroups, size_t iters, double* ops) {
+    CHECK(c, kind == 0 || kind == 1, "MFMA kind %d", kind);
+    CHECK(c, workgroups > 0 && workgroups <= (1u << 20) && iters > 0 && iters < (1u << 31), "probe size");
+    int rc = ensure_tmp(c, workgroups * 256);
+    if (rc) return rc;
+    HIPCHK(c, kr::launch_mfma_spin(c->stream, kind, (int*)c->tmp, workgroups, (uint32_t)iters, ops));
+    return KR_OK;
+}
+
 int kr_synthetic_values(kr_ctx* c, kr_buf out, size_t n, uint64_t seed, float stddev) {
     BUF(ob, out, n);
     HIPCHK(c, kr::launch_synthetic_values(c->stream, ob->p, n, seed, stddev));

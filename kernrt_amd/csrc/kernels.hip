@@ -3512,6 +3512,43 @@ hipError_t launch_synthetic_q8(hipStream_t st, const DevMatrix& m, uint64_t seed
     return hipGetLastError();
 }
 
+// int8 MFMA throughput probe for benchmarks: every wave keeps four
+// independent accumulators in flight through `iters` rounds of the int8 MFMA
+// of the kind asked (0: 32x32x32, 1: 16x16x32, the one the Q8_0 GEMM uses);
+// the sums go to `sink` so the work is not removed.
+template <int KIND>
+__global__ __launch_bounds__(256) void k_mfma_spin(int* __restrict__ sink, uint32_t iters) {
+    const int t = (int)threadIdx.x;
+    int s = 0;
+    if (KIND == 0) {
+        const v4i a = {t, t + 1, t + 2, t + 3}, b = {3 * t, t ^ 5, t + 7, 1};
+        v16i acc[4] = {};
+        for (uint32_t i = 0; i < iters; i++)
+#pragma unroll
+            for (int c = 0; c < 4; c++) acc[c] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, acc[c], 0, 0, 0);
+#pragma unroll
+        for (int c = 0; c < 4; c++) s += acc[c][c];
+    } else {
+        const long a = (long)t * 0x0101010101LL, b = (long)(t ^ 3) * 0x0303030303LL;
+        v4i acc[4] = {};
+        for (uint32_t i = 0; i < iters; i++)
+#pragma unroll
+            for (int c = 0; c < 4; c++) acc[c] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, acc[c], 0, 0, 0);
+#pragma unroll
+        for (int c = 0; c < 4; c++) s += acc[c][c];
+    }
+    sink[(size_t)blockIdx.x * blockDim.x + t] = s;
+}
+hipError_t launch_mfma_spin(hipStream_t st, int kind, int* sink, size_t blocks, uint32_t iters, double* ops) {
+    const double per = kind == 0 ? 2.0 * 32 * 32 * 32 : 2.0 * 16 * 16 * 32;  // int8 ops per instruction
+    *ops = per * 4 * iters * 4 * (double)blocks;  // 4 per round x 4 waves per workgroup
+    if (kind == 0)
+        hipLaunchKernelGGL(k_mfma_spin<0>, dim3((unsigned)blocks), dim3(256), 0, st, sink, iters);
+    else
+        hipLaunchKernelGGL(k_mfma_spin<1>, dim3((unsigned)blocks), dim3(256), 0, st, sink, iters);
+    return hipGetLastError();
+}
+
 // The f32 values k_synth_q8 quantizes (element i of the flattened matrix).
 __global__ void k_synth_values(float* __restrict__ out, size_t n, uint64_t seed, float stddev) {
     size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;

@@ -141,6 +141,9 @@ hipError_t launch_greedy_step(hipStream_t st, const float* logits, size_t n, uin
                               size_t ring_len);
 hipError_t launch_synthetic_q8(hipStream_t st, const DevMatrix& m, uint64_t seed, float stddev);
 hipError_t launch_synthetic_normal(hipStream_t st, float* out, size_t n, uint64_t seed);
+// int8 MFMA throughput probe: blocks x 256 threads, `iters` rounds; *ops = int8 ops issued;
+// sink holds blocks * 256 ints
+hipError_t launch_mfma_spin(hipStream_t st, int kind, int* sink, size_t blocks, uint32_t iters, double* ops);
 // the f32 values launch_synthetic_q8 quantizes, element i of the flattened matrix
 hipError_t launch_synthetic_values(hipStream_t st, float* out, size_t n, uint64_t seed, float stddev);
 // counts Q8_0x4 blocks whose max |q| is neither 0 nor 127

@@ -281,6 +281,29 @@ def test_attention_two_positions_by_hand(name):
     close(got, [p0 * 1 + (1 - p0) * 3, p0 * 2 + (1 - p0) * 4])
 
 
+def test_softmax_subtracts_the_maximum():
+    # elementwise.rs:81-91 subtracts the row maximum before exp: scores near 1000
+    # would overflow exp without it (e^1000 = inf in f32, inf / inf = NaN).
+    got = O.softmax(np.array([1000.0, 1001.0, 999.0], np.float32))
+    e = [math.exp(-1.0), 1.0, math.exp(-2.0)]
+    close(got, [v / sum(e) for v in e], rel=1e-6, abs_=0.0)
+
+
+@pytest.mark.parametrize("name", BACKENDS)
+def test_attention_large_scores_by_hand(name):
+    # q.k = 1000/sqrt 2 and 999/sqrt 2 after scaling: finite only when the
+    # maximum is taken out first
+    kc = np.array([[1000.0, 0.0], [999.0, 0.0]], np.float32)
+    vc = np.array([[1.0, 2.0], [3.0, 4.0]], np.float32)
+    got = attention_case(name, kc, vc, np.array([1.0, 0.0], np.float32), [(0, 1, 0, 0)], 1, 1, 2, 2, 4)
+    # scores are rounded to f32 (dot * (1 / sqrt hs), cpu.rs:591-609): at 700
+    # their ulp is 6e-5, so the hand computation takes the same roundings
+    scale = np.float32(1.0) / np.sqrt(np.float32(2.0))
+    d = float(np.float32(1000.0) * scale) - float(np.float32(999.0) * scale)
+    p0 = 1.0 / (1.0 + math.exp(-d))
+    close(got, [p0 * 1 + (1 - p0) * 3, p0 * 2 + (1 - p0) * 4], rel=1e-5, abs_=1e-6)
+
+
 @pytest.mark.parametrize("name", BACKENDS)
 def test_attention_grouped_heads_and_windows(name):
     # 4 cache rows, kv_dim 4 = two KV heads of 2; q has 4 heads (kv_mul 2):

@@ -94,6 +94,16 @@ int kr_matrix_synthetic(kr_ctx* ctx, int storage, size_t out_dim, size_t in_dim,
  * of the flattened [out_dim, in_dim] matrix into out[i], i < n -- so a checker
  * can quantize them the reference's way and compare with kr_matrix_read. */
 int kr_synthetic_values(kr_ctx* ctx, kr_buf out, size_t n, uint64_t seed, float stddev);
+/* Checkpoint weights quantized on the device: `data` holds out_dim rows of
+ * in_dim values, f32 (KR_SRC_F32) or bf16 bit patterns (KR_SRC_BF16, widened
+ * exactly as hf.rs:93-103 does), row-major, in host memory; the result is the
+ * matrix Matrix::from_f32_q8_0 (quant.rs:544-557) or Q8_0x4::from_f32
+ * (quant.rs:124-164) would build from those values, as matrix_from_raw
+ * (hf.rs:151-200) asks for it. Q8_0x4 needs out_dim % 4 == 0. */
+#define KR_SRC_F32 0
+#define KR_SRC_BF16 1
+int kr_matrix_quantize(kr_ctx* ctx, int storage, int src_kind, const void* data, size_t out_dim, size_t in_dim,
+                       kr_mat* out);
 int kr_matrix_free(kr_ctx* ctx, kr_mat m);
 
 /* Bind matrices into the model layout, then `prepare` (mod.rs:272). */

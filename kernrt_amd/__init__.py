@@ -2,12 +2,14 @@
 
 The compute lives in libkernrt_hip.so (hand-written HIP kernels behind the C
 ABI in include/kernrt_hip.h); this package is the thin host mirror of the
-reference's backend seam (`backends`) and model drivers (`llm`).
+reference's backend seam (`backends`), model drivers (`llm`) and checkpoint
+loaders (`safetensors`, `hf`).
 """
 
 from .backends import (AttnSpec, BackendError, Hip, KvSpec, LayerWeights, ModelWeights, Q8Matrix,
-                       RopeSpec, Window, available, from_env, open)
+                       RopeSpec, SourceMatrix, Window, available, from_env, open)
 from .llm import Config, Model
+from . import hf, safetensors
 
 __all__ = ["AttnSpec", "BackendError", "Config", "Hip", "KvSpec", "LayerWeights", "Model", "ModelWeights",
-           "Q8Matrix", "RopeSpec", "Window", "available", "from_env", "open"]
+           "Q8Matrix", "RopeSpec", "SourceMatrix", "Window", "available", "from_env", "hf", "open", "safetensors"]

@@ -12,6 +12,10 @@ import os
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libkernrt_hip.so")
 
+# kr_matrix_quantize source kinds (include/kernrt_hip.h)
+SRC_F32 = 0
+SRC_BF16 = 1
+
 sz = C.c_size_t
 vp = C.c_void_p
 u32 = C.c_uint32
@@ -56,6 +60,7 @@ _SIGS = {
     "kr_matrix_q8_0": (i32, [vp, sz, sz, vp, vp, C.POINTER(u32)]),
     "kr_matrix_q8_0x4": (i32, [vp, sz, sz, vp, C.POINTER(u32)]),
     "kr_matrix_synthetic": (i32, [vp, i32, sz, sz, C.c_uint64, C.c_float, C.POINTER(u32)]),
+    "kr_matrix_quantize": (i32, [vp, i32, i32, vp, sz, sz, C.POINTER(u32)]),
     "kr_mfma_rate": (i32, [vp, i32, sz, sz, C.POINTER(C.c_double)]),
     "kr_synthetic_values": (i32, [vp, u32, sz, C.c_uint64, C.c_float]),
     "kr_matrix_free": (i32, [vp, u32]),

@@ -109,6 +109,24 @@ class Q8Matrix:
 
 
 @dataclass
+class SourceMatrix:
+    """A checkpoint weight matrix in the storage the loader chose for it
+    (`matrix_from_raw`, hf.rs:151-200). `kind` is the reference's
+    `Matrix::kind()` (quant.rs:565-572): "q8_0" / "q8_0x4" carry the f32 values
+    or bf16 bit patterns they are quantized from, on the device, at upload
+    (`kr_matrix_quantize`); "f32" / "bf16" carry the values themselves, which
+    this backend does not hold."""
+    kind: str
+    out_dim: int
+    in_dim: int
+    values: np.ndarray  # flat float32, or uint16 bf16 bits
+
+    @property
+    def storage(self) -> str:
+        return self.kind
+
+
+@dataclass
 class LayerWeights:  # formats/llama2c.rs:49-76
     rms_att: np.ndarray
     rms_ffn: np.ndarray
@@ -196,9 +214,23 @@ class Hip:
         return buf.value.decode()
 
     # ---- weights
-    def upload_matrix(self, m: Q8Matrix) -> int:
+    def upload_matrix(self, m) -> int:
         h = C.c_uint32()
-        if m.storage == "q8_0":
+        if isinstance(m, SourceMatrix):
+            if m.kind not in ("q8_0", "q8_0x4"):
+                raise RuntimeError(f"the hip backend stores Q8_0/Q8_0x4 weights only, not {m.kind} "
+                                   "(KERNRT_Q8_0=1 or KERNRT_Q8_0X4=1 loads a checkpoint as Q8)")
+            v = m.values
+            if v.dtype == np.uint16:
+                src = _lib.SRC_BF16
+            else:
+                src, v = _lib.SRC_F32, _f32(v)
+            v = np.ascontiguousarray(v)
+            if v.size != m.out_dim * m.in_dim:
+                raise ValueError(f"matrix [{m.out_dim}, {m.in_dim}] given {v.size} values")
+            kind = STORAGE_Q8_0 if m.kind == "q8_0" else STORAGE_Q8_0X4
+            self._ck(self._L.kr_matrix_quantize(self.ctx, kind, src, _p(v), m.out_dim, m.in_dim, C.byref(h)))
+        elif m.storage == "q8_0":
             q = np.ascontiguousarray(m.quants, np.int8)
             s = _f32(m.scales)
             self._ck(self._L.kr_matrix_q8_0(self.ctx, m.out_dim, m.in_dim, _p(q), _p(s), C.byref(h)))

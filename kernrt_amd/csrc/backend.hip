@@ -13,6 +13,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
 #include <array>
 #include <map>
 #include <mutex>
@@ -544,6 +545,31 @@ int kr_matrix_q8_0x4(kr_ctx* c, size_t n, size_t k, const void* blocks, kr_mat* 
     HIPCHK(c, hipMemcpy(m->m.q, q.data(), q.size(), hipMemcpyHostToDevice));
     HIPCHK(c, hipMemcpy(m->m.s, s.data(), s.size() * sizeof(uint16_t), hipMemcpyHostToDevice));
     return KR_OK;
+}
+
+int kr_matrix_quantize(kr_ctx* c, int storage, int src_kind, const void* data, size_t n, size_t k, kr_mat* out) {
+    CHECK(c, src_kind == KR_SRC_F32 || src_kind == KR_SRC_BF16, "unknown source kind %d", src_kind);
+    CHECK(c, data != nullptr, "no source data");
+    Mat* m;
+    int rc = new_mat(c, storage, n, k, out, &m);
+    if (rc) return rc;
+    // rows go through a device staging buffer in chunks of about 64 MiB
+    const size_t esz = src_kind == KR_SRC_F32 ? 4 : 2, row_bytes = k * esz;
+    const size_t chunk = std::max<size_t>(1, (64u << 20) / row_bytes);
+    void* stage_dev = nullptr;
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    HIPCHK(c, hipMalloc(&stage_dev, std::min(chunk, n) * row_bytes));
+    int err = KR_OK;
+    for (size_t r0 = 0; r0 < n && err == KR_OK; r0 += chunk) {
+        const size_t rows = std::min(chunk, n - r0);
+        hipError_t e = hipMemcpy(stage_dev, (const uint8_t*)data + r0 * row_bytes, rows * row_bytes,
+                                 hipMemcpyHostToDevice);
+        if (e == hipSuccess) e = kr::launch_quant_weights(c->stream, m->m, r0, rows, stage_dev, src_kind == KR_SRC_BF16);
+        if (e == hipSuccess) e = hipStreamSynchronize(c->stream);  // the next chunk reuses the staging buffer
+        if (e != hipSuccess) err = fail(c, KR_ERR_HIP, "quantizing matrix [%zu, %zu]: %s", n, k, hipGetErrorString(e));
+    }
+    (void)hipFree(stage_dev);
+    return err;
 }
 
 int kr_matrix_synthetic(kr_ctx* c, int storage, size_t n, size_t k, uint64_t seed, float stddev, kr_mat* out) {

@@ -3505,6 +3505,51 @@ __global__ void k_synth_q8(int8_t* __restrict__ q, void* __restrict__ s, int f16
     else
         ((float*)s)[b] = d;
 }
+// Checkpoint weights to Q8 on the device: Matrix::from_f32_q8_0 (Q8Vec::quantize,
+// quant.rs:544-557, 856-874) and Q8_0x4::from_f32 (quant.rs:124-164) for rows
+// [row0, row0 + rows) of a matrix, from f32 values or from bf16 bits widened
+// exactly (bits << 16, hf.rs widen). One half-wave per 32-block, as k_quantize:
+// coalesced loads, the block amax by an order-free max reduction, then every
+// lane rounds its own element with the f32 reciprocal; Q8_0 keeps the f32 scale,
+// Q8_0x4 its f16 bits.
+template <bool BF16>
+__global__ __launch_bounds__(256) void k_quant_weights(const void* __restrict__ src, size_t blocks,
+                                                      int8_t* __restrict__ q, void* __restrict__ s, int f16) {
+    const size_t gid = (size_t)blockIdx.x * 256 + threadIdx.x;
+    const size_t blk = gid >> 5;
+    const int lane = threadIdx.x & 31;
+    const bool valid = blk < blocks;
+    const size_t e = valid ? blk * 32 + lane : 0;
+    const float v = BF16 ? u2f((uint32_t)((const uint16_t*)src)[e] << 16) : ((const float*)src)[e];
+    float m = fmaxf(0.0f, fabsf(v));
+    m = group_max32(m);
+    const float d = div_rn(m, 127.0f);
+    const float inv = d > 0.0f ? div_rn(1.0f, d) : 0.0f;
+    if (valid) {
+        q[e] = q8_round(v * inv);
+        if (lane == 0) {
+            if (f16)
+                ((uint16_t*)s)[blk] = f16_bits(d);
+            else
+                ((float*)s)[blk] = d;
+        }
+    }
+}
+hipError_t launch_quant_weights(hipStream_t st, const DevMatrix& m, size_t row0, size_t rows, const void* src,
+                                int bf16) {
+    const size_t nb = m.k / 32, blocks = rows * nb;
+    if (blocks == 0) return hipSuccess;
+    int8_t* q = m.q + row0 * m.k;
+    const int f16 = m.storage == kStorageQ8_0 ? 0 : 1;
+    void* s = f16 ? (void*)((uint16_t*)m.s + row0 * nb) : (void*)((float*)m.s + row0 * nb);
+    const dim3 grid((unsigned)((blocks * 32 + 255) / 256));
+    if (bf16)
+        hipLaunchKernelGGL(k_quant_weights<true>, grid, dim3(256), 0, st, src, blocks, q, s, f16);
+    else
+        hipLaunchKernelGGL(k_quant_weights<false>, grid, dim3(256), 0, st, src, blocks, q, s, f16);
+    return hipGetLastError();
+}
+
 hipError_t launch_synthetic_q8(hipStream_t st, const DevMatrix& m, uint64_t seed, float stddev) {
     size_t blocks = m.n * m.k / 32;
     hipLaunchKernelGGL(k_synth_q8, dim3((unsigned)((blocks + 255) / 256)), dim3(256), 0, st, m.q, m.s,

@@ -140,6 +140,9 @@ hipError_t launch_argmax(hipStream_t st, const float* x, size_t n, uint32_t* out
 hipError_t launch_greedy_step(hipStream_t st, const float* logits, size_t n, uint32_t* step, uint32_t* ring,
                               size_t ring_len);
 hipError_t launch_synthetic_q8(hipStream_t st, const DevMatrix& m, uint64_t seed, float stddev);
+// rows [row0, row0 + rows) of m quantized from f32 values or bf16 bits (src holds those rows only)
+hipError_t launch_quant_weights(hipStream_t st, const DevMatrix& m, size_t row0, size_t rows, const void* src,
+                                int bf16);
 hipError_t launch_synthetic_normal(hipStream_t st, float* out, size_t n, uint64_t seed);
 // int8 MFMA throughput probe: blocks x 256 threads, `iters` rounds; *ops = int8 ops issued;
 // sink holds blocks * 256 ints

@@ -97,3 +97,114 @@ def assert_bits_equal(got, want, what=""):
         gf, wf = np.asarray(got, np.float32).ravel(), np.asarray(want, np.float32).ravel()
         raise AssertionError(f"{what}: {bad.size} of {g.size} values differ; first at {i}: "
                              f"got {gf[i]!r} want {wf[i]!r}")
+
+
+# ---- checkpoint files for the loader tests ------------------------------------
+
+def st_image(tensors, metadata=None) -> bytes:
+    """A safetensors byte image: `tensors` maps name -> (dtype, shape, payload
+    bytes), laid out in order with 8-byte aligned data offsets."""
+    import json
+    header, data = {}, bytearray()
+    for name, (dtype, shape, payload) in tensors.items():
+        start = len(data)
+        data += payload
+        header[name] = {"dtype": dtype, "shape": list(shape), "data_offsets": [start, len(data)]}
+        data += b"\0" * (-len(data) % 8)
+    if metadata is not None:
+        header["__metadata__"] = metadata
+    hb = json.dumps(header).encode()
+    hb += b" " * (-len(hb) % 8)
+    return len(hb).to_bytes(8, "little") + hb + bytes(data)
+
+
+def st_encode(a: np.ndarray, dtype: str):
+    """(dtype, shape, payload) of an f32 array stored as F32, BF16 (rounded to
+    nearest even, as torch does) or F16."""
+    a = np.ascontiguousarray(a, np.float32)
+    if dtype == "F32":
+        return "F32", a.shape, a.tobytes()
+    if dtype == "F16":
+        return "F16", a.shape, a.astype("<f2").tobytes()
+    u = a.view(np.uint32).astype(np.uint64)
+    b = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    return "BF16", a.shape, b.tobytes()
+
+
+def st_decode(dtype: str, shape, payload: bytes) -> np.ndarray:
+    """The f32 values a loader reads back from st_encode's output."""
+    if dtype == "F32":
+        return np.frombuffer(payload, "<f4").reshape(shape).copy()
+    if dtype == "F16":
+        return np.frombuffer(payload, "<f2").astype(np.float32).reshape(shape)
+    b = np.frombuffer(payload, "<u2").astype(np.uint32) << 16
+    return b.view(np.float32).reshape(shape)
+
+
+def llama_tensors(c, tied=True, qk_norm=False, dtype="BF16", seed=3, drop=None):
+    rng = np.random.default_rng(seed)
+    t = {}
+
+    def put(name, shape, scale=0.02):
+        t[name] = st_encode(rng.normal(0, scale, size=shape).astype(np.float32), dtype)
+
+    put("model.embed_tokens.weight", (c.vocab_size, c.dim))
+    put("model.norm.weight", (c.dim,), 1.0)
+    for l in range(c.n_layers):
+        p = f"model.layers.{l}"
+        put(f"{p}.input_layernorm.weight", (c.dim,), 1.0)
+        put(f"{p}.post_attention_layernorm.weight", (c.dim,), 1.0)
+        put(f"{p}.self_attn.q_proj.weight", (c.q_dim, c.dim))
+        put(f"{p}.self_attn.k_proj.weight", (c.kv_dim, c.dim))
+        put(f"{p}.self_attn.v_proj.weight", (c.kv_dim, c.dim))
+        put(f"{p}.self_attn.o_proj.weight", (c.dim, c.q_dim))
+        put(f"{p}.mlp.gate_proj.weight", (c.hidden_dim, c.dim))
+        put(f"{p}.mlp.down_proj.weight", (c.dim, c.hidden_dim))
+        put(f"{p}.mlp.up_proj.weight", (c.hidden_dim, c.dim))
+        if qk_norm:
+            put(f"{p}.self_attn.q_norm.weight", (c.head_dim,), 1.0)
+            put(f"{p}.self_attn.k_norm.weight", (c.head_dim,), 1.0)
+    if not tied:
+        put("lm_head.weight", (c.vocab_size, c.dim))
+    t["model.rotary_emb.inv_freq"] = st_encode(np.ones(4, np.float32), "F32")  # ignored, as the reference does
+    if drop:
+        del t[drop]
+    return t
+
+
+def tiny_config(**kw):
+    from kernrt_amd.llm import Config
+    base = dict(dim=64, hidden_dim=128, n_layers=2, n_heads=4, n_kv_heads=2, vocab_size=96, seq_len=64,
+                rms_eps=1e-5, rope_theta=10000.0, rope_interleaved=False, head_dim=16)
+    base.update(kw)
+    return Config(**base)
+
+
+def lfm2_tensors(c, is_attn, dtype="F32", seed=4, conv_shape=None, k=3):
+    rng = np.random.default_rng(seed)
+    t = {}
+
+    def put(name, shape, scale=0.02):
+        t[name] = st_encode(rng.normal(0, scale, size=shape).astype(np.float32), dtype)
+
+    put("model.embed_tokens.weight", (c.vocab_size, c.dim))
+    put("model.embedding_norm.weight", (c.dim,), 1.0)
+    for l, attn in enumerate(is_attn):
+        p = f"model.layers.{l}"
+        if attn:
+            put(f"{p}.self_attn.q_proj.weight", (c.q_dim, c.dim))
+            put(f"{p}.self_attn.k_proj.weight", (c.kv_dim, c.dim))
+            put(f"{p}.self_attn.v_proj.weight", (c.kv_dim, c.dim))
+            put(f"{p}.self_attn.out_proj.weight", (c.dim, c.q_dim))
+            put(f"{p}.self_attn.q_layernorm.weight", (c.head_dim,), 1.0)
+            put(f"{p}.self_attn.k_layernorm.weight", (c.head_dim,), 1.0)
+        else:
+            put(f"{p}.conv.in_proj.weight", (3 * c.dim, c.dim))
+            put(f"{p}.conv.out_proj.weight", (c.dim, c.dim))
+            put(f"{p}.conv.conv.weight", conv_shape or (c.dim, 1, k), 0.2)
+        put(f"{p}.operator_norm.weight", (c.dim,), 1.0)
+        put(f"{p}.ffn_norm.weight", (c.dim,), 1.0)
+        put(f"{p}.feed_forward.w1.weight", (c.hidden_dim, c.dim))
+        put(f"{p}.feed_forward.w2.weight", (c.dim, c.hidden_dim))
+        put(f"{p}.feed_forward.w3.weight", (c.hidden_dim, c.dim))
+    return t

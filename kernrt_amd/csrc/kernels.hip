@@ -115,8 +115,22 @@ __device__ __forceinline__ float group_max32(float v) {
     v = group_max16(v);  // then lane ^ 16 within the 32-lane group (ds_swizzle bit mode)
     return fmaxf(v, __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F)));
 }
-// a + (a of the neighbouring lane l ^ 1): exact integer sum of a lane pair
-__device__ __forceinline__ int lane_pair_sum(int a) { return a + __builtin_amdgcn_mov_dpp(a, 0xB1, 0xf, 0xf, false); }
+// Two blocks' exact sums from one lane pair: for chunks u0 and u1 the even
+// lane holds the dots of the first 16 bytes of each block (d0, d1), the odd
+// lane those of the second 16 bytes. One swap gives the even lane block u0
+// and the odd lane block u1, so each lane finishes one block's epilogue
+// instead of both lanes of the pair repeating it.
+__device__ __forceinline__ int pair_blocks(int d0, int d1, bool even) {
+    const int recv = __builtin_amdgcn_mov_dpp(even ? d1 : d0, 0xB1, 0xf, 0xf, false);
+    return (even ? d0 : d1) + recv;
+}
+__device__ __forceinline__ int dot16(const v4i& w, const v4i& x) {
+    int acc = 0;
+    acc = __builtin_amdgcn_sdot4(w.x, x.x, acc, false);
+    acc = __builtin_amdgcn_sdot4(w.y, x.y, acc, false);
+    acc = __builtin_amdgcn_sdot4(w.z, x.z, acc, false);
+    return __builtin_amdgcn_sdot4(w.w, x.w, acc, false);
+}
 
 // f32 -> IEEE binary16 bits, round to nearest even, as f32_to_f16_bits
 // (quant.rs:722-758): the hardware conversion gives the same bits for every
@@ -192,12 +206,15 @@ hipError_t launch_quantize(hipStream_t st, const float* x, size_t rows, size_t k
 // bytes of the row-major int8 matrix. Thread t takes the 16-byte chunks
 // t, t+256, t+512, ... of the tile, so every wave load is 1 KiB, fully
 // coalesced. All of a thread's loads are issued before any is used -- its
-// weight chunks, the matching activation chunks and the two scales of each
-// chunk's block -- and none sits behind a branch, so a tile costs one memory
-// round trip. A lane pair holds one 32-byte Q8 block: each lane does four
-// v_dot4_i32_i8 on its half and the pair sums with one lane swap, so the
-// per-block i32 is exact. The even lane turns it into the reference's
-// epilogue operand and parks it in LDS; after one barrier the f32 chains run
+// weight chunks, the matching activation chunks and the two scales of the
+// blocks it finishes -- and none sits behind a branch, so a tile costs one
+// memory round trip. A lane pair holds the two 16-byte halves of a 32-byte
+// Q8 block: each lane does four v_dot4_i32_i8 on its half, so the per-block
+// i32 is exact. Chunks go in pairs (u0, u1): one lane swap hands the even
+// lane the whole of block u0 and the odd lane the whole of block u1, and
+// each lane turns its block into the reference's epilogue operand and parks
+// it in LDS (half the epilogue instructions of a pair in which both lanes
+// finish each block); after one barrier the f32 chains run
 // in the reference order: one lane per output for the FMA chain
 // (quant.rs:276-288), four lanes per output for the four partial sums
 // (dot.rs:35-44), which are joined as ((t0 + t1) + t2) + t3.
@@ -433,55 +450,57 @@ __global__ __launch_bounds__(256) void k_gemv(MatSet ms, QuantAct x, uint32_t K,
     // chunk tid + 256u sits at (row, col) of the tile; 256 chunks further is
     // (step_rows, step_cols) further, with carry
     uint32_t row = tid / kc, col = tid - (tid / kc) * kc;
+    // chunks 2v (even lane) and 2v + 1 (odd lane) are the blocks this lane
+    // finishes; only their scales are loaded
+    const bool even = (tid & 1) == 0;
     v4i wv[CPT], xv[CPT][M];
-    uint32_t wsb[CPT], xsb[CPT][M], rowu[CPT], blku[CPT];
+    uint32_t wsb[CPT / 2], xsb[CPT / 2][M], rowu[CPT / 2], blku[CPT / 2];
 #pragma unroll
     for (int u = 0; u < CPT; u++) {
         const bool in = tid + 256 * u < C;
         const uint32_t rr = in ? row : rows - 1, cc = in ? col : kc - 1;  // clamped: no branch
-        const uint32_t b = cc >> 1;
-        rowu[u] = rr, blku[u] = b;
         wv[u] = __builtin_nontemporal_load((const v4i*)(wt + (size_t)rr * K + cc * 16));
-        wsb[u] = scale_bits(WF16, WS, (size_t)(row0 + rr) * nb + b);
 #pragma unroll
-        for (int m = 0; m < M; m++) {
-            xv[u][m] = *(const v4i*)(x.q + (size_t)m * K + cc * 16);
-            xsb[u][m] = XF16 ? (uint32_t)x.h[m * nb + b] : f2u(x.s[m * nb + b]);
-        }
+        for (int m = 0; m < M; m++) xv[u][m] = *(const v4i*)(x.q + (size_t)m * K + cc * 16);
+        if ((u & 1) == 0) rowu[u / 2] = rr, blku[u / 2] = cc >> 1;
+        else if (!even) rowu[u / 2] = rr, blku[u / 2] = cc >> 1;
         col += step_cols;
         row += step_rows;
         if (col >= kc) col -= kc, row += 1;
     }
+#pragma unroll
+    for (int v = 0; v < CPT / 2; v++) {
+        const uint32_t b = blku[v];
+        wsb[v] = scale_bits(WF16, WS, (size_t)(row0 + rowu[v]) * nb + b);
+#pragma unroll
+        for (int m = 0; m < M; m++) xsb[v][m] = XF16 ? (uint32_t)x.h[m * nb + b] : f2u(x.s[m * nb + b]);
+    }
 
     const uint32_t per = gemv_out_floats(SEM, nb), q4p = gemv_q4p(nb);
-    const uint32_t dummy = M * rows * per;  // LDS slot for the stores of lanes that own no block
-    const bool even = (tid & 1) == 0;
+    // LDS slots for the stores of lanes that own no block, one per lane: a
+    // store of many lanes to one address is serialised like a bank conflict
+    const uint32_t dummy = M * rows * per + 2 * (tid & 63);
 #pragma unroll
-    for (int u = 0; u < CPT; u++) {
-        const bool valid = tid + 256 * u < C;
-        const uint32_t r = rowu[u], b = blku[u];
-        const float ws = scale_value(WF16, wsb[u]);
+    for (int v = 0; v < CPT / 2; v++) {
+        const bool valid = tid + 256 * (even ? 2 * v : 2 * v + 1) < C;
+        const uint32_t r = rowu[v], b = blku[v];
+        const float ws = scale_value(WF16, wsb[v]);
 #pragma unroll
         for (int m = 0; m < M; m++) {
-            int acc = 0;
-            acc = __builtin_amdgcn_sdot4(wv[u].x, xv[u][m].x, acc, false);
-            acc = __builtin_amdgcn_sdot4(wv[u].y, xv[u][m].y, acc, false);
-            acc = __builtin_amdgcn_sdot4(wv[u].z, xv[u][m].z, acc, false);
-            acc = __builtin_amdgcn_sdot4(wv[u].w, xv[u][m].w, acc, false);
-            const int isum = lane_pair_sum(acc);
-            // every lane forms the operand and stores it (lanes that own no
-            // block to a dummy slot): with no branch around the use, the
-            // scale loads stay at the top of the kernel
+            const int isum = pair_blocks(dot16(wv[2 * v], xv[2 * v][m]), dot16(wv[2 * v + 1], xv[2 * v + 1][m]), even);
+            // every lane forms the operand and stores it (a lane whose chunk
+            // is past the tile to a dummy slot): with no branch around the
+            // use, the scale loads stay at the top of the kernel
             float v0, v1 = 0.0f;
             if (SEM == SEM_FMA_CHAIN) {
                 // quant.rs: slot = (isum as f32).mul_add(f16w(ws) * f16w(xs), slot)
                 v0 = (float)isum;
-                v1 = ws * f16w((uint16_t)xsb[u][m]);
+                v1 = ws * f16w((uint16_t)xsb[v][m]);
             } else {
                 // dot.rs: t[b & 3] += (sa * sb) * (isum as f32)
-                v0 = (ws * u2f(xsb[u][m])) * (float)isum;
+                v0 = (ws * u2f(xsb[v][m])) * (float)isum;
             }
-            const bool own = valid && even;
+            const bool own = valid;
             if (dbg && own) dbg[((size_t)m * N + row0 + r) * nb + b] = isum;
             const uint32_t base = (m * rows + r) * per;
             if (SEM == SEM_FMA_CHAIN) {
@@ -546,7 +565,7 @@ static hipError_t gemv_launch(hipStream_t st, MatSet ms, size_t k, QuantAct x, i
         if (i < ms.count) total += (uint32_t)((ms.n[i] + R - 1) / R);
         ms.tile_end[i] = total;
     }
-    const size_t lds = ((size_t)M * R * gemv_out_floats(SEM, (uint32_t)(k / 32)) + 2) * sizeof(float);
+    const size_t lds = ((size_t)M * R * gemv_out_floats(SEM, (uint32_t)(k / 32)) + 128) * sizeof(float);
     const size_t chunks = R * (k / 16);
     const size_t cpt = (chunks + 255) / 256;
     if (cpt <= 2)
@@ -589,7 +608,7 @@ static constexpr int PRO_NORM = 1, PRO_QUANT = 3;
 // norm weight): with PRO_NORM the residual add, the serial RMS sum on one
 // lane (rms_norm_row, cpu.rs:635-641) and out = w * (scale * x) (cpu.rs:643);
 // then Q8Vec::quantize_into (quant.rs:864-873) of the row into LDS (xq, and
-// the scale bits xsb: f16 for the FMA-chain format, else f32), a block per 8
+// the scale values xsb: f16-rounded for the FMA-chain format, else f32), a block per 8
 // threads. Every thread of the workgroup calls this; the row is spread over
 // threads 0..255 (VPT float4 each), further threads only join the barriers.
 template <int SEM, int PRO, int VPT>
@@ -646,7 +665,9 @@ __device__ __forceinline__ void gemv_produce(const GemvPro& pro, uint32_t K, flo
             qq.z = q8_round(v.z * inv);
             qq.w = q8_round(v.w * inv);
             ((char4*)xq)[f] = qq;
-            if ((f & 7) == 0) xsb[f / 8] = XF16 ? (uint32_t)f16_bits(d) : f2u(d);
+            // the block scale as the epilogue uses it: f16-rounded and widened
+            // (quant.rs:276-288) for the FMA-chain format, else the f32 scale
+            if ((f & 7) == 0) xsb[f / 8] = f2u(XF16 ? f16w(f16_bits(d)) : d);
         }
     }
     __syncthreads();
@@ -687,19 +708,22 @@ __global__ __launch_bounds__(256) void k_gemv_pro(MatSet ms, GemvPro pro, uint32
     // 2. the weight tile, as k_gemv loads it
     const int8_t* wt = W + (size_t)row0 * K;
     uint32_t row = tid / kc, col = tid - (tid / kc) * kc;
+    static_assert(CPT == 2, "one block per lane: chunk 0 on even lanes, chunk 1 on odd lanes");
+    const bool even = (tid & 1) == 0;
     v4i wv[CPT];
-    uint32_t wsb[CPT], rowu[CPT], colu[CPT];
+    uint32_t rowu[CPT], colu[CPT];
 #pragma unroll
     for (int u = 0; u < CPT; u++) {
         const bool in = tid + 256 * u < C;
         const uint32_t rr = in ? row : rows - 1, cc = in ? col : kc - 1;
         rowu[u] = rr, colu[u] = cc;
         wv[u] = __builtin_nontemporal_load((const v4i*)(wt + (size_t)rr * K + cc * 16));
-        wsb[u] = scale_bits(WF16, WS, (size_t)(row0 + rr) * nb + (cc >> 1));
         col += step_cols;
         row += step_rows;
         if (col >= kc) col -= kc, row += 1;
     }
+    const uint32_t r_own = even ? rowu[0] : rowu[1], b_own = (even ? colu[0] : colu[1]) >> 1;
+    const uint32_t wsb = scale_bits(WF16, WS, (size_t)(row0 + r_own) * nb + b_own);
 
     // 3. the producer, while the weights are in flight
     gemv_produce<SEM, PRO, VPT>(pro, K, va, vb, vw, xq, xsb, scratch, &s_scale);
@@ -707,28 +731,20 @@ __global__ __launch_bounds__(256) void k_gemv_pro(MatSet ms, GemvPro pro, uint32
     // 4. block dots against the LDS row, then the epilogue of k_gemv
     const uint32_t per = gemv_out_floats(SEM, nb), q4p = gemv_q4p(nb);
     float* res = scratch;
-    const uint32_t dummy = rows * per;
-    const bool even = (tid & 1) == 0;
-#pragma unroll
-    for (int u = 0; u < CPT; u++) {
-        const bool valid = tid + 256 * u < C;
-        const uint32_t r = rowu[u], b = colu[u] >> 1;
-        const float ws = scale_value(WF16, wsb[u]);
-        const v4i xv = *(const v4i*)(xq + colu[u] * 16);
-        const uint32_t xs = xsb[b];
-        int acc = 0;
-        acc = __builtin_amdgcn_sdot4(wv[u].x, xv.x, acc, false);
-        acc = __builtin_amdgcn_sdot4(wv[u].y, xv.y, acc, false);
-        acc = __builtin_amdgcn_sdot4(wv[u].z, xv.z, acc, false);
-        acc = __builtin_amdgcn_sdot4(wv[u].w, xv.w, acc, false);
-        const int isum = lane_pair_sum(acc);
-        const bool own = valid && even;
+    const uint32_t dummy = rows * per + 2 * (tid & 63);  // a slot per lane, as in k_gemv
+    {
+        const bool own = tid + 256 * (even ? 0 : 1) < C;
+        const uint32_t r = r_own, b = b_own;
+        const float ws = scale_value(WF16, wsb);
+        const float xs = u2f(xsb[b]);
+        const v4i xv0 = *(const v4i*)(xq + colu[0] * 16), xv1 = *(const v4i*)(xq + colu[1] * 16);
+        const int isum = pair_blocks(dot16(wv[0], xv0), dot16(wv[1], xv1), even);
         const uint32_t base = r * per;
         if (SEM == SEM_FMA_CHAIN) {
             float2* op = (float2*)(res + (own ? base + 2 * b : dummy));
-            *op = make_float2((float)isum, ws * f16w((uint16_t)xs));
+            *op = make_float2((float)isum, ws * xs);
         } else {
-            res[own ? base + (b & 3) * q4p + (b >> 2) : dummy] = (ws * u2f(xs)) * (float)isum;
+            res[own ? base + (b & 3) * q4p + (b >> 2) : dummy] = (ws * xs) * (float)isum;
         }
     }
     __syncthreads();
@@ -758,7 +774,7 @@ static hipError_t gemv_pro_go(hipStream_t st, MatSet ms, size_t k, const GemvPro
         ms.tile_end[i] = total;
     }
     const size_t nb = k / 32, head = (k / 4 + nb + 3) & ~(size_t)3;
-    const size_t ops = R * gemv_out_floats(SEM, (uint32_t)nb) + 2;
+    const size_t ops = R * gemv_out_floats(SEM, (uint32_t)nb) + 128;
     const size_t lds = (head + (ops > k ? ops : k)) * sizeof(float);
     const size_t vpt = (k / 4 + 255) / 256;
     const uint32_t kc = (uint32_t)(k / 16);
@@ -819,7 +835,7 @@ hipError_t launch_project_pro(hipStream_t st, int sem, const DevMatrix* const* w
 // followed by k_silu_quant, with one launch fewer per layer. Tile row r < 32
 // is gate row 32 t + r, r >= 32 up row 32 t + r - 32.
 static constexpr uint32_t kSwigluMaxK = 1024;
-static constexpr uint32_t kSwigluThreads = 512;  // the producer runs on the first 256 (K <= 1024)
+static constexpr uint32_t kSwigluThreads = 1024;  // the producer runs on the first 256 (K <= 1024)
 template <int SEM, int CPT>
 __global__ __launch_bounds__(kSwigluThreads) void k_gemv_swiglu(MatSet ms, GemvPro pro, uint32_t K, uint32_t step_rows,
                                                      uint32_t step_cols, int8_t* __restrict__ hq,
@@ -851,8 +867,11 @@ __global__ __launch_bounds__(kSwigluThreads) void k_gemv_swiglu(MatSet ms, GemvP
     // 2. the weight tile: chunk tid + NT u is (tile row, 16-byte column). The
     // two matrices' bases are read once (uniform) and selected per chunk: an
     // argument array indexed per lane would be loaded from memory per lane.
+    // chunk 2v (even lane) or 2v + 1 (odd lane) is the block a lane finishes
+    static_assert(CPT % 2 == 0, "chunks pair up");
+    const bool even = (tid & 1) == 0;
     v4i wv[CPT];
-    uint32_t wsb[CPT];
+    uint32_t colu[CPT], wsb[CPT / 2], rowo[CPT / 2], blko[CPT / 2];
     {
         const int8_t* const wq0 = ms.q[0];
         const int8_t* const wq1 = ms.q[1];
@@ -865,11 +884,18 @@ __global__ __launch_bounds__(kSwigluThreads) void k_gemv_swiglu(MatSet ms, GemvP
             const uint32_t rr = in ? row : RT - 1, cc = in ? col : kc - 1;
             const bool up_row = rr >= 32;
             const uint32_t grow = 32 * t + (rr & 31);
+            colu[u] = cc;
             wv[u] = __builtin_nontemporal_load((const v4i*)((up_row ? wq1 : wq0) + (size_t)grow * K + cc * 16));
-            wsb[u] = scale_bits(WF16, up_row ? ws1 : ws0, (size_t)grow * nb + (cc >> 1));
+            if ((u & 1) == 0) rowo[u / 2] = rr, blko[u / 2] = cc >> 1;
+            else if (!even) rowo[u / 2] = rr, blko[u / 2] = cc >> 1;
             col += step_cols;
             row += step_rows;
             if (col >= kc) col -= kc, row += 1;
+        }
+#pragma unroll
+        for (int v = 0; v < CPT / 2; v++) {
+            const uint32_t rr = rowo[v];
+            wsb[v] = scale_bits(WF16, rr >= 32 ? ws1 : ws0, (size_t)(32 * t + (rr & 31)) * nb + blko[v]);
         }
     }
     if (tid < 32) etab[tid] = etv;  // read after the producer's barriers
@@ -879,34 +905,21 @@ __global__ __launch_bounds__(kSwigluThreads) void k_gemv_swiglu(MatSet ms, GemvP
     // 4. block dots against the LDS row, the epilogue operands to LDS
     const uint32_t per = gemv_out_floats(SEM, nb), q4p = gemv_q4p(nb);
     float* res = scratch;
-    const uint32_t dummy = RT * per;
-    const bool even = (tid & 1) == 0;
-    {
-        uint32_t row = tid / kc, col = tid - (tid / kc) * kc;
+    const uint32_t dummy = RT * per + 2 * (tid & 63);  // a slot per lane, as in k_gemv
 #pragma unroll
-        for (int u = 0; u < CPT; u++) {
-            const bool valid = tid + NT * u < C;
-            const uint32_t r = valid ? row : RT - 1, cc = valid ? col : kc - 1, b = cc >> 1;
-            const float ws = scale_value(WF16, wsb[u]);
-            const v4i xv = *(const v4i*)(xq + cc * 16);
-            const uint32_t xs = xsb[b];
-            int acc = 0;
-            acc = __builtin_amdgcn_sdot4(wv[u].x, xv.x, acc, false);
-            acc = __builtin_amdgcn_sdot4(wv[u].y, xv.y, acc, false);
-            acc = __builtin_amdgcn_sdot4(wv[u].z, xv.z, acc, false);
-            acc = __builtin_amdgcn_sdot4(wv[u].w, xv.w, acc, false);
-            const int isum = lane_pair_sum(acc);
-            const bool own = valid && even;
-            const uint32_t base = r * per;
-            if (SEM == SEM_FMA_CHAIN) {
-                float2* op = (float2*)(res + (own ? base + 2 * b : dummy));
-                *op = make_float2((float)isum, ws * f16w((uint16_t)xs));
-            } else {
-                res[own ? base + (b & 3) * q4p + (b >> 2) : dummy] = (ws * u2f(xs)) * (float)isum;
-            }
-            col += step_cols;
-            row += step_rows;
-            if (col >= kc) col -= kc, row += 1;
+    for (int v = 0; v < CPT / 2; v++) {
+        const bool own = tid + NT * (even ? 2 * v : 2 * v + 1) < C;
+        const uint32_t r = rowo[v], b = blko[v];
+        const float ws = scale_value(WF16, wsb[v]);
+        const float xs = u2f(xsb[b]);
+        const v4i xv0 = *(const v4i*)(xq + colu[2 * v] * 16), xv1 = *(const v4i*)(xq + colu[2 * v + 1] * 16);
+        const int isum = pair_blocks(dot16(wv[2 * v], xv0), dot16(wv[2 * v + 1], xv1), even);
+        const uint32_t base = r * per;
+        if (SEM == SEM_FMA_CHAIN) {
+            float2* op = (float2*)(res + (own ? base + 2 * b : dummy));
+            *op = make_float2((float)isum, ws * xs);
+        } else {
+            res[own ? base + (b & 3) * q4p + (b >> 2) : dummy] = (ws * xs) * (float)isum;
         }
     }
     __syncthreads();
@@ -941,7 +954,7 @@ hipError_t launch_gate_up_swiglu(hipStream_t st, int sem, const DevMatrix& gate,
     ms.q[1] = up.q, ms.s[1] = up.s, ms.n[1] = (uint32_t)n;
     GemvPro pro{x, add, norm_w, x_out, eps};
     const size_t nb = k / 32, kc = k / 16, head = (k / 4 + nb + 3) & ~(size_t)3;
-    const size_t ops = 64 * gemv_out_floats(sem, (uint32_t)nb) + 2;
+    const size_t ops = 64 * gemv_out_floats(sem, (uint32_t)nb) + 128;
     const size_t lds = (head + (ops > k ? ops : k)) * sizeof(float);
     const size_t cpt = (64 * kc + kSwigluThreads - 1) / kSwigluThreads;
     const dim3 grid((unsigned)(n / 32));
@@ -949,10 +962,10 @@ hipError_t launch_gate_up_swiglu(hipStream_t st, int sem, const DevMatrix& gate,
     hipLaunchKernelGGL((k_gemv_swiglu<SEMV, CPTV>), grid, dim3(kSwigluThreads), lds, st, ms, pro, (uint32_t)k,  \
                        (uint32_t)(kSwigluThreads / kc), (uint32_t)(kSwigluThreads % kc), hq, hs, hh, hf)
 #define KR_SWIGLU_CPT(SEMV) \
-    if (cpt <= 4)           \
-        KR_SWIGLU(SEMV, 4); \
+    if (cpt <= 2)           \
+        KR_SWIGLU(SEMV, 2); \
     else                    \
-        KR_SWIGLU(SEMV, 8);
+        KR_SWIGLU(SEMV, 4);
     switch (sem) {
         case SEM_FMA_CHAIN: KR_SWIGLU_CPT(SEM_FMA_CHAIN) break;
         case SEM_FOUR_PARTIALS_F32: KR_SWIGLU_CPT(SEM_FOUR_PARTIALS_F32) break;

@@ -65,11 +65,12 @@ KR_HD uint16_t f32_to_f16_bits(float value) {
 // The reference's normal-only f16 widening (quant.rs:764-769). A code with a
 // zero exponent field widens to 2^-15 * (1 + m/1024), not to zero/subnormal,
 // which is why a hardware f16->f32 convert cannot be used here.
+// sign | ((exp + 112) << 23) | (mant << 13), as two masks, a shift-add and
+// a shift-or: the exponent and mantissa move up 13 bits together and the
+// rebase by 112 is one add (exp + 112 <= 143 never reaches the sign bit).
 KR_HD float f16w(uint16_t bits) {
-    uint32_t sign = (uint32_t)(bits >> 15) << 31;
-    uint32_t exp = (uint32_t)((bits >> 10) & 0x1fu);
-    uint32_t mant = (uint32_t)(bits & 0x03ffu);
-    return u2f(sign | ((exp + 112u) << 23) | (mant << 13));
+    const uint32_t h = bits;
+    return u2f(((h & 0x8000u) << 16) | (((h & 0x7fffu) << 13) + (112u << 23)));
 }
 
 // `(t).round().clamp(-127.0, 127.0) as i8` (quant.rs:843): round half away

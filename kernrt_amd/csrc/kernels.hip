@@ -2296,9 +2296,10 @@ hipError_t launch_attention_split(hipStream_t st, const float* q, const float* k
 // o0 += p[i] * v[i * KS], o1 += p[i] * v[i * KS + 1] for i < n in position
 // order (each a rounded product, then a rounded add): p is a 16-byte aligned
 // LDS row, v an LDS tile with row stride KS. Batches of kAttnVBatch
-// positions, the next batch's reads issued before the current batch's adds,
-// so the chains wait on the previous add rather than on LDS; the last
-// n % kAttnVBatch positions run one at a time.
+// positions in two register sets used in turn (no copies between them): the
+// reads of batch b + 1 are issued before the adds of batch b, so the chains
+// wait on the previous add rather than on LDS; the last n % kAttnVBatch
+// positions run one at a time.
 static constexpr uint32_t kAttnVBatch = 8;
 template <uint32_t KS>
 __device__ __forceinline__ void attn_v_chain(const float* __restrict__ p, const float* __restrict__ v, uint32_t n,
@@ -2324,20 +2325,24 @@ __device__ __forceinline__ void attn_v_chain(const float* __restrict__ p, const 
             o1 += pk * b.vv[k].y;
         }
     };
-    uint32_t i = 0;
-    if (n >= B) {
-        Batch cur;
-        ld(cur, 0);
-        for (; i + 2 * B <= n; i += B) {
-            Batch nxt;
-            ld(nxt, i + B);
-            apply(cur);
-            cur = nxt;
+    const uint32_t nb = n / B;  // whole batches
+    uint32_t b = 0;
+    if (nb > 0) {
+        Batch x, y;
+        ld(x, 0);
+        // x holds batch b; y is loaded with b + 1 before x's adds, and so on
+        for (; b + 2 <= nb; b += 2) {
+            ld(y, (b + 1) * B);
+            apply(x);
+            ld(x, (b + 2 < nb ? b + 2 : b + 1) * B);  // past the end: re-read a valid batch, not applied
+            apply(y);
         }
-        apply(cur);
-        i += B;
+        if (b < nb) {
+            apply(x);
+            b++;
+        }
     }
-    for (; i < n; i++) {
+    for (uint32_t i = nb * B; i < n; i++) {
         const float pk = p[i];
         const v2f vk = *(const v2f*)(v + i * KS);
         o0 += pk * vk.x;
@@ -2500,56 +2505,49 @@ __global__ __launch_bounds__(64 * NWAVES) void k_attn_rows(const float* __restri
             kfetch(st + 1);
         else  // the first V stage, for phase 3
             vfetch(0);
-        {  // lane = position, wave = its RPW pairs; the pairs' q rows are wave-uniform
-           // (scalar loads), so each 4 FMAs per pair cost one LDS read of K
-            // q in blocks of UB float4 per pair, the next block loaded during this
-            // one (2 RPW UB 4 = 64 scalar registers)
-            constexpr uint32_t UB = 8 / RPW;
-            static_assert(FK % UB == 0, "q blocks");
+        {  // lane = position, wave = its RPW pairs. The pairs' q values are
+           // wave-uniform: QB float4 per pair at a time go to scalar registers
+           // (RPW QB 4 = 32), then each LDS read of 4 K values feeds 4 FMAs
+           // per pair. K is read a group of GS float4 ahead, into two register
+           // sets used in turn, so only LDS reads are waited on inside a block.
+            constexpr uint32_t QB = 8 / RPW < 2 ? 2 : 8 / RPW, GS = QB < 4 ? QB : 4, NG = QB / GS;
+            static_assert(FK % QB == 0 && QB % GS == 0, "q blocks");
             const uint32_t ug = h * FK;  // first dim block of this stage
             const uint32_t pos = lane;
             if (h == 0) {
 #pragma unroll
                 for (uint32_t k = 0; k < RPW; k++) a[k][0] = a[k][1] = a[k][2] = a[k][3] = 0.0f;
             }
-            float4 qc[RPW][UB];
-            auto load_q = [&](float4(&qv)[RPW][UB], uint32_t u0) {
+            const float* krow = kt + pos * KSK;
+#pragma unroll 1
+            for (uint32_t q0 = 0; q0 < FK; q0 += QB) {
+                float4 qv[RPW][QB];
 #pragma unroll
                 for (uint32_t k = 0; k < RPW; k++)
 #pragma unroll
-                    for (uint32_t u = 0; u < UB; u++) qv[k][u] = *(const float4*)(qrow[k] + 4 * (ug + u0 + u));
-            };
-            // the K values of block u0 + UB are read before block u0's FMAs
-            float4 kc[UB];
-            auto load_k = [&](float4(&kv)[UB], uint32_t u0) {
+                    for (uint32_t u = 0; u < QB; u++) qv[k][u] = *(const float4*)(qrow[k] + 4 * (ug + q0 + u));
+                float4 kb[2][GS];
 #pragma unroll
-                for (uint32_t u = 0; u < UB; u++) kv[u] = *(const float4*)(kt + pos * KSK + 4 * (u0 + u));
-            };
-            load_q(qc, 0);
-            load_k(kc, 0);
-#pragma unroll 1
-            for (uint32_t u0 = 0; u0 < FK; u0 += UB) {
-                const uint32_t un = u0 + UB < FK ? u0 + UB : u0;
-                float4 qn[RPW][UB], kn[UB];
-                load_q(qn, un);
-                load_k(kn, un);
+                for (uint32_t t = 0; t < GS; t++) kb[0][t] = *(const float4*)(krow + 4 * (q0 + t));
 #pragma unroll
-                for (uint32_t u = 0; u < UB; u++) {
-                    const float4 kk = kc[u];
+                for (uint32_t g = 0; g < NG; g++) {
+                    if (g + 1 < NG) {
 #pragma unroll
-                    for (uint32_t k = 0; k < RPW; k++) {
-                        const float4 qq = qc[k][u];
-                        a[k][0] = __builtin_fmaf(qq.x, kk.x, a[k][0]);
-                        a[k][1] = __builtin_fmaf(qq.y, kk.y, a[k][1]);
-                        a[k][2] = __builtin_fmaf(qq.z, kk.z, a[k][2]);
-                        a[k][3] = __builtin_fmaf(qq.w, kk.w, a[k][3]);
+                        for (uint32_t t = 0; t < GS; t++)
+                            kb[(g + 1) & 1][t] = *(const float4*)(krow + 4 * (q0 + GS * (g + 1) + t));
                     }
-                }
 #pragma unroll
-                for (uint32_t u = 0; u < UB; u++) {
-                    kc[u] = kn[u];
+                    for (uint32_t t = 0; t < GS; t++) {
+                        const float4 kk = kb[g & 1][t];
 #pragma unroll
-                    for (uint32_t k = 0; k < RPW; k++) qc[k][u] = qn[k][u];
+                        for (uint32_t k = 0; k < RPW; k++) {
+                            const float4 qq = qv[k][GS * g + t];
+                            a[k][0] = __builtin_fmaf(qq.x, kk.x, a[k][0]);
+                            a[k][1] = __builtin_fmaf(qq.y, kk.y, a[k][1]);
+                            a[k][2] = __builtin_fmaf(qq.z, kk.z, a[k][2]);
+                            a[k][3] = __builtin_fmaf(qq.w, kk.w, a[k][3]);
+                        }
+                    }
                 }
             }
 #pragma unroll
@@ -2579,9 +2577,16 @@ __global__ __launch_bounds__(64 * NWAVES) void k_attn_rows(const float* __restri
         for (uint32_t i = lane; i < n; i += 64) e[i] = glibc_expf(e[i] - m, etab);  // independent: 4 in flight
     }
     __builtin_amdgcn_wave_barrier();
-    if (lane < RPW) {  // sum left to right (elementwise.rs:81-91), one lane per pair
-        const uint32_t rg = wave * RPW + lane;
-        if (rg < RG) s_sum[rg] = chain_sum(sc + rg * scs, s_cnt[rg]);
+    // sum left to right (elementwise.rs:81-91), the wave's pairs one after the
+    // other, each a register-fed chain across the wave's lanes
+#pragma unroll
+    for (uint32_t k = 0; k < RPW; k++) {
+        const uint32_t rg = wave * RPW + k;
+        if (rg < RG) {  // wave-uniform
+            const uint32_t n = s_cnt[rg];
+            const float sum = n <= 4096 ? wave_chain_sum(sc + rg * scs, n) : chain_sum(sc + rg * scs, n);
+            if (lane == 0) s_sum[rg] = sum;
+        }
     }
     __builtin_amdgcn_wave_barrier();
 #pragma unroll

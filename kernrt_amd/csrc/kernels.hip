@@ -329,32 +329,30 @@ __device__ __forceinline__ float chain_sum(const float* __restrict__ e, uint32_t
 // chain -- and a DPP wave_shr:1 move hands lane L's sum to lane L + 1 as its
 // start. Register-fed dependent adds run at ~4.5 clocks each against ~8-9
 // for an LDS-fed one-lane chain; a hand-off costs ~25 clocks, once per 64
-// values. e is 16-byte aligned LDS readable up to round4(n) (values past n
-// are read but never added), n <= 4096.
-__device__ __forceinline__ float wave_chain_sum(const float* __restrict__ e, uint32_t n) {
+// values. Past n the values are zeros (e[n .. round4(n)) is cleared first,
+// later ones are not loaded), and adding +0.0 leaves a sum of non-negative
+// terms unchanged, so every lane adds all 64 of its values and the code has
+// one path. e is 16-byte aligned LDS, writable up to round4(n), holding
+// values >= 0 (squares, exponentials); n <= 4096.
+__device__ __forceinline__ float wave_chain_sum(float* __restrict__ e, uint32_t n) {
     constexpr int VPL = 64;
     const uint32_t lane = threadIdx.x & 63, base = lane * VPL, n4 = (n + 3) & ~3u;
+    if (lane < n4 - n) e[n + lane] = 0.0f;  // a wave's LDS accesses complete in order
     float v[VPL];
 #pragma unroll
     for (int u = 0; u < VPL / 4; u++) {
         const float4 f = base + 4 * u < n4 ? *(const float4*)(e + base + 4 * u) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         v[4 * u] = f.x, v[4 * u + 1] = f.y, v[4 * u + 2] = f.z, v[4 * u + 3] = f.w;
     }
-    const uint32_t full = n / VPL, rest = n - full * VPL;
+    const uint32_t runs = (n + VPL - 1) / VPL;
     float acc = 0.0f;
-    for (uint32_t L = 0; L < full; L++) {
+    for (uint32_t L = 0; L < runs; L++) {
 #pragma unroll
         for (int k = 0; k < VPL; k++) acc += v[k];
-        if (L + 1 < full || rest)  // wave_shr:1 -- lane L + 1 continues from lane L
+        if (L + 1 < runs)  // wave_shr:1 -- lane L + 1 continues from lane L
             acc = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(acc), 0x138, 0xf, 0xf, false));
     }
-    if (rest) {
-#pragma unroll
-        for (int k = 0; k < VPL; k++)
-            if ((uint32_t)k < rest) acc += v[k];
-        return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), full));
-    }
-    return full ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), full - 1)) : 0.0f;
+    return runs ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), runs - 1)) : 0.0f;
 }
 
 // Serial f32 dot o += p[i] * v[i] (a rounded product, then a rounded add),

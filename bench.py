@@ -397,7 +397,7 @@ def bench_prefill_model(K, n_tokens: int = 128, reps: int = 5):
     return dict(tokens=n_tokens, tok_s=n_tokens / best, best_ms=best * 1e3, first_call_ms=first * 1e3)
 
 
-def bench_cfg4(K, n_prompt: int = 128, n_decode: int = 256):
+def bench_cfg4(K, n_prompt: int = 128, n_decode: int = 256, use_graph: bool = True):
     """`configs[3]`: the LFM2-700M-shaped hybrid with Q8_0x4 weights, a
     128-token prefill of seeded random ids, then 256 greedy decode tokens
     (context cap 8192), the decode replaying the captured step graph."""
@@ -410,10 +410,10 @@ def bench_cfg4(K, n_prompt: int = 128, n_decode: int = 256):
     logits = model.prefill(toks, 0)
     prefill_s = time.perf_counter() - t0
     first = int(np.argmax(logits))
-    model.generate_greedy(first, n_prompt, 8)
+    model.generate_greedy(first, n_prompt, 8, use_graph=use_graph)
     hip.synchronize()
     t0 = time.perf_counter()
-    model.generate_greedy(first, n_prompt, n_decode)
+    model.generate_greedy(first, n_prompt, n_decode, use_graph=use_graph)
     hip.synchronize()
     decode_s = time.perf_counter() - t0
     model.close()
@@ -636,7 +636,7 @@ def main():
         res["prefill"]["model"] = bench_prefill_model(K)
         log(f"prefill model: {res['prefill']['model']['tok_s']:.0f} tok/s")
     if args.only in (None, "cfg4"):
-        res["cfg4"] = bench_cfg4(K)
+        res["cfg4"] = bench_cfg4(K, use_graph=not args.no_graph)
         log(f"cfg4: prefill {res['cfg4']['prefill_tok_s']:.0f} tok/s, decode {res['cfg4']['decode_tok_s']:.1f} tok/s")
     if args.only in (None, "cfg5"):
         res["cfg5"] = bench_cfg5(K)

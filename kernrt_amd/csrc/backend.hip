@@ -1440,6 +1440,17 @@ int conv_block_decode(kr_ctx* c, kr_buf y, kr_buf bcx, kr_buf kernel, kr_buf sta
 
 // The conv of `rows` rows of x as if they were fed one at a time through
 // conv_decode (the ring supplies the history, then advances by `rows`).
+int mul_rows(kr_ctx* c, kr_buf out, size_t oo, size_t os, kr_buf a, size_t ao, size_t as, kr_buf b, size_t bo,
+             size_t bs, size_t rows, size_t n) {
+    CHECK(c, out != a && out != b, "mul_rows: the output may not alias an input");
+    if (rows == 0 || n == 0) return KR_OK;
+    BUF(o, out, oo + (rows - 1) * os + n);
+    BUF(ab, a, ao + (rows - 1) * as + n);
+    BUF(bb, b, bo + (rows - 1) * bs + n);
+    HIPCHK(c, kr::launch_mul_rows(c->stream, o->p + oo, os, ab->p + ao, as, bb->p + bo, bs, rows, n));
+    return KR_OK;
+}
+
 int conv_prefill_stepped(kr_ctx* c, kr_buf out, kr_buf x, kr_buf kernel, kr_buf state, size_t rows, size_t dim,
                          size_t k) {
     CHECK(c, k >= 1 && k <= 16, "conv kernel width %zu outside 1..16", k);

@@ -45,6 +45,10 @@ constexpr kr_buf KR_NO_BUF = 0xffffffffu;
 int norm_quant(kr_ctx* c, kr_buf x, kr_buf add, kr_buf w, kr_buf out, size_t rows, size_t dim, float eps);
 // projections of the quantized workspace rows; one launch when they share in_dim and storage
 int project_q(kr_ctx* c, size_t layer, const int* projs, const kr_buf* ys, int n, size_t rows);
+// out[oo + r os + i] = a[ao + r as + i] * b[bo + r bs + i], r < rows, i < n, one launch
+// (out must not be a or b)
+int mul_rows(kr_ctx* c, kr_buf out, size_t oo, size_t os, kr_buf a, size_t ao, size_t as, kr_buf b, size_t bo,
+             size_t bs, size_t rows, size_t n);
 // gate = silu(gate) * up, quantized
 int silu_quant(kr_ctx* c, kr_buf gate, kr_buf up, size_t rows, size_t width);
 // rope of q and k, then k and v into the cache; positions and slots from the

@@ -333,9 +333,10 @@ __device__ __forceinline__ float chain_sum(const float* __restrict__ e, uint32_t
 // later ones are not loaded), and adding +0.0 leaves a sum of non-negative
 // terms unchanged, so every lane adds all 64 of its values and the code has
 // one path. e is 16-byte aligned LDS, writable up to round4(n), holding
-// values >= 0 (squares, exponentials); n <= 4096.
+// values >= 0 (squares, exponentials); n <= 64 VPL (VPL values per lane:
+// fewer registers for a few more hand-offs).
+template <int VPL = 64>
 __device__ __forceinline__ float wave_chain_sum(float* __restrict__ e, uint32_t n) {
-    constexpr int VPL = 64;
     const uint32_t lane = threadIdx.x & 63, base = lane * VPL, n4 = (n + 3) & ~3u;
     if (lane < n4 - n) e[n + lane] = 0.0f;  // a wave's LDS accesses complete in order
     float v[VPL];
@@ -609,7 +610,7 @@ static constexpr int PRO_NORM = 1, PRO_QUANT = 3;
 // the scale values xsb: f16-rounded for the FMA-chain format, else f32), a block per 8
 // threads. Every thread of the workgroup calls this; the row is spread over
 // threads 0..255 (VPT float4 each), further threads only join the barriers.
-template <int SEM, int PRO, int VPT>
+template <int SEM, int PRO, int VPT, int CVPL = 64>
 __device__ __forceinline__ void gemv_produce(const GemvPro& pro, uint32_t K, float4 (&va)[VPT], const float4 (&vb)[VPT],
                                              const float4 (&vw)[VPT], int8_t* xq, uint32_t* xsb, float* scratch,
                                              float* s_scale_p) {
@@ -630,7 +631,7 @@ __device__ __forceinline__ void gemv_produce(const GemvPro& pro, uint32_t K, flo
         }
         __syncthreads();
         if (tid < 64) {  // rms_norm_row (cpu.rs:635-641): the serial sum on wave 0
-            float ss = K <= 4096 ? wave_chain_sum(scratch, K) : chain_sum(scratch, K);
+            float ss = K <= 64 * CVPL ? wave_chain_sum<CVPL>(scratch, K) : chain_sum(scratch, K);
             ss = div_rn(ss, (float)K);
             ss += pro.eps;
             if (tid == 0) *s_scale_p = div_rn(1.0f, sqrt_rn(ss));
@@ -824,7 +825,7 @@ hipError_t launch_project_pro(hipStream_t st, int sem, const DevMatrix* const* w
 }
 
 // Decode gate/up with the SwiGLU product and its quantization fused behind
-// (M = 1, K <= 1024). Workgroup t computes rows 32 t .. 32 t + 31 of both the
+// (M = 1, K <= 2048). Workgroup t computes rows 32 t .. 32 t + 31 of both the
 // gate and the up matrix, with the residual add + RMSNorm + Q8 producer in
 // front exactly as k_gemv_pro<PRO_NORM>; then one half-wave forms
 // h = silu(gate) * up (cpu.rs:708-710, then cpu.rs:494-499) for those 32
@@ -832,14 +833,13 @@ hipError_t launch_project_pro(hipStream_t st, int sem, const DevMatrix* const* w
 // of the down projection. The results are bit-identical to k_gemv_pro
 // followed by k_silu_quant, with one launch fewer per layer. Tile row r < 32
 // is gate row 32 t + r, r >= 32 up row 32 t + r - 32.
-static constexpr uint32_t kSwigluMaxK = 1024;
-static constexpr uint32_t kSwigluThreads = 1024;  // the producer runs on the first 256 (K <= 1024)
-template <int SEM, int CPT>
+static constexpr uint32_t kSwigluMaxK = 2048;
+static constexpr uint32_t kSwigluThreads = 1024;  // the producer runs on the first 256, VPT float4 each
+template <int SEM, int CPT, int VPT>
 __global__ __launch_bounds__(kSwigluThreads) void k_gemv_swiglu(MatSet ms, GemvPro pro, uint32_t K, uint32_t step_rows,
                                                      uint32_t step_cols, int8_t* __restrict__ hq,
                                                      float* __restrict__ hsc, uint16_t* __restrict__ hh,
                                                      float* __restrict__ hf) {
-    constexpr int VPT = 1;              // K <= 1024: one float4 of the row per thread
     constexpr uint32_t RT = 64;         // tile rows: 32 gate + 32 up
     extern __shared__ __align__(16) float sm[];  // x quants [K] | x scale bits [nb] | squares, then epilogue operands
     __shared__ float s_scale;
@@ -857,10 +857,14 @@ __global__ __launch_bounds__(kSwigluThreads) void k_gemv_swiglu(MatSet ms, GemvP
 
     // 1. the producer's inputs first, so waiting for them never waits for the weights
     float4 va[VPT], vb[VPT], vw[VPT];
-    if (tid < n4) {
-        va[0] = ((const float4*)pro.a)[tid];
-        vb[0] = pro.b ? ((const float4*)pro.b)[tid] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        vw[0] = ((const float4*)pro.w)[tid];
+#pragma unroll
+    for (int u = 0; u < VPT; u++) {
+        const uint32_t f = tid + 256 * u;
+        if (f < n4) {
+            va[u] = ((const float4*)pro.a)[f];
+            vb[u] = pro.b ? ((const float4*)pro.b)[f] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            vw[u] = ((const float4*)pro.w)[f];
+        }
     }
     // 2. the weight tile: chunk tid + NT u is (tile row, 16-byte column). The
     // two matrices' bases are read once (uniform) and selected per chunk: an
@@ -898,7 +902,8 @@ __global__ __launch_bounds__(kSwigluThreads) void k_gemv_swiglu(MatSet ms, GemvP
     }
     if (tid < 32) etab[tid] = etv;  // read after the producer's barriers
     // 3. the producer, while the weights are in flight
-    gemv_produce<SEM, PRO_NORM, VPT>(pro, K, va, vb, vw, xq, xsb, scratch, &s_scale);
+    // with eight chunks per thread in flight the chain holds 32 values a lane
+    gemv_produce<SEM, PRO_NORM, VPT, CPT >= 8 ? 32 : 64>(pro, K, va, vb, vw, xq, xsb, scratch, &s_scale);
 
     // 4. block dots against the LDS row, the epilogue operands to LDS
     const uint32_t per = gemv_out_floats(SEM, nb), q4p = gemv_q4p(nb);
@@ -956,14 +961,19 @@ hipError_t launch_gate_up_swiglu(hipStream_t st, int sem, const DevMatrix& gate,
     const size_t lds = (head + (ops > k ? ops : k)) * sizeof(float);
     const size_t cpt = (64 * kc + kSwigluThreads - 1) / kSwigluThreads;
     const dim3 grid((unsigned)(n / 32));
-#define KR_SWIGLU(SEMV, CPTV)                                                                                     \
-    hipLaunchKernelGGL((k_gemv_swiglu<SEMV, CPTV>), grid, dim3(kSwigluThreads), lds, st, ms, pro, (uint32_t)k,  \
+    const size_t vpt = (k / 4 + 255) / 256;
+#define KR_SWIGLU(SEMV, CPTV, VPTV)                                                                                    \
+    hipLaunchKernelGGL((k_gemv_swiglu<SEMV, CPTV, VPTV>), grid, dim3(kSwigluThreads), lds, st, ms, pro, (uint32_t)k, \
                        (uint32_t)(kSwigluThreads / kc), (uint32_t)(kSwigluThreads % kc), hq, hs, hh, hf)
-#define KR_SWIGLU_CPT(SEMV) \
-    if (cpt <= 2)           \
-        KR_SWIGLU(SEMV, 2); \
-    else                    \
-        KR_SWIGLU(SEMV, 4);
+#define KR_SWIGLU_CPT(SEMV)    \
+    if (cpt <= 2)              \
+        KR_SWIGLU(SEMV, 2, 1); \
+    else if (cpt <= 4)         \
+        KR_SWIGLU(SEMV, 4, 1); \
+    else if (vpt <= 1)         \
+        KR_SWIGLU(SEMV, 8, 1); \
+    else                       \
+        KR_SWIGLU(SEMV, 8, 2);
     switch (sem) {
         case SEM_FMA_CHAIN: KR_SWIGLU_CPT(SEM_FMA_CHAIN) break;
         case SEM_FOUR_PARTIALS_F32: KR_SWIGLU_CPT(SEM_FOUR_PARTIALS_F32) break;
@@ -3218,6 +3228,25 @@ hipError_t launch_mul(hipStream_t st, float* o, const float* a, const float* b, 
         hipLaunchKernelGGL(k_mul_seq, dim3(1), dim3(64), 0, st, o, a, b, n);
     else
         hipLaunchKernelGGL(k_mul, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, o, a, b, n);
+    return hipGetLastError();
+}
+
+// rows x n products o[r os + i] = a[r as + i] * b[r bs + i] in one launch:
+// the per-row mul calls of a batched LFM2 conv layer (lfm2.rs:584-622), whose
+// outputs never overlap their inputs
+__global__ void k_mul_rows(float* __restrict__ o, size_t os, const float* __restrict__ a, size_t as,
+                           const float* __restrict__ b, size_t bs, size_t rows, size_t n) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= rows * n) return;
+    const size_t r = i / n, e = i - r * n;
+    const float x = a[r * as + e], y = b[r * bs + e];
+    o[r * os + e] = x * y;
+}
+hipError_t launch_mul_rows(hipStream_t st, float* o, size_t os, const float* a, size_t as, const float* b, size_t bs,
+                           size_t rows, size_t n) {
+    if (rows * n == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_mul_rows, dim3((unsigned)((rows * n + 255) / 256)), dim3(256), 0, st, o, os, a, as, b, bs,
+                       rows, n);
     return hipGetLastError();
 }
 

@@ -114,6 +114,9 @@ bool attention_rows_uniform(const DevWindow* host_windows, size_t n_rows, size_t
 hipError_t launch_add(hipStream_t st, float* dst, const float* src, size_t n);
 hipError_t launch_mul(hipStream_t st, float* out, const float* a, const float* b, size_t n,
                       int sequential);
+// o[r os + i] = a[r as + i] * b[r bs + i] for r < rows, i < n (no overlap of o with a or b)
+hipError_t launch_mul_rows(hipStream_t st, float* o, size_t os, const float* a, size_t as, const float* b, size_t bs,
+                           size_t rows, size_t n);
 hipError_t launch_copy(hipStream_t st, float* dst, const float* src, size_t n);
 // reads n floats (n % 4 == 0) and discards them; `sink` is never written in practice
 hipError_t launch_stream_read(hipStream_t st, const float* p, size_t n, int* sink);

@@ -425,11 +425,11 @@ int prefill_rows(krl_model* m, const std::vector<Row>& rows, bool stepped_conv =
             } else {
                 int ci[1] = {KR_PROJ_CONV_IN};
                 KRC(m, kri::project_q(b, l, ci, &p.bcx, 1, n_tok));
-                for (size_t r = 0; r < n_tok; r++)
-                    KRC(m, kr_mul(b, p.h, r * g.dim, p.bcx, r * 3 * g.dim, p.bcx, r * 3 * g.dim + 2 * g.dim, g.dim));
+                // the per-row B * x products (lfm2.rs:584-595), all rows in one launch
+                KRC(m, kri::mul_rows(b, p.h, 0, g.dim, p.bcx, 0, 3 * g.dim, p.bcx, 2 * g.dim, 3 * g.dim, n_tok, g.dim));
                 TRY(prefill_conv(m, l, n_tok, stepped_conv));
-                for (size_t r = 0; r < n_tok; r++)
-                    KRC(m, kr_mul(b, p.cy, r * g.dim, p.bcx, r * 3 * g.dim + g.dim, p.co, r * g.dim, g.dim));
+                // the per-row C * conv_out products (lfm2.rs:611-622), all rows in one launch
+                KRC(m, kri::mul_rows(b, p.cy, 0, g.dim, p.bcx, g.dim, 3 * g.dim, p.co, 0, g.dim, n_tok, g.dim));
                 KRC(m, kr_project(b, l, KR_PROJ_CONV_OUT, p.cy, p.o, n_tok));
             }
             KRC(m, kri::norm_quant(b, p.x, p.o, n.ffn, p.xb, n_tok, g.dim, g.eps));

@@ -2450,12 +2450,12 @@ __global__ __launch_bounds__(64 * NWAVES) void k_attn_rows(const float* __restri
                                                    int8_t* __restrict__ qo, float* __restrict__ so,
                                                    uint16_t* __restrict__ ho) {
     using Sh = AttnRowsShape<HS, NWAVES>;
-    constexpr uint32_t NW = Sh::NW, NT = Sh::NT, LPR = Sh::LPR, RPW = Sh::RPW, F = HS / 4;
-    constexpr uint32_t TV = Sh::TV, KSV = Sh::KSV;
+    constexpr uint32_t NW = Sh::NW, NT = Sh::NT, LPR = Sh::LPR, RPW = Sh::RPW, T = Sh::T, F = HS / 4;
+    constexpr uint32_t NH = Sh::NH, FK = Sh::FK, KSK = Sh::KSK, TV = Sh::TV, KSV = Sh::KSV;
     constexpr uint32_t R = NW * RPW / G, RG = R * G;
     extern __shared__ __align__(16) float sm[];
     float* sc = sm;             // [RG][scs]
-    float* kt = sc + RG * scs;  // K stage [T][KSK] or V stage [TV][KSV]
+    float* kt = sc + RG * scs;  // K stage [T][KSK] (HS < 128) or V stage [TV][KSV]
     __shared__ uint32_t s_cnt[NW * RPW];
     __shared__ float s_sum[NW * RPW];
     __shared__ uint64_t etab[32];
@@ -2479,108 +2479,196 @@ __global__ __launch_bounds__(64 * NWAVES) void k_attn_rows(const float* __restri
     for (uint32_t rg = 0; rg < RG; rg++) cmax = max(cmax, s_cnt[rg]);
     const float* kbase = kc + loff + kvo;
     const float* vbase = vc + loff + kvo;
-    // V stages are fetched into registers one stage ahead (PT float4 per
-    // thread) and stored to LDS after the current stage is consumed, so the
-    // global latency overlaps the compute; the barrier after the compute
-    // waits for LDS only, leaving the fetch in flight.
+    // K (HS < 128) and V stages are fetched into registers one stage ahead
+    // (PT float4 per thread) and stored to LDS after the current stage is
+    // consumed, so the global latency overlaps the compute; the barrier after
+    // the compute waits for LDS only, leaving the fetch in flight.
     constexpr uint32_t PT = TV * F / NT;
-    static_assert(PT * NT == TV * F, "V stage pieces");
+    static_assert(PT * NT == T * FK && PT * NT == TV * F, "K and V stages hold the same pieces");
     attn_v4f pre[PT];
     const bool off32 = (uint64_t)seq_len * kv_dim * 4 <= 0xFFFFFFFFull;  // every slot's byte offset fits 32 bits
+    auto tile_len = [&](uint32_t i0) { return i0 < cmax ? min(T, cmax - i0) : 0u; };
     auto vlen = [&](uint32_t i0) { return i0 < cmax ? min(TV, cmax - i0) : 0u; };
+    // K stage s: positions of tile s / NH, dims half s % NH; V stage s: positions s TV ..
+    auto kfetch = [&](uint32_t st) {
+        const uint32_t i0 = st / NH * T;
+        attn_tile_fetch<FK, PT, NT, T>(pre, kbase, w0, n_shared, kv_dim, off32, i0, tile_len(i0), st % NH * FK);
+    };
     auto vfetch = [&](uint32_t st) {
         attn_tile_fetch<F, PT, NT, TV>(pre, vbase, w0, n_shared, kv_dim, off32, st * TV, vlen(st * TV), 0);
     };
-    vfetch(0);  // the first V stage lands while the scores and the softmax run
 
-    // 1. scores. Wave w takes window positions 64 (NW t + w) .. + 63 of round
-    // t, lane = position, for every pair of the block: the lane's K row comes
-    // from memory straight into registers, KD dims at a time (the next chunk
-    // in flight while one is used), and the pairs' q values, the same for
-    // every lane, sit in scalar registers QD dims at a time. Each K value
-    // feeds one FMA per pair and no K passes through LDS.
-    {
-        constexpr uint32_t PGS = attn_pair_group(RG);  // pairs per group: the largest divisor of RG up to 8
-        static_assert(RG % PGS == 0, "pair groups");
-        // q dims per scalar block: a power of two with PGS QD <= 32 registers
-        constexpr uint32_t QD = 32 / PGS >= 32 ? 32 : 32 / PGS >= 16 ? 16 : 32 / PGS >= 8 ? 8 : 4;
-        constexpr uint32_t KD = HS < 32 ? HS : 32, NKC = HS / KD;  // K chunk dims, chunks per row
-        static_assert(KD % QD == 0 && QD % 4 == 0 && HS % KD == 0, "blocks");
-        const uint32_t nvalid = min(RG, nr * G);  // pairs past the block's end read the last valid pair
-        const uint32_t nround = (cmax + 64 * NW - 1) / (64 * NW);
-#pragma unroll 1
-        for (uint32_t t = 0; t < nround; t++) {
-            const uint32_t pos = (t * NW + wv) * 64 + lane;
-            const uint32_t pc = pos < cmax ? pos : cmax - 1;
-            const float* krow = kbase + (size_t)win_slot(w0, n_shared, pc) * kv_dim;
-#pragma unroll 1
-            for (uint32_t g0 = 0; g0 < RG; g0 += PGS) {
-                const float* qp[PGS];
-#pragma unroll
-                for (uint32_t k = 0; k < PGS; k++) {
-                    const uint32_t rg = min(g0 + k, nvalid - 1), r = rg / G, j = rg - r * G;
-                    qp[k] = q + (size_t)(r0 + r) * width + (size_t)(h0 + j) * HS;
-                }
-                float acc[PGS][4];
-#pragma unroll
-                for (uint32_t k = 0; k < PGS; k++) acc[k][0] = acc[k][1] = acc[k][2] = acc[k][3] = 0.0f;
-                // the FMAs of K chunk c (in kk) against the pairs' q, QD dims at a
-                // time; the q offsets pass through an empty asm so that no q
-                // block is loaded before the one in use (all of them at once
-                // would not fit the scalar registers)
-                auto qblocks = [&](const float4(&kk)[KD / 4], uint32_t c) {
-#pragma unroll
-                    for (uint32_t d0 = 0; d0 < KD; d0 += QD) {
-                        float4 qv[PGS][QD / 4];
-#pragma unroll
-                        for (uint32_t k = 0; k < PGS; k++) {
-                            uint32_t off = c * KD + d0;
-                            asm volatile("" : "+s"(off));
-                            const float* qk = qp[k] + off;
-#pragma unroll
-                            for (uint32_t u = 0; u < QD / 4; u++) qv[k][u] = *(const float4*)(qk + 4 * u);
-                        }
-#pragma unroll
-                        for (uint32_t u = 0; u < QD / 4; u++) {
-                            const float4 kv = kk[d0 / 4 + u];
-#pragma unroll
-                            for (uint32_t k = 0; k < PGS; k++) {
-                                const float4 qq = qv[k][u];
-                                acc[k][0] = __builtin_fmaf(qq.x, kv.x, acc[k][0]);
-                                acc[k][1] = __builtin_fmaf(qq.y, kv.y, acc[k][1]);
-                                acc[k][2] = __builtin_fmaf(qq.z, kv.z, acc[k][2]);
-                                acc[k][3] = __builtin_fmaf(qq.w, kv.w, acc[k][3]);
-                            }
-                        }
-                        __builtin_amdgcn_sched_barrier(0);  // the next q block's loads stay below
+    if constexpr (HS == 128) {
+        vfetch(0);  // the first V stage lands while the scores and the softmax run
+        // 1. scores. Wave w takes window positions 64 (NW t + w) .. + 63 of round
+        // t, lane = position, for every pair of the block: the lane's K row comes
+        // from memory straight into registers, KD dims at a time (the next chunk
+        // in flight while one is used), and the pairs' q values, the same for
+        // every lane, sit in scalar registers QD dims at a time. Each K value
+        // feeds one FMA per pair and no K passes through LDS.
+        {
+            constexpr uint32_t PGS = attn_pair_group(RG);  // pairs per group: the largest divisor of RG up to 8
+            static_assert(RG % PGS == 0, "pair groups");
+            // q dims per scalar block: a power of two with PGS QD <= 32 registers
+            constexpr uint32_t QD = 32 / PGS >= 32 ? 32 : 32 / PGS >= 16 ? 16 : 32 / PGS >= 8 ? 8 : 4;
+            constexpr uint32_t KD = HS < 32 ? HS : 32, NKC = HS / KD;  // K chunk dims, chunks per row
+            static_assert(KD % QD == 0 && QD % 4 == 0 && HS % KD == 0, "blocks");
+            const uint32_t nvalid = min(RG, nr * G);  // pairs past the block's end read the last valid pair
+            const uint32_t nround = (cmax + 64 * NW - 1) / (64 * NW);
+    #pragma unroll 1
+            for (uint32_t t = 0; t < nround; t++) {
+                const uint32_t pos = (t * NW + wv) * 64 + lane;
+                const uint32_t pc = pos < cmax ? pos : cmax - 1;
+                const float* krow = kbase + (size_t)win_slot(w0, n_shared, pc) * kv_dim;
+    #pragma unroll 1
+                for (uint32_t g0 = 0; g0 < RG; g0 += PGS) {
+                    const float* qp[PGS];
+    #pragma unroll
+                    for (uint32_t k = 0; k < PGS; k++) {
+                        const uint32_t rg = min(g0 + k, nvalid - 1), r = rg / G, j = rg - r * G;
+                        qp[k] = q + (size_t)(r0 + r) * width + (size_t)(h0 + j) * HS;
                     }
-                };
-                auto kload = [&](float4(&kk)[KD / 4], uint32_t c) {
-#pragma unroll
-                    for (uint32_t u = 0; u < KD / 4; u++) kk[u] = *(const float4*)(krow + c * KD + 4 * u);
-                };
-                // chunks in two register sets used in turn: the next chunk is in
-                // flight while one is used
-                float4 ka[KD / 4], kb[KD / 4];
-                kload(ka, 0);
-#pragma unroll 1
-                for (uint32_t c = 0; c < NKC; c += 2) {
-                    if (c + 1 < NKC) kload(kb, c + 1);
-                    qblocks(ka, c);
-                    if (c + 2 < NKC) kload(ka, c + 2);
-                    if (c + 1 < NKC) qblocks(kb, c + 1);
-                }
-#pragma unroll
-                for (uint32_t k = 0; k < PGS; k++) {
-                    const uint32_t rg = g0 + k;
-                    // dot.rs:360: (acc0 + acc1) + (acc2 + acc3), then * scale (cpu.rs:609)
-                    if (rg < RG && pos < s_cnt[rg])
-                        sc[rg * scs + pos] = ((acc[k][0] + acc[k][1]) + (acc[k][2] + acc[k][3])) * scale;
+                    float acc[PGS][4];
+    #pragma unroll
+                    for (uint32_t k = 0; k < PGS; k++) acc[k][0] = acc[k][1] = acc[k][2] = acc[k][3] = 0.0f;
+                    // the FMAs of K chunk c (in kk) against the pairs' q, QD dims at a
+                    // time; the q offsets pass through an empty asm so that no q
+                    // block is loaded before the one in use (all of them at once
+                    // would not fit the scalar registers)
+                    auto qblocks = [&](const float4(&kk)[KD / 4], uint32_t c) {
+    #pragma unroll
+                        for (uint32_t d0 = 0; d0 < KD; d0 += QD) {
+                            float4 qv[PGS][QD / 4];
+    #pragma unroll
+                            for (uint32_t k = 0; k < PGS; k++) {
+                                uint32_t off = c * KD + d0;
+                                asm volatile("" : "+s"(off));
+                                const float* qk = qp[k] + off;
+    #pragma unroll
+                                for (uint32_t u = 0; u < QD / 4; u++) qv[k][u] = *(const float4*)(qk + 4 * u);
+                            }
+    #pragma unroll
+                            for (uint32_t u = 0; u < QD / 4; u++) {
+                                const float4 kv = kk[d0 / 4 + u];
+    #pragma unroll
+                                for (uint32_t k = 0; k < PGS; k++) {
+                                    const float4 qq = qv[k][u];
+                                    acc[k][0] = __builtin_fmaf(qq.x, kv.x, acc[k][0]);
+                                    acc[k][1] = __builtin_fmaf(qq.y, kv.y, acc[k][1]);
+                                    acc[k][2] = __builtin_fmaf(qq.z, kv.z, acc[k][2]);
+                                    acc[k][3] = __builtin_fmaf(qq.w, kv.w, acc[k][3]);
+                                }
+                            }
+                            __builtin_amdgcn_sched_barrier(0);  // the next q block's loads stay below
+                        }
+                    };
+                    auto kload = [&](float4(&kk)[KD / 4], uint32_t c) {
+    #pragma unroll
+                        for (uint32_t u = 0; u < KD / 4; u++) kk[u] = *(const float4*)(krow + c * KD + 4 * u);
+                    };
+                    // chunks in two register sets used in turn: the next chunk is in
+                    // flight while one is used
+                    float4 ka[KD / 4], kb[KD / 4];
+                    kload(ka, 0);
+    #pragma unroll 1
+                    for (uint32_t c = 0; c < NKC; c += 2) {
+                        if (c + 1 < NKC) kload(kb, c + 1);
+                        qblocks(ka, c);
+                        if (c + 2 < NKC) kload(ka, c + 2);
+                        if (c + 1 < NKC) qblocks(kb, c + 1);
+                    }
+    #pragma unroll
+                    for (uint32_t k = 0; k < PGS; k++) {
+                        const uint32_t rg = g0 + k;
+                        // dot.rs:360: (acc0 + acc1) + (acc2 + acc3), then * scale (cpu.rs:609)
+                        if (rg < RG && pos < s_cnt[rg])
+                            sc[rg * scs + pos] = ((acc[k][0] + acc[k][1]) + (acc[k][2] + acc[k][3])) * scale;
+                    }
                 }
             }
         }
+        __syncthreads();  // every pair's scores are in LDS
+    } else {
+        // the q rows of this wave's pairs (wave-uniform addresses: scalar
+        // loads; pairs past the block's end read the last valid pair)
+        const float* qrow[RPW];
+#pragma unroll
+        for (uint32_t k = 0; k < RPW; k++) {
+            const uint32_t rg = min(wv * RPW + k, min(RG, nr * G) - 1), r = rg / G, j = rg - r * G;
+            qrow[k] = q + (size_t)(r0 + r) * width + (size_t)(h0 + j) * HS;
+        }
+        // 1. scores of every (pair, position) of each K tile, staged through LDS
+        const uint32_t nks = (cmax + T - 1) / T * NH;
+        kfetch(0);
+        attn_tile_put<FK, PT, NT, T, KSK>(pre, kt, tile_len(0));
+        __syncthreads();
+        float a[RPW][4];
+        for (uint32_t st = 0; st < nks; st++) {
+            const uint32_t i0 = st / NH * T, h = st % NH, nt = tile_len(i0);
+            if (st + 1 < nks)
+                kfetch(st + 1);
+            else  // the first V stage, for phase 3
+                vfetch(0);
+            {  // lane = position, wave = its RPW pairs. The pairs' q values are
+               // wave-uniform: QB float4 per pair at a time go to scalar registers
+               // (RPW QB 4 = 32), then each LDS read of 4 K values feeds 4 FMAs
+               // per pair. K is read a group of GS float4 ahead, into two register
+               // sets used in turn, so only LDS reads are waited on inside a block.
+                constexpr uint32_t QB = 8 / RPW < 2 ? 2 : 8 / RPW, GS = QB < 4 ? QB : 4, NG = QB / GS;
+                static_assert(FK % QB == 0 && QB % GS == 0, "q blocks");
+                const uint32_t ug = h * FK;  // first dim block of this stage
+                const uint32_t pos = lane;
+                if (h == 0) {
+    #pragma unroll
+                    for (uint32_t k = 0; k < RPW; k++) a[k][0] = a[k][1] = a[k][2] = a[k][3] = 0.0f;
+                }
+                const float* krow = kt + pos * KSK;
+    #pragma unroll 1
+                for (uint32_t q0 = 0; q0 < FK; q0 += QB) {
+                    float4 qv[RPW][QB];
+    #pragma unroll
+                    for (uint32_t k = 0; k < RPW; k++)
+    #pragma unroll
+                        for (uint32_t u = 0; u < QB; u++) qv[k][u] = *(const float4*)(qrow[k] + 4 * (ug + q0 + u));
+                    float4 kb[2][GS];
+    #pragma unroll
+                    for (uint32_t t = 0; t < GS; t++) kb[0][t] = *(const float4*)(krow + 4 * (q0 + t));
+    #pragma unroll
+                    for (uint32_t g = 0; g < NG; g++) {
+                        if (g + 1 < NG) {
+    #pragma unroll
+                            for (uint32_t t = 0; t < GS; t++)
+                                kb[(g + 1) & 1][t] = *(const float4*)(krow + 4 * (q0 + GS * (g + 1) + t));
+                        }
+    #pragma unroll
+                        for (uint32_t t = 0; t < GS; t++) {
+                            const float4 kk = kb[g & 1][t];
+    #pragma unroll
+                            for (uint32_t k = 0; k < RPW; k++) {
+                                const float4 qq = qv[k][GS * g + t];
+                                a[k][0] = __builtin_fmaf(qq.x, kk.x, a[k][0]);
+                                a[k][1] = __builtin_fmaf(qq.y, kk.y, a[k][1]);
+                                a[k][2] = __builtin_fmaf(qq.z, kk.z, a[k][2]);
+                                a[k][3] = __builtin_fmaf(qq.w, kk.w, a[k][3]);
+                            }
+                        }
+                    }
+                }
+    #pragma unroll
+                for (uint32_t k = 0; k < RPW; k++) {
+                    const uint32_t rg = wv * RPW + k;
+                    // dot.rs:360: (acc0 + acc1) + (acc2 + acc3), then * scale (cpu.rs:609)
+                    if (h == NH - 1 && rg < RG && pos < nt && i0 + pos < s_cnt[rg])
+                        sc[rg * scs + i0 + pos] = ((a[k][0] + a[k][1]) + (a[k][2] + a[k][3])) * scale;
+                }
+            }
+            lds_barrier();  // the stage is consumed
+            if (st + 1 < nks) {
+                attn_tile_put<FK, PT, NT, T, KSK>(pre, kt, tile_len((st + 1) / NH * T));
+                lds_barrier();
+            }
+        }
     }
-    __syncthreads();  // every pair's scores are in LDS
 
     // 2. softmax of each pair, by the wave that computed its scores
 #pragma unroll

@@ -179,13 +179,24 @@ def bench_gemv(K, reps: int = 3, use_graph: bool = True):
             if fn(ctx, ws, ys, nm, 1) != 0:
                 raise RuntimeError(hip._L.kr_last_error(ctx).decode())
 
+    # Without graphs (for profilers) the launches are issued one by one from
+    # here, slower than the GPU retires them; an MFMA spin of a few ms ahead
+    # of them keeps the GPU busy while they queue, so they then run back to
+    # back as a graph replay runs them (not each after an idle gap).
+    hip.mfma_rate(0, 256, 100)
+    hip.synchronize()
+    hip.timer_start()
+    hip.mfma_rate(0, 256, 2000)
+    spin_iters_per_ms = 2000 / hip.timer_stop()
+
     def timed(group, passes):
         """One pass captured into a HIP graph, as the decode driver replays its
         step; the graph is then replayed `passes` times between two events.
-        Without graphs (for profilers), the launches are issued directly."""
+        Without graphs the launches are issued directly behind a spin."""
         run(group)  # warm-up pass (also evicts the other group from the MALL)
         if not use_graph:
             hip.synchronize()
+            hip.mfma_rate(0, 256, max(1, int(spin_iters_per_ms * 0.03 * passes * len(group))))
             hip.timer_start()
             for _ in range(passes):
                 run(group)
@@ -239,6 +250,7 @@ def bench_gemv(K, reps: int = 3, use_graph: bool = True):
         hip.replay(reps)
     else:
         hip.synchronize()
+        hip.mfma_rate(0, 256, max(1, int(spin_iters_per_ms * 0.03 * reps * len(read_sizes))))
         hip.timer_start()
         for _ in range(reps):
             reads()

@@ -19,7 +19,10 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libkernrt_hip.so")
 
-SOURCES = ["kernels.hip", "backend.hip", "llm.cpp"]
+SOURCES = ["kernels.hip", "attn_mx.hip", "backend.hip", "llm.cpp"]
+# per-source extra flags: the matrix-core attention keeps f32 MFMA results in
+# ordinary vector registers (its vector adds read them directly)
+EXTRA = {"attn_mx.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
 
 FLAGS = [
     "-O3", "-std=c++17", "--offload-arch=gfx950", "-fPIC", "-shared",
@@ -37,10 +40,7 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (ROCm is required to build the HIP backend)")
 
 
-def build(verbose: bool = False) -> str:
-    srcs = [os.path.join(CSRC, s) for s in SOURCES if os.path.exists(os.path.join(CSRC, s))]
-    tmp = LIB + ".tmp"
-    cmd = [hipcc(), *FLAGS, *srcs, "-o", tmp]
+def _run(cmd, verbose: bool) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -51,6 +51,32 @@ def build(verbose: bool = False) -> str:
         raise RuntimeError(f"hipcc failed ({res.returncode}):\n{err}")
     if verbose and err.strip():
         print(err, file=sys.stderr)
+
+
+def build(verbose: bool = False) -> str:
+    """Each source to an object (with its own extra flags), compiled in
+    parallel, then one shared library."""
+    objdir = os.path.join(HERE, "_build")
+    os.makedirs(objdir, exist_ok=True)
+    flags = [f for f in FLAGS if f != "-shared"]
+    jobs = []
+    for src in SOURCES:
+        path = os.path.join(CSRC, src)
+        obj = os.path.join(objdir, src + ".o")
+        cmd = [hipcc(), *flags, *EXTRA.get(src, []), "-c", path, "-o", obj]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        jobs.append((cmd, obj, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)))
+    noise = "'-packed-fp32-ops' is not a recognized feature"
+    for cmd, obj, p in jobs:
+        _, stderr = p.communicate()
+        err = "\n".join(l for l in stderr.splitlines() if noise not in l)
+        if p.returncode != 0:
+            raise RuntimeError(f"hipcc failed ({p.returncode}) on {cmd[-3]}:\n{err}")
+        if verbose and err.strip():
+            print(err, file=sys.stderr)
+    tmp = LIB + ".tmp"
+    _run([hipcc(), "--offload-arch=gfx950", "-fPIC", "-shared", *[o for _, o, _ in jobs], "-o", tmp], verbose)
     os.replace(tmp, LIB)
     return LIB
 

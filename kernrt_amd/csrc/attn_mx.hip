@@ -1,0 +1,410 @@
+// Prefill attention on the matrix core (k_attn_mx_*). Built as its own
+// translation unit with -mllvm -amdgpu-mfma-vgpr-form=1, so that the f32
+// MFMA results land in ordinary vector registers: the vector unit adds them
+// to its chains without a register-file move per value.
+#include <hip/hip_runtime.h>
+
+#include "device.hpp"
+#include "kernels.hpp"
+#include "numerics.hpp"
+
+namespace kr {
+
+// Serial f32 sum of VPL register values per lane, lane 0's first (values
+// past the end are +0.0, which leaves a sum of non-negative terms
+// unchanged): each lane adds its values to the running sum, which passes
+// from lane L to lane L + 1 by DPP (wave_shr:1), as in wave_chain_sum.
+template <int VPL>
+__device__ __forceinline__ float reg_chain_sum(const float (&v)[VPL], uint32_t n) {
+    const uint32_t runs = (n + VPL - 1) / VPL;
+    float acc = 0.0f;
+    for (uint32_t L = 0; L < runs; L++) {
+#pragma unroll
+        for (int k = 0; k < VPL; k++) acc += v[k];
+        if (L + 1 < runs) acc = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(acc), 0x138, 0xf, 0xf, false));
+    }
+    return runs ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), runs - 1)) : 0.0f;
+}
+
+typedef float mx_v32f __attribute__((ext_vector_type(32)));
+// Attention of prefill rows on the matrix core, in three launches over
+// blocks of 32 (row, head) pairs (G query heads of one KV head x 32 / G
+// rows whose windows share a layout). f32 MFMA with one nonzero product per
+// output is an exact fused multiply-add (every output of
+// v_mfma_f32_32x32x1_2b_f32 with a zero or accumulating C is fmaf(a, b, c),
+// subnormals and cancellation included), so the reference's chains run on
+// it unchanged:
+//  1. k_attn_mx_scores: per 32-position tile, the four FMA chains of the dot
+//     (dot.rs:360) over 32 pairs x 32 positions, two chains per instruction
+//     (blocks 0 and 1 = chains 0 and 2, then 1 and 3; lane l of half h
+//     brings dims 4s + 2h and 4s + 2h + 1 of its pair's q and of its
+//     position's key), then ((a0 + a1) + (a2 + a3)) * scale (cpu.rs:609) on
+//     the vector unit. Raw scores go to `att`.
+//  2. k_attn_softmax_att: a wave per pair (elementwise.rs:65-91): the row
+//     from `att` into registers, VPL values per lane; max, exp, the serial
+//     sum (reg_chain_sum), the division; the probabilities back to `att`,
+//     where the reference leaves them.
+//  3. k_attn_mx_v: per two positions one instruction forms the 32 pairs x
+//     32 dims products p_i * v_i[e] (each the correctly rounded product), and
+//     the vector unit adds them to the chains in position order. Positions a
+//     pair's window does not reach get p = 0; the zero products leave the
+//     sums unchanged (the sums start at +0 and never become -0), unless the
+//     V row there holds an infinity or NaN.
+struct MxBlock {
+    uint32_t r0, nr, h0, kvo, n_shared, cmax;
+    DevWindow w0;
+};
+template <int G>
+__device__ __forceinline__ MxBlock mx_block(const DevWindow* windows, uint32_t n_rows, uint32_t kv_mul, uint32_t hs,
+                                            uint32_t* s_cnt) {
+    constexpr uint32_t R = 32 / G;
+    MxBlock b;
+    b.r0 = blockIdx.y * R;
+    b.nr = min(R, n_rows - b.r0);
+    b.h0 = blockIdx.x * G;
+    b.kvo = (b.h0 / kv_mul) * hs;
+    b.w0 = windows[b.r0];
+    b.n_shared = b.w0.shared_end - b.w0.shared_start;
+    if (threadIdx.x < 32) {
+        const uint32_t r = threadIdx.x / G;
+        s_cnt[threadIdx.x] = r < b.nr ? b.n_shared + windows[b.r0 + r].slot - b.w0.att_start + 1 : 0;
+    }
+    __syncthreads();
+    b.cmax = 0;
+    for (uint32_t k = 0; k < 32; k++) b.cmax = max(b.cmax, s_cnt[k]);
+    return b;
+}
+
+template <int G, int HS>
+__global__ __launch_bounds__(256) void k_attn_mx_scores(const float* __restrict__ q, float* __restrict__ att,
+                                                        const float* __restrict__ kc, size_t loff,
+                                                        const DevWindow* __restrict__ windows, uint32_t n_rows,
+                                                        uint32_t n_heads, uint32_t kv_mul, uint32_t kv_dim,
+                                                        uint32_t seq_len, float scale) {
+    constexpr uint32_t NS = HS / 4, KCH = 8, QST = HS + 4;
+    static_assert(32 % G == 0 && (HS == 64 || HS == 128) && NS % KCH == 0, "shape");
+    __shared__ __align__(16) float s_q[32 * QST];  // the pairs' q rows
+    __shared__ uint32_t s_cnt[32];
+    const uint32_t tid = threadIdx.x, lane = tid & 63, h = lane >> 5, pr = lane & 31;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t width = n_heads * HS;
+    const MxBlock B = mx_block<G>(windows, n_rows, kv_mul, HS, s_cnt);
+    const uint32_t r0 = B.r0, nr = B.nr, h0 = B.h0, n_shared = B.n_shared, cmax = B.cmax;
+    const DevWindow w0 = B.w0;
+    // q rows of the 32 pairs (pairs past the block read the last one)
+    for (uint32_t f = tid; f < 32 * (HS / 4); f += 256) {
+        const uint32_t pair = f / (HS / 4), col = f - pair * (HS / 4);
+        const uint32_t qp = min(pair, nr * G - 1), qr = qp / G, qj = qp - qr * G;
+        *(float4*)(s_q + pair * QST + 4 * col) =
+            *(const float4*)(q + (size_t)(r0 + qr) * width + (size_t)(h0 + qj) * HS + 4 * col);
+    }
+    __syncthreads();
+    const float* kbase = kc + loff + B.kvo;
+    auto att_row = [&](uint32_t pair) {
+        const uint32_t r = pair / G, j = pair - r * G;
+        return att + (size_t)(r0 + r) * n_heads * seq_len + (size_t)(h0 + j) * seq_len;
+    };
+    // 1. scores
+    {
+        // this lane's pair's q dims 4s + 2h, 4s + 2h + 1, from LDS
+        const float* qrow = s_q + pr * QST + 2 * h;
+        const uint32_t ntile = (cmax + 31) / 32;
+        // this wave's tiles t = wave, wave + 4, ...; key chunks of KCH steps in
+        // two register sets used in turn, the next chunk (the next tile's first
+        // at a tile's end) in flight while one is used
+        constexpr uint32_t NCH = NS / KCH;
+        static_assert(NCH % 2 == 0, "a tile starts in the first register set");
+        auto krow_of = [&](uint32_t t) {
+            const uint32_t pos = min(32 * t + pr, cmax - 1);
+            return kbase + (size_t)win_slot(w0, n_shared, pos) * kv_dim + 2 * h;
+        };
+        auto kload = [&](float2(&k)[KCH], const float* krow, uint32_t c) {
+#pragma unroll
+            for (uint32_t u = 0; u < KCH; u++) k[u] = *(const float2*)(krow + 4 * (c * KCH + u));
+        };
+        float2 ka[KCH], kb[KCH];
+        const float* krow = krow_of(wave);
+        if (wave < ntile) kload(ka, krow, 0);
+        for (uint32_t t = wave; t < ntile; t += 4) {
+            const float* knext = krow_of(min(t + 4, ntile - 1));
+            mx_v32f a02 = {}, a13 = {};
+            auto steps = [&](const float2(&k)[KCH], uint32_t c) {
+#pragma unroll
+                for (uint32_t u = 0; u < KCH; u++) {
+                    const float2 qq = *(const float2*)(qrow + 4 * (c * KCH + u));
+                    a02 = __builtin_amdgcn_mfma_f32_32x32x1f32(qq.x, k[u].x, a02, 0, 0, 0);
+                    a13 = __builtin_amdgcn_mfma_f32_32x32x1f32(qq.y, k[u].y, a13, 0, 0, 0);
+                }
+                __builtin_amdgcn_sched_barrier(0);  // no chunk's q reads move above the previous chunk
+            };
+#pragma unroll
+            for (uint32_t c = 0; c < NCH; c += 2) {
+                kload(kb, krow, c + 1);
+                steps(ka, c);
+                if (c + 2 < NCH)
+                    kload(ka, krow, c + 2);
+                else
+                    kload(ka, knext, 0);  // the next tile's first chunk (the last tile's again at the end)
+                steps(kb, c + 1);
+            }
+            krow = knext;
+            // element v: pair 8 (v / 4) + 4 h + v % 4, position 32 t + pr; a02 = chains 0 | 2, a13 = 1 | 3
+            const uint32_t pos = 32 * t + pr;
+#pragma unroll
+            for (uint32_t v = 0; v < 16; v++) {
+                const uint32_t pair = 8 * (v >> 2) + 4 * h + (v & 3);
+                const float sv = ((a02[v] + a13[v]) + (a02[16 + v] + a13[16 + v])) * scale;
+                if (pos < s_cnt[pair]) att_row(pair)[pos] = sv;
+            }
+        }
+    }
+}
+
+// Softmax of 64 (row, head) pairs of `att` per workgroup (elementwise.rs:65-91),
+// in three passes over 64-position chunks; wave w serves pairs 16 w .. +15,
+// one pair per load (lane = position: 256 contiguous bytes). (a) the max;
+// (b) the exps, to `att` and to an LDS tile [pair][position], and the serial
+// sums: lane p of wave 0 runs pair p's chain over the tile in position
+// order, so one wave carries 64 chains; (c) the divisions, the probabilities
+// back to `att`.
+__global__ __launch_bounds__(256) void k_attn_softmax_att(float* __restrict__ att,
+                                                          const DevWindow* __restrict__ windows, uint32_t n_rows,
+                                                          uint32_t n_heads, uint32_t seq_len) {
+    constexpr uint32_t C = 64, TS = C + 1, PW = 16;  // chunk positions, tile row stride, pairs per wave
+    __shared__ float s_e[2][64 * TS];
+    __shared__ uint64_t etab[32];
+    __shared__ float s_sum[64];
+    __shared__ uint32_t s_n[64];
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t n_pairs = n_rows * n_heads, p0 = blockIdx.x * 64;
+    if (tid < 32) etab[tid] = kExp2Tab[tid];
+    if (tid < 64) {
+        uint32_t n = 0;
+        if (p0 + tid < n_pairs) {
+            const DevWindow w = windows[(p0 + tid) / n_heads];
+            n = w.shared_end - w.shared_start + w.slot - w.att_start + 1;
+        }
+        s_n[tid] = n;
+    }
+    __syncthreads();
+    uint32_t nmax = 0;
+    for (uint32_t k = 0; k < 64; k++) nmax = max(nmax, s_n[k]);
+    const uint32_t nch = (nmax + C - 1) / C;
+    auto row = [&](uint32_t k) { return att + (size_t)min(p0 + PW * wave + k, n_pairs - 1) * seq_len; };
+    // every load is unconditional, at a position inside the longest window
+    // (values past a pair's own window are selected away, never used), so
+    // the loads of a batch are all in flight together
+    auto at = [&](uint32_t i) { return i < nmax ? i : nmax - 1; };
+    // (a) max of each of the wave's pairs, 8 chunks a batch
+    float m[PW];
+#pragma unroll
+    for (uint32_t k = 0; k < PW; k++) {
+        const float* e = row(k);
+        const uint32_t n = s_n[PW * wave + k];
+        float mk = -INFINITY;
+        for (uint32_t c0 = 0; c0 < nch; c0 += 8) {
+            float x[8];
+#pragma unroll
+            for (uint32_t u = 0; u < 8; u++) x[u] = e[at((c0 + u) * C + lane)];
+#pragma unroll
+            for (uint32_t u = 0; u < 8; u++)
+                if ((c0 + u) * C + lane < n) mk = fmaxf(mk, x[u]);
+        }
+        m[k] = wave_max(mk);
+    }
+    // (b) exps and the serial sums
+    float sum = 0.0f;  // lane p of wave 0: pair p's running sum
+    for (uint32_t c = 0; c < nch; c++) {
+        const uint32_t i = c * C + lane;
+        float* t = s_e[c & 1] + PW * wave * TS + lane;
+        float x[PW];
+#pragma unroll
+        for (uint32_t k = 0; k < PW; k++) x[k] = row(k)[at(i)];
+#pragma unroll
+        for (uint32_t k = 0; k < PW; k++) {
+            const bool live = i < s_n[PW * wave + k];
+            const float ev = live ? glibc_expf(x[k] - m[k], etab) : 0.0f;
+            if (live) row(k)[i] = ev;
+            t[k * TS] = ev;
+        }
+        __syncthreads();  // the tile is complete (the other buffer's chain is done)
+        if (tid < 64) {
+            const float* r = s_e[c & 1] + tid * TS;
+#pragma unroll 16
+            for (uint32_t k = 0; k < C; k++) sum += r[k];  // past a window's end: +0.0, which leaves the sum unchanged
+        }
+    }
+    if (tid < 64) s_sum[tid] = sum;
+    __syncthreads();
+    // (c) the probabilities, 8 chunks a batch
+#pragma unroll
+    for (uint32_t k = 0; k < PW; k++) {
+        float* e = row(k);
+        const uint32_t n = s_n[PW * wave + k];
+        const float sj = s_sum[PW * wave + k];
+        for (uint32_t c0 = 0; c0 < nch; c0 += 8) {
+            float x[8];
+#pragma unroll
+            for (uint32_t u = 0; u < 8; u++) x[u] = e[at((c0 + u) * C + lane)];
+#pragma unroll
+            for (uint32_t u = 0; u < 8; u++) {
+                const uint32_t i = (c0 + u) * C + lane;
+                if (i < n) e[i] = div_rn(x[u], sj);
+            }
+        }
+    }
+}
+
+template <int G, int HS>
+__global__ __launch_bounds__(256) void k_attn_mx_v(const float* __restrict__ att, float* __restrict__ out,
+                                                   const float* __restrict__ vc, size_t loff,
+                                                   const DevWindow* __restrict__ windows, uint32_t n_rows,
+                                                   uint32_t n_heads, uint32_t kv_mul, uint32_t kv_dim,
+                                                   uint32_t seq_len, int8_t* __restrict__ qo, float* __restrict__ so,
+                                                   uint16_t* __restrict__ ho) {
+    constexpr uint32_t VST = HS + 4, PST = 33;
+    static_assert(32 % G == 0 && (HS == 64 || HS == 128), "shape");
+    __shared__ __align__(16) float s_v[2][32 * VST];  // V chunk [position][dim]
+    __shared__ float s_p[2][32 * PST];                // probability chunk [position][pair]
+    __shared__ uint32_t s_cnt[32];
+    const uint32_t tid = threadIdx.x, lane = tid & 63, h = lane >> 5, pr = lane & 31;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t width = n_heads * HS;
+    const MxBlock B = mx_block<G>(windows, n_rows, kv_mul, HS, s_cnt);
+    const uint32_t r0 = B.r0, nr = B.nr, h0 = B.h0, n_shared = B.n_shared, cmax = B.cmax;
+    const DevWindow w0 = B.w0;
+    const float* vbase = vc + loff + B.kvo;
+    auto att_row = [&](uint32_t pair) {
+        const uint32_t r = pair / G, j = pair - r * G;
+        return att + (size_t)(r0 + r) * n_heads * seq_len + (size_t)(h0 + j) * seq_len;
+    };
+    // 3. V sums: wave w owns dims 32 w .. 32 w + 31 (HS / 32 waves); chunks
+    // of 32 positions staged through LDS, the next chunk's loads in flight
+    struct VStage {
+        float4 v[HS / 32];
+        float4 p;
+    };
+    const uint32_t nch = (cmax + 31) / 32;
+    // loader: V piece f = tid + 256 k (position f / (HS/4), float4 f % (HS/4)); probabilities: pair tid / 8,
+    // positions 4 (tid % 8) .. + 3
+    auto gload = [&](VStage& st, uint32_t c) {
+        c = c < nch ? c : nch - 1;
+#pragma unroll
+        for (uint32_t k = 0; k < HS / 32; k++) {
+            const uint32_t f = tid + 256 * k, rr = f / (HS / 4), col = f - rr * (HS / 4);
+            st.v[k] = *(const float4*)(vbase + (size_t)win_slot(w0, n_shared, min(32 * c + rr, cmax - 1)) * kv_dim + 4 * col);
+        }
+        const uint32_t pair = tid >> 3, i0 = 32 * c + 4 * (tid & 7), n = s_cnt[pair];
+        const float* row = att_row(min(pair, nr * G - 1));
+        st.p.x = i0 < n ? row[i0] : 0.0f;
+        st.p.y = i0 + 1 < n ? row[i0 + 1] : 0.0f;
+        st.p.z = i0 + 2 < n ? row[i0 + 2] : 0.0f;
+        st.p.w = i0 + 3 < n ? row[i0 + 3] : 0.0f;
+    };
+    auto lstore = [&](const VStage& st, int buf) {
+#pragma unroll
+        for (uint32_t k = 0; k < HS / 32; k++) {
+            const uint32_t f = tid + 256 * k, rr = f / (HS / 4), col = f - rr * (HS / 4);
+            *(float4*)(s_v[buf] + rr * VST + 4 * col) = st.v[k];
+        }
+        const uint32_t pair = tid >> 3, i0 = 4 * (tid & 7);
+        s_p[buf][i0 * PST + pair] = st.p.x;
+        s_p[buf][(i0 + 1) * PST + pair] = st.p.y;
+        s_p[buf][(i0 + 2) * PST + pair] = st.p.z;
+        s_p[buf][(i0 + 3) * PST + pair] = st.p.w;
+    };
+    float o[16];
+#pragma unroll
+    for (uint32_t v = 0; v < 16; v++) o[v] = 0.0f;
+    const bool vwave = wave < HS / 32;
+    const uint32_t d0 = 32 * (vwave ? wave : 0);
+    auto compute = [&](int buf, uint32_t c) {
+        if (c >= nch || !vwave) return;
+        const float* pb = s_p[buf] + h * PST + pr;
+        const float* vb = s_v[buf] + h * VST + d0 + pr;
+        // the next step's instruction is issued before this step's adds, its
+        // operands read two steps ahead, so neither waits on the other
+        float pa[16], va[16];
+#pragma unroll
+        for (uint32_t k = 0; k < 16; k++) pa[k] = pb[2 * k * PST], va[k] = vb[2 * k * VST];
+        mx_v32f d = __builtin_amdgcn_mfma_f32_32x32x1f32(pa[0], va[0], mx_v32f{}, 0, 0, 0);
+#pragma unroll
+        for (uint32_t k = 0; k < 16; k++) {
+            mx_v32f dn;
+            if (k + 1 < 16) dn = __builtin_amdgcn_mfma_f32_32x32x1f32(pa[k + 1], va[k + 1], mx_v32f{}, 0, 0, 0);
+#pragma unroll
+            for (uint32_t v = 0; v < 16; v++) o[v] += d[v];  // position 2 k
+#pragma unroll
+            for (uint32_t v = 0; v < 16; v++) o[v] += d[16 + v];  // position 2 k + 1
+            if (k + 1 < 16) d = dn;
+        }
+    };
+    gemm_pipeline<4, VStage>(nch, gload, lstore, compute);
+    if (!vwave) return;
+    // element v: pair 8 (v / 4) + 4 h + v % 4, dim d0 + pr
+#pragma unroll
+    for (uint32_t v = 0; v < 16; v++) {
+        const uint32_t pair = 8 * (v >> 2) + 4 * h + (v & 3), r = pair / G, j = pair - r * G;
+        const bool live = r < nr;
+        const size_t oi = (size_t)(r0 + r) * width + (size_t)(h0 + j) * HS + d0 + pr;
+        if (live) out[oi] = o[v];
+        if (qo) quant_lane(o[v], live, qo + oi, so + oi / 32, ho + oi / 32);  // quant.rs:864-873
+    }
+}
+
+static constexpr size_t kAttnMxMinWindow = 1024;
+// k_attn_mx: query heads per workgroup (the largest of 8, 4, 2, 1 dividing
+// kv_mul), and whether a launch can take it: head size 64 or 128, windows
+// of at most 4096 positions, n_rows >= 2 and every block of 32 / G rows
+// sharing one window layout (prefill).
+static size_t attn_mx_group(size_t kv_mul) {
+    for (size_t g : {8, 4, 2})
+        if (kv_mul % g == 0) return g;
+    return 1;
+}
+bool attention_mx_ok(const DevWindow* w, size_t n_rows, size_t max_count, size_t kv_mul, size_t hs) {
+    // shorter windows run faster on k_attn_rows (one launch, more workgroups)
+    if ((hs != 64 && hs != 128) || max_count < kAttnMxMinWindow || max_count > 64 * 64 || n_rows < 2) return false;
+    const size_t R = 32 / attn_mx_group(kv_mul);
+    for (size_t r = 0; r < n_rows; r++) {
+        const DevWindow& a = w[r - r % R];
+        if (a.att_start != w[r].att_start || a.shared_start != w[r].shared_start || a.shared_end != w[r].shared_end)
+            return false;
+    }
+    return true;
+}
+
+hipError_t launch_attention_mx(hipStream_t st, const float* q, float* out, float* att, const float* kc,
+                               const float* vc, size_t layer, const DevWindow* windows, size_t n_rows,
+                               size_t max_count, size_t n_heads, size_t kv_mul, size_t hs, size_t kv_dim,
+                               size_t seq_len, float scale, int8_t* qo, float* so, uint16_t* ho) {
+    const size_t G = attn_mx_group(kv_mul), R = 32 / G;
+    const dim3 grid((unsigned)(n_heads / G), (unsigned)((n_rows + R - 1) / R));
+    const dim3 gsm((unsigned)((n_rows * n_heads + 63) / 64));
+#define KR_ATTN_MX(g, h)                                                                                      \
+    hipLaunchKernelGGL((k_attn_mx_scores<g, h>), grid, dim3(256), 0, st, q, att, kc, layer * seq_len * kv_dim,       \
+                   windows, (uint32_t)n_rows, (uint32_t)n_heads, (uint32_t)kv_mul, (uint32_t)kv_dim,            \
+                   (uint32_t)seq_len, scale);                                                                   \
+    hipLaunchKernelGGL(k_attn_softmax_att, gsm, dim3(256), 0, st, att, windows, (uint32_t)n_rows, (uint32_t)n_heads, \
+                   (uint32_t)seq_len);                                                                          \
+    hipLaunchKernelGGL((k_attn_mx_v<g, h>), grid, dim3(256), 0, st, att, out, vc, layer * seq_len * kv_dim, windows, \
+                   (uint32_t)n_rows, (uint32_t)n_heads, (uint32_t)kv_mul, (uint32_t)kv_dim, (uint32_t)seq_len,  \
+                   qo, so, ho)
+#define KR_ATTN_MX_G(g)      \
+    if (hs == 64) {          \
+    KR_ATTN_MX(g, 64);   \
+    } else {                 \
+    KR_ATTN_MX(g, 128);  \
+    }
+    switch (G) {
+        case 8: KR_ATTN_MX_G(8) break;
+        case 4: KR_ATTN_MX_G(4) break;
+        case 2: KR_ATTN_MX_G(2) break;
+        default: KR_ATTN_MX_G(1) break;
+    }
+#undef KR_ATTN_MX_G
+#undef KR_ATTN_MX
+    return hipGetLastError();
+}
+
+}  // namespace kr

@@ -11,6 +11,7 @@
 
 #include <algorithm>
 
+#include "device.hpp"
 #include "kernels.hpp"
 #include "numerics.hpp"
 
@@ -20,12 +21,6 @@ static constexpr int kStorageQ8_0 = 2;
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-// Correctly rounded f32 division and square root, as the reference's x86 SSE
-// arithmetic gives. The IEEE double operation rounded once to f32 is the
-// correctly rounded f32 result (53 >= 2*24 + 2 makes the double rounding
-// innocuous for / and sqrt); the f32 library forms are not exact here.
-__device__ __forceinline__ float div_rn(float a, float b) { return (float)((double)a / (double)b); }
-__device__ __forceinline__ float sqrt_rn(float a) { return (float)__builtin_sqrt((double)a); }
 
 // Serial f32 chains, software-pipelined: operands are fetched in batches of
 // kPipe elements, the next batch's loads issued before the current batch's
@@ -96,25 +91,6 @@ __device__ __forceinline__ float seq_fma(const float2* __restrict__ e, uint32_t 
                              [](float s, float2 v) { return __builtin_fmaf(v.x, v.y, s); });
 }
 
-// NaN-ignoring max across lanes with DPP (a few cycles per step, no LDS
-// round trip as with __shfl_xor). Max is order-free, so every grouping gives
-// the same result.
-template <int CTRL, int ROWS>
-__device__ __forceinline__ float dpp_max_step(float v) {
-    return fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, ROWS, 0xf,
-                                                               false)));
-}
-// max over each aligned group of 8 / 16 / 32 lanes, in every lane of the group
-__device__ __forceinline__ float group_max8(float v) {
-    v = dpp_max_step<0xB1, 0xf>(v);      // quad_perm [1,0,3,2]
-    v = dpp_max_step<0x4E, 0xf>(v);      // quad_perm [2,3,0,1]
-    return dpp_max_step<0x141, 0xf>(v);  // row_half_mirror
-}
-__device__ __forceinline__ float group_max16(float v) { return dpp_max_step<0x140, 0xf>(group_max8(v)); }  // row_mirror
-__device__ __forceinline__ float group_max32(float v) {
-    v = group_max16(v);  // then lane ^ 16 within the 32-lane group (ds_swizzle bit mode)
-    return fmaxf(v, __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F)));
-}
 // Two blocks' exact sums from one lane pair: for chunks u0 and u1 the even
 // lane holds the dots of the first 16 bytes of each block (d0, d1), the odd
 // lane those of the second 16 bytes. One swap gives the even lane block u0
@@ -132,33 +108,7 @@ __device__ __forceinline__ int dot16(const v4i& w, const v4i& x) {
     return __builtin_amdgcn_sdot4(w.w, x.w, acc, false);
 }
 
-// f32 -> IEEE binary16 bits, round to nearest even, as f32_to_f16_bits
-// (quant.rs:722-758): the hardware conversion gives the same bits for every
-// non-NaN input (all 2^32 inputs compared on gfx950); NaN keeps the software
-// routine's quiet-NaN pattern. A couple of instructions instead of a branchy
-// integer routine on the quantizers' critical path.
-__device__ __forceinline__ uint16_t f16_bits(float v) {
-    const uint32_t b = f2u(v);
-    const uint16_t hw = __builtin_bit_cast(uint16_t, (_Float16)v);
-    return (b & 0x7fffffffu) > 0x7f800000u ? (uint16_t)(((b >> 16) & 0x8000u) | 0x7e00u) : hw;
-}
 
-// Quantize one f32 value per lane as part of a 32-lane Q8 block (lanes
-// 32k..32k+31 hold one block), exactly as Q8Vec::quantize_into does
-// (quant.rs:864-873). Every lane of the half-wave must call this.
-__device__ __forceinline__ void quant_lane(float v, bool valid, int8_t* q, float* s, uint16_t* h) {
-    float m = fmaxf(0.0f, fabsf(v));
-    m = group_max32(m);
-    float d = div_rn(m, 127.0f);
-    float inv = d > 0.0f ? div_rn(1.0f, d) : 0.0f;
-    if (valid) {
-        *q = q8_round(v * inv);
-        if ((threadIdx.x & 31) == 0) {
-            *s = d;
-            *h = f16_bits(d);
-        }
-    }
-}
 
 // ---------------------------------------------------------------------------
 // Activation quantization (quant.rs:856-874 per row, cpu.rs:143-158 batched).
@@ -415,18 +365,6 @@ __device__ __forceinline__ float quad_bcast(float v) {
     return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), K * 0x55, 0xf, 0xf, false));
 }
 
-// NaN-ignoring max over the 64 lanes of a wave, returned to every lane: DPP
-// swaps within quads, half-rows and rows, then row broadcasts 15 and 31 into
-// lane 63 (a few cycles each, no LDS round trip). Max is order-free.
-__device__ __forceinline__ float wave_max(float v) {
-    v = dpp_max_step<0xB1, 0xf>(v);   // quad_perm [1,0,3,2]
-    v = dpp_max_step<0x4E, 0xf>(v);   // quad_perm [2,3,0,1]
-    v = dpp_max_step<0x141, 0xf>(v);  // row_half_mirror
-    v = dpp_max_step<0x140, 0xf>(v);  // row_mirror
-    v = dpp_max_step<0x142, 0xa>(v);  // row_bcast:15 into rows 1, 3
-    v = dpp_max_step<0x143, 0xc>(v);  // row_bcast:31 into rows 2, 3
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
-}
 
 template <int SEM, int M, int CPT>
 __global__ __launch_bounds__(256) void k_gemv(MatSet ms, QuantAct x, uint32_t K, uint32_t R, uint32_t step_rows,
@@ -1069,32 +1007,6 @@ __device__ __forceinline__ void gemm_row_scales(float (&xs)[16], const float* co
     }
 }
 
-// The chunk pipeline shared by both GEMM kernels. At chunk c, the register
-// stage (c + 1) % NS holds chunk c + 1 and LDS buffer c & 1 holds chunk c.
-// The chunk count is padded to a multiple of NS and every load and store is
-// unconditional (loads clamp to the last chunk, compute skips blocks past
-// the end), so all paths issue the same loads and each wait covers only the
-// chunk about to be stored.
-template <int NS, typename Stage, typename Load, typename Store, typename Compute>
-__device__ __forceinline__ void gemm_pipeline(uint32_t nchunks, Load&& gload, Store&& lstore, Compute&& compute) {
-    static_assert(NS % 2 == 0, "the LDS buffer parity follows the register stage");
-    Stage st[NS];
-#pragma unroll
-    for (int s = 0; s < NS; s++) gload(st[s], s);
-    lstore(st[0], 0);
-    gload(st[0], NS);
-    __syncthreads();
-    const uint32_t steps = (nchunks + NS - 1) / NS * NS;
-    for (uint32_t c0 = 0; c0 < steps; c0 += NS) {
-#pragma unroll
-        for (int u = 0; u < NS; u++) {
-            compute(u & 1, c0 + u);
-            lstore(st[(u + 1) % NS], (u + 1) & 1);
-            gload(st[(u + 1) % NS], c0 + u + 1 + NS);
-            __syncthreads();
-        }
-    }
-}
 
 // Q8_0 GEMM, four partial sums (dot.rs:34-45), on 16x16x32 int8 MFMA. The
 // reference's four partial sums t[j] (blocks b with b % 4 == j, in order) are
@@ -1686,9 +1598,6 @@ hipError_t launch_kv_write(hipStream_t st, float* kc, float* vc, size_t layer, s
 static constexpr uint32_t kAttnThreads = 512;
 static constexpr size_t kAttnLds = 150 * 1024;
 
-__device__ __forceinline__ uint32_t win_slot(const DevWindow& w, uint32_t n_shared, uint32_t i) {
-    return i < n_shared ? w.shared_start + i : w.att_start + (i - n_shared);
-}
 
 __global__ __launch_bounds__(512) void k_attention(const float* __restrict__ q, float* __restrict__ out,
                                                    float* __restrict__ att, const float* __restrict__ kc,
@@ -2990,6 +2899,11 @@ hipError_t launch_attention(hipStream_t st, const float* q, float* out, float* a
     if (hs == 0 || hs > 256 || hs % 4 != 0 || kv_mul == 0 || n_heads % kv_mul != 0) return hipErrorInvalidValue;
     if (qo && hs % 32 != 0) return hipErrorInvalidValue;
     if (max_count > seq_len) max_count = seq_len;
+    if (host_windows && attention_mx_ok(host_windows, n_rows, max_count, kv_mul, hs)) {
+        // blocks of 32 (row, head) pairs on the matrix core (attn_mx.hip)
+        return launch_attention_mx(st, q, out, att, kc, vc, layer, windows, n_rows, max_count, n_heads, kv_mul, hs,
+                                   kv_dim, seq_len, scale, qo, so, ho);
+    }
     if (host_windows && attention_rows_uniform(host_windows, n_rows, max_count, kv_mul, hs)) {
         // many rows whose blocks share a window layout: k_attn_rows
         const size_t G = attn_rows_group(kv_mul), nw = attn_rows_waves(G, hs, max_count);

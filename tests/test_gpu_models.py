@@ -246,3 +246,21 @@ def test_greedy_256_tokens_at_360m_width():
     cpu.prefill(prompt, 0)
     want = _oracle_greedy(cpu, int(prompt[-1]), len(prompt), 256)
     assert list(got) == want
+
+
+@pytest.mark.parametrize("n_heads,n_kv,hs,storage", [(4, 2, 128, "q8_0"), (4, 4, 64, "q8_0x4"), (6, 2, 64, "q8_0")])
+def test_long_prefill_attention_on_the_matrix_core(n_heads, n_kv, hs, storage):
+    # Windows of 1024+ positions take the three-launch matrix-core attention
+    # (k_attn_mx_scores / k_attn_softmax_att / k_attn_mx_v: the score and V
+    # chains as exact f32 MFMA), head groups 2, 1 and 3 (run as 1): a
+    # 1100-token pass (causal windows from 1 to 1100 in 32-pair blocks), a
+    # 150-token chunk over the cache, then two decode steps.
+    c = O.Config(dim=n_heads * hs, hidden_dim=128, n_layers=1, n_heads=n_heads, n_kv_heads=n_kv, vocab_size=64,
+                 seq_len=1280, rms_eps=1e-5, rope_theta=10_000.0, rope_interleaved=False, head_dim=hs)
+    ow = gaussian_weights(c, storage, seed=hs + n_heads)
+    prompt = [(i * 7 + 3) % c.vocab_size for i in range(1250)]
+    gpu, cpu = gpu_model(c, ow), O.Model(c, ow, "cpu")
+    assert_bits_equal(gpu.prefill(prompt[:1100], 0), cpu.prefill(prompt[:1100], 0), "prefill 1100")
+    assert_bits_equal(gpu.prefill(prompt[1100:], 1100), cpu.prefill(prompt[1100:], 1100), "chunk at 1100")
+    for t in range(2):
+        assert_bits_equal(gpu.forward(9 + t, 1250 + t), cpu.forward(9 + t, 1250 + t), f"decode at {1250 + t}")

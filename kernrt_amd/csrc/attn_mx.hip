@@ -163,15 +163,15 @@ __global__ __launch_bounds__(256) void k_attn_mx_scores(const float* __restrict_
 // Softmax of 64 (row, head) pairs of `att` per workgroup (elementwise.rs:65-91),
 // in three passes over 64-position chunks; wave w serves pairs 16 w .. +15,
 // one pair per load (lane = position: 256 contiguous bytes). (a) the max;
-// (b) the exps, to `att` and to an LDS tile [pair][position], and the serial
-// sums: lane p of wave 0 runs pair p's chain over the tile in position
-// order, so one wave carries 64 chains; (c) the divisions, the probabilities
-// back to `att`.
+// (b) the exps, to `att` and to the wave's rows of an LDS tile
+// [pair][position], and the serial sums: lane k < 16 runs pair 16 w + k's
+// chain over its row in position order; (c) the divisions, the
+// probabilities back to `att`.
 __global__ __launch_bounds__(256) void k_attn_softmax_att(float* __restrict__ att,
                                                           const DevWindow* __restrict__ windows, uint32_t n_rows,
                                                           uint32_t n_heads, uint32_t seq_len) {
     constexpr uint32_t C = 64, TS = C + 1, PW = 16;  // chunk positions, tile row stride, pairs per wave
-    __shared__ float s_e[2][64 * TS];
+    __shared__ float s_e[1][64 * TS];
     __shared__ uint64_t etab[32];
     __shared__ float s_sum[64];
     __shared__ uint32_t s_n[64];
@@ -212,11 +212,13 @@ __global__ __launch_bounds__(256) void k_attn_softmax_att(float* __restrict__ at
         }
         m[k] = wave_max(mk);
     }
-    // (b) exps and the serial sums
-    float sum = 0.0f;  // lane p of wave 0: pair p's running sum
+    // (b) exps and the serial sums: lane k < 16 of wave w runs pair 16 w + k's
+    // chain over the wave's own tile rows (written by this wave only: a
+    // wave-local LDS ordering, no workgroup barrier)
+    float sum = 0.0f;
+    float* tw = s_e[0] + PW * wave * TS;
     for (uint32_t c = 0; c < nch; c++) {
         const uint32_t i = c * C + lane;
-        float* t = s_e[c & 1] + PW * wave * TS + lane;
         float x[PW];
 #pragma unroll
         for (uint32_t k = 0; k < PW; k++) x[k] = row(k)[at(i)];
@@ -225,17 +227,19 @@ __global__ __launch_bounds__(256) void k_attn_softmax_att(float* __restrict__ at
             const bool live = i < s_n[PW * wave + k];
             const float ev = live ? glibc_expf(x[k] - m[k], etab) : 0.0f;
             if (live) row(k)[i] = ev;
-            t[k * TS] = ev;
+            tw[k * TS + lane] = ev;
         }
-        __syncthreads();  // the tile is complete (the other buffer's chain is done)
-        if (tid < 64) {
-            const float* r = s_e[c & 1] + tid * TS;
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's tile stores have landed
+        __builtin_amdgcn_wave_barrier();
+        if (lane < PW) {
+            const float* r = tw + lane * TS;
 #pragma unroll 16
             for (uint32_t k = 0; k < C; k++) sum += r[k];  // past a window's end: +0.0, which leaves the sum unchanged
         }
+        __builtin_amdgcn_wave_barrier();  // the chains have read the tile before it is rewritten
     }
-    if (tid < 64) s_sum[tid] = sum;
-    __syncthreads();
+    if (lane < PW) s_sum[PW * wave + lane] = sum;
+    __builtin_amdgcn_wave_barrier();
     // (c) the probabilities, 8 chunks a batch
 #pragma unroll
     for (uint32_t k = 0; k < PW; k++) {
@@ -280,9 +284,10 @@ __global__ __launch_bounds__(256) void k_attn_mx_v(const float* __restrict__ att
     };
     // 3. V sums: wave w owns dims 32 w .. 32 w + 31 (HS / 32 waves); chunks
     // of 32 positions staged through LDS, the next chunk's loads in flight
+    typedef float vs4 __attribute__((ext_vector_type(4)));  // native vectors: the stages stay in registers
     struct VStage {
-        float4 v[HS / 32];
-        float4 p;
+        vs4 v[HS / 32];
+        vs4 p;
     };
     const uint32_t nch = (cmax + 31) / 32;
     // loader: V piece f = tid + 256 k (position f / (HS/4), float4 f % (HS/4)); probabilities: pair tid / 8,
@@ -292,20 +297,21 @@ __global__ __launch_bounds__(256) void k_attn_mx_v(const float* __restrict__ att
 #pragma unroll
         for (uint32_t k = 0; k < HS / 32; k++) {
             const uint32_t f = tid + 256 * k, rr = f / (HS / 4), col = f - rr * (HS / 4);
-            st.v[k] = *(const float4*)(vbase + (size_t)win_slot(w0, n_shared, min(32 * c + rr, cmax - 1)) * kv_dim + 4 * col);
+            st.v[k] = *(const vs4*)(vbase + (size_t)win_slot(w0, n_shared, min(32 * c + rr, cmax - 1)) * kv_dim + 4 * col);
         }
         const uint32_t pair = tid >> 3, i0 = 32 * c + 4 * (tid & 7), n = s_cnt[pair];
         const float* row = att_row(min(pair, nr * G - 1));
-        st.p.x = i0 < n ? row[i0] : 0.0f;
-        st.p.y = i0 + 1 < n ? row[i0 + 1] : 0.0f;
-        st.p.z = i0 + 2 < n ? row[i0 + 2] : 0.0f;
-        st.p.w = i0 + 3 < n ? row[i0 + 3] : 0.0f;
+        // loads inside the longest window (always), values past the pair's own set to 0
+        const uint32_t lim = cmax - 1;
+        const float p0 = row[min(i0, lim)], p1 = row[min(i0 + 1, lim)], p2 = row[min(i0 + 2, lim)],
+                    p3 = row[min(i0 + 3, lim)];
+        st.p = vs4{i0 < n ? p0 : 0.0f, i0 + 1 < n ? p1 : 0.0f, i0 + 2 < n ? p2 : 0.0f, i0 + 3 < n ? p3 : 0.0f};
     };
     auto lstore = [&](const VStage& st, int buf) {
 #pragma unroll
         for (uint32_t k = 0; k < HS / 32; k++) {
             const uint32_t f = tid + 256 * k, rr = f / (HS / 4), col = f - rr * (HS / 4);
-            *(float4*)(s_v[buf] + rr * VST + 4 * col) = st.v[k];
+            *(vs4*)(s_v[buf] + rr * VST + 4 * col) = st.v[k];
         }
         const uint32_t pair = tid >> 3, i0 = 4 * (tid & 7);
         s_p[buf][i0 * PST + pair] = st.p.x;
@@ -339,7 +345,24 @@ __global__ __launch_bounds__(256) void k_attn_mx_v(const float* __restrict__ att
             if (k + 1 < 16) d = dn;
         }
     };
-    gemm_pipeline<4, VStage>(nch, gload, lstore, compute);
+    // two register stages, named (not an array), so they stay in registers:
+    // chunk c + 2 is in flight while chunk c is computed from LDS
+    VStage sa, sb;
+    gload(sa, 0);
+    gload(sb, 1);
+    lstore(sa, 0);
+    gload(sa, 2);
+    __syncthreads();
+    for (uint32_t c = 0; c < nch; c += 2) {
+        compute(0, c);
+        lstore(sb, 1);  // chunk c + 1
+        gload(sb, c + 3);
+        __syncthreads();
+        compute(1, c + 1);
+        lstore(sa, 0);  // chunk c + 2
+        gload(sa, c + 4);
+        __syncthreads();
+    }
     if (!vwave) return;
     // element v: pair 8 (v / 4) + 4 h + v % 4, dim d0 + pr
 #pragma unroll

@@ -80,11 +80,12 @@ __global__ __launch_bounds__(256) void k_attn_mx_scores(const float* __restrict_
                                                         const float* __restrict__ kc, size_t loff,
                                                         const DevWindow* __restrict__ windows, uint32_t n_rows,
                                                         uint32_t n_heads, uint32_t kv_mul, uint32_t kv_dim,
-                                                        uint32_t seq_len, float scale) {
+                                                        uint32_t seq_len, float scale, float* __restrict__ pmax) {
     constexpr uint32_t NS = HS / 4, KCH = 8, QST = HS + 4;
     static_assert(32 % G == 0 && (HS == 64 || HS == 128) && NS % KCH == 0, "shape");
     __shared__ __align__(16) float s_q[32 * QST];  // the pairs' q rows
     __shared__ uint32_t s_cnt[32];
+    __shared__ float s_mx[4][32];
     const uint32_t tid = threadIdx.x, lane = tid & 63, h = lane >> 5, pr = lane & 31;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t width = n_heads * HS;
@@ -123,6 +124,9 @@ __global__ __launch_bounds__(256) void k_attn_mx_scores(const float* __restrict_
             for (uint32_t u = 0; u < KCH; u++) k[u] = *(const float2*)(krow + 4 * (c * KCH + u));
         };
         float2 ka[KCH], kb[KCH];
+        float mloc[16];  // the max of element v's pair over this lane's positions (order-free)
+#pragma unroll
+        for (uint32_t v = 0; v < 16; v++) mloc[v] = -INFINITY;
         const float* krow = krow_of(wave);
         if (wave < ntile) kload(ka, krow, 0);
         for (uint32_t t = wave; t < ntile; t += 4) {
@@ -154,26 +158,43 @@ __global__ __launch_bounds__(256) void k_attn_mx_scores(const float* __restrict_
             for (uint32_t v = 0; v < 16; v++) {
                 const uint32_t pair = 8 * (v >> 2) + 4 * h + (v & 3);
                 const float sv = ((a02[v] + a13[v]) + (a02[16 + v] + a13[16 + v])) * scale;
-                if (pos < s_cnt[pair]) att_row(pair)[pos] = sv;
+                if (pos < s_cnt[pair]) {
+                    att_row(pair)[pos] = sv;
+                    mloc[v] = fmaxf(mloc[v], sv);
+                }
             }
         }
+        // each pair's max (NaN ignored, as f32::max): over the 32 positions of a
+        // half-wave, then over the waves
+#pragma unroll
+        for (uint32_t v = 0; v < 16; v++) {
+            const float mv = group_max32(mloc[v]);
+            if (pr == 0) s_mx[wave][8 * (v >> 2) + 4 * h + (v & 3)] = mv;
+        }
+    }
+    __syncthreads();
+    if (tid < 32 && s_cnt[tid] > 0) {
+        const uint32_t r = tid / G, j = tid - r * G;
+        pmax[(size_t)(r0 + r) * n_heads + h0 + j] =
+            fmaxf(fmaxf(s_mx[0][tid], s_mx[1][tid]), fmaxf(s_mx[2][tid], s_mx[3][tid]));
     }
 }
 
-// Softmax of 64 (row, head) pairs of `att` per workgroup (elementwise.rs:65-91),
-// in three passes over 64-position chunks; wave w serves pairs 16 w .. +15,
-// one pair per load (lane = position: 256 contiguous bytes). (a) the max;
-// (b) the exps, to `att` and to the wave's rows of an LDS tile
-// [pair][position], and the serial sums: lane k < 16 runs pair 16 w + k's
-// chain over its row in position order; (c) the divisions, the
-// probabilities back to `att`.
+// Exps and sums of the softmax of 64 (row, head) pairs of `att` per
+// workgroup (elementwise.rs:65-91), over 64-position chunks; wave w serves
+// pairs 16 w .. +15, one pair per load (lane = position: 256 contiguous
+// bytes). With each pair's max from k_attn_mx_scores, the exps go to `att`
+// and to the wave's rows of an LDS tile [pair][position], and lane k < 16
+// runs pair 16 w + k's serial sum over its row in position order. The
+// division by the sum happens where the probabilities are next read
+// (k_attn_mx_v).
 __global__ __launch_bounds__(256) void k_attn_softmax_att(float* __restrict__ att,
                                                           const DevWindow* __restrict__ windows, uint32_t n_rows,
-                                                          uint32_t n_heads, uint32_t seq_len) {
+                                                          uint32_t n_heads, uint32_t seq_len,
+                                                          const float* __restrict__ pmax, float* __restrict__ psum) {
     constexpr uint32_t C = 64, TS = C + 1, PW = 16;  // chunk positions, tile row stride, pairs per wave
-    __shared__ float s_e[1][64 * TS];
+    __shared__ float s_e[64 * TS];
     __shared__ uint64_t etab[32];
-    __shared__ float s_sum[64];
     __shared__ uint32_t s_n[64];
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t n_pairs = n_rows * n_heads, p0 = blockIdx.x * 64;
@@ -190,33 +211,17 @@ __global__ __launch_bounds__(256) void k_attn_softmax_att(float* __restrict__ at
     uint32_t nmax = 0;
     for (uint32_t k = 0; k < 64; k++) nmax = max(nmax, s_n[k]);
     const uint32_t nch = (nmax + C - 1) / C;
-    auto row = [&](uint32_t k) { return att + (size_t)min(p0 + PW * wave + k, n_pairs - 1) * seq_len; };
+    auto pidx = [&](uint32_t k) { return min(p0 + PW * wave + k, n_pairs - 1); };
+    auto row = [&](uint32_t k) { return att + (size_t)pidx(k) * seq_len; };
     // every load is unconditional, at a position inside the longest window
     // (values past a pair's own window are selected away, never used), so
     // the loads of a batch are all in flight together
     auto at = [&](uint32_t i) { return i < nmax ? i : nmax - 1; };
-    // (a) max of each of the wave's pairs, 8 chunks a batch
     float m[PW];
 #pragma unroll
-    for (uint32_t k = 0; k < PW; k++) {
-        const float* e = row(k);
-        const uint32_t n = s_n[PW * wave + k];
-        float mk = -INFINITY;
-        for (uint32_t c0 = 0; c0 < nch; c0 += 8) {
-            float x[8];
-#pragma unroll
-            for (uint32_t u = 0; u < 8; u++) x[u] = e[at((c0 + u) * C + lane)];
-#pragma unroll
-            for (uint32_t u = 0; u < 8; u++)
-                if ((c0 + u) * C + lane < n) mk = fmaxf(mk, x[u]);
-        }
-        m[k] = wave_max(mk);
-    }
-    // (b) exps and the serial sums: lane k < 16 of wave w runs pair 16 w + k's
-    // chain over the wave's own tile rows (written by this wave only: a
-    // wave-local LDS ordering, no workgroup barrier)
+    for (uint32_t k = 0; k < PW; k++) m[k] = pmax[pidx(k)];
     float sum = 0.0f;
-    float* tw = s_e[0] + PW * wave * TS;
+    float* tw = s_e + PW * wave * TS;
     for (uint32_t c = 0; c < nch; c++) {
         const uint32_t i = c * C + lane;
         float x[PW];
@@ -238,34 +243,16 @@ __global__ __launch_bounds__(256) void k_attn_softmax_att(float* __restrict__ at
         }
         __builtin_amdgcn_wave_barrier();  // the chains have read the tile before it is rewritten
     }
-    if (lane < PW) s_sum[PW * wave + lane] = sum;
-    __builtin_amdgcn_wave_barrier();
-    // (c) the probabilities, 8 chunks a batch
-#pragma unroll
-    for (uint32_t k = 0; k < PW; k++) {
-        float* e = row(k);
-        const uint32_t n = s_n[PW * wave + k];
-        const float sj = s_sum[PW * wave + k];
-        for (uint32_t c0 = 0; c0 < nch; c0 += 8) {
-            float x[8];
-#pragma unroll
-            for (uint32_t u = 0; u < 8; u++) x[u] = e[at((c0 + u) * C + lane)];
-#pragma unroll
-            for (uint32_t u = 0; u < 8; u++) {
-                const uint32_t i = (c0 + u) * C + lane;
-                if (i < n) e[i] = div_rn(x[u], sj);
-            }
-        }
-    }
+    if (lane < PW && p0 + PW * wave + lane < n_pairs) psum[p0 + PW * wave + lane] = sum;
 }
 
 template <int G, int HS>
-__global__ __launch_bounds__(256) void k_attn_mx_v(const float* __restrict__ att, float* __restrict__ out,
+__global__ __launch_bounds__(256) void k_attn_mx_v(float* __restrict__ att, float* __restrict__ out,
                                                    const float* __restrict__ vc, size_t loff,
                                                    const DevWindow* __restrict__ windows, uint32_t n_rows,
                                                    uint32_t n_heads, uint32_t kv_mul, uint32_t kv_dim,
                                                    uint32_t seq_len, int8_t* __restrict__ qo, float* __restrict__ so,
-                                                   uint16_t* __restrict__ ho) {
+                                                   uint16_t* __restrict__ ho, const float* __restrict__ psum) {
     constexpr uint32_t VST = HS + 4, PST = 33;
     static_assert(32 % G == 0 && (HS == 64 || HS == 128), "shape");
     __shared__ __align__(16) float s_v[2][32 * VST];  // V chunk [position][dim]
@@ -307,7 +294,18 @@ __global__ __launch_bounds__(256) void k_attn_mx_v(const float* __restrict__ att
                     p3 = row[min(i0 + 3, lim)];
         st.p = vs4{i0 < n ? p0 : 0.0f, i0 + 1 < n ? p1 : 0.0f, i0 + 2 < n ? p2 : 0.0f, i0 + 3 < n ? p3 : 0.0f};
     };
-    auto lstore = [&](const VStage& st, int buf) {
+    // the probabilities: each exp divided by its pair's sum (elementwise.rs:88-91),
+    // written back to `att` where the reference leaves them, and to LDS
+    const uint32_t lpair = tid >> 3, lr = lpair / G, lj = lpair - lr * G;
+    const float lsum = s_cnt[lpair] > 0 ? psum[(size_t)(r0 + lr) * n_heads + h0 + lj] : 1.0f;
+    uint32_t lchunk = 0;  // the chunk lstore is given next
+    auto lstore = [&](VStage& st, int buf) {
+        const uint32_t g0 = 32 * lchunk++ + 4 * (tid & 7), n = s_cnt[lpair];
+        float* arow = att_row(min(lpair, nr * G - 1));
+        if (g0 < n) st.p.x = div_rn(st.p.x, lsum), arow[g0] = st.p.x;
+        if (g0 + 1 < n) st.p.y = div_rn(st.p.y, lsum), arow[g0 + 1] = st.p.y;
+        if (g0 + 2 < n) st.p.z = div_rn(st.p.z, lsum), arow[g0 + 2] = st.p.z;
+        if (g0 + 3 < n) st.p.w = div_rn(st.p.w, lsum), arow[g0 + 3] = st.p.w;
 #pragma unroll
         for (uint32_t k = 0; k < HS / 32; k++) {
             const uint32_t f = tid + 256 * k, rr = f / (HS / 4), col = f - rr * (HS / 4);
@@ -400,24 +398,26 @@ bool attention_mx_ok(const DevWindow* w, size_t n_rows, size_t max_count, size_t
 hipError_t launch_attention_mx(hipStream_t st, const float* q, float* out, float* att, const float* kc,
                                const float* vc, size_t layer, const DevWindow* windows, size_t n_rows,
                                size_t max_count, size_t n_heads, size_t kv_mul, size_t hs, size_t kv_dim,
-                               size_t seq_len, float scale, int8_t* qo, float* so, uint16_t* ho) {
+                               size_t seq_len, float scale, int8_t* qo, float* so, uint16_t* ho, float* scratch) {
     const size_t G = attn_mx_group(kv_mul), R = 32 / G;
     const dim3 grid((unsigned)(n_heads / G), (unsigned)((n_rows + R - 1) / R));
     const dim3 gsm((unsigned)((n_rows * n_heads + 63) / 64));
-#define KR_ATTN_MX(g, h)                                                                                      \
-    hipLaunchKernelGGL((k_attn_mx_scores<g, h>), grid, dim3(256), 0, st, q, att, kc, layer * seq_len * kv_dim,       \
-                   windows, (uint32_t)n_rows, (uint32_t)n_heads, (uint32_t)kv_mul, (uint32_t)kv_dim,            \
-                   (uint32_t)seq_len, scale);                                                                   \
+    float* pmax = scratch;                  // each pair's max
+    float* psum = scratch + n_rows * n_heads;  // and its sum of exps
+#define KR_ATTN_MX(g, h)                                                                                         \
+    hipLaunchKernelGGL((k_attn_mx_scores<g, h>), grid, dim3(256), 0, st, q, att, kc, layer * seq_len * kv_dim,      \
+                       windows, (uint32_t)n_rows, (uint32_t)n_heads, (uint32_t)kv_mul, (uint32_t)kv_dim,           \
+                       (uint32_t)seq_len, scale, pmax);                                                            \
     hipLaunchKernelGGL(k_attn_softmax_att, gsm, dim3(256), 0, st, att, windows, (uint32_t)n_rows, (uint32_t)n_heads, \
-                   (uint32_t)seq_len);                                                                          \
+                       (uint32_t)seq_len, pmax, psum);                                                             \
     hipLaunchKernelGGL((k_attn_mx_v<g, h>), grid, dim3(256), 0, st, att, out, vc, layer * seq_len * kv_dim, windows, \
-                   (uint32_t)n_rows, (uint32_t)n_heads, (uint32_t)kv_mul, (uint32_t)kv_dim, (uint32_t)seq_len,  \
-                   qo, so, ho)
-#define KR_ATTN_MX_G(g)      \
-    if (hs == 64) {          \
-    KR_ATTN_MX(g, 64);   \
-    } else {                 \
-    KR_ATTN_MX(g, 128);  \
+                       (uint32_t)n_rows, (uint32_t)n_heads, (uint32_t)kv_mul, (uint32_t)kv_dim, (uint32_t)seq_len, \
+                       qo, so, ho, psum)
+#define KR_ATTN_MX_G(g)     \
+    if (hs == 64) {         \
+        KR_ATTN_MX(g, 64);  \
+    } else {                \
+        KR_ATTN_MX(g, 128); \
     }
     switch (G) {
         case 8: KR_ATTN_MX_G(8) break;

@@ -814,9 +814,12 @@ int attention_many(kr_ctx* c, const float* q, float* out, float* att, size_t lay
         if (qo) HIPCHK(c, kr::launch_quantize(c->stream, out, n, width, width, qo, so, ho));
         return KR_OK;
     }
+    // the matrix-core prefill attention keeps each pair's max and sum in the scratch
+    int rc = ensure_attn_scratch(c, 2 * n * sp->n_heads);
+    if (rc) return rc;
     HIPCHK(c, kr::launch_attention(c->stream, q, out, att, c->kc, c->vc, layer, (const kr::DevWindow*)wd, n, max_count,
                                    sp->n_heads, sp->kv_mul, sp->head_size, sp->kv_dim, sp->seq_len, scale, qo, so, ho,
-                                   hw));
+                                   hw, c->attn_scratch));
     return KR_OK;
 }
 

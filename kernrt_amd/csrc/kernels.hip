@@ -2894,15 +2894,15 @@ hipError_t launch_attention(hipStream_t st, const float* q, float* out, float* a
                             const float* vc, size_t layer, const DevWindow* windows, size_t n_rows,
                             size_t max_count, size_t n_heads, size_t kv_mul, size_t hs, size_t kv_dim,
                             size_t seq_len, float scale, int8_t* qo, float* so, uint16_t* ho,
-                            const DevWindow* host_windows) {
+                            const DevWindow* host_windows, float* mx_scratch) {
     if (n_rows == 0) return hipSuccess;
     if (hs == 0 || hs > 256 || hs % 4 != 0 || kv_mul == 0 || n_heads % kv_mul != 0) return hipErrorInvalidValue;
     if (qo && hs % 32 != 0) return hipErrorInvalidValue;
     if (max_count > seq_len) max_count = seq_len;
-    if (host_windows && attention_mx_ok(host_windows, n_rows, max_count, kv_mul, hs)) {
+    if (host_windows && mx_scratch && attention_mx_ok(host_windows, n_rows, max_count, kv_mul, hs)) {
         // blocks of 32 (row, head) pairs on the matrix core (attn_mx.hip)
         return launch_attention_mx(st, q, out, att, kc, vc, layer, windows, n_rows, max_count, n_heads, kv_mul, hs,
-                                   kv_dim, seq_len, scale, qo, so, ho);
+                                   kv_dim, seq_len, scale, qo, so, ho, mx_scratch);
     }
     if (host_windows && attention_rows_uniform(host_windows, n_rows, max_count, kv_mul, hs)) {
         // many rows whose blocks share a window layout: k_attn_rows

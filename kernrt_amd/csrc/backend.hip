@@ -804,7 +804,7 @@ int attention_many(kr_ctx* c, const float* q, float* out, float* att, size_t lay
     const kr::DevWindow* hw = (const kr::DevWindow*)w.data();
     const float scale = 1.0f / sqrtf((float)sp->head_size);  // cpu.rs:591
     if (n >= 2 && !kr::attention_rows_uniform(hw, n, max_count, sp->kv_mul, sp->head_size) &&
-        kr::attention_split_ok(max_count, sp->kv_mul, sp->head_size)) {
+        kr::attention_split_rows_ok(max_count, sp->kv_mul, sp->head_size)) {
         int rc = ensure_attn_scratch(c, n * kr::attention_split_scratch(sp->n_heads, c->seq_len));
         if (rc) return rc;
         HIPCHK(c, kr::launch_attention_split_rows(c->stream, q, out, att, c->kc, c->vc, layer, (const kr::DevWindow*)wd,

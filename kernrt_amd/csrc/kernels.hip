@@ -256,13 +256,19 @@ __device__ __forceinline__ float chain_sum(const float* __restrict__ e, uint32_t
             s += r[u].w;
         }
     };
+    // one wait per batch: lgkmcnt(8), the batch before the one just issued
+    // (LDS reads of a wave complete in order); a wait per value would cost
+    // the chain about 0.8 clocks per add
+    constexpr int kWaitPrev = 0xC07F | (8 << 8);
     uint32_t b = 0;
     if (nb > 0) ld(A, 0);
     for (; b + 2 <= nb; b += 2) {
         ld(B, b + 1);
+        __builtin_amdgcn_s_waitcnt(kWaitPrev);
         __builtin_amdgcn_sched_barrier(0);
         add(A);
         ld(A, b + 2 < nb ? b + 2 : b);
+        __builtin_amdgcn_s_waitcnt(kWaitPrev);
         __builtin_amdgcn_sched_barrier(0);
         add(B);
     }
@@ -304,59 +310,6 @@ __device__ __forceinline__ float wave_chain_sum(float* __restrict__ e, uint32_t 
             acc = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(acc), 0x138, 0xf, 0xf, false));
     }
     return runs ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), runs - 1)) : 0.0f;
-}
-
-// Serial f32 dot o += p[i] * v[i] (a rounded product, then a rounded add),
-// i = 0..n-1 in order, both operands 16-byte aligned LDS rows. 16 steps per
-// batch. While the dependent adds of batch b run, each add is paired with
-// one product of batch b + 1 (pinned in that order, so the products fill the
-// add latency instead of preceding it), and the operands of batch b + 2 are
-// already being loaded into the other operand registers.
-__device__ __forceinline__ float chain_dot(const float* __restrict__ p, const float* __restrict__ v, uint32_t n) {
-    const uint32_t nb = n / 16;
-    float o = 0.0f;
-    float4 P0[4], V0[4], P1[4], V1[4];
-    float pa[16], pb[16];
-    auto ld = [&](float4(&pr)[4], float4(&vr)[4], uint32_t b) {
-        b = b < nb ? b : nb - 1;  // past the end: re-read a valid batch (its products are not used)
-#pragma unroll
-        for (int u = 0; u < 4; u++) pr[u] = *(const float4*)(p + 16 * b + 4 * u), vr[u] = *(const float4*)(v + 16 * b + 4 * u);
-    };
-    auto mul = [&](const float4(&pr)[4], const float4(&vr)[4], int k) {
-        const float4 a = pr[k / 4], c = vr[k / 4];
-        return (k & 3) == 0 ? a.x * c.x : (k & 3) == 1 ? a.y * c.y : (k & 3) == 2 ? a.z * c.z : a.w * c.w;
-    };
-    // o += cur[k] for k = 0..15, each followed by nxt[k] = product k of (pr, vr)
-    auto step = [&](const float(&cur)[16], float(&nxt)[16], const float4(&pr)[4], const float4(&vr)[4]) {
-#pragma unroll
-        for (int k = 0; k < 16; k++) {
-            o += cur[k];
-            nxt[k] = mul(pr, vr, k);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-    };
-    uint32_t b = 0;
-    if (nb > 0) {
-        ld(P0, V0, 0);
-#pragma unroll
-        for (int k = 0; k < 16; k++) pa[k] = mul(P0, V0, k);
-        ld(P0, V0, 1);
-        ld(P1, V1, 2);
-        for (; b + 2 <= nb; b += 2) {
-            __builtin_amdgcn_sched_barrier(0);
-            step(pa, pb, P0, V0);  // adds of batch b, products of batch b + 1
-            ld(P0, V0, b + 3);
-            __builtin_amdgcn_sched_barrier(0);
-            step(pb, pa, P1, V1);  // adds of batch b + 1, products of batch b + 2
-            ld(P1, V1, b + 4);
-        }
-        if (b < nb) {
-#pragma unroll
-            for (int k = 0; k < 16; k++) o += pa[k];
-        }
-    }
-    for (uint32_t i = 16 * nb; i < n; i++) o += p[i] * v[i];
-    return o;
 }
 
 // Lane k (0..3) of each quad, to every lane of the quad (DPP quad_perm).
@@ -2030,15 +1983,22 @@ __global__ __launch_bounds__(64) void k_attn_scores(const float* __restrict__ q,
 // the loads of the V slice into registers (they land while the rest runs);
 // all waves run the exp; one lane per head runs the serial softmax sum while
 // waves 8-15 store the V slice transposed ([dim][position]); all waves
-// divide; then one lane per (query head, dim) runs the weighted V sum in
-// position order, reading both operands 4 positions per LDS load. The
-// probabilities are left in `att` (slice 0), as the reference leaves them.
-// LDS: probabilities [G][scs] | V slice [DW][vst], vst = round64(scs) + 4
-// (the 16 rows of a transposed read start 16 bytes apart, on distinct banks).
-static constexpr uint32_t kAttnVRegs = 8;  // V float4 per thread held in registers (1024 positions)
+// divide; all waves form every product p_i * v_i[e] (rounded) into a table
+// with a row per (query head, dim); then one lane per row runs the weighted V
+// sum in position order, a chain of adds whose operands arrive 32 at a time
+// (a chain step that also loaded its two operands and multiplied them would
+// take about twice as long). The probabilities are left in `att` (slice 0),
+// as the reference leaves them.
+// LDS: probabilities [G][scs] | V slice [DW][vst] | products [G * DW][vst],
+// vst = round64(scs) + 4 (the 16 rows of a transposed read start 16 bytes
+// apart, on distinct banks).
+static constexpr uint32_t kAttnVRegs = 8;  // V float4 per thread held in registers
 __host__ __device__ inline size_t attn_split_vst(size_t scs) { return ((scs + 63) & ~(size_t)63) + 4; }
-__host__ __device__ inline size_t attn_split_lds(size_t scs, size_t G, size_t DW) {
-    return (G * scs + DW * attn_split_vst(scs)) * sizeof(float);
+// dims per workgroup: G * DW chain lanes, at most 32
+__host__ __device__ constexpr uint32_t attn_split_dw(size_t G) { return G <= 4 ? 8 : 4; }
+__host__ __device__ inline size_t attn_split_lds(size_t scs, size_t G) {
+    const size_t DW = attn_split_dw(G);
+    return (G * scs + (DW + G * DW) * attn_split_vst(scs)) * sizeof(float);
 }
 __host__ __device__ inline size_t attn_split_ms(size_t seq_len) { return ((seq_len + 63) / 64 + 3) & ~(size_t)3; }
 template <int G, int HS, int DW>
@@ -2145,14 +2105,33 @@ __global__ __launch_bounds__(1024) void k_attn_softmax_v(const float* __restrict
         }
     }
     lds_barrier();  // the `att` stores need not complete first
-    // 5. out[h][d0 + e] = sum_i p_i * v_i[e], lane (j, e), i in order
-    if (tid < G * DW) {
+    // 5. out[h][d0 + e] = sum_i p_i * v_i[e], i in order: the products into
+    // row j * DW + e, +0.0 from count to round32(count) (adding +0.0 leaves
+    // every reachable running sum unchanged: it starts at +0.0 and so is
+    // never -0.0), then the chains
+    constexpr uint32_t NL = G * DW;
+    float* prod = vt + DW * vst;
+    const uint32_t n32 = (count + 31) & ~31u;
+    for (uint32_t r = wave; r < NL; r += T / 64) {
+        const uint32_t j = r / DW, e = r - j * DW;
+        for (uint32_t i = 4 * lane; i < n32; i += 256) {
+            const uint32_t ii = i < count ? i : 0;
+            const float4 p = *(const float4*)(ps + j * scs + ii), v = *(const float4*)(vt + e * vst + ii);
+            float4 y;
+            y.x = i < count ? p.x * v.x : 0.0f;
+            y.y = i + 1 < count ? p.y * v.y : 0.0f;
+            y.z = i + 2 < count ? p.z * v.z : 0.0f;
+            y.w = i + 3 < count ? p.w * v.w : 0.0f;
+            *(float4*)(prod + r * vst + i) = y;
+        }
+    }
+    __syncthreads();
+    if (tid < NL) {
         const uint32_t j = tid / DW, e = tid % DW;
-        out[(size_t)(hk * G + j) * HS + d0 + e] = chain_dot(ps + j * scs, vt + e * vst, count);
+        out[(size_t)(hk * G + j) * HS + d0 + e] = chain_sum(prod + tid * vst, n32);
     }
 }
 
-static constexpr uint32_t kAttnSplitDW = 16;
 static constexpr size_t kAttnSplitLds = 150 * 1024;
 
 bool attention_split_ok(size_t max_count, size_t kv_mul, size_t hs) {
@@ -2160,7 +2139,15 @@ bool attention_split_ok(size_t max_count, size_t kv_mul, size_t hs) {
     if (hs != 32 && hs != 64 && hs != 128) return false;
     const size_t scs = (max_count + 3) & ~(size_t)3;
     // max_count <= 4096: one chunk maximum per lane of a wave in k_attn_softmax_v
-    return max_count >= 1 && max_count <= 64 * 64 && attn_split_lds(scs, kv_mul, kAttnSplitDW) <= kAttnSplitLds;
+    return max_count >= 1 && max_count <= 64 * 64 && attn_split_lds(scs, kv_mul) <= kAttnSplitLds;
+}
+
+// k_attn_softmax_v_rows: scores [G][scs] | V [64][HS]; at most 2048 positions
+bool attention_split_rows_ok(size_t max_count, size_t kv_mul, size_t hs) {
+    if (kv_mul != 1 && kv_mul != 2 && kv_mul != 3 && kv_mul != 4 && kv_mul != 8) return false;
+    if (hs != 32 && hs != 64 && hs != 128) return false;
+    const size_t scs = (max_count + 3) & ~(size_t)3;
+    return max_count >= 1 && max_count <= 2048 && (kv_mul * scs + 64 * hs) * sizeof(float) <= kAttnSplitLds;
 }
 
 // scores [n_heads][round4(seq_len)] | chunk maxima [n_heads][attn_split_ms(seq_len)]
@@ -2181,15 +2168,14 @@ hipError_t launch_attention_split(hipStream_t st, const float* q, const float* k
     const uint32_t ss = (uint32_t)((seq_len + 3) & ~(size_t)3);  // scratch row stride
     const uint32_t ms = (uint32_t)attn_split_ms(seq_len);
     float* mxp = scratch + n_heads * ss;
-    const size_t lds = attn_split_lds(scs, kv_mul, kAttnSplitDW);
-    const dim3 g1((unsigned)n_kv, (unsigned)nchunks), g2((unsigned)(n_kv * (hs / kAttnSplitDW)));
+    const size_t lds = attn_split_lds(scs, kv_mul);
+    const dim3 g1((unsigned)n_kv, (unsigned)nchunks), g2((unsigned)(n_kv * (hs / attn_split_dw(kv_mul))));
 #define KR_SPLIT(G, H)                                                                                              \
     do {                                                                                                            \
         hipLaunchKernelGGL((k_attn_scores<G, H, true>), g1, dim3(64), 0, st, q, k, v, kc, vc, loff, window, pos,    \
                            table, interleaved, (uint32_t)kv_dim, scale, sc, ss, mxp, ms, (uint32_t)(n_heads * hs)); \
-        hipLaunchKernelGGL((k_attn_softmax_v<G, H, kAttnSplitDW>), g2, dim3(1024), lds, st, sc, ss, mxp, ms, vc, loff, \
-                           window,                                                                                  \
-                           (uint32_t)kv_dim, (uint32_t)seq_len, (uint32_t)scs, att, out);                           \
+        hipLaunchKernelGGL((k_attn_softmax_v<G, H, attn_split_dw(G)>), g2, dim3(1024), lds, st, sc, ss, mxp, ms, vc,  \
+                           loff, window, (uint32_t)kv_dim, (uint32_t)seq_len, (uint32_t)scs, att, out);             \
     } while (0)
 #define KR_SPLIT_H(G)              \
     if (hs == 32)                  \
@@ -2802,7 +2788,7 @@ hipError_t launch_attention_split_rows(hipStream_t st, const float* q, float* ou
                                        size_t max_count, size_t n_heads, size_t kv_mul, size_t hs, size_t kv_dim,
                                        size_t seq_len, float scale, float* scratch) {
     if (n_rows == 0) return hipSuccess;
-    if (!attention_split_ok(max_count, kv_mul, hs) || n_heads % kv_mul != 0 || max_count > seq_len)
+    if (!attention_split_rows_ok(max_count, kv_mul, hs) || n_heads % kv_mul != 0 || max_count > seq_len)
         return hipErrorInvalidValue;
     const size_t n_kv = n_heads / kv_mul, nchunks = (max_count + 63) / 64, loff = layer * seq_len * kv_dim;
     const size_t scs = (max_count + 3) & ~(size_t)3;

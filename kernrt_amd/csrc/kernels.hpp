@@ -101,9 +101,12 @@ hipError_t launch_attention_mx(hipStream_t st, const float* q, float* out, float
                                size_t max_count, size_t n_heads, size_t kv_mul, size_t hs, size_t kv_dim,
                                size_t seq_len, float scale, int8_t* qo, float* so, uint16_t* ho, float* scratch);
 // Decode attention of one row in two launches (scores by 64-row chunks with
-// RoPE and the kv_write of k/v folded in, then softmax + V by 16-wide head
-// slices); `scratch` holds attention_split_scratch(n_heads, seq_len) floats.
+// RoPE and the kv_write of k/v folded in, then softmax + V by head slices of
+// 8 dims, 4 with eight query heads per KV head); `scratch` holds
+// attention_split_scratch(n_heads, seq_len) floats.
 bool attention_split_ok(size_t max_count, size_t kv_mul, size_t hs);
+// launch_attention_split_rows's geometry check (k_attn_softmax_v_rows).
+bool attention_split_rows_ok(size_t max_count, size_t kv_mul, size_t hs);
 size_t attention_split_scratch(size_t n_heads, size_t seq_len);
 hipError_t launch_attention_split(hipStream_t st, const float* q, const float* k, const float* v, float* out,
                                   float* att, float* kc, float* vc, size_t layer, const DevWindow* window,

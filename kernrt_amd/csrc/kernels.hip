@@ -2099,12 +2099,9 @@ __global__ __launch_bounds__(1024) void k_attn_softmax_v(const float* __restrict
 #pragma unroll
         for (int j = 0; j < G; j++) pv[j] = div_rn(ps[j * scs + i], sj[j]);
 #pragma unroll
-        for (int j = 0; j < G; j++) {
-            ps[j * scs + i] = pv[j];
-            if (sidx == 0) att[(size_t)(hk * G + j) * seq_len + i] = pv[j];
-        }
+        for (int j = 0; j < G; j++) ps[j * scs + i] = pv[j];
     }
-    lds_barrier();  // the `att` stores need not complete first
+    lds_barrier();
     // 5. out[h][d0 + e] = sum_i p_i * v_i[e], i in order: the products into
     // row j * DW + e, +0.0 from count to round32(count) (adding +0.0 leaves
     // every reachable running sum unchanged: it starts at +0.0 and so is
@@ -2129,6 +2126,13 @@ __global__ __launch_bounds__(1024) void k_attn_softmax_v(const float* __restrict
     if (tid < NL) {
         const uint32_t j = tid / DW, e = tid % DW;
         out[(size_t)(hk * G + j) * HS + d0 + e] = chain_sum(prod + tid * vst, n32);
+    } else if (sidx == 0 && tid >= 64) {
+        // the probabilities to `att` while the chains run (global stores
+        // issued earlier would hold up every later wait on the memory counter)
+        for (uint32_t t = tid - 64; t < G * count; t += T - 64) {
+            const uint32_t j = t / count, i = t - j * count;
+            att[(size_t)(hk * G + j) * seq_len + i] = ps[j * scs + i];
+        }
     }
 }
 

@@ -214,13 +214,15 @@ def test_greedy_decode_matches_the_oracle(use_graph):
 
 @pytest.mark.parametrize("n_heads,n_kv,hs,ctx", [(2, 1, 64, 1100), (8, 8, 32, 300), (8, 2, 128, 300),
                                                  (8, 1, 64, 200), (16, 4, 64, 150), (15, 5, 64, 1000),
-                                                 (6, 2, 32, 1020)])
+                                                 (6, 2, 32, 1020), (6, 2, 64, 1500), (2, 2, 64, 2100)])
 def test_split_decode_attention_windows(n_heads, n_kv, hs, ctx):
     # The fused decode step's two-launch attention (k_attn_scores +
-    # k_attn_softmax_v) for head groups 2, 1, 4, 8, 4, 3 and 3 and head sizes
-    # 32-128, after a long prefill; the first case's window (1101+ positions)
-    # runs past the 1024 positions whose V the softmax launch keeps in
-    # registers, the last ends at 1023 of them.
+    # k_attn_softmax_v) for head groups 2, 1, 4, 8, 4, 3, 3, 3 and 1 and head
+    # sizes 32-128, after a long prefill. The softmax launch takes 8-dim
+    # slices where its product table fits in LDS and 4-dim slices otherwise
+    # (eight heads per KV head, and the 1500-position window at three); the
+    # last window (2101+ positions at 8-dim slices) runs past the 2048
+    # positions whose V the launch keeps in registers.
     c = O.Config(dim=n_heads * hs, hidden_dim=128, n_layers=1, n_heads=n_heads, n_kv_heads=n_kv, vocab_size=64,
                  seq_len=ctx + 4, rms_eps=1e-5, rope_theta=10_000.0, rope_interleaved=False, head_dim=hs)
     ow = gaussian_weights(c, "q8_0", seed=ctx + hs)

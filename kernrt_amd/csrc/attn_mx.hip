@@ -247,7 +247,7 @@ __global__ __launch_bounds__(256) void k_attn_softmax_att(float* __restrict__ at
 }
 
 template <int G, int HS>
-__global__ __launch_bounds__(256) void k_attn_mx_v(float* __restrict__ att, float* __restrict__ out,
+__global__ __launch_bounds__(256, 3) void k_attn_mx_v(float* __restrict__ att, float* __restrict__ out,
                                                    const float* __restrict__ vc, size_t loff,
                                                    const DevWindow* __restrict__ windows, uint32_t n_rows,
                                                    uint32_t n_heads, uint32_t kv_mul, uint32_t kv_dim,
@@ -329,11 +329,16 @@ __global__ __launch_bounds__(256) void k_attn_mx_v(float* __restrict__ att, floa
         // the next step's instruction is issued before this step's adds, its
         // operands read two steps ahead, so neither waits on the other
         float pa[16], va[16];
+        // operands a quarter at a time, each issued a quarter ahead of its use
 #pragma unroll
-        for (uint32_t k = 0; k < 16; k++) pa[k] = pb[2 * k * PST], va[k] = vb[2 * k * VST];
+        for (uint32_t k = 0; k < 8; k++) pa[k] = pb[2 * k * PST], va[k] = vb[2 * k * VST];
         mx_v32f d = __builtin_amdgcn_mfma_f32_32x32x1f32(pa[0], va[0], mx_v32f{}, 0, 0, 0);
 #pragma unroll
         for (uint32_t k = 0; k < 16; k++) {
+            if (k % 4 == 0 && k + 8 < 16) {
+#pragma unroll
+                for (uint32_t q = k + 8; q < k + 12; q++) pa[q] = pb[2 * q * PST], va[q] = vb[2 * q * VST];
+            }
             mx_v32f dn;
             if (k + 1 < 16) dn = __builtin_amdgcn_mfma_f32_32x32x1f32(pa[k + 1], va[k + 1], mx_v32f{}, 0, 0, 0);
 #pragma unroll

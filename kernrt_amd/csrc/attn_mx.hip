@@ -192,8 +192,10 @@ __global__ __launch_bounds__(256) void k_attn_softmax_att(float* __restrict__ at
                                                           const DevWindow* __restrict__ windows, uint32_t n_rows,
                                                           uint32_t n_heads, uint32_t seq_len,
                                                           const float* __restrict__ pmax, float* __restrict__ psum) {
-    constexpr uint32_t C = 64, TS = C + 1, PW = 16;  // chunk positions, tile row stride, pairs per wave
-    __shared__ float s_e[64 * TS];
+    // chunk positions, tile row stride (16-byte rows, each 16 bytes further
+    // along the banks than the one above), pairs per wave
+    constexpr uint32_t C = 64, TS = C + 4, PW = 16;
+    __shared__ __align__(16) float s_e[64 * TS];
     __shared__ uint64_t etab[32];
     __shared__ uint32_t s_n[64];
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -236,10 +238,16 @@ __global__ __launch_bounds__(256) void k_attn_softmax_att(float* __restrict__ at
         }
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's tile stores have landed
         __builtin_amdgcn_wave_barrier();
-        if (lane < PW) {
-            const float* r = tw + lane * TS;
-#pragma unroll 16
-            for (uint32_t k = 0; k < C; k++) sum += r[k];  // past a window's end: +0.0, which leaves the sum unchanged
+        if (lane < PW) {  // past a window's end: +0.0, which leaves the sum unchanged
+            const float4* r = (const float4*)(tw + lane * TS);
+#pragma unroll
+            for (uint32_t k = 0; k < C / 4; k++) {
+                const float4 f = r[k];
+                sum += f.x;
+                sum += f.y;
+                sum += f.z;
+                sum += f.w;
+            }
         }
         __builtin_amdgcn_wave_barrier();  // the chains have read the tile before it is rewritten
     }

@@ -1977,7 +1977,7 @@ __global__ __launch_bounds__(64) void k_attn_scores(const float* __restrict__ q,
     }
 }
 
-// k_attn_softmax_v, workgroup = (KV head, DW = 8 or 4 of its HS output dims), 16
+// k_attn_softmax_v, workgroup = (KV head, DW of its HS output dims), 16
 // waves. Every wave reduces the per-chunk maxima of the G heads (written by
 // k_attn_scores) while the scores arrive by LDS DMA; then waves 8-15 issue
 // the loads of the V slice into registers (they land while the rest runs);
@@ -2134,19 +2134,16 @@ __global__ __launch_bounds__(1024) void k_attn_softmax_v(const float* __restrict
 }
 
 static constexpr size_t kAttnSplitLds = 150 * 1024;
+// dims per k_attn_softmax_v workgroup: 4 (twice the workgroups of 8, each
+// with half the products to form; measured faster)
+static constexpr size_t kAttnSplitDW = 4;
 
 bool attention_split_ok(size_t max_count, size_t kv_mul, size_t hs) {
     if (kv_mul != 1 && kv_mul != 2 && kv_mul != 3 && kv_mul != 4 && kv_mul != 8) return false;
     if (hs != 32 && hs != 64 && hs != 128) return false;
     const size_t scs = (max_count + 3) & ~(size_t)3;
     // max_count <= 4096: one chunk maximum per lane of a wave in k_attn_softmax_v
-    return max_count >= 1 && max_count <= 64 * 64 && attn_split_lds(scs, kv_mul, 4) <= kAttnSplitLds;
-}
-
-// dims per k_attn_softmax_v workgroup: 8 (G * 8 chain lanes, fewer
-// workgroups) where the product table fits, else 4
-static size_t attn_split_dw(size_t scs, size_t G) {
-    return G <= 4 && attn_split_lds(scs, G, 8) <= kAttnSplitLds ? 8 : 4;
+    return max_count >= 1 && max_count <= 64 * 64 && attn_split_lds(scs, kv_mul, kAttnSplitDW) <= kAttnSplitLds;
 }
 
 // k_attn_softmax_v_rows: scores [G][scs] | V [64][HS]; at most 2048 positions
@@ -2175,18 +2172,14 @@ hipError_t launch_attention_split(hipStream_t st, const float* q, const float* k
     const uint32_t ss = (uint32_t)((seq_len + 3) & ~(size_t)3);  // scratch row stride
     const uint32_t ms = (uint32_t)attn_split_ms(seq_len);
     float* mxp = scratch + n_heads * ss;
-    const size_t dw = attn_split_dw(scs, kv_mul), lds = attn_split_lds(scs, kv_mul, dw);
-    const dim3 g1((unsigned)n_kv, (unsigned)nchunks), g2((unsigned)(n_kv * (hs / dw)));
+    const size_t lds = attn_split_lds(scs, kv_mul, kAttnSplitDW);
+    const dim3 g1((unsigned)n_kv, (unsigned)nchunks), g2((unsigned)(n_kv * (hs / kAttnSplitDW)));
 #define KR_SPLIT(G, H)                                                                                              \
     do {                                                                                                            \
         hipLaunchKernelGGL((k_attn_scores<G, H, true>), g1, dim3(64), 0, st, q, k, v, kc, vc, loff, window, pos,    \
                            table, interleaved, (uint32_t)kv_dim, scale, sc, ss, mxp, ms, (uint32_t)(n_heads * hs)); \
-        if (G <= 4 && dw == 8)                                                                                      \
-            hipLaunchKernelGGL((k_attn_softmax_v<G, H, 8>), g2, dim3(1024), lds, st, sc, ss, mxp, ms, vc, loff,      \
-                               window, (uint32_t)kv_dim, (uint32_t)seq_len, (uint32_t)scs, att, out);               \
-        else                                                                                                        \
-            hipLaunchKernelGGL((k_attn_softmax_v<G, H, 4>), g2, dim3(1024), lds, st, sc, ss, mxp, ms, vc, loff,      \
-                               window, (uint32_t)kv_dim, (uint32_t)seq_len, (uint32_t)scs, att, out);               \
+        hipLaunchKernelGGL((k_attn_softmax_v<G, H, kAttnSplitDW>), g2, dim3(1024), lds, st, sc, ss, mxp, ms, vc,   \
+                           loff, window, (uint32_t)kv_dim, (uint32_t)seq_len, (uint32_t)scs, att, out);             \
     } while (0)
 #define KR_SPLIT_H(G)              \
     if (hs == 32)                  \

@@ -102,8 +102,7 @@ hipError_t launch_attention_mx(hipStream_t st, const float* q, float* out, float
                                size_t seq_len, float scale, int8_t* qo, float* so, uint16_t* ho, float* scratch);
 // Decode attention of one row in two launches (scores by 64-row chunks with
 // RoPE and the kv_write of k/v folded in, then softmax + V by head slices of
-// 8 dims, 4 with eight query heads per KV head or a window too long for the
-// 8-dim product table); `scratch` holds
+// 4 dims); `scratch` holds
 // attention_split_scratch(n_heads, seq_len) floats.
 bool attention_split_ok(size_t max_count, size_t kv_mul, size_t hs);
 // launch_attention_split_rows's geometry check (k_attn_softmax_v_rows).

@@ -218,11 +218,9 @@ def test_greedy_decode_matches_the_oracle(use_graph):
 def test_split_decode_attention_windows(n_heads, n_kv, hs, ctx):
     # The fused decode step's two-launch attention (k_attn_scores +
     # k_attn_softmax_v) for head groups 2, 1, 4, 8, 4, 3, 3, 3 and 1 and head
-    # sizes 32-128, after a long prefill. The softmax launch takes 8-dim
-    # slices where its product table fits in LDS and 4-dim slices otherwise
-    # (eight heads per KV head, and the 1500-position window at three); the
-    # last window (2101+ positions at 8-dim slices) runs past the 2048
-    # positions whose V the launch keeps in registers.
+    # sizes 32-128, after a long prefill, up to windows of 2100+ positions
+    # (the softmax launch's LDS holds its scores, V slice and product table
+    # up to about 2000 positions at three query heads per KV head).
     c = O.Config(dim=n_heads * hs, hidden_dim=128, n_layers=1, n_heads=n_heads, n_kv_heads=n_kv, vocab_size=64,
                  seq_len=ctx + 4, rms_eps=1e-5, rope_theta=10_000.0, rope_interleaved=False, head_dim=hs)
     ow = gaussian_weights(c, "q8_0", seed=ctx + hs)

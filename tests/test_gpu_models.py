@@ -142,6 +142,31 @@ def test_decode_batch_split_attention(n_seq):
                 cpus[i].forward(seqs[i][t], t)
 
 
+def test_decode_batch_split_attention_long_windows():
+    # the batched two-launch attention (k_attn_softmax_v_rows) with eight
+    # query heads per KV head over windows of 1500-1800 positions, two
+    # sequences in one cache; compared with per-sequence forward() at the
+    # end and every 300 steps
+    c = O.Config(dim=256, hidden_dim=128, n_layers=1, n_heads=8, n_kv_heads=1, vocab_size=64, seq_len=3800,
+                 rms_eps=1e-5, rope_theta=10_000.0, rope_interleaved=False, head_dim=32)
+    ow = gaussian_weights(c, "q8_0", seed=1800)
+    rng = np.random.default_rng(18)
+    room = c.seq_len // 2
+    seqs = [[int(t) for t in rng.integers(0, c.vocab_size, size=n)] for n in (1500, 1800)]
+    g = gpu_model(c, ow)
+    cpus = [O.Model(c, ow, "cpu") for _ in seqs]
+    n_max = max(len(x) for x in seqs)
+    for t in range(n_max):
+        live = [i for i, x in enumerate(seqs) if t < len(x)]
+        got = g.decode_batch([seqs[i][t] for i in live], [t] * len(live), [i * room + t for i in live],
+                             [i * room for i in live])
+        check = t % 300 == 299 or any(t + 1 == len(seqs[i]) for i in live)
+        for r, i in enumerate(live):
+            want = cpus[i].forward(seqs[i][t], t)
+            if check:
+                assert_bits_equal(got[r], want, f"decode_batch step {t} sequence {i}")
+
+
 @pytest.mark.parametrize("storage", ["q8_0", "q8_0x4"])
 @pytest.mark.parametrize("dim,hidden", [(128, 256), (1024, 2048)])
 def test_decode_at_fused_swiglu_widths(storage, dim, hidden):

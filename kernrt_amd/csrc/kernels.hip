@@ -2087,38 +2087,33 @@ __global__ __launch_bounds__(1024) void k_attn_softmax_v(const float* __restrict
         }
     }
     __syncthreads();
-    // 4. probabilities, the G heads of a position together
-    float sj[G];
-#pragma unroll
-    for (int j = 0; j < G; j++) sj[j] = s_sum[j];
-    for (uint32_t i = tid; i < count; i += T) {
-        float pv[G];
-#pragma unroll
-        for (int j = 0; j < G; j++) pv[j] = div_rn(ps[j * scs + i], sj[j]);
-#pragma unroll
-        for (int j = 0; j < G; j++) ps[j * scs + i] = pv[j];
-    }
-    lds_barrier();
-    // 5. out[h][d0 + e] = sum_i p_i * v_i[e], i in order: the products into
-    // row j * DW + e, +0.0 from count to round32(count) (adding +0.0 leaves
-    // every reachable running sum unchanged: it starts at +0.0 and so is
-    // never -0.0), then the chains
+    // 4. probabilities, the G heads of a position together (elementwise.rs:88-91),
+    // and at once the products p_i * v_i[e] of out[h][d0 + e] = sum_i p_i *
+    // v_i[e] into row j * DW + e; +0.0 from count to round32(count) (adding
+    // +0.0 leaves every reachable running sum unchanged: it starts at +0.0
+    // and so is never -0.0)
     constexpr uint32_t NL = G * DW;
     float* prod = vt + DW * vst;
     const uint32_t n32 = (count + 31) & ~31u;
-    for (uint32_t r = wave; r < NL; r += T / 64) {
-        const uint32_t j = r / DW, e = r - j * DW;
-        for (uint32_t i = 4 * lane; i < n32; i += 256) {
-            const uint32_t ii = i < count ? i : 0;
-            const float4 p = *(const float4*)(ps + j * scs + ii), v = *(const float4*)(vt + e * vst + ii);
-            float4 y;
-            y.x = i < count ? p.x * v.x : 0.0f;
-            y.y = i + 1 < count ? p.y * v.y : 0.0f;
-            y.z = i + 2 < count ? p.z * v.z : 0.0f;
-            y.w = i + 3 < count ? p.w * v.w : 0.0f;
-            *(float4*)(prod + r * vst + i) = y;
+    float sj[G];
+#pragma unroll
+    for (int j = 0; j < G; j++) sj[j] = s_sum[j];
+    for (uint32_t i = tid; i < n32; i += T) {
+        const bool live = i < count;
+        const uint32_t ii = live ? i : 0;
+        float pv[G], vv[DW];
+#pragma unroll
+        for (int e = 0; e < (int)DW; e++) vv[e] = vt[e * vst + ii];
+#pragma unroll
+        for (int j = 0; j < G; j++) pv[j] = div_rn(ps[j * scs + ii], sj[j]);
+#pragma unroll
+        for (int j = 0; j < G; j++) {
+            if (live) ps[j * scs + i] = pv[j];
+#pragma unroll
+            for (int e = 0; e < (int)DW; e++) prod[(j * DW + e) * vst + i] = live ? pv[j] * vv[e] : 0.0f;
         }
     }
+    // 5. the chains, i in order
     __syncthreads();
     if (tid < NL) {
         const uint32_t j = tid / DW, e = tid % DW;

@@ -1979,9 +1979,9 @@ __global__ __launch_bounds__(64) void k_attn_scores(const float* __restrict__ q,
 
 // k_attn_softmax_v, workgroup = (KV head, DW of its HS output dims), 16
 // waves. Every wave reduces the per-chunk maxima of the G heads (written by
-// k_attn_scores) while the scores arrive by LDS DMA; then waves 8-15 issue
-// the loads of the V slice into registers (they land while the rest runs);
-// all waves run the exp; wave j runs head j's serial softmax sum while
+// k_attn_scores) while the scores arrive by LDS DMA; all waves run the exp;
+// then waves 8-15 issue the loads of the V slice into registers (they land
+// while the sum runs); wave j runs head j's serial softmax sum while
 // waves 8-15 store the V slice transposed ([dim][position]); all waves
 // divide; all waves form every product p_i * v_i[e] (rounded) into a table
 // with a row per (query head, dim); then one lane per row runs the weighted V
@@ -2042,8 +2042,19 @@ __global__ __launch_bounds__(1024) void k_attn_softmax_v(const float* __restrict
 #pragma unroll
     for (int j = 0; j < G; j++) mx[j] = wave_max(pm[j]);
     lds_barrier();  // the scores and the exp table are in LDS
+    // 2. exp with the head's max; the G heads of a position together, so a
+    // thread's exps are independent chains that overlap
+    for (uint32_t i = tid; i < count; i += T) {
+        float e[G];
+#pragma unroll
+        for (int j = 0; j < G; j++) e[j] = ps[j * scs + i];
+#pragma unroll
+        for (int j = 0; j < G; j++) ps[j * scs + i] = glibc_expf(e[j] - mx[j], etab);
+    }
+    lds_barrier();
     // waves 8-15: the V slice into registers (unit f = position f / FV,
-    // float4 f % FV); it lands while the exp and the softmax sum run
+    // float4 f % FV); it lands while the softmax sum runs (issued before the
+    // exp, it held up the exp phase's barrier)
     const float* vbase = vc + loff + (size_t)hk * HS + d0;
     const uint32_t units = count * FV, tv = tid - TV;
     float4 vr[kAttnVRegs];
@@ -2057,16 +2068,6 @@ __global__ __launch_bounds__(1024) void k_attn_softmax_v(const float* __restrict
             }
         }
     }
-    // 2. exp with the head's max; the G heads of a position together, so a
-    // thread's exps are independent chains that overlap
-    for (uint32_t i = tid; i < count; i += T) {
-        float e[G];
-#pragma unroll
-        for (int j = 0; j < G; j++) e[j] = ps[j * scs + i];
-#pragma unroll
-        for (int j = 0; j < G; j++) ps[j * scs + i] = glibc_expf(e[j] - mx[j], etab);
-    }
-    lds_barrier();
     // 3. softmax sum, left to right (elementwise.rs:81-91), one wave per head,
     // while waves 8-15 store the V slice transposed
     if (wave < G) {

@@ -1380,11 +1380,11 @@ __global__ __launch_bounds__(256) void k_rms_norm(float* __restrict__ out, const
         sq[i] = v * v;
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        float ss = chain_sum(sq, dim);
+    if (threadIdx.x < 64) {  // the register chain across wave 0 where dim allows
+        float ss = dim <= 64 * 64 ? wave_chain_sum(sq, dim) : chain_sum(sq, dim);
         ss = div_rn(ss, (float)dim);
         ss += eps;
-        s_scale = div_rn(1.0f, sqrt_rn(ss));
+        if (threadIdx.x == 0) s_scale = div_rn(1.0f, sqrt_rn(ss));
     }
     __syncthreads();
     float scale = s_scale;
@@ -3026,13 +3026,14 @@ __global__ __launch_bounds__(256) void k_add_rms_quant(float* __restrict__ x, co
         }
     }
     __syncthreads();
-    if (tid == 0) {
+    if (tid < 64) {
         // rms_norm_row (cpu.rs:635-641): ss = sum of squares left to right,
-        // ss /= dim, ss += eps, scale = 1 / sqrt(ss)
-        float ss = chain_sum(sq, dim);
+        // ss /= dim, ss += eps, scale = 1 / sqrt(ss); the sum as the
+        // register chain across wave 0 where dim allows
+        float ss = dim <= 64 * 64 ? wave_chain_sum(sq, dim) : chain_sum(sq, dim);
         ss = div_rn(ss, (float)dim);
         ss += eps;
-        s_scale = div_rn(1.0f, sqrt_rn(ss));
+        if (tid == 0) s_scale = div_rn(1.0f, sqrt_rn(ss));
     }
     __syncthreads();
     const float scale = s_scale;

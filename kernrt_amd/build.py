@@ -19,10 +19,11 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libkernrt_hip.so")
 
-SOURCES = ["kernels.hip", "attn_mx.hip", "backend.hip", "llm.cpp"]
-# per-source extra flags: the matrix-core attention keeps f32 MFMA results in
-# ordinary vector registers (its vector adds read them directly)
-EXTRA = {"attn_mx.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+SOURCES = ["kernels.hip", "gemm.hip", "attn_mx.hip", "backend.hip", "llm.cpp"]
+# per-source extra flags: the matrix-core attention and the Q8_0 GEMM keep
+# MFMA results in ordinary vector registers (their vector epilogues read them
+# directly)
+EXTRA = {"attn_mx.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"], "gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
 
 FLAGS = [
     "-O3", "-std=c++17", "--offload-arch=gfx950", "-fPIC", "-shared",

@@ -79,6 +79,31 @@ __device__ __forceinline__ uint32_t win_slot(const DevWindow& w, uint32_t n_shar
     return i < n_shared ? w.shared_start + i : w.att_start + (i - n_shared);
 }
 
+// Up to three matrices with the same K projected in one launch (q/k/v, or
+// gate/up): the grid is the concatenation of their column-tile ranges.
+struct MatSet {
+    const int8_t* q[3];
+    const void* s[3];
+    float* y[3];
+    uint32_t n[3];
+    uint32_t ld[3];
+    uint32_t tile_end[3];  // cumulative tile counts
+    int count;
+};
+
+// A scale as loaded: f32 bits, or f16 bits that are widened only where the
+// value is used (widening right after the load would make its wait immediate).
+__device__ __forceinline__ uint32_t scale_bits(bool f16, const void* p, size_t i) {
+    return f16 ? (uint32_t)((const uint16_t*)p)[i] : f2u(((const float*)p)[i]);
+}
+__device__ __forceinline__ float scale_value(bool f16, uint32_t bits) {
+    return f16 ? f16w((uint16_t)bits) : u2f(bits);
+}
+
+// The four-partial Q8_0 GEMM (gemm.hip) over a matrix set, rows >= 8.
+hipError_t launch_gemm_q8(hipStream_t st, int sem, const MatSet& ms, size_t k, QuantAct x, size_t rows,
+                          int32_t* dbg);
+
 // The chunk pipeline shared by both GEMM kernels. At chunk c, the register
 // stage (c + 1) % NS holds chunk c + 1 and LDS buffer c & 1 holds chunk c.
 // The chunk count is padded to a multiple of NS and every load and store is

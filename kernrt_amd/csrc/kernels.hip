@@ -171,25 +171,6 @@ hipError_t launch_quantize(hipStream_t st, const float* x, size_t rows, size_t k
 //
 // One launch may cover up to three matrices with the same K (q/k/v, or
 // gate/up): the grid is the concatenation of their tile ranges.
-struct MatSet {
-    const int8_t* q[3];
-    const void* s[3];
-    float* y[3];
-    uint32_t n[3];
-    uint32_t ld[3];
-    uint32_t tile_end[3];  // cumulative tile counts
-    int count;
-};
-
-// A scale as loaded: f32 bits, or f16 bits that are widened only where the
-// value is used (widening right after the load would make its wait immediate).
-__device__ __forceinline__ uint32_t scale_bits(bool f16, const void* p, size_t i) {
-    return f16 ? (uint32_t)((const uint16_t*)p)[i] : f2u(((const float*)p)[i]);
-}
-__device__ __forceinline__ float scale_value(bool f16, uint32_t bits) {
-    return f16 ? f16w((uint16_t)bits) : u2f(bits);
-}
-
 // LDS layout of the epilogue operands of one output (one weight row for one
 // activation row). Four partial sums: residue j of the blocks at
 // [j*q4p, j*q4p + count_j), q4p = ceil(nb/4) + 1 (odd, so the four lanes
@@ -883,44 +864,32 @@ bool swiglu_fusable(const DevMatrix& gate, const DevMatrix& up) {
 
 // ---------------------------------------------------------------------------
 // Quantized GEMM on int8 MFMA (prefill and batched rows, M >= kGemmMinRows).
+// The four-partial Q8_0 GEMM (dot.rs:35-44) is k_gemm_q8 in gemm.hip; this
+// file holds the Q8_0x4 FMA chain (quant.rs:276-288, k_gemm_chain).
 //
 // v_mfma_i32_32x32x32_i8 multiplies a 32x32 int8 tile of activations by a
 // 32x32 int8 tile of weights over K = 32, exactly one Q8 block, so each
 // instruction yields the exact i32 block dots of a 32x32 output tile. Every
 // block's dots go straight into the reference's f32 epilogue, so each output
-// keeps the per-row path's rounding sequence (quant.rs:276-288 for Q8_0x4,
-// dot.rs:35-44 for Q8_0).
+// keeps the per-row path's rounding sequence.
 //
 // Operand layout: lane l feeds row l % 32 of the activation tile and column
 // l % 32 of the weight tile with bytes 16*(l/32) .. +16 of the block; both
 // operands use the same byte map, so the integer sum covers the block once.
 // Accumulator v of lane l is output (row 8*(v/4) + 4*(l/32) + v%4, col l%32).
 //
-// Operands are staged through LDS in chunks of KC blocks: every row's KC*32
-// bytes are read with coalesced 16-byte loads (whole cache lines), several
-// chunks ahead in registers, and written to a double-buffered LDS tile whose
-// rows are padded by 16 bytes so that the fragment reads of 32 consecutive
-// rows spread over all banks. One barrier per chunk.
-//
-// Two kernels:
-//  * four partial sums (Q8_0, dot.rs:35-44, k_gemm_q8): t[b & 3] are
-//    independent chains, so they run on different waves, each over a
-//    sub-tile of the workgroup's tile; the chains meet in LDS and are summed
-//    in the reference order ((t0 + t1) + t2) + t3. This is a 4-way split of
-//    K that changes no rounding. Tiles 64x128, 64x64 or 32x32 by grid size.
-//  * one FMA chain (Q8_0x4, quant.rs:276-288, k_gemm_chain, 4 waves): the
-//    chain is serial, so each wave owns its own 32x32 tile over all of K; the
-//    workgroup tile is 32x128 and the 4 waves share the activation chunk.
-//    KC = 4.
+// The chain is serial, so each wave owns its own 32x32 tile over all of K;
+// the workgroup tile is 32x128 and the 4 waves share the activation chunk.
+// Operands are staged through LDS in chunks of KC = 4 blocks: every row's
+// KC*32 bytes are read with coalesced 16-byte loads (whole cache lines),
+// several chunks ahead in registers, and written to a double-buffered LDS
+// tile whose rows are padded by 16 bytes so that the fragment reads of 32
+// consecutive rows spread over all banks. One barrier per chunk.
 //
 // Workgroups are numbered XCD-aware: the row tiles that share a column tile
 // of weights run on one XCD and share its L2.
 typedef int v16i __attribute__((ext_vector_type(16)));
 static constexpr size_t kGemmMinRows = 8;
-// workgroups a 64 x 128 (64 x 64) tiling must give before the four-partial
-// GEMM uses it rather than a narrower one (256 CUs)
-static constexpr uint32_t kGemmWideTiles = 200;
-static constexpr uint32_t kGemmMidTiles = 160;
 // chunks each thread keeps in flight in registers (even: LDS buffer parity)
 static constexpr int kGemmStages = 4;
 
@@ -945,11 +914,6 @@ __device__ __forceinline__ GemmPos gemm_pos(const MatSet& ms, uint32_t mtiles, u
     return GemmPos{mi, mt * 32, tile * cols};
 }
 
-__device__ __forceinline__ float gemm_wscale(int sem, const void* ws, size_t i) {
-    return sem == SEM_FOUR_PARTIALS_F32 ? ((const float*)ws)[i] : f16w(((const uint16_t*)ws)[i]);
-}
-
-
 // The 16 activation scales of accumulator rows 8g + 4*half + (0..3).
 __device__ __forceinline__ void gemm_row_scales(float (&xs)[16], const float* col) {
     const float4* q = (const float4*)col;
@@ -957,207 +921,6 @@ __device__ __forceinline__ void gemm_row_scales(float (&xs)[16], const float* co
     for (int g = 0; g < 4; g++) {
         const float4 f = q[2 * g];
         xs[4 * g] = f.x, xs[4 * g + 1] = f.y, xs[4 * g + 2] = f.z, xs[4 * g + 3] = f.w;
-    }
-}
-
-
-// Q8_0 GEMM, four partial sums (dot.rs:34-45), on 16x16x32 int8 MFMA. The
-// reference's four partial sums t[j] (blocks b with b % 4 == j, in order) are
-// independent chains, so they are the unit of work: a workgroup owns a TM x TN
-// output tile, and each of its waves runs CPW of the four chains over a
-// WM x WN sub-tile. Per block a wave reads one A fragment and four activation
-// scales per 16-row slice and one B fragment and one weight scale per
-// 16-column slice from LDS and reuses them across the other dimension, so the
-// LDS read traffic per output falls with the sub-tile size and the per-block
-// f32 epilogue (cvt, two multiplies, add: 4 VALU operations per output)
-// dominates the instruction stream. Chunks of KC blocks of the A and B rows
-// and their scales are staged through a double-buffered, padded LDS tile, NS
-// chunks ahead in registers. At the end the chains of every output meet --
-// in registers when one wave holds all four, else in LDS -- and are summed as
-// ((t0 + t1) + t2) + t3.
-template <int SEM, int TM, int TN, int WM, int WN, int CPW, int KC, int NS, int WPE, bool DBG>
-__global__ __launch_bounds__(64 * (TM / WM) * (TN / WN) * (4 / CPW), WPE) void k_gemm_q8(MatSet ms, QuantAct x,
-                                                                                 uint32_t M, uint32_t K,
-                                                                                 uint32_t mtiles,
-                                                                                 int32_t* __restrict__ dbg) {
-    constexpr int ROW = KC * 32 + 16, PPR = KC * 2, MI = WM / 16, NI = WN / 16, CG = 4 / CPW;
-    constexpr int SM = TM / WM, NSUB = SM * (TN / WN), NT = 64 * NSUB * CG;
-    constexpr int A_BYTES = TM * ROW, B_BYTES = TN * ROW;
-    constexpr int BUF_BYTES = A_BYTES + B_BYTES + KC * (TM + TN) * 4;
-    constexpr int PART_BYTES = CPW == 4 ? 0 : 4 * TM * TN * 4;
-    constexpr int LDS_BYTES = 2 * BUF_BYTES > PART_BYTES ? 2 * BUF_BYTES : PART_BYTES;
-    constexpr int NQ = (TM + TN) * PPR, NP = (NQ + NT - 1) / NT;  // 16-byte pieces per chunk, per thread
-    constexpr int NSC = ((TM + TN) * KC + NT - 1) / NT;  // scales per thread per chunk
-    static_assert(WM % 16 == 0 && WN % 16 == 0 && TM % WM == 0 && TN % WN == 0 && KC % 4 == 0, "tile shape");
-    static_assert(CPW == 1 || CPW == 2 || CPW == 4, "chains per wave");
-    static_assert(NT % PPR == 0, "a thread's pieces share their column");
-    __shared__ __align__(16) int8_t lds[LDS_BYTES];
-    auto sA = [&](int buf) { return lds + buf * BUF_BYTES; };
-    auto sB = [&](int buf) { return lds + buf * BUF_BYTES + A_BYTES; };
-    auto sX = [&](int buf) { return (float*)(lds + buf * BUF_BYTES + A_BYTES + B_BYTES); };  // [block][row]
-    auto sW = [&](int buf) { return sX(buf) + KC * TM; };                                     // [block][col]
-
-    const uint32_t nb = K >> 5, nchunks = (nb + KC - 1) / KC;
-    const uint32_t L = xcd_tile(blockIdx.x, gridDim.x);
-    const uint32_t mt = L % mtiles, nt = L / mtiles;
-    const int mi_ = nt < ms.tile_end[0] ? 0 : (nt < ms.tile_end[1] ? 1 : 2);
-    const uint32_t m0 = mt * TM, n0 = (nt - (mi_ == 0 ? 0 : ms.tile_end[mi_ - 1])) * TN;
-    const int8_t* __restrict__ W = ms.q[mi_];
-    const void* __restrict__ WS = ms.s[mi_];
-    const uint32_t N = ms.n[mi_];
-    const uint32_t tid = threadIdx.x, lane = tid & 63;
-    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t cg = wave % CG, sub = wave / CG;                // chains cg*CPW .. +CPW-1
-    const uint32_t wm0 = (sub % SM) * WM, wn0 = (sub / SM) * WN;  // the wave's sub-tile
-    const uint32_t r = lane & 15, quad = lane >> 4;
-    constexpr bool WF16 = SEM == SEM_FOUR_PARTIALS_F16;
-
-    // loader map: piece q = tid + NT i is the 16-byte piece (row q / PPR,
-    // column 16 (q % PPR)) of the A chunk for q < PPR TM, else of the B
-    // chunk; scale s = tid + NT i is an activation scale (row s / KC, block
-    // s % KC) for s < KC TM, else a weight scale. Rows past M or N read the
-    // last row, blocks past the row end its last block.
-    const int8_t* gp[NP];
-    uint32_t lp[NP];
-#pragma unroll
-    for (int i = 0; i < NP; i++) {
-        const uint32_t q = min(tid + NT * i, (uint32_t)NQ - 1), isb = q >= PPR * TM;
-        const uint32_t row = (isb ? q - PPR * TM : q) / PPR;
-        gp[i] = isb ? W + (size_t)min(n0 + row, N - 1) * K : x.q + (size_t)min(m0 + row, M - 1) * K;
-        lp[i] = (isb ? A_BYTES : 0) + row * ROW + (q % PPR) * 16;
-    }
-    const uint32_t pc = (tid % PPR) * 16;
-
-    struct Stage {
-        v4i p[NP];
-        uint32_t sc[NSC];
-    };
-    auto gload = [&](Stage& st, uint32_t c) {
-        c = c < nchunks ? c : nchunks - 1;
-        const uint32_t col = min(c * KC * 32 + pc, K - 16);  // past the row end: a piece no block uses
-#pragma unroll
-        for (int i = 0; i < NP; i++) st.p[i] = *(const v4i*)(gp[i] + col);
-#pragma unroll
-        for (int i = 0; i < NSC; i++) {
-            const uint32_t sidx = tid + NT * i;
-            const uint32_t blk = min(c * KC + sidx % KC, nb - 1);
-            if (sidx < KC * TM) {
-                st.sc[i] = f2u(x.s[(size_t)min(m0 + sidx / KC, M - 1) * nb + blk]);
-            } else if (sidx < KC * (TM + TN)) {
-                const uint32_t col2 = (sidx - KC * TM) / KC;
-                st.sc[i] = scale_bits(WF16, WS, (size_t)min(n0 + col2, N - 1) * nb + blk);
-            }
-        }
-    };
-    auto lstore = [&](const Stage& st, int buf) {
-#pragma unroll
-        for (int i = 0; i < NP; i++)
-            if (NQ % NT == 0 || i + 1 < NP || tid + NT * i < NQ) *(v4i*)(sA(buf) + lp[i]) = st.p[i];
-#pragma unroll
-        for (int i = 0; i < NSC; i++) {
-            const uint32_t sidx = tid + NT * i, blk = sidx % KC;
-            if (sidx < KC * TM)
-                sX(buf)[blk * TM + sidx / KC] = u2f(st.sc[i]);
-            else if (sidx < KC * (TM + TN))
-                sW(buf)[blk * TN + (sidx - KC * TM) / KC] = scale_value(WF16, st.sc[i]);
-        }
-    };
-
-    float t[CPW][MI][NI][4];
-#pragma unroll
-    for (int c2 = 0; c2 < CPW; c2++)
-#pragma unroll
-        for (int i = 0; i < MI; i++)
-#pragma unroll
-            for (int j = 0; j < NI; j++)
-#pragma unroll
-                for (int v = 0; v < 4; v++) t[c2][i][j][v] = 0.0f;
-    const v4i zero = {0, 0, 0, 0};
-    auto compute = [&](int buf, uint32_t c) {
-#pragma unroll
-        for (int h = 0; h < KC / 4; h++)
-#pragma unroll
-            for (int c2 = 0; c2 < CPW; c2++) {
-                const uint32_t blk = cg * CPW + c2 + 4 * h, b = c * KC + blk;
-                if (b >= nb) break;
-                long a[MI], bq[NI];
-                float w[NI];
-                float4 xs[MI];
-#pragma unroll
-                for (int i = 0; i < MI; i++) {
-                    a[i] = *(const long*)(sA(buf) + (wm0 + i * 16 + r) * ROW + blk * 32 + 8 * quad);
-                    xs[i] = *(const float4*)(sX(buf) + blk * TM + wm0 + i * 16 + 4 * quad);
-                }
-#pragma unroll
-                for (int j = 0; j < NI; j++) {
-                    bq[j] = *(const long*)(sB(buf) + (wn0 + j * 16 + r) * ROW + blk * 32 + 8 * quad);
-                    w[j] = sW(buf)[blk * TN + wn0 + j * 16 + r];
-                }
-#pragma unroll
-                for (int i = 0; i < MI; i++)
-#pragma unroll
-                    for (int j = 0; j < NI; j++) {
-                        const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[i], bq[j], zero, 0, 0, 0);
-                        if (DBG) {
-                            const uint32_t n = n0 + wn0 + j * 16 + r;
-#pragma unroll
-                            for (int v = 0; v < 4; v++) {
-                                const uint32_t m = m0 + wm0 + i * 16 + 4 * quad + v;
-                                if (m < M && n < N) dbg[((size_t)m * N + n) * nb + b] = d[v];
-                            }
-                        }
-                        // dot.rs: t[b & 3] += (sa * sb) * (isum as f32)
-                        t[c2][i][j][0] += (w[j] * xs[i].x) * (float)d[0];
-                        t[c2][i][j][1] += (w[j] * xs[i].y) * (float)d[1];
-                        t[c2][i][j][2] += (w[j] * xs[i].z) * (float)d[2];
-                        t[c2][i][j][3] += (w[j] * xs[i].w) * (float)d[3];
-                    }
-            }
-    };
-
-    gemm_pipeline<NS, Stage>(nchunks, gload, lstore, compute);
-
-    float* Y = ms.y[mi_];
-    const uint32_t ld = ms.ld[mi_];
-    if constexpr (CPW == 4) {
-        // one wave holds all four chains of its outputs
-#pragma unroll
-        for (int i = 0; i < MI; i++)
-#pragma unroll
-            for (int j = 0; j < NI; j++)
-#pragma unroll
-                for (int v = 0; v < 4; v++) {
-                    const uint32_t m = m0 + wm0 + i * 16 + 4 * quad + v, n = n0 + wn0 + j * 16 + r;
-                    if (m < M && n < N)
-                        Y[(size_t)m * ld + n] = ((t[0][i][j][v] + t[1][i][j][v]) + t[2][i][j][v]) + t[3][i][j][v];
-                }
-    } else {
-        // the chains meet in LDS: part[chain][sub][((i * NI + j) * 4 + v) * 64 + lane]
-        constexpr int WOUT = WM * WN;
-        float* part = (float*)lds;
-#pragma unroll
-        for (int c2 = 0; c2 < CPW; c2++)
-#pragma unroll
-            for (int i = 0; i < MI; i++)
-#pragma unroll
-                for (int j = 0; j < NI; j++)
-#pragma unroll
-                    for (int v = 0; v < 4; v++)
-                        part[((cg * CPW + c2) * NSUB + sub) * WOUT + ((i * NI + j) * 4 + v) * 64 + lane] =
-                            t[c2][i][j][v];
-        __syncthreads();
-#pragma unroll
-        for (int k = 0; k < TM * TN / NT; k++) {
-            const uint32_t o = tid + NT * k, sb = o / WOUT, oo = o % WOUT;
-            const uint32_t l = oo & 63, v = (oo >> 6) & 3, ij = oo >> 8, i = ij / NI, j = ij % NI;
-            const uint32_t m = m0 + (sb % SM) * WM + i * 16 + 4 * (l >> 4) + v;
-            const uint32_t n = n0 + (sb / SM) * WN + j * 16 + (l & 15);
-            if (m < M && n < N) {
-                const float p0 = part[o], p1 = part[TM * TN + o], p2 = part[2 * TM * TN + o];
-                const float p3 = part[3 * TM * TN + o];
-                Y[(size_t)m * ld + n] = ((p0 + p1) + p2) + p3;
-            }
-        }
     }
 }
 
@@ -1255,26 +1018,10 @@ __global__ __launch_bounds__(256, 2) void k_gemm_chain(MatSet ms, QuantAct x, ui
     }
 }
 
-template <int SEM, int TM, int TN, int WM, int WN, int CPW, int KC, int NS, int WPE>
-static void launch_q8(hipStream_t st, MatSet ms, QuantAct x, size_t rows, size_t k, int32_t* dbg) {
-    uint32_t total = 0;
-    for (int i = 0; i < 3; i++) {
-        if (i < ms.count) total += (uint32_t)((ms.n[i] + TN - 1) / TN);
-        ms.tile_end[i] = total;
-    }
-    const uint32_t mtiles = (uint32_t)((rows + TM - 1) / TM);
-    const dim3 grid(total * mtiles), block(64 * (TM / WM) * (TN / WN) * (4 / CPW));
-    if (dbg)
-        hipLaunchKernelGGL((k_gemm_q8<SEM, TM, TN, WM, WN, CPW, KC, NS, WPE, true>), grid, block, 0, st, ms, x,
-                           (uint32_t)rows, (uint32_t)k, mtiles, dbg);
-    else
-        hipLaunchKernelGGL((k_gemm_q8<SEM, TM, TN, WM, WN, CPW, KC, NS, WPE, false>), grid, block, 0, st, ms, x,
-                           (uint32_t)rows, (uint32_t)k, mtiles, dbg);
-}
-
 template <int SEM>
 static hipError_t gemm_launch(hipStream_t st, MatSet ms, size_t k, QuantAct x, size_t rows, int32_t* dbg) {
-    const uint32_t cols = SEM == SEM_FMA_CHAIN ? 128 : 32;
+    if (SEM != SEM_FMA_CHAIN) return launch_gemm_q8(st, SEM, ms, k, x, rows, dbg);
+    const uint32_t cols = 128;
     uint32_t total = 0;
     for (int i = 0; i < 3; i++) {
         if (i < ms.count) total += (uint32_t)((ms.n[i] + cols - 1) / cols);
@@ -1283,28 +1030,10 @@ static hipError_t gemm_launch(hipStream_t st, MatSet ms, size_t k, QuantAct x, s
     const uint32_t mtiles = (uint32_t)((rows + 31) / 32);
     dim3 grid(total * mtiles);
     const uint32_t m = (uint32_t)rows, kk = (uint32_t)k;
-    if (SEM == SEM_FMA_CHAIN) {
-        if (dbg)
-            hipLaunchKernelGGL(k_gemm_chain<true>, grid, dim3(256), 0, st, ms, x, m, kk, mtiles, dbg);
-        else
-            hipLaunchKernelGGL(k_gemm_chain<false>, grid, dim3(256), 0, st, ms, x, m, kk, mtiles, dbg);
-    } else {
-        // the widest tile that still gives the grid enough workgroups: wider
-        // tiles stage fewer bytes per output (A and B rows are shared by more
-        // outputs) but give fewer, longer workgroups
-        uint32_t n128 = 0, n64 = 0;
-        for (int i = 0; i < ms.count; i++) {
-            n128 += (uint32_t)((ms.n[i] + 127) / 128);
-            n64 += (uint32_t)((ms.n[i] + 63) / 64);
-        }
-        const size_t m64 = (rows + 63) / 64;
-        if (rows >= 64 && m64 * n128 >= kGemmWideTiles)
-            launch_q8<SEM, 64, 128, 32, 64, 1, 8, 2, 1>(st, ms, x, rows, k, dbg);
-        else if (rows >= 64 && m64 * n64 >= kGemmMidTiles)
-            launch_q8<SEM, 64, 64, 32, 32, 1, 4, 4, 1>(st, ms, x, rows, k, dbg);
-        else
-            launch_q8<SEM, 32, 32, 16, 16, 1, 8, 4, 1>(st, ms, x, rows, k, dbg);
-    }
+    if (dbg)
+        hipLaunchKernelGGL(k_gemm_chain<true>, grid, dim3(256), 0, st, ms, x, m, kk, mtiles, dbg);
+    else
+        hipLaunchKernelGGL(k_gemm_chain<false>, grid, dim3(256), 0, st, ms, x, m, kk, mtiles, dbg);
     return hipGetLastError();
 }
 

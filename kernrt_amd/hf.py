@@ -38,13 +38,13 @@ class LoadError(Exception):
 
 class MissingTensor(LoadError):
     def __init__(self, name: str):
-        super().__init__(f"weight file is missing {name!r}")
+        super().__init__(f"no tensor named {name!r} in the weight files")
         self.name = name
 
 
 class BadConfig(LoadError):
     def __init__(self, msg: str):
-        super().__init__(f"invalid config: {msg}")
+        super().__init__(f"config not usable: {msg}")
 
 
 def storage_from_env(bf16: bool) -> str:
@@ -97,7 +97,7 @@ def matrix_from_raw(t: RawTensor, storage: str) -> SourceMatrix:
         raise ValueError(f"unknown storage {storage!r}")
     shape = t.shape
     if len(shape) != 2:
-        raise BadConfig("a weight matrix was not rank 2")
+        raise BadConfig("weight matrices must have two dimensions")
     out_dim, in_dim = shape
     aligned_q8x4 = in_dim % Q8_0_BLOCK == 0 and out_dim % Q8_0X4_ROWS == 0
     if t.dtype == "BF16":
@@ -125,11 +125,11 @@ def _read_json(path):
         with open(path, "rb") as f:
             raw = f.read()
     except OSError as e:
-        raise LoadError(f"i/o error: {e}") from e
+        raise LoadError(f"could not read the checkpoint: {e}") from e
     try:
         return json.loads(raw)
     except ValueError as e:
-        raise LoadError(f"invalid config.json: {e}") from e
+        raise LoadError(f"config.json does not parse: {e}") from e
 
 
 def _u64(value: dict, key: str) -> Optional[int]:
@@ -154,7 +154,7 @@ def _bool(value: dict, key: str) -> Optional[bool]:
 def _get(value: dict, key: str) -> int:
     v = _u64(value, key)
     if v is None:
-        raise BadConfig(f"missing integer {key!r}")
+        raise BadConfig(f"{key!r} must be present as a non-negative integer")
     return v
 
 
@@ -166,7 +166,7 @@ def _f32(x: float) -> float:
 def _check_heads(c: Config):
     # hf.rs:265-270 / 398-403; a zero head count is refused rather than divided by
     if c.n_kv_heads == 0 or c.head_dim == 0 or c.n_heads % c.n_kv_heads != 0:
-        raise BadConfig("head counts do not divide the model dimension")
+        raise BadConfig("the model dimension is not a multiple of the head counts")
 
 
 def parse_hf_config(path) -> Tuple[Config, bool]:
@@ -185,7 +185,7 @@ def parse_hf_config(path) -> Tuple[Config, bool]:
     head_dim = _u64(value, "head_dim")
     if head_dim is None:
         if n_heads == 0:
-            raise BadConfig("head counts do not divide the model dimension")
+            raise BadConfig("the model dimension is not a multiple of the head counts")
         head_dim = dim // n_heads
     eps = _f64(value, "rms_norm_eps")
     inter = _bool(value, "rope_interleaved")
@@ -208,7 +208,7 @@ def lfm2_ff_dim(block_ff_dim: int, auto_adjust: bool, multiplier: Optional[float
             x = multiplier * float(dim)
             dim = 0 if (math.isnan(x) or x <= 0) else int(x)  # `as usize` saturates
         if multiple_of == 0:
-            raise BadConfig("block_multiple_of is 0")
+            raise BadConfig("block_multiple_of must be at least 1")
         dim = multiple_of * (-(-dim // multiple_of))
     return dim
 
@@ -235,7 +235,7 @@ def parse_lfm2_config(path) -> Tuple[Config, bool, List[bool], int]:
     eps = _f64(value, "norm_eps")
     theta = _f64(value, "rope_theta")
     if n_heads == 0:
-        raise BadConfig("head counts do not divide the model dimension")
+        raise BadConfig("the model dimension is not a multiple of the head counts")
     c = Config(dim=dim, hidden_dim=hidden, n_layers=n_layers, n_heads=n_heads, n_kv_heads=n_kv,
                vocab_size=_get(value, "vocab_size"), seq_len=min(_get(value, "max_position_embeddings"), 8192),
                rms_eps=_f32(1e-5 if eps is None else eps),
@@ -299,7 +299,7 @@ def lfm2_weights(config: Config, is_attention: List[bool], storage: str,
             proj["conv_out"] = take_matrix_raw(tensors, f"{p}.conv.out_proj.weight", storage)
             raw = take_f32(tensors, f"{p}.conv.conv.weight")  # stored [dim, 1, k]
             if raw.ndim != 3 or raw.shape[1] != 1:
-                raise BadConfig(f"{p}.conv.conv.weight has shape {list(raw.shape)}, expected [dim, 1, k]")
+                raise BadConfig(f"{p}.conv.conv.weight is {list(raw.shape)}; a depthwise kernel is [dim, 1, k]")
             kernel = np.ascontiguousarray(raw.reshape(raw.shape[0], raw.shape[2]), np.float32)
         rms_att = take_f32(tensors, f"{p}.operator_norm.weight")
         rms_ffn = take_f32(tensors, f"{p}.ffn_norm.weight")
@@ -319,7 +319,7 @@ def _tensors(d):
     except SafeTensorsError as e:
         raise LoadError(str(e)) from e
     except OSError as e:
-        raise LoadError(f"i/o error: {e}") from e
+        raise LoadError(f"could not read the checkpoint: {e}") from e
 
 
 def llama_from_hf_with(d, backend, storage: Optional[str] = None) -> Model:

@@ -30,29 +30,29 @@ class SafeTensorsError(Exception):
 
 class HeaderTooShort(SafeTensorsError):
     def __init__(self, file_len: int, needed: int):
-        super().__init__(f"file of {file_len} bytes is too short for a {needed}-byte header")
+        super().__init__(f"need {needed} bytes for the header, the file holds {file_len}")
         self.file_len, self.needed = file_len, needed
 
 
 class InvalidJson(SafeTensorsError):
     def __init__(self, err: Exception):
-        super().__init__(f"invalid header JSON: {err}")
+        super().__init__(f"the header is not UTF-8 JSON ({err})")
 
 
 class InvalidHeader(SafeTensorsError):
     def __init__(self, msg: str):
-        super().__init__(f"invalid header: {msg}")
+        super().__init__(f"malformed header: {msg}")
 
 
 class UnsupportedDtype(SafeTensorsError):
     def __init__(self, dtype: str):
-        super().__init__(f"unsupported dtype {dtype!r} (F32, BF16 and F16 are read)")
+        super().__init__(f"dtype {dtype!r} cannot be read; F32, BF16 and F16 can")
         self.dtype = dtype
 
 
 class InvalidOffsets(SafeTensorsError):
     def __init__(self, name: str, start: int, end: int):
-        super().__init__(f"tensor {name!r} has byte range {start}..{end} that does not match its shape")
+        super().__init__(f"bytes [{start}, {end}) of {name!r} disagree with its dtype, its shape or the file length")
         self.name, self.start, self.end = name, start, end
 
 
@@ -106,31 +106,31 @@ def _read_with(buf: np.ndarray, decode: Callable[[str, np.ndarray, Tuple[int, ..
         raise InvalidJson(e) from None
     data = buf[8 + header_len:]
     if not isinstance(header, dict):
-        raise InvalidHeader("top level is not an object")
+        raise InvalidHeader("the header must be a JSON object")
     out = {}
     for name, spec in header.items():
         if name == "__metadata__":
             continue
         if not isinstance(spec, dict):
-            raise InvalidHeader(f"tensor {name!r} is not an object")
+            raise InvalidHeader(f"entry {name!r} must be a JSON object")
         dtype = spec.get("dtype")
         if not isinstance(dtype, str):
-            raise InvalidHeader(f"tensor {name!r} has no dtype")
+            raise InvalidHeader(f"entry {name!r} lacks a string dtype")
         if dtype not in _WIDTH:
             raise UnsupportedDtype(dtype)
         shape = spec.get("shape")
         if not isinstance(shape, list):
-            raise InvalidHeader(f"tensor {name!r} has no shape array")
+            raise InvalidHeader(f"entry {name!r} lacks a shape list")
         dims = [_as_uint(d) for d in shape]
         if any(d is None for d in dims):
-            raise InvalidHeader(f"tensor {name!r} has a non-integer shape")
+            raise InvalidHeader(f"entry {name!r}: each dimension must be a non-negative integer")
         offs = spec.get("data_offsets")
         if not isinstance(offs, list):
-            raise InvalidHeader(f"tensor {name!r} has no data_offsets")
+            raise InvalidHeader(f"entry {name!r} lacks a data_offsets list")
         start = _as_uint(offs[0]) if len(offs) > 0 else None
         end = _as_uint(offs[1]) if len(offs) > 1 else None
         if start is None or end is None:
-            raise InvalidHeader(f"tensor {name!r} needs two integer data_offsets")
+            raise InvalidHeader(f"entry {name!r}: data_offsets must be a start and an end, non-negative integers")
         numel = 1
         for d in dims:
             numel *= d

@@ -186,7 +186,8 @@ int kr_stream_read(kr_ctx* ctx, kr_buf src, size_t offset, size_t len);
  * reference): `workgroups` x 4 waves, each keeping four independent int8 MFMAs
  * in flight for `iters` rounds (kind 0: v_mfma_i32_32x32x32_i8, kind 1:
  * v_mfma_i32_16x16x32_i8); *ops gets the int8 operations issued. Time it with
- * kr_timer_start / kr_timer_stop to measure the chip's dense int8 rate. */
+ * kr_timer_start / kr_timer_stop to measure the chip's dense int8 rate.
+ * workgroups x iters is capped at 2^32 (about half a second of MFMA work). */
 int kr_mfma_rate(kr_ctx* ctx, int kind, size_t workgroups, size_t iters, double* ops);
 
 /* Launch capture: the ops issued between kr_capture_begin and
@@ -216,7 +217,10 @@ int kr_dbg_block_dots(kr_ctx* ctx, kr_mat w, kr_buf x, size_t rows, int32_t* out
  * block scales [out_dim][in_dim/32] (f32 for Q8_0, f16 bits for Q8_0x4) --
  * so a host checker can rebuild the reference's Matrix from the very bytes a
  * kernel reads (e.g. the device-generated synthetic weights). */
-int kr_matrix_read(kr_ctx* ctx, kr_mat m, int8_t* quants, void* scales);
+int kr_matrix_read(kr_ctx* ctx, kr_mat m, int8_t* quants, size_t quants_bytes, void* scales,
+                   size_t scales_bytes); /* the byte sizes must be the matrix's exactly */
+/* out_dim, in_dim and storage (KR_STORAGE_*) of a device matrix. */
+int kr_matrix_shape(kr_ctx* ctx, kr_mat m, size_t* out_dim, size_t* in_dim, int* storage);
 
 /* ---- key/value cache access, for benchmarks that start from a filled cache */
 /* which: 0 keys, 1 values; element offset into [n_layers, seq_len, kv_dim]. */

@@ -104,7 +104,8 @@ _SIGS = {
     "kr_dbg_block_dots": (i32, [vp, u32, u32, sz, vp]),
     "kr_kv_upload": (i32, [vp, i32, sz, vp, sz]),
     "kr_kv_read": (i32, [vp, i32, sz, vp, sz]),
-    "kr_matrix_read": (i32, [vp, u32, vp, vp]),
+    "kr_matrix_read": (i32, [vp, u32, vp, sz, vp, sz]),
+    "kr_matrix_shape": (i32, [vp, u32, C.POINTER(sz), C.POINTER(sz), C.POINTER(i32)]),
     "kr_kv_synthetic": (i32, [vp, sz, C.c_uint64]),
     "kr_argmax": (i32, [vp, u32, sz, sz]),
     "kr_read_tokens": (i32, [vp, vp, sz]),

@@ -433,12 +433,22 @@ class Hip:
         self._ck(self._L.kr_synthetic_values(self.ctx, b, n, seed, stddev))
         return self.read(b, n)
 
-    def read_matrix(self, mat: int, storage: str, out_dim: int, in_dim: int):
+    def matrix_shape(self, mat: int):
+        """(storage, out_dim, in_dim) of a device matrix."""
+        n, k, st = C.c_size_t(), C.c_size_t(), C.c_int()
+        self._ck(self._L.kr_matrix_shape(self.ctx, mat, C.byref(n), C.byref(k), C.byref(st)))
+        return ("q8_0" if st.value == STORAGE_Q8_0 else "q8_0x4"), n.value, k.value
+
+    def read_matrix(self, mat: int, storage: str = None, out_dim: int = None, in_dim: int = None):
         """The device bytes of a matrix: int8 quants [out_dim, in_dim] and the
-        block scales (f32 for q8_0, f16 bits as uint16 for q8_0x4)."""
-        q = np.empty((out_dim, in_dim), np.int8)
-        s = np.empty((out_dim, in_dim // 32), np.float32 if storage == "q8_0" else np.uint16)
-        self._ck(self._L.kr_matrix_read(self.ctx, mat, _p(q), _p(s)))
+        block scales (f32 for q8_0, f16 bits as uint16 for q8_0x4). The shape
+        comes from the library; the optional arguments are checked against it."""
+        st, n, k = self.matrix_shape(mat)
+        if (storage, out_dim, in_dim) != (None, None, None) and (storage, out_dim, in_dim) != (st, n, k):
+            raise ValueError(f"matrix {mat} is {st} [{n}, {k}], not {storage} [{out_dim}, {in_dim}]")
+        q = np.empty((n, k), np.int8)
+        s = np.empty((n, k // 32), np.float32 if st == "q8_0" else np.uint16)
+        self._ck(self._L.kr_matrix_read(self.ctx, mat, _p(q), q.nbytes, _p(s), s.nbytes))
         return q, s
 
     def kv_synthetic(self, slots: int, seed: int):

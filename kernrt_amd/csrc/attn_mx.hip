@@ -48,8 +48,9 @@ typedef float mx_v32f __attribute__((ext_vector_type(32)));
 //     32 dims products p_i * v_i[e] (each the correctly rounded product), and
 //     the vector unit adds them to the chains in position order. Positions a
 //     pair's window does not reach get p = 0; the zero products leave the
-//     sums unchanged (the sums start at +0 and never become -0), unless the
-//     V row there holds an infinity or NaN.
+//     sums unchanged (the sums start at +0 and never become -0). A block
+//     whose V rows past its shortest window hold an infinity or NaN (0 * inf
+//     is NaN) recomputes its sums over each pair's own window instead.
 struct MxBlock {
     uint32_t r0, nr, h0, kvo, n_shared, cmax;
     DevWindow w0;
@@ -277,6 +278,14 @@ __global__ __launch_bounds__(256, 3) void k_attn_mx_v(float* __restrict__ att, f
         const uint32_t r = pair / G, j = pair - r * G;
         return att + (size_t)(r0 + r) * n_heads * seq_len + (size_t)(h0 + j) * seq_len;
     };
+    // Positions past a pair's window enter its sums as p = 0 times v, which
+    // is 0 only for a finite v. The shortest live window: V rows from there
+    // on are checked as they are staged, and a block that met an infinite or
+    // NaN one recomputes its sums under each pair's own window at the end.
+    uint32_t cmin = cmax;
+    for (uint32_t k = 0; k < nr * G; k++) cmin = min(cmin, s_cnt[k]);
+    cmin = __builtin_amdgcn_readfirstlane(cmin);
+    bool vbad = false;
     // 3. V sums: wave w owns dims 32 w .. 32 w + 31 (HS / 32 waves); chunks
     // of 32 positions staged through LDS, the next chunk's loads in flight
     typedef float vs4 __attribute__((ext_vector_type(4)));  // native vectors: the stages stay in registers
@@ -318,6 +327,16 @@ __global__ __launch_bounds__(256, 3) void k_attn_mx_v(float* __restrict__ att, f
         for (uint32_t k = 0; k < HS / 32; k++) {
             const uint32_t f = tid + 256 * k, rr = f / (HS / 4), col = f - rr * (HS / 4);
             *(vs4*)(s_v[buf] + rr * VST + 4 * col) = st.v[k];
+        }
+        if (32 * lchunk > cmin) {  // this chunk reaches past the shortest window
+#pragma unroll
+            for (uint32_t k = 0; k < HS / 32; k++) {
+                const uint32_t rr = (tid + 256 * k) / (HS / 4);
+                const vs4 x = st.v[k];
+                if (32 * (lchunk - 1) + rr >= cmin && !(__builtin_isfinite(x.x) && __builtin_isfinite(x.y) &&
+                                                        __builtin_isfinite(x.z) && __builtin_isfinite(x.w)))
+                    vbad = true;
+            }
         }
         const uint32_t pair = tid >> 3, i0 = 4 * (tid & 7);
         s_p[buf][i0 * PST + pair] = st.p.x;
@@ -373,6 +392,20 @@ __global__ __launch_bounds__(256, 3) void k_attn_mx_v(float* __restrict__ att, f
         lstore(sa, 0);  // chunk c + 2
         gload(sa, c + 4);
         __syncthreads();
+    }
+    if (__syncthreads_or(vbad) && vwave) {
+        // the reference's loop for each element, in position order, over its
+        // own window only: the probabilities from `att`, V from the cache
+#pragma unroll
+        for (uint32_t v = 0; v < 16; v++) {
+            const uint32_t pair = 8 * (v >> 2) + 4 * h + (v & 3);
+            const uint32_t n = pair < nr * G ? s_cnt[pair] : 0;
+            const float* prow = att_row(min(pair, nr * G - 1));
+            float acc = 0.0f;
+            for (uint32_t i = 0; i < n; i++)
+                acc += prow[i] * vbase[(size_t)win_slot(w0, n_shared, i) * kv_dim + d0 + pr];
+            o[v] = acc;
+        }
     }
     if (!vwave) return;
     // element v: pair 8 (v / 4) + 4 h + v % 4, dim d0 + pr

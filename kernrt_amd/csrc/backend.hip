@@ -316,6 +316,19 @@ int new_mat(kr_ctx* c, int storage, size_t n, size_t k, kr_mat* out, Mat** mp) {
     return KR_OK;
 }
 
+void free_devmatrix(DevMatrix& m);
+
+// A matrix whose contents could not be produced: freed and its handle
+// retired, so a failed constructor leaves nothing behind; returns rc.
+int drop_new_mat(kr_ctx* c, kr_mat* out, int rc) {
+    Mat* m = c->mats[*out];
+    free_devmatrix(m->m);
+    delete m;
+    c->mats[*out] = nullptr;
+    *out = KR_NO_MAT;
+    return rc;
+}
+
 void free_devmatrix(DevMatrix& m) {
     if (m.q) (void)hipFree(m.q);
     if (m.s) (void)hipFree(m.s);
@@ -404,6 +417,17 @@ int classifier_matrix(kr_ctx* c, Mat* mt, const DevMatrix** use, int* sem) {
         *sem = kr::SEM_FOUR_PARTIALS_F32;
     }
     return KR_OK;
+}
+
+// The bound classifier (the embedding when tied) settles its x86 logits form
+// here, at set-up: the re-quantization check reads a counter back, and doing
+// it inside the first logits() would make that call a host barrier.
+int prime_classifier(kr_ctx* c) {
+    Mat* mt = mat_of(c, c->classifier == KR_NO_MAT ? c->embedding : c->classifier);
+    if (!mt) return KR_OK;
+    const DevMatrix* m;
+    int sem;
+    return classifier_matrix(c, mt, &m, &sem);
 }
 
 int logits_with(kr_ctx* c, Mat* mt, kr_buf x, kr_buf y) {
@@ -512,8 +536,10 @@ int kr_matrix_q8_0(kr_ctx* c, size_t n, size_t k, const int8_t* quants, const fl
     Mat* m;
     int rc = new_mat(c, KR_STORAGE_Q8_0, n, k, out, &m);
     if (rc) return rc;
-    HIPCHK(c, hipMemcpy(m->m.q, quants, n * k, hipMemcpyHostToDevice));
-    HIPCHK(c, hipMemcpy(m->m.s, scales, n * (k / 32) * sizeof(float), hipMemcpyHostToDevice));
+    hipError_t e = hipMemcpy(m->m.q, quants, n * k, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(m->m.s, scales, n * (k / 32) * sizeof(float), hipMemcpyHostToDevice);
+    if (e != hipSuccess)
+        return drop_new_mat(c, out, fail(c, KR_ERR_HIP, "uploading matrix [%zu, %zu]: %s", n, k, hipGetErrorString(e)));
     return KR_OK;
 }
 
@@ -542,8 +568,10 @@ int kr_matrix_q8_0x4(kr_ctx* c, size_t n, size_t k, const void* blocks, kr_mat* 
                     for (size_t lane = 0; lane < 4; lane++) dst[seg * 4 + lane] = qs[seg * 16 + r * 4 + lane];
             }
         }
-    HIPCHK(c, hipMemcpy(m->m.q, q.data(), q.size(), hipMemcpyHostToDevice));
-    HIPCHK(c, hipMemcpy(m->m.s, s.data(), s.size() * sizeof(uint16_t), hipMemcpyHostToDevice));
+    hipError_t e = hipMemcpy(m->m.q, q.data(), q.size(), hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(m->m.s, s.data(), s.size() * sizeof(uint16_t), hipMemcpyHostToDevice);
+    if (e != hipSuccess)
+        return drop_new_mat(c, out, fail(c, KR_ERR_HIP, "uploading matrix [%zu, %zu]: %s", n, k, hipGetErrorString(e)));
     return KR_OK;
 }
 
@@ -557,8 +585,11 @@ int kr_matrix_quantize(kr_ctx* c, int storage, int src_kind, const void* data, s
     const size_t esz = src_kind == KR_SRC_F32 ? 4 : 2, row_bytes = k * esz;
     const size_t chunk = std::max<size_t>(1, (64u << 20) / row_bytes);
     void* stage_dev = nullptr;
-    HIPCHK(c, hipStreamSynchronize(c->stream));
-    HIPCHK(c, hipMalloc(&stage_dev, std::min(chunk, n) * row_bytes));
+    hipError_t e0 = hipStreamSynchronize(c->stream);
+    if (e0 == hipSuccess) e0 = hipMalloc(&stage_dev, std::min(chunk, n) * row_bytes);
+    if (e0 != hipSuccess)
+        return drop_new_mat(c, out, fail(c, e0 == hipErrorOutOfMemory ? KR_ERR_OOM : KR_ERR_HIP,
+                                         "staging matrix [%zu, %zu]: %s", n, k, hipGetErrorString(e0)));
     int err = KR_OK;
     for (size_t r0 = 0; r0 < n && err == KR_OK; r0 += chunk) {
         const size_t rows = std::min(chunk, n - r0);
@@ -569,20 +600,30 @@ int kr_matrix_quantize(kr_ctx* c, int storage, int src_kind, const void* data, s
         if (e != hipSuccess) err = fail(c, KR_ERR_HIP, "quantizing matrix [%zu, %zu]: %s", n, k, hipGetErrorString(e));
     }
     (void)hipFree(stage_dev);
-    return err;
+    return err == KR_OK ? KR_OK : drop_new_mat(c, out, err);
 }
 
 int kr_matrix_synthetic(kr_ctx* c, int storage, size_t n, size_t k, uint64_t seed, float stddev, kr_mat* out) {
     Mat* m;
     int rc = new_mat(c, storage, n, k, out, &m);
     if (rc) return rc;
-    HIPCHK(c, kr::launch_synthetic_q8(c->stream, m->m, seed, stddev));
+    hipError_t e = kr::launch_synthetic_q8(c->stream, m->m, seed, stddev);
+    if (e != hipSuccess)
+        return drop_new_mat(c, out, fail(c, KR_ERR_HIP, "synthetic matrix [%zu, %zu]: %s", n, k, hipGetErrorString(e)));
     return KR_OK;
 }
+
+// workgroups x rounds of kr_mfma_rate: 2^32 is ~0.6 s of 32x32x32 int8 MFMAs
+static constexpr uint64_t kMfmaProbeMax = 1ull << 32;
 
 int kr_mfma_rate(kr_ctx* c, int kind, size_t workgroups, size_t iters, double* ops) {
     CHECK(c, kind == 0 || kind == 1, "MFMA kind %d", kind);
     CHECK(c, workgroups > 0 && workgroups <= (1u << 20) && iters > 0 && iters < (1u << 31), "probe size");
+    // about a second of MFMA work at the chip's rate at most: a longer probe
+    // would hold the GPU like a hang
+    CHECK(c, (double)workgroups * (double)iters <= (double)kMfmaProbeMax,
+          "probe of %zu workgroups x %zu rounds exceeds the %llu limit", workgroups, iters,
+          (unsigned long long)kMfmaProbeMax);
     int rc = ensure_tmp(c, workgroups * 256);
     if (rc) return rc;
     HIPCHK(c, kr::launch_mfma_spin(c->stream, kind, (int*)c->tmp, workgroups, (uint32_t)iters, ops));
@@ -609,13 +650,13 @@ int kr_matrix_free(kr_ctx* c, kr_mat h) {
 int kr_bind_embedding(kr_ctx* c, kr_mat m) {
     CHECK(c, mat_of(c, m) != nullptr, "unknown matrix %u", (unsigned)m);
     c->embedding = m;
-    return KR_OK;
+    return c->prepared ? prime_classifier(c) : KR_OK;
 }
 
 int kr_bind_classifier(kr_ctx* c, kr_mat m) {
     CHECK(c, m == KR_NO_MAT || mat_of(c, m) != nullptr, "unknown matrix %u", (unsigned)m);
     c->classifier = m;
-    return KR_OK;
+    return c->prepared ? prime_classifier(c) : KR_OK;
 }
 
 int kr_bind_proj(kr_ctx* c, size_t layer, int proj, kr_mat m) {
@@ -652,7 +693,7 @@ int kr_prepare(kr_ctx* c, size_t n_layers, size_t kv_dim, size_t seq_len) {
     c->seq_len = seq_len;
     c->storage = e->m.storage == KR_STORAGE_Q8_0 ? "q8_0" : "q8_0x4";
     c->prepared = true;
-    return KR_OK;
+    return prime_classifier(c);
 }
 
 int kr_alloc(kr_ctx* c, size_t len, kr_buf* out) {
@@ -1093,10 +1134,22 @@ int kr_kv_read(kr_ctx* c, int which, size_t offset, float* out, size_t len) {
     return KR_OK;
 }
 
-int kr_matrix_read(kr_ctx* c, kr_mat w, int8_t* quants, void* scales) {
+int kr_matrix_shape(kr_ctx* c, kr_mat w, size_t* out_dim, size_t* in_dim, int* storage) {
+    Mat* m = mat_of(c, w);
+    CHECK(c, m != nullptr, "unknown matrix %u", (unsigned)w);
+    *out_dim = m->m.n;
+    *in_dim = m->m.k;
+    *storage = m->m.storage;
+    return KR_OK;
+}
+
+int kr_matrix_read(kr_ctx* c, kr_mat w, int8_t* quants, size_t quants_bytes, void* scales, size_t scales_bytes) {
     Mat* m = mat_of(c, w);
     CHECK(c, m != nullptr, "unknown matrix %u", (unsigned)w);
     const size_t nk = m->m.n * m->m.k, ns = m->m.n * (m->m.k / 32) * (m->m.storage == KR_STORAGE_Q8_0 ? 4 : 2);
+    CHECK(c, quants_bytes == nk && scales_bytes == ns,
+          "matrix %u holds %zu quant and %zu scale bytes; the buffers hold %zu and %zu", (unsigned)w, nk, ns,
+          quants_bytes, scales_bytes);
     HIPCHK(c, hipMemcpyAsync(quants, m->m.q, nk, hipMemcpyDeviceToHost, c->stream));
     HIPCHK(c, hipMemcpyAsync(scales, m->m.s, ns, hipMemcpyDeviceToHost, c->stream));
     HIPCHK(c, hipStreamSynchronize(c->stream));

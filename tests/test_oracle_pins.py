@@ -346,3 +346,43 @@ def test_cpu_and_reference_transcriptions_agree_bitwise(interleaved):
         b.rms_norm(ob, xb, wb, rows, 48, 1e-5)
         outs[name] = np.concatenate([b.read(qb, q.size), b.read(kb, k.size), b.read(ob, x.size)])
     assert np.array_equal(outs["cpu"].view(np.uint32), outs["reference"].view(np.uint32))
+
+
+# ---- dot_scalar: four FMA chains (src/ops/dot.rs:350-366) -------------------
+#
+# The attention scores use this dot, on the CPU and (restated) on the GPU.
+# Each case is worked by hand in f32 so that a plausible restatement mistake
+# gives a different exact answer: a single left-to-right chain, separate
+# multiply and add instead of mul_add, the chains joined in sequence instead
+# of pairwise, or the tail summed on its own.
+
+
+def test_dot_scalar_runs_four_chains_not_one():
+    # chain 0: fma(1e8, 1, 0) = 1e8, fma(-1e8, 1, 1e8) = 0; chains 1-3: 1 + 1 = 2
+    # -> (0 + 2) + (2 + 2) = 6. One chain: 1e8 + 1 = 1e8 (ulp 8) three times,
+    # then -1e8 -> 0, then + 1 + 1 + 1 = 3.
+    a = [1e8, 1, 1, 1, -1e8, 1, 1, 1]
+    assert O.dot_scalar(a, np.ones(8)) == 6.0
+
+
+def test_dot_scalar_fuses_the_multiply_add():
+    # chain 0: fma(-1, 1 + 2^-11, 0) = -(1 + 2^-11), then
+    # fma(1 + 2^-12, 1 + 2^-12, -(1 + 2^-11)) = exactly 2^-24. A separate
+    # product rounds (1 + 2^-12)^2 = 1 + 2^-11 + 2^-24 (a tie) to even,
+    # 1 + 2^-11, and the sum is 0.
+    u, v = 1 + 2.0 ** -12, 1 + 2.0 ** -11
+    a = [-1.0, 0, 0, 0, u, 0, 0, 0]
+    b = [v, 0, 0, 0, u, 0, 0, 0]
+    assert O.dot_scalar(a, b) == 2.0 ** -24
+
+
+def test_dot_scalar_joins_the_chains_pairwise():
+    # acc = [1, 1e8, -1e8, 1]: (1 + 1e8) + (-1e8 + 1) = 1e8 + -1e8 = 0;
+    # in sequence ((1 + 1e8) - 1e8) + 1 = 1.
+    assert O.dot_scalar([1.0, 1e8, -1e8, 1.0], np.ones(4)) == 0.0
+
+
+def test_dot_scalar_continues_the_tail_from_the_joined_sum():
+    # chains give 1e8; the tail: fma(-1e8, 1, 1e8) = 0, fma(1, 1, 0) = 1.
+    # A tail summed apart (-1e8 + 1 = -1e8) and then added would give 0.
+    assert O.dot_scalar([1e8, 0, 0, 0, -1e8, 1.0], np.ones(6)) == 1.0

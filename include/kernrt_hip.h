@@ -213,6 +213,15 @@ int kr_dbg_quantize(kr_ctx* ctx, kr_buf x, size_t rows, size_t width, int8_t* qu
  * x: out [rows][out_dim][in_dim/32], through the same dot code as kr_matmul. */
 int kr_dbg_block_dots(kr_ctx* ctx, kr_mat w, kr_buf x, size_t rows, int32_t* out);
 
+/* One v_mfma_f32_32x32x1_2b_f32 per group on host operands: a, b [groups][64]
+ * (lane l: block l / 32, row / column l % 32), acc and out [groups][32][64]
+ * (register v of lane l; registers 16 blk .. +15 hold block blk's 32 x 32
+ * outputs, element (8 (j / 4) + 4 (l / 32) + j % 4, l % 32) in register
+ * 16 blk + j). The prefill GEMM's scale products and the prefill attention's
+ * chains rely on every output being fmaf(a, b, acc); a test checks it with
+ * this. groups <= 4096. No counterpart in the reference. */
+int kr_dbg_mfma_f32(kr_ctx* ctx, const float* a, const float* b, const float* acc, float* out, size_t groups);
+
 /* A device matrix as stored: row-major int8 quants [out_dim][in_dim] and the
  * block scales [out_dim][in_dim/32] (f32 for Q8_0, f16 bits for Q8_0x4) --
  * so a host checker can rebuild the reference's Matrix from the very bytes a

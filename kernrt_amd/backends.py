@@ -433,6 +433,15 @@ class Hip:
         self._ck(self._L.kr_synthetic_values(self.ctx, b, n, seed, stddev))
         return self.read(b, n)
 
+    def dbg_mfma_f32(self, a, b, acc) -> np.ndarray:
+        """kr_dbg_mfma_f32: a, b [groups, 64], acc [groups, 32, 64] -> out like acc."""
+        a = np.ascontiguousarray(a, np.float32)
+        b = np.ascontiguousarray(b, np.float32)
+        acc = np.ascontiguousarray(acc, np.float32)
+        out = np.empty_like(acc)
+        self._ck(self._L.kr_dbg_mfma_f32(self.ctx, _p(a), _p(b), _p(acc), _p(out), a.shape[0]))
+        return out
+
     def matrix_shape(self, mat: int):
         """(storage, out_dim, in_dim) of a device matrix."""
         n, k, st = C.c_size_t(), C.c_size_t(), C.c_int()

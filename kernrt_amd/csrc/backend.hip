@@ -1134,6 +1134,25 @@ int kr_kv_read(kr_ctx* c, int which, size_t offset, float* out, size_t len) {
     return KR_OK;
 }
 
+int kr_dbg_mfma_f32(kr_ctx* c, const float* a, const float* b, const float* acc, float* out, size_t groups) {
+    CHECK(c, groups > 0 && groups <= 4096, "groups %zu (1..4096)", groups);
+    CHECK(c, a && b && acc && out, "null operand");
+    const size_t na = groups * 64, nc = groups * 32 * 64;
+    int rc = ensure_tmp(c, 2 * na + 2 * nc);
+    if (rc) return rc;
+    float* da = (float*)c->tmp;
+    float* db = da + na;
+    float* dc = db + na;
+    float* dout = dc + nc;
+    HIPCHK(c, hipMemcpyAsync(da, a, na * sizeof(float), hipMemcpyHostToDevice, c->stream));
+    HIPCHK(c, hipMemcpyAsync(db, b, na * sizeof(float), hipMemcpyHostToDevice, c->stream));
+    HIPCHK(c, hipMemcpyAsync(dc, acc, nc * sizeof(float), hipMemcpyHostToDevice, c->stream));
+    HIPCHK(c, kr::launch_mfma_f32_probe(c->stream, da, db, dc, dout, groups));
+    HIPCHK(c, hipMemcpyAsync(out, dout, nc * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    return KR_OK;
+}
+
 int kr_matrix_shape(kr_ctx* c, kr_mat w, size_t* out_dim, size_t* in_dim, int* storage) {
     Mat* m = mat_of(c, w);
     CHECK(c, m != nullptr, "unknown matrix %u", (unsigned)w);

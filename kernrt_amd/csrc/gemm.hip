@@ -594,6 +594,28 @@ static hipError_t gemm_q8_go(hipStream_t st, const MatSet& ms, size_t k, QuantAc
     return hipGetLastError();
 }
 
+// One v_mfma_f32_32x32x1_2b_f32 per wave on given operands: lane l brings
+// a[g][l] and b[g][l] (block l / 32, row or column l % 32) and its 32
+// accumulator registers c[g][v][l]; out[g][v][l] is register v afterwards.
+// The GEMM's scale products and the prefill attention's chains rely on each
+// output being fmaf(a, b, c) of its operands; this lets a test check that.
+__global__ __launch_bounds__(64) void k_mfma_f32_probe(const float* __restrict__ a, const float* __restrict__ b,
+                                                       const float* __restrict__ c, float* __restrict__ out) {
+    const uint32_t g = blockIdx.x, l = threadIdx.x;
+    g_v32f acc;
+#pragma unroll
+    for (int v = 0; v < 32; v++) acc[v] = c[((size_t)g * 32 + v) * 64 + l];
+    acc = __builtin_amdgcn_mfma_f32_32x32x1f32(a[(size_t)g * 64 + l], b[(size_t)g * 64 + l], acc, 0, 0, 0);
+#pragma unroll
+    for (int v = 0; v < 32; v++) out[((size_t)g * 32 + v) * 64 + l] = acc[v];
+}
+
+hipError_t launch_mfma_f32_probe(hipStream_t st, const float* a, const float* b, const float* c, float* out,
+                                 size_t groups) {
+    hipLaunchKernelGGL(k_mfma_f32_probe, dim3((unsigned)groups), dim3(64), 0, st, a, b, c, out);
+    return hipGetLastError();
+}
+
 hipError_t launch_gemm_q8(hipStream_t st, int sem, const MatSet& ms, size_t k, QuantAct x, size_t rows,
                           int32_t* dbg) {
     if (sem == SEM_FOUR_PARTIALS_F32) return gemm_q8_go<SEM_FOUR_PARTIALS_F32>(st, ms, k, x, rows, dbg);

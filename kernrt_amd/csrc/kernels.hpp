@@ -163,6 +163,11 @@ hipError_t launch_synthetic_normal(hipStream_t st, float* out, size_t n, uint64_
 // int8 MFMA throughput probe: blocks x 256 threads, `iters` rounds; *ops = int8 ops issued;
 // sink holds blocks * 256 ints
 hipError_t launch_mfma_spin(hipStream_t st, int kind, int* sink, size_t blocks, uint32_t iters, double* ops);
+// One f32 matrix instruction (v_mfma_f32_32x32x1_2b_f32) per group of 64
+// lanes on given operands, for exactness checks: a, b [groups][64], c and out
+// [groups][32][64] (register v of lane l)
+hipError_t launch_mfma_f32_probe(hipStream_t st, const float* a, const float* b, const float* c, float* out,
+                                 size_t groups);
 // the f32 values launch_synthetic_q8 quantizes, element i of the flattened matrix
 hipError_t launch_synthetic_values(hipStream_t st, float* out, size_t n, uint64_t seed, float stddev);
 // counts Q8_0x4 blocks whose max |q| is neither 0 nor 127

@@ -102,19 +102,27 @@ def bench_decode(K, steps: int, warmup: int, use_graph: bool = True):
     toks = model.generate_greedy(token0, PREFILL_POS, steps, use_graph=use_graph)
     hip.synchronize()
     dt = time.perf_counter() - t0
-    # the per-call forward() path (logits back to the host each token)
-    t1 = time.perf_counter()
-    n_fwd = min(32, steps)
-    for i in range(n_fwd):
-        model.forward(token0, PREFILL_POS + i)
-    fwd_dt = time.perf_counter() - t1
+    # the per-call forward() path (logits back to the host each call) with
+    # the reference's decode_rate method (examples/decode_rate.rs:62-79): 5
+    # warm-up calls, then 300 timed calls of one token at one position; p10
+    # and median
+    for _ in range(5):
+        model.forward(token0, PREFILL_POS)
+    samples = []
+    for _ in range(300):
+        t1 = time.perf_counter()
+        model.forward(token0, PREFILL_POS)
+        samples.append(time.perf_counter() - t1)
+    samples.sort()
+    fwd_p10, fwd_med = samples[len(samples) // 10], samples[len(samples) // 2]
     weights = sum(n * k for n, k in [(c.q_dim, c.dim), (c.kv_dim, c.dim), (c.kv_dim, c.dim), (c.dim, c.q_dim),
                                      (c.hidden_dim, c.dim), (c.hidden_dim, c.dim),
                                      (c.dim, c.hidden_dim)]) * c.n_layers + c.vocab_size * c.dim
     p_mean = PREFILL_POS + steps / 2
     kv_bytes = 2 * c.n_layers * (p_mean + 1) * c.kv_dim * 4
     bytes_tok = weights * (1 + 2 / 32) + kv_bytes  # int8 + f16 scales per 32-block
-    out = dict(tok_s=steps / dt, ms_per_tok=dt * 1e3 / steps, forward_tok_s=n_fwd / fwd_dt,
+    out = dict(tok_s=steps / dt, ms_per_tok=dt * 1e3 / steps, forward_tok_s=1.0 / fwd_med,
+               forward_p10_tok_s=1.0 / fwd_p10, forward_samples=len(samples),
                bytes_per_token=bytes_tok, hbm_gbs_per_token_model=bytes_tok * steps / dt / 1e9,
                first_tokens=[int(t) for t in toks[:8]])
     model.close()
@@ -358,14 +366,20 @@ def bench_prefill(K, reps: int = 2):
         valu_floor_us = m_rows * n * (k // 32) * 4 / VALU_LANE_OPS_PER_S * 1e6
         per_shape[f"{name} {n}x{k}"] = dict(avg_us=us, tops=2 * m_rows * n * k / (us * 1e-6) / 1e12,
                                            weight_gbs=n * k * (1 + 4 / 32) / (us * 1e-6) / 1e9,
-                                           valu_floor_us=valu_floor_us, frac_of_valu_floor=valu_floor_us / us)
+                                           valu_floor_us=valu_floor_us, frac_of_valu_floor=valu_floor_us / us,
+                                           valu_floor_3op_us=valu_floor_us * 3 / 4,
+                                           frac_of_valu_floor_3op=valu_floor_us * 3 / 4 / us)
     ops = 2 * m_rows * sum(n * k for _, shapes in groups for n, k in shapes) * c.n_layers
     tops = ops / (gemm_ms * 1e-3) / 1e12
     triples = m_rows * sum(n * k // 32 for _, shapes in groups for n, k in shapes) * c.n_layers
     valu_floor_ms = triples * 4 / VALU_LANE_OPS_PER_S * 1e3
     hip.close()
+    # valu_floor: the exact epilogue's 4 vector operations per (row, column,
+    # block) -- cvt, two multiplies, add; valu_floor_3op: 3, with the scale
+    # product sa * sb on the matrix core as the wide tiles do
     return dict(rows=m_rows, gemm_ms=gemm_ms, int8_tops=tops, mfma_util=tops / INT8_PEAK_TOPS, ops=ops,
                 valu_floor_ms=valu_floor_ms, frac_of_valu_floor=valu_floor_ms / gemm_ms,
+                valu_floor_3op_ms=valu_floor_ms * 3 / 4, frac_of_valu_floor_3op=valu_floor_ms * 3 / 4 / gemm_ms,
                 projection_ms_with_quantize=proj_ms, per_shape=per_shape)
 
 
@@ -387,26 +401,35 @@ def bench_mfma_peak(K, workgroups: int = 2048, iters: int = 20000):
     return out
 
 
-def bench_prefill_model(K, n_tokens: int = 128, reps: int = 5):
-    """`configs[2]` end to end: a 128-token prefill of the synthetic
-    SmolLM2-1.7B-shaped Llama with Q8_0 weights, seeded random token ids.
-    As the reference's prefill_rate harness does, the first call is timed
-    apart and the best of the following calls is reported."""
-    log("prefill model: building the 1.7B-shaped Q8_0 model on the device")
-    hip, model, c = synthetic_model(K, CFG3, "q8_0", seed=7)
-    toks = [int(t) for t in np.random.default_rng(8).integers(0, c.vocab_size, size=n_tokens)]
+def prefill_rate(model, toks, reps: int = 20):
+    """The reference's prefill_rate method (examples/prefill_rate.rs:98-119):
+    the first call timed on its own, then `reps` calls; best and median.
+    Each call reads its logits back, so it ends with the device idle."""
     t0 = time.perf_counter()
     model.prefill(toks, 0)
     first = time.perf_counter() - t0
-    best = None
+    samples = []
     for _ in range(reps):
         t0 = time.perf_counter()
         model.prefill(toks, 0)
-        dt = time.perf_counter() - t0
-        best = dt if best is None else min(best, dt)
+        samples.append(time.perf_counter() - t0)
+    samples.sort()
+    best, median = samples[0], samples[len(samples) // 2]
+    n = len(toks)
+    return dict(tokens=n, tok_s=n / best, median_tok_s=n / median, best_ms=best * 1e3, median_ms=median * 1e3,
+                first_call_ms=first * 1e3, calls=reps)
+
+
+def bench_prefill_model(K, n_tokens: int = 128):
+    """`configs[2]` end to end: a 128-token prefill of the synthetic
+    SmolLM2-1.7B-shaped Llama with Q8_0 weights, seeded random token ids."""
+    log("prefill model: building the 1.7B-shaped Q8_0 model on the device")
+    hip, model, c = synthetic_model(K, CFG3, "q8_0", seed=7)
+    toks = [int(t) for t in np.random.default_rng(8).integers(0, c.vocab_size, size=n_tokens)]
+    out = prefill_rate(model, toks)
     model.close()
     hip.close()
-    return dict(tokens=n_tokens, tok_s=n_tokens / best, best_ms=best * 1e3, first_call_ms=first * 1e3)
+    return out
 
 
 def bench_cfg4(K, n_prompt: int = 128, n_decode: int = 256, use_graph: bool = True):
@@ -416,12 +439,8 @@ def bench_cfg4(K, n_prompt: int = 128, n_decode: int = 256, use_graph: bool = Tr
     log("cfg4: building the LFM2-700M-shaped Q8_0x4 hybrid on the device")
     hip, model, c = synthetic_model(K, CFG4, "q8_0x4", seed=11, qk_norm=True, lfm2_attention=CFG4_ATTENTION)
     toks = [int(t) for t in np.random.default_rng(12).integers(0, c.vocab_size, size=n_prompt)]
-    logits = model.prefill(toks, 0)
-    hip.synchronize()
-    t0 = time.perf_counter()
-    logits = model.prefill(toks, 0)
-    prefill_s = time.perf_counter() - t0
-    first = int(np.argmax(logits))
+    pre = prefill_rate(model, toks)
+    first = int(np.argmax(model.prefill(toks, 0)))
     model.generate_greedy(first, n_prompt, 8, use_graph=use_graph)
     hip.synchronize()
     t0 = time.perf_counter()
@@ -430,29 +449,22 @@ def bench_cfg4(K, n_prompt: int = 128, n_decode: int = 256, use_graph: bool = Tr
     decode_s = time.perf_counter() - t0
     model.close()
     hip.close()
-    return dict(prefill_tokens=n_prompt, prefill_tok_s=n_prompt / prefill_s, decode_tokens=n_decode,
-                decode_tok_s=n_decode / decode_s)
+    return dict(prefill_tokens=n_prompt, prefill_tok_s=pre["tok_s"], prefill_median_tok_s=pre["median_tok_s"],
+                prefill_first_ms=pre["first_call_ms"], decode_tokens=n_decode, decode_tok_s=n_decode / decode_s)
 
 
 def bench_cfg5(K, n_prompt: int = 2048, n_seq: int = 64, ctx: int = 1024, steps: int = 8):
     """`configs[4]`: the Qwen3-0.6B-shaped Llama (head_dim 128, QK-norm) with
-    Q8_0 weights. (i) a 2048-token prefill of seeded random ids (best of 3
-    after a timed first call); (ii) batched decode of 64 sequences, each with
+    Q8_0 weights. (i) a 2048-token prefill of seeded random ids (best and
+    median of 20 after a timed first call); (ii) batched decode of 64 sequences, each with
     a 1024-position KV cache of its own (N(0, 1), 64 x 1024 slots in one
     cache): every step is one row per sequence, so every projection and the
     151936x1024 lm_head run as M = 64 int8 GEMMs; logits stay on the device."""
     log("cfg5: building the Qwen3-0.6B-shaped Q8_0 model (prefill)")
     hip, model, c = synthetic_model(K, CFG5, "q8_0", seed=21, qk_norm=True)
     toks = [int(t) for t in np.random.default_rng(22).integers(0, c.vocab_size, size=n_prompt)]
-    t0 = time.perf_counter()
-    model.prefill(toks, 0)
-    first = time.perf_counter() - t0
-    best = None
-    for _ in range(3):
-        t0 = time.perf_counter()
-        model.prefill(toks, 0)
-        dt = time.perf_counter() - t0
-        best = dt if best is None else min(best, dt)
+    pre = prefill_rate(model, toks)
+    best, first = pre["best_ms"] * 1e-3, pre["first_call_ms"] * 1e-3
     model.close()
     hip.close()
     log("cfg5: batched decode, 64 sequences x 1024-position caches")
@@ -475,7 +487,8 @@ def bench_cfg5(K, n_prompt: int = 2048, n_seq: int = 64, ctx: int = 1024, steps:
     model.close()
     hip.close()
     return dict(prefill_tokens=n_prompt, prefill_tok_s=n_prompt / best, prefill_best_ms=best * 1e3,
-                prefill_first_ms=first * 1e3, batch_sequences=n_seq, batch_ctx=ctx,
+                prefill_median_ms=pre["median_ms"], prefill_first_ms=first * 1e3, batch_sequences=n_seq,
+                batch_ctx=ctx,
                 batch_step_ms=dt * 1e3 / steps, batch_tok_s=n_seq * steps / dt,
                 batch_kv_gbs=kv_bytes * steps / dt / 1e9)
 
@@ -498,44 +511,37 @@ def host_cpu():
     return name, os.cpu_count(), usable
 
 
-def bench_cpu_baseline(K, gpu_first_tokens=None, decode_budget: float = 20.0, prefill_budget: float = 15.0):
-    """The oracle's cpu backend -- a C++ restatement of the reference's x86
-    path (Q8_0x4: quantize_rows + gemm_q8_0x4_batched, re-quantizing logits;
-    Q8_0: per-row quantize + dot_q8_0_scalar), built -O2 -ffp-contract=off,
-    scalar, no autovectorization -- on 1 core, on the very bytes the GPU legs
-    use: the synthetic weights and the pre-filled cache are generated on the
-    device with the decode / prefill legs' seeds and read back.
-
-    decode: greedy steps from the decode leg's token at position
-    512, bounded by `decode_budget` seconds; p10 and median step as the
-    reference's decode_rate harness reports (examples/decode_rate.rs:62-79),
-    and the first tokens checked against the GPU decode's.
-    prefill (configs[2]): one layer's seven Q8_0 projections at 128 rows
-    (layer 0 of the prefill leg's weights), the first call timed apart and
-    the best of the repeats that fit `prefill_budget`
-    (examples/prefill_rate.rs:98-119), scaled to the 24-layer model."""
+def cpu_decode_leg(K, budget: float, max_steps: int = 300):
+    """The oracle's cpu backend decoding the decode leg's model on one core:
+    the synthetic weights and the pre-filled cache are generated on the
+    device with the decode leg's seeds and read back, so both sides hold the
+    same bytes. A GPU greedy run of `max_steps` tokens from the same start is
+    the reference sequence: every CPU token is compared with it. Each CPU
+    greedy step is one tg1 sample; p10 and median as the reference's
+    decode_rate reports (examples/decode_rate.rs:62-79), over the steps that
+    fit `budget` seconds (at most `max_steps`)."""
     import oracle as O
     cpu_name, n_cpu, usable = host_cpu()
-    log("cpu baseline: reading the decode leg's weights and cache back from the device")
+    log(f"cpu baseline ({O.VARIANT or 'o2'} oracle): reading the decode leg's weights and cache back")
     hip, model, c = synthetic_model(K, CFG2, "q8_0x4", seed=2)
     hip.kv_synthetic(PREFILL_POS, seed=5)
     token0 = int(np.random.default_rng(2).integers(0, c.vocab_size))
+    gpu_tokens = [int(t) for t in model.generate_greedy(token0, PREFILL_POS, max_steps, use_graph=True)]
     emb, handles = model.weight_handles
     oc = O.Config(**CFG2)
     w = O.Weights(c.n_layers)
 
-    def omat(h, n, k):
-        q, sc = hip.read_matrix(h, "q8_0x4", n, k)
+    def omat(h):
+        _, n, k = hip.matrix_shape(h)
+        q, sc = hip.read_matrix(h)
         return O.Matrix.from_q8_0x4_blocks(K.backends.q8_0x4_records(q, sc), n, k)
 
-    shapes = {"q": (c.q_dim, c.dim), "k": (c.kv_dim, c.dim), "v": (c.kv_dim, c.dim), "o": (c.dim, c.q_dim),
-              "gate": (c.hidden_dim, c.dim), "up": (c.hidden_dim, c.dim), "down": (c.dim, c.hidden_dim)}
     for l in range(c.n_layers):
-        for name, (n, k) in shapes.items():
-            w.set_proj(l, name, omat(handles[l][name], n, k))
+        for name, h in handles[l].items():
+            w.set_proj(l, name, omat(h))
         w.set_norm(l, "att", np.ones(c.dim, np.float32))
         w.set_norm(l, "ffn", np.ones(c.dim, np.float32))
-    w.set_embedding(omat(emb, c.vocab_size, c.dim))
+    w.set_embedding(omat(emb))
     w.set_final_norm(np.ones(c.dim, np.float32))
     w.set_classifier(None)
     cpu = O.Model(oc, w, "cpu")
@@ -545,9 +551,9 @@ def bench_cpu_baseline(K, gpu_first_tokens=None, decode_budget: float = 20.0, pr
             cpu.kv_upload(which, l * c.seq_len * c.kv_dim, hip.kv_read(which, l * c.seq_len * c.kv_dim, per))
     model.close()
     hip.close()
-    log("cpu baseline: timing decode steps on one core")
+    log(f"cpu baseline ({O.VARIANT or 'o2'} oracle): timing greedy decode steps on one core")
     tok, toks, times, t0 = token0, [], [], time.perf_counter()
-    while len(times) < 300 and time.perf_counter() - t0 < decode_budget:
+    while len(times) < max_steps and time.perf_counter() - t0 < budget:
         s0 = time.perf_counter()
         logits = cpu.forward(tok, PREFILL_POS + len(times))
         times.append(time.perf_counter() - s0)
@@ -556,9 +562,29 @@ def bench_cpu_baseline(K, gpu_first_tokens=None, decode_budget: float = 20.0, pr
     del cpu, w
     st = sorted(times)
     median, p10 = st[len(st) // 2], st[len(st) // 10]
-    check = gpu_first_tokens[:len(toks)] if gpu_first_tokens else []
-    match = bool(check) and toks[:len(check)] == list(check)
+    return dict(median_s=median, p10_s=p10, steps=len(times), tokens=toks, tokens_compared=len(toks),
+                all_tokens_match_gpu=toks == gpu_tokens[:len(toks)], host_cpu=cpu_name, nproc=n_cpu,
+                cores_usable=usable)
 
+
+def bench_cpu_baseline(K, decode_budget: float = 30.0, prefill_budget: float = 15.0, max_steps: int = 300,
+                       o3=None):
+    """The oracle's cpu backend -- a C++ restatement of the reference's x86
+    path (Q8_0x4: quantize_rows + gemm_q8_0x4_batched, re-quantizing logits;
+    Q8_0: per-row quantize + dot_q8_0_scalar), built -O2 -ffp-contract=off,
+    on 1 core, on the very bytes the GPU legs use.
+
+    decode: cpu_decode_leg. `o3` is the same leg run on the -O3
+    build of the oracle (the same bits, labelled as this build's variant),
+    measured in a child process before this one touched the GPU.
+    prefill (configs[2]): one layer's seven Q8_0 projections at 128 rows
+    (layer 0 of the prefill leg's weights), the first call timed apart and
+    the best of the repeats that fit `prefill_budget`
+    (examples/prefill_rate.rs:98-119), scaled to the 24-layer model."""
+    import oracle as O
+    dec = cpu_decode_leg(K, decode_budget, max_steps)
+    median, p10, cpu_name, n_cpu, usable = dec["median_s"], dec["p10_s"], dec["host_cpu"], dec["nproc"], \
+        dec["cores_usable"]
     log("cpu baseline: one 1.7B layer's prefill projections on one core")
     hip, pm, c3 = synthetic_model(K, CFG3, "q8_0", seed=7)
     _, handles3 = pm.weight_handles
@@ -588,15 +614,24 @@ def bench_cpu_baseline(K, gpu_first_tokens=None, decode_budget: float = 20.0, pr
     ops = 2 * 128 * sum(n * k for n, k in shapes3.values())
     prefill = dict(tokens=128, layer_first_s=first, layer_best_s=best, layer_repeats=len(reps),
                    tok_s_24_layers=128 / (best * c3.n_layers), gops=ops / best / 1e9)
-    return dict(value=1.0 / median, unit="tok/s", cores=1, kind="port",
-                sample=f"{len(times)} greedy decode steps of the cfg2 360M-shaped Q8_0x4 model (the decode leg's "
-                       f"device-generated weights and cache, read back) from position {PREFILL_POS}, oracle cpu "
-                       f"backend (scalar C++ port of the reference's x86 path, g++ -O2, no autovectorization), "
-                       f"1 thread on {cpu_name} ({usable} of {n_cpu} cores usable); median step "
-                       f"{median * 1e3:.1f} ms, p10 {p10 * 1e3:.1f} ms",
-                host_cpu=cpu_name, nproc=n_cpu, cores_usable=usable, p10_tok_s=1.0 / p10,
-                median_ms=median * 1e3, steps=len(times), first_tokens=toks[:8],
-                first_tokens_match_gpu=match, tokens_compared=len(check), prefill=prefill)
+    out = dict(value=1.0 / median, unit="tok/s", cores=1, kind="port",
+               sample=f"{dec['steps']} greedy decode steps of the cfg2 360M-shaped Q8_0x4 model (the decode leg's "
+                      f"device-generated weights and cache, read back) from position {PREFILL_POS}, oracle cpu "
+                      f"backend (scalar C++ port of the reference's x86 path, g++ -O2 -ffp-contract=off), "
+                      f"1 thread on {cpu_name} ({usable} of {n_cpu} cores usable); median step "
+                      f"{median * 1e3:.1f} ms, p10 {p10 * 1e3:.1f} ms; every token compared with a GPU greedy run",
+               host_cpu=cpu_name, nproc=n_cpu, cores_usable=usable, p10_tok_s=1.0 / p10,
+               median_ms=median * 1e3, steps=dec["steps"], first_tokens=dec["tokens"][:8],
+               all_tokens_match_gpu=dec["all_tokens_match_gpu"], tokens_compared=dec["tokens_compared"],
+               prefill=prefill)
+    if o3:
+        out["o3_variant"] = dict(
+            label="this build's variant: the same oracle at g++ -O3 -ffp-contract=off (no fast-math; "
+                  "the same bits), 1 thread",
+            tok_s=1.0 / o3["median_s"], p10_tok_s=1.0 / o3["p10_s"], median_ms=o3["median_s"] * 1e3,
+            steps=o3["steps"], all_tokens_match_gpu=o3["all_tokens_match_gpu"],
+            tokens_compared=o3["tokens_compared"])
+    return out
 
 
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "k_gemv_q8_0_1p7b_decode_pmc.md")
@@ -622,7 +657,13 @@ def main():
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--skip-cpu", action="store_true")
-    ap.add_argument("--only", choices=["decode", "gemv", "prefill", "cfg4", "cfg5", "cpu"], default=None)
+    ap.add_argument("--only", choices=["decode", "gemv", "prefill", "cfg4", "cfg5", "cpu", "cpu-decode-leg"],
+                    default=None)
+    ap.add_argument("--cpu-budget", type=float, default=30.0,
+                    help="seconds of CPU decode steps per oracle build (at most --cpu-steps; the reference's "
+                         "decode_rate takes 300)")
+    ap.add_argument("--cpu-steps", type=int, default=300)
+    ap.add_argument("--no-o3", action="store_true", help="skip the -O3 oracle figure")
     ap.add_argument("--no-graph", action="store_true",
                     help="launch the decode step's and the GEMV passes' kernels directly instead of replaying "
                          "captured HIP graphs (same kernels; for profilers that cannot trace graph launches)")
@@ -632,6 +673,27 @@ def main():
               "shard by output rows, with an all-gather of the f32 input rows in front of O and down, so that "
               "each output's f32 chain stays on one GPU).", file=sys.stderr)
         sys.exit(2)
+    if args.only == "cpu-decode-leg":
+        # child mode: one oracle build's decode leg, JSON on stdout
+        import kernrt_amd as K
+        dec = cpu_decode_leg(K, args.cpu_budget, args.cpu_steps)
+        dec.pop("tokens")
+        print(json.dumps(dec), flush=True)
+        return
+    want_cpu = not args.skip_cpu and args.only in (None, "cpu")
+    o3 = None
+    if want_cpu and not args.no_o3:
+        # the -O3 oracle's decode leg runs in a child process started before
+        # this process touches the GPU (the oracle library is chosen at load)
+        import subprocess
+        log("cpu baseline: the -O3 oracle's decode leg in a child process")
+        r = subprocess.run([sys.executable, os.path.abspath(__file__), "--only", "cpu-decode-leg", "--cpu-budget",
+                            str(args.cpu_budget), "--cpu-steps", str(args.cpu_steps)],
+                           env=dict(os.environ, KERNRT_ORACLE_VARIANT="o3"), stdout=subprocess.PIPE, text=True)
+        if r.returncode == 0:
+            o3 = json.loads(r.stdout.strip().splitlines()[-1])
+        else:
+            log(f"cpu baseline: the -O3 leg failed ({r.returncode})")
     import kernrt_amd as K
 
     res = {}
@@ -654,12 +716,12 @@ def main():
         res["cfg5"] = bench_cfg5(K)
         log(f"cfg5: prefill {res['cfg5']['prefill_tok_s']:.0f} tok/s, batched decode "
             f"{res['cfg5']['batch_tok_s']:.0f} tok/s")
-    if args.skip_cpu or (args.only and args.only != "cpu"):
+    if not want_cpu:
         cpu = None
     else:
-        cpu = bench_cpu_baseline(K, res["decode"]["first_tokens"] if "decode" in res else None)
-        log(f"cpu baseline: {cpu['value']:.2f} tok/s on one core (first tokens match the GPU: "
-            f"{cpu['first_tokens_match_gpu']})")
+        cpu = bench_cpu_baseline(K, decode_budget=args.cpu_budget, max_steps=args.cpu_steps, o3=o3)
+        log(f"cpu baseline: {cpu['value']:.2f} tok/s on one core ({cpu['tokens_compared']} tokens, all equal to "
+            f"the GPU's: {cpu['all_tokens_match_gpu']})")
 
     d, g, p = res.get("decode"), res.get("gemv"), res.get("prefill")
     line = {

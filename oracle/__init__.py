@@ -20,7 +20,11 @@ from dataclasses import dataclass
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "_build", "liboracle.so")
+# KERNRT_ORACLE_VARIANT=o3 loads the -O3 build of the same source (bench.py's
+# second CPU figure); the default is the -O2 build.
+VARIANT = os.environ.get("KERNRT_ORACLE_VARIANT", "")
+LIB_PATH = os.path.join(HERE, "_build", "liboracle_o3.so" if VARIANT == "o3" else "liboracle.so")
+LIB_PATHS = (os.path.join(HERE, "_build", "liboracle.so"), os.path.join(HERE, "_build", "liboracle_o3.so"))
 
 KIND = {"f32": 0, "bf16": 1, "q8_0": 2, "q8_0x4": 3}
 KIND_NAME = {v: k for k, v in KIND.items()}
@@ -34,8 +38,8 @@ SOURCES = ("oracle.cpp", "capi.cpp", "oracle.hpp", "Makefile")
 
 def build(force: bool = False) -> str:
     """Compile the oracle with its Makefile (g++, -O2 -ffp-contract=off)."""
-    stale = not os.path.exists(LIB_PATH) or any(
-        os.path.getmtime(os.path.join(HERE, s)) > os.path.getmtime(LIB_PATH) for s in SOURCES)
+    stale = any(not os.path.exists(p) or any(os.path.getmtime(os.path.join(HERE, s)) > os.path.getmtime(p)
+                                             for s in SOURCES) for p in LIB_PATHS)
     if force or stale:
         subprocess.run(["make", "-s", "-B" if force else "-s", "-C", HERE], check=True)
     return LIB_PATH

@@ -138,6 +138,41 @@ def gemv_algo_bytes(n: int, k: int) -> int:
     return n * k + n * nb * 4 + k + nb * 4 + n * 4
 
 
+def read_sweep(hip, big, big_n: int, sizes: dict, passes: int = 3):
+    """The bare streaming read (kr_stream_read_shape) of each launch size in
+    every shape: 1, 2, 4 or 8 16-byte loads per lane per round, one round
+    per workgroup or 256..2048 workgroups looping. Each size is read from
+    distinct offsets of a 2 GiB buffer, over 2x the 256 MB MALL per pass, so
+    the reads are cold as the decode pass's are; a pass is captured and
+    replayed like the GEMV's."""
+    out = {}
+    for key, b in sizes.items():
+        n4 = ((b + 15) // 16) * 4
+        launches = max(24, -(-(512 << 20) // (4 * n4)))
+        offs = [(i * n4) % (big_n - n4) // 4 * 4 for i in range(launches)]
+        rows = []
+        for cpl in (1, 2, 4, 8):
+            full = -(-n4 // (4 * 256 * cpl))
+            for wgs in (0, 256, 512, 1024, 2048):
+                if wgs >= full:
+                    continue
+                hip.capture_begin()
+                for off in offs:
+                    hip.stream_read(big, off, n4, cpl, wgs)
+                hip.capture_end()
+                hip.replay(1)
+                hip.synchronize()
+                hip.replay(1)
+                hip.timer_start()
+                hip.replay(passes)
+                us = hip.timer_stop() * 1e3 / (passes * launches)
+                rows.append(dict(chunks_per_lane=cpl, workgroups=wgs or full, us=round(us, 3),
+                                 gbs=round(4 * n4 / (us * 1e-6) / 1e9, 1)))
+        best = min(rows, key=lambda r: r["us"])
+        out[key] = dict(bytes=b, launches_per_pass=launches, best=best, shapes=rows)
+    return out
+
+
 def bench_gemv(K, reps: int = 3, use_graph: bool = True):
     """Q8_0 decode GEMVs (M = 1) at SmolLM2-1.7B shapes, launched as a decode
     step launches them: per layer the fused QKV (3 x 2048x2048, one launch),
@@ -264,6 +299,7 @@ def bench_gemv(K, reps: int = 3, use_graph: bool = True):
             reads()
     read_ms = hip.timer_stop()
     read_gbs = sum(read_sizes) * 4 * reps / (read_ms * 1e-3) / 1e9
+    sweep = read_sweep(hip, big, big_n, {key: b for key, (_, b) in kinds.items()}) if use_graph else None
     # per launch shape: time each kind alone over the same distinct matrices
     per_shape = {}
     for key, (count, b) in kinds.items():
@@ -306,8 +342,17 @@ def bench_gemv(K, reps: int = 3, use_graph: bool = True):
         hip.copy(src, 0, dst, 0, n_copy)
     copy_us = hip.timer_stop() * 1e3 / 10
     hip.close()
+    swept = None
+    if sweep:
+        # the pass read at each launch size's best shape: the ceiling the
+        # GEMV's launch sizes allow a read-only kernel
+        t_best = sum(cnt * sweep[key]["best"]["us"] for key, (cnt, _) in kinds.items())
+        swept = dict(gbs=round(sum(cnt * b for cnt, b in kinds.values()) / (t_best * 1e-6) / 1e9, 1),
+                     us_per_launch=round(t_best / sum(cnt for cnt, _ in kinds.values()), 3),
+                     per_size={key: v["best"] for key, v in sweep.items()})
     return dict(achieved_gbs=gbs, avg_launch_us=total_ms * 1e3 / total_launches,
                 read_ceiling_gbs=read_gbs, read_ceiling_us_per_launch=read_ms * 1e3 / total_launches,
+                swept_read_ceiling=swept, read_sweep=sweep,
                 bytes_per_launch=total_bytes / total_launches, launches_per_pass=len(group_a) + len(group_b),
                 bytes_per_pass=total_bytes // reps, per_shape=per_shape,
                 cfg1_1536x576_us=cfg1_us, cfg1_bytes=1_003_776,
@@ -752,6 +797,9 @@ def main():
                             "avg_launch_us": round(g["avg_launch_us"], 3),
                             "read_ceiling": round(g["read_ceiling_gbs"], 1),
                             "frac_of_read_ceiling": round(g["achieved_gbs"] / g["read_ceiling_gbs"], 4),
+                            "swept_read_ceiling": g["swept_read_ceiling"]["gbs"] if g["swept_read_ceiling"] else None,
+                            "frac_of_swept_read_ceiling": (round(g["achieved_gbs"] / g["swept_read_ceiling"]["gbs"], 4)
+                                                           if g["swept_read_ceiling"] else None),
                             "bytes_per_launch": round(g["bytes_per_launch"])}
         line["gemv"] = g
     if p:

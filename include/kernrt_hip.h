@@ -181,6 +181,13 @@ int kr_matmul_quantized_set(kr_ctx* ctx, const kr_mat* w, const kr_buf* y, int n
  * of 4): the practical ceiling of a read-dominated kernel of that size, for
  * benchmarks. No counterpart in the reference. */
 int kr_stream_read(kr_ctx* ctx, kr_buf src, size_t offset, size_t len);
+/* The same read with its shape chosen: chunks_per_lane 16-byte loads per
+ * lane per round (1, 2, 4, 8), on `workgroups` workgroups of 256 threads
+ * (0: as many as one round each needs; fewer loop over the data). Used to
+ * sweep for the best bare read of each launch size. kr_stream_read is
+ * chunks_per_lane 2, workgroups 0. */
+int kr_stream_read_shape(kr_ctx* ctx, kr_buf src, size_t offset, size_t len, int chunks_per_lane,
+                         size_t workgroups);
 
 /* An int8 MFMA throughput probe for benchmarks (no counterpart in the
  * reference): `workgroups` x 4 waves, each keeping four independent int8 MFMAs

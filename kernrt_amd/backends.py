@@ -373,9 +373,11 @@ class Hip:
         yb = (C.c_uint32 * n)(*ys)
         self._ck(self._L.kr_matmul_quantized_set(self.ctx, ws, yb, n, rows))
 
-    def stream_read(self, src: Buf, offset: int, n: int):
-        """Read n floats of src and discard them (a bandwidth reference)."""
-        self._ck(self._L.kr_stream_read(self.ctx, src, offset, n))
+    def stream_read(self, src: Buf, offset: int, n: int, chunks_per_lane: int = 2, workgroups: int = 0):
+        """Read n floats of src and discard them (a bandwidth reference):
+        chunks_per_lane 16-byte loads per lane per round on `workgroups`
+        workgroups (0: one round each)."""
+        self._ck(self._L.kr_stream_read_shape(self.ctx, src, offset, n, chunks_per_lane, workgroups))
 
     def capture_begin(self):
         """Record the following ops into one HIP graph instead of running them."""

@@ -1025,9 +1025,17 @@ int kr_matmul_quantized_set(kr_ctx* c, const kr_mat* w, const kr_buf* y, int n, 
 }
 
 int kr_stream_read(kr_ctx* c, kr_buf src, size_t offset, size_t len) {
+    return kr_stream_read_shape(c, src, offset, len, 2, 0);
+}
+
+int kr_stream_read_shape(kr_ctx* c, kr_buf src, size_t offset, size_t len, int chunks_per_lane,
+                         size_t workgroups) {
     BUF(s, src, offset + len);
     CHECK(c, offset % 4 == 0 && len % 4 == 0, "offset and length are multiples of 4 floats");
-    HIPCHK(c, kr::launch_stream_read(c->stream, s->p + offset, len, (int*)c->counter));
+    CHECK(c, chunks_per_lane == 1 || chunks_per_lane == 2 || chunks_per_lane == 4 || chunks_per_lane == 8,
+          "chunks per lane %d (1, 2, 4 or 8)", chunks_per_lane);
+    CHECK(c, workgroups <= (1u << 20), "workgroups %zu", workgroups);
+    HIPCHK(c, kr::launch_stream_read(c->stream, s->p + offset, len, (int*)c->counter, chunks_per_lane, workgroups));
     return KR_OK;
 }
 

@@ -2979,21 +2979,38 @@ hipError_t launch_copy(hipStream_t st, float* d, const float* s, size_t n) {
 }
 
 // A bare streaming read, the practical ceiling a read-dominated kernel of the
-// same size can reach: two 16-byte loads per lane, issued together, folded
-// into a value that is stored only if it matches an impossible pattern.
+// same size can reach: CPL 16-byte loads per lane per round, issued
+// together, over rounds of 256 CPL pieces per workgroup (a grid-stride loop
+// when the grid is smaller than the data), folded into a value that is
+// stored only if it matches an impossible pattern.
+template <int CPL>
 __global__ __launch_bounds__(256) void k_stream_read(const v4i* __restrict__ p, size_t n16, int* __restrict__ sink) {
-    const size_t i = (size_t)blockIdx.x * 512 + threadIdx.x;
-    const v4i a = __builtin_nontemporal_load(p + (i < n16 ? i : 0));
-    const v4i b = __builtin_nontemporal_load(p + (i + 256 < n16 ? i + 256 : 0));
-    const v4i c = a ^ b;
-    if (c.x == 0x7eadbeef && c.y == 0x1b2c3d4e && c.z == c.w) sink[0] = c.x;
+    v4i acc = {0, 0, 0, 0};
+    for (size_t base = (size_t)blockIdx.x * 256 * CPL; base < n16; base += (size_t)gridDim.x * 256 * CPL) {
+        v4i r[CPL];
+#pragma unroll
+        for (int c = 0; c < CPL; c++) {
+            const size_t i = base + (size_t)c * 256 + threadIdx.x;
+            r[c] = __builtin_nontemporal_load(p + (i < n16 ? i : 0));
+        }
+#pragma unroll
+        for (int c = 0; c < CPL; c++) acc ^= r[c];
+    }
+    if (acc.x == 0x7eadbeef && acc.y == 0x1b2c3d4e && acc.z == acc.w) sink[0] = acc.x;
 }
 
-hipError_t launch_stream_read(hipStream_t st, const float* p, size_t n, int* sink) {
+hipError_t launch_stream_read(hipStream_t st, const float* p, size_t n, int* sink, int cpl, size_t workgroups) {
     const size_t n16 = n / 4;
     if (n16 == 0) return hipSuccess;
-    hipLaunchKernelGGL(k_stream_read, dim3((unsigned)((n16 + 511) / 512)), dim3(256), 0, st, (const v4i*)p, n16,
-                       sink);
+    const size_t full = (n16 + 256 * (size_t)cpl - 1) / (256 * (size_t)cpl);
+    const dim3 grid((unsigned)(workgroups == 0 ? full : std::min(workgroups, full)));
+    switch (cpl) {
+        case 1: hipLaunchKernelGGL(k_stream_read<1>, grid, dim3(256), 0, st, (const v4i*)p, n16, sink); break;
+        case 2: hipLaunchKernelGGL(k_stream_read<2>, grid, dim3(256), 0, st, (const v4i*)p, n16, sink); break;
+        case 4: hipLaunchKernelGGL(k_stream_read<4>, grid, dim3(256), 0, st, (const v4i*)p, n16, sink); break;
+        case 8: hipLaunchKernelGGL(k_stream_read<8>, grid, dim3(256), 0, st, (const v4i*)p, n16, sink); break;
+        default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 

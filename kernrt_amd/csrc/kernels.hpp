@@ -131,8 +131,11 @@ hipError_t launch_mul(hipStream_t st, float* out, const float* a, const float* b
 hipError_t launch_mul_rows(hipStream_t st, float* o, size_t os, const float* a, size_t as, const float* b, size_t bs,
                            size_t rows, size_t n);
 hipError_t launch_copy(hipStream_t st, float* dst, const float* src, size_t n);
-// reads n floats (n % 4 == 0) and discards them; `sink` is never written in practice
-hipError_t launch_stream_read(hipStream_t st, const float* p, size_t n, int* sink);
+// reads n floats (n % 4 == 0) and discards them, cpl (1, 2, 4, 8) 16-byte
+// loads per lane per round, on `workgroups` workgroups of 256 (0: one round
+// each); `sink` is never written in practice
+hipError_t launch_stream_read(hipStream_t st, const float* p, size_t n, int* sink, int cpl = 2,
+                              size_t workgroups = 0);
 hipError_t launch_silu_mul(hipStream_t st, float* g, const float* u, size_t n);
 // causal depthwise conv of rows of x; history before row 0 is zero padding
 // (state null) or the ring `state` of k - 1 rows, oldest first

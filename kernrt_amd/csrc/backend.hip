@@ -1582,15 +1582,16 @@ int norm_swiglu(kr_ctx* c, size_t layer, kr_buf x, kr_buf add, kr_buf w, kr_buf 
     return KR_OK;
 }
 
-bool split_attention_ok(kr_ctx* c, const kr_attn_spec* sp) {
-    return sp && c->prepared && sp->seq_len == c->seq_len &&
-           kr::attention_split_ok(c->seq_len, sp->kv_mul, sp->head_size);
+bool split_attention_ok(kr_ctx* c, const kr_attn_spec* sp, size_t max_count) {
+    return sp && c->prepared && sp->seq_len == c->seq_len && max_count >= 1 && max_count <= c->seq_len &&
+           kr::attention_split_ok(max_count, sp->kv_mul, sp->head_size);
 }
 
 int rope_attention(kr_ctx* c, kr_buf q, kr_buf k, kr_buf v, kr_buf out, kr_buf att, size_t layer, size_t pos_host,
-                   const uint32_t* step_dev, const kr_attn_spec* sp, const kr_rope_spec* rs) {
+                   const uint32_t* step_dev, const kr_attn_spec* sp, const kr_rope_spec* rs, size_t dev_max_count) {
     CHECK(c, c->prepared && layer < c->n_layers, "layer %zu out of range", layer);
-    CHECK(c, split_attention_ok(c, sp) && sp->kv_dim == c->kv_dim && sp->n_heads % sp->kv_mul == 0,
+    const size_t cap = step_dev ? dev_max_count : pos_host + 1;
+    CHECK(c, split_attention_ok(c, sp, cap) && sp->kv_dim == c->kv_dim && sp->n_heads % sp->kv_mul == 0,
           "split decode attention does not apply to this geometry");
     CHECK(c, rs && rs->head_size == sp->head_size, "rope and attention head sizes differ");
     const size_t width = sp->n_heads * sp->head_size;
@@ -1607,11 +1608,11 @@ int rope_attention(kr_ctx* c, kr_buf q, kr_buf k, kr_buf v, kr_buf out, kr_buf a
     size_t max_count;
     int rc;
     if (step_dev) {  // window at step[1..4], position (== slot) at step[2]
-        rc = rope_table(c, rs->theta, rs->head_size, c->seq_len, &tab);
+        rc = rope_table(c, rs->theta, rs->head_size, cap, &tab);
         if (rc) return rc;
         wd = step_dev + 1;
         pd = step_dev + 2;
-        max_count = c->seq_len;
+        max_count = cap;
     } else {
         CHECK(c, pos_host < c->seq_len, "position %zu out of range", pos_host);
         rc = rope_table(c, rs->theta, rs->head_size, pos_host + 1, &tab);

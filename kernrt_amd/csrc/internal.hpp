@@ -91,11 +91,14 @@ int quant_project(kr_ctx* c, size_t layer, int proj, kr_buf x, kr_buf y, size_t 
 
 // Decode attention of one row as two launches that spread the cache reads
 // over many CUs, with rope of q and k and the kv_write of k and v folded in:
-// the same values as rope_kv + attention. Whether it applies to `spec`:
-bool split_attention_ok(kr_ctx* c, const kr_attn_spec* spec);
+// the same values as rope_kv + attention. Whether it applies to `spec` for
+// windows of up to max_count positions:
+bool split_attention_ok(kr_ctx* c, const kr_attn_spec* spec, size_t max_count);
 // window {0, pos, 0, 0} and position from the host (pos_host), or from the
-// device step record (step_dev: window at step[1..4], position at step[2])
+// device step record (step_dev: window at step[1..4], position at step[2],
+// the window at most dev_max_count positions: the launch is sized for it)
 int rope_attention(kr_ctx* c, kr_buf q, kr_buf k, kr_buf v, kr_buf out, kr_buf att, size_t layer, size_t pos_host,
-                   const uint32_t* step_dev, const kr_attn_spec* spec, const kr_rope_spec* rope);
+                   const uint32_t* step_dev, const kr_attn_spec* spec, const kr_rope_spec* rope,
+                   size_t dev_max_count);
 
 }  // namespace kri

@@ -51,6 +51,7 @@ struct krl_model {
     hipGraph_t graph = nullptr;  // one captured decode step
     hipGraphExec_t graph_exec = nullptr;
     uint64_t graph_epoch = 0;
+    size_t graph_cap = 0;  // the longest window the captured step serves
     bool fused = true;  // KERNRT_HIP_UNFUSED=1 runs the reference's op-by-op schedule
 };
 
@@ -177,12 +178,15 @@ Geometry geometry(const krl_config& c) {
 // of the projection that consumes them; the residual row then alternates
 // between two buffers, because that launch's workgroups all still read the
 // old row while one of them writes the new one.
-int decode_step_fused(krl_model* m, size_t token, size_t pos, bool dev) {
+// dev: the token, window and position come from the device step record, and
+// `cap` bounds the window (the launches are sized for it); else from the host.
+int decode_step_fused(krl_model* m, size_t token, size_t pos, bool dev, size_t cap) {
     kr_ctx* b = m->b;
     Geometry g = geometry(m->c);
     const uint32_t* s = m->step;
     const bool pro = kri::pro_fusable(g.dim) && kri::pro_fusable(g.q_dim);
-    const bool split = kri::split_attention_ok(b, &g.as);
+    const size_t wmax = dev ? cap : pos + 1;
+    const bool split = kri::split_attention_ok(b, &g.as, wmax);
     kr_buf X[2] = {m->x, m->x2};
     int cur = 0;
     if (dev)
@@ -218,7 +222,7 @@ int decode_step_fused(krl_model* m, size_t token, size_t pos, bool dev) {
             if (split && pro) {
                 // rope + kv_write + attention in two launches; O quantizes its input
                 KRC(m, kri::rope_attention(b, m->q, m->k, m->v, m->attn, m->att, l, pos, dev ? s : nullptr, &g.as,
-                                           &g.rs));
+                                           &g.rs, wmax));
                 KRC(m, kri::quant_project(b, l, KR_PROJ_O, m->attn, m->o, g.q_dim));
             } else {
                 KRC(m, kri::rope_kv(b, m->q, m->k, m->v, g.q_dim, g.kv_dim, 1, dev ? nullptr : positions,
@@ -272,8 +276,8 @@ int decode_step_fused(krl_model* m, size_t token, size_t pos, bool dev) {
 
 // One decode step, llama.rs:816-859 / lfm2.rs:414-474. With `dev`, the
 // token, position and window come from the device step record.
-int decode_step(krl_model* m, size_t token, size_t pos, bool dev) {
-    if (m->fused) return decode_step_fused(m, token, pos, dev);
+int decode_step(krl_model* m, size_t token, size_t pos, bool dev, size_t cap) {
+    if (m->fused) return decode_step_fused(m, token, pos, dev, cap);
     kr_ctx* b = m->b;
     Geometry g = geometry(m->c);
     const uint32_t* s = m->step;
@@ -522,14 +526,15 @@ int drop_graph(krl_model* m) {
     return KR_OK;
 }
 
-// Capture one device-driven decode step as a graph (kept until the backend
-// moves a buffer the captured kernels reference).
-int capture_step(krl_model* m) {
+// Capture one device-driven decode step as a graph for windows of up to
+// `cap` positions (kept until the backend moves a buffer the captured kernels
+// reference, or a generation needs a longer window).
+int capture_step(krl_model* m, size_t cap) {
     hipStream_t st = kri::stream(m->b);
     drop_graph(m);
     if (hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal) != hipSuccess)
         return fail(m, "graph capture could not start");
-    int rc = decode_step(m, 0, 0, true);
+    int rc = decode_step(m, 0, 0, true, cap);
     hipGraph_t graph = nullptr;
     hipError_t e = hipStreamEndCapture(st, &graph);
     if (rc != KR_OK) {
@@ -543,6 +548,7 @@ int capture_step(krl_model* m) {
     }
     m->graph = graph;
     m->graph_epoch = kri::epoch(m->b);
+    m->graph_cap = cap;
     return KR_OK;
 }
 
@@ -572,7 +578,7 @@ const char* krl_last_error(const krl_model* m) { return m ? m->err.c_str() : "no
 
 int krl_forward(krl_model* m, size_t token, size_t pos, float* logits) {
     if (pos >= m->c.seq_len) return fail(m, "position past the context length");
-    TRY(decode_step(m, token, pos, false));
+    TRY(decode_step(m, token, pos, false, pos + 1));
     KRC(m, kr_read(m->b, m->logits, logits, m->c.vocab_size));
     return KR_OK;
 }
@@ -682,20 +688,28 @@ int krl_generate_greedy(krl_model* m, size_t token, size_t pos, size_t n_steps, 
     if (hipMemcpyAsync(m->step, init, sizeof init, hipMemcpyHostToDevice, st) != hipSuccess ||
         hipStreamSynchronize(st) != hipSuccess)
         return fail(m, "step record upload failed");
+    // the window bucket: the smallest power of two from 512 covering the
+    // last step's window (pos + n_steps positions), at most the context, so
+    // that short generations on a long context take the split attention
+    const size_t need = pos + n_steps;
+    size_t cap = 512;
+    while (cap < need) cap *= 2;
+    cap = std::min(cap, (size_t)m->c.seq_len);
     size_t i = 0;
     if (use_graph) {
         // The first step runs eagerly when no valid graph exists: it performs
-        // every lazy allocation, so the capture records kernels only.
-        if (!m->graph_exec || m->graph_epoch != kri::epoch(m->b)) {
-            TRY(decode_step(m, 0, 0, true));
+        // every lazy allocation, so the capture records kernels only. A graph
+        // captured for a shorter window is replaced.
+        if (!m->graph_exec || m->graph_epoch != kri::epoch(m->b) || m->graph_cap < need) {
+            TRY(decode_step(m, 0, 0, true, cap));
             i = 1;
-            if (n_steps > 1) TRY(capture_step(m));
+            if (n_steps > 1) TRY(capture_step(m, cap));
         }
         hipError_t e = hipSuccess;
         for (; i < n_steps && e == hipSuccess; i++) e = hipGraphLaunch(m->graph_exec, st);
         if (e != hipSuccess) return fail(m, "graph launch failed");
     } else {
-        for (; i < n_steps; i++) TRY(decode_step(m, 0, 0, true));
+        for (; i < n_steps; i++) TRY(decode_step(m, 0, 0, true, cap));
     }
     KRC(m, kr_read_tokens(m->b, out_tokens, n_steps));
     return KR_OK;

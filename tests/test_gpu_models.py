@@ -289,3 +289,36 @@ def test_long_prefill_attention_on_the_matrix_core(n_heads, n_kv, hs, storage):
     assert_bits_equal(gpu.prefill(prompt[1100:], 1100), cpu.prefill(prompt[1100:], 1100), "chunk at 1100")
     for t in range(2):
         assert_bits_equal(gpu.forward(9 + t, 1250 + t), cpu.forward(9 + t, 1250 + t), f"decode at {1250 + t}")
+
+
+def test_greedy_graph_per_window_bucket():
+    # The captured step is sized for a window bucket (a power of two from 512
+    # covering the generation): three query heads per KV head on a 4100-slot
+    # context, where the whole-context step cannot take the split attention
+    # but the 512 and 1024 buckets do. Generations that stay in the captured
+    # bucket reuse its graph; one that needs more recaptures it.
+    c = O.Config(dim=384, hidden_dim=256, n_layers=1, n_heads=6, n_kv_heads=2, vocab_size=64, seq_len=4100,
+                 rms_eps=1e-5, rope_theta=1_000_000.0, rope_interleaved=False, head_dim=64)
+    ow = gaussian_weights(c, "q8_0x4", seed=77)
+    gpu, cpu = gpu_model(c, ow), O.Model(c, ow, "cpu")
+    prompt = [(i * 5 + 1) % c.vocab_size for i in range(16)]
+    assert_bits_equal(gpu.prefill(prompt, 0), cpu.prefill(prompt, 0), "prefill")
+    tok, pos = 3, len(prompt)
+    for n in (40, 500, 30):  # windows to 56 (bucket 512), to 556 (recaptured at 1024), to 586 (kept)
+        got = gpu.generate_greedy(tok, pos, n, use_graph=True)
+        want = _oracle_greedy(cpu, tok, pos, n)
+        assert list(got) == want, f"{n} steps from {pos}"
+        tok, pos = want[-1], pos + n
+
+
+def test_greedy_graph_past_the_split_attention_range():
+    # a window past 2048 positions at three query heads per KV head: the
+    # 4096 bucket (the whole context here) takes the general attention
+    c = O.Config(dim=384, hidden_dim=256, n_layers=1, n_heads=6, n_kv_heads=2, vocab_size=64, seq_len=4100,
+                 rms_eps=1e-5, rope_theta=1_000_000.0, rope_interleaved=False, head_dim=64)
+    ow = gaussian_weights(c, "q8_0x4", seed=78)
+    gpu, cpu = gpu_model(c, ow), O.Model(c, ow, "cpu")
+    prompt = [(i * 7 + 2) % c.vocab_size for i in range(2040)]
+    assert_bits_equal(gpu.prefill(prompt, 0), cpu.prefill(prompt, 0), "prefill")
+    got = gpu.generate_greedy(5, len(prompt), 60, use_graph=True)
+    assert list(got) == _oracle_greedy(cpu, 5, len(prompt), 60)

@@ -229,6 +229,15 @@ int kr_dbg_block_dots(kr_ctx* ctx, kr_mat w, kr_buf x, size_t rows, int32_t* out
  * this. groups <= 4096. No counterpart in the reference. */
 int kr_dbg_mfma_f32(kr_ctx* ctx, const float* a, const float* b, const float* acc, float* out, size_t groups);
 
+/* The serial f32 sum of each of `count` vectors of n non-negative values
+ * (values [count][n], n <= 2048): s = +0, s += v[i] in order, as the
+ * reference's RMS and softmax sums (cpu.rs:635-641, cpu.rs:575-630), by
+ * the kernels' parallel exact form over `waves` waves (1, 2, 4 or 16) and by the
+ * one-wave chain. out [count][5]: the parallel form's sum bits, 1 if it
+ * applied (else the kernels use the chain), the chain's sum bits, and the
+ * shader clocks each took. No counterpart in the reference. */
+int kr_dbg_serial_sum(kr_ctx* ctx, const float* values, size_t n, size_t count, int waves, uint32_t* out);
+
 /* A device matrix as stored: row-major int8 quants [out_dim][in_dim] and the
  * block scales [out_dim][in_dim/32] (f32 for Q8_0, f16 bits for Q8_0x4) --
  * so a host checker can rebuild the reference's Matrix from the very bytes a

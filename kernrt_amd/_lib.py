@@ -104,6 +104,7 @@ _SIGS = {
     "kr_dbg_quantize": (i32, [vp, u32, sz, sz, vp, vp, vp]),
     "kr_dbg_block_dots": (i32, [vp, u32, u32, sz, vp]),
     "kr_dbg_mfma_f32": (i32, [vp, vp, vp, vp, vp, sz]),
+    "kr_dbg_serial_sum": (i32, [vp, vp, sz, sz, i32, vp]),
     "kr_kv_upload": (i32, [vp, i32, sz, vp, sz]),
     "kr_kv_read": (i32, [vp, i32, sz, vp, sz]),
     "kr_matrix_read": (i32, [vp, u32, vp, sz, vp, sz]),

@@ -444,6 +444,18 @@ class Hip:
         self._ck(self._L.kr_dbg_mfma_f32(self.ctx, _p(a), _p(b), _p(acc), _p(out), a.shape[0]))
         return out
 
+    def dbg_serial_sum(self, values, waves: int = 1):
+        """kr_dbg_serial_sum: values [count, n] summed by the parallel exact
+        form over `waves` waves and by the chain -> (fast sums, fast applied,
+        chain sums, fast clocks, chain clocks), each [count]."""
+        v = np.ascontiguousarray(values, np.float32)
+        if v.ndim != 2:
+            raise ValueError("values must be [count, n]")
+        out = np.empty((v.shape[0], 5), np.uint32)
+        self._ck(self._L.kr_dbg_serial_sum(self.ctx, _p(v), v.shape[1], v.shape[0], waves, _p(out)))
+        return (out[:, 0].view(np.float32).copy(), out[:, 1].astype(bool), out[:, 2].view(np.float32).copy(),
+                out[:, 3].copy(), out[:, 4].copy())
+
     def matrix_shape(self, mat: int):
         """(storage, out_dim, in_dim) of a device matrix."""
         n, k, st = C.c_size_t(), C.c_size_t(), C.c_int()

@@ -1161,6 +1161,22 @@ int kr_dbg_mfma_f32(kr_ctx* c, const float* a, const float* b, const float* acc,
     return KR_OK;
 }
 
+int kr_dbg_serial_sum(kr_ctx* c, const float* values, size_t n, size_t count, int waves, uint32_t* out) {
+    CHECK(c, waves == 1 || waves == 2 || waves == 4 || waves == 16, "waves %d (1, 2, 4 or 16)", waves);
+    CHECK(c, n >= 1 && n <= 2048, "n %zu (1..2048)", n);
+    CHECK(c, count >= 1 && count <= 65536, "count %zu (1..65536)", count);
+    CHECK(c, values && out, "null operand");
+    int rc = ensure_tmp(c, n * count + 5 * count);
+    if (rc) return rc;
+    float* dx = (float*)c->tmp;
+    uint32_t* dout = (uint32_t*)(dx + n * count);
+    HIPCHK(c, hipMemcpyAsync(dx, values, n * count * sizeof(float), hipMemcpyHostToDevice, c->stream));
+    HIPCHK(c, kr::launch_serial_sum_probe(c->stream, dx, n, count, waves, dout));
+    HIPCHK(c, hipMemcpyAsync(out, dout, 5 * count * sizeof(uint32_t), hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    return KR_OK;
+}
+
 int kr_matrix_shape(kr_ctx* c, kr_mat w, size_t* out_dim, size_t* in_dim, int* storage) {
     Mat* m = mat_of(c, w);
     CHECK(c, m != nullptr, "unknown matrix %u", (unsigned)w);

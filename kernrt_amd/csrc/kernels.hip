@@ -293,6 +293,255 @@ __device__ __forceinline__ float wave_chain_sum(float* __restrict__ e, uint32_t 
     return runs ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), runs - 1)) : 0.0f;
 }
 
+// ---- exact serial sums, evaluated in parallel --------------------------------
+//
+// The reference's serial sums of non-negative terms (the RMS sum of squares,
+// the softmax sum of exponentials) are s_{k+1} = fl(s_k + a_k) from s_0 = +0.
+// wave_exact_sum gives the same bits without a chain of n dependent adds:
+//
+//   While s stays in one binade [2^e, 2^(e+1)) it is a multiple of that
+//   binade's ulp g = 2^(e-23), and so is each rounded result; then
+//   fl(s + a) = s + g * rne(a / g) unless a / g is exactly halfway between two
+//   integers (a tie, whose rounding depends on the last bit of s). So inside
+//   a binade the sum is s plus an exact integer sum of per-term roundings,
+//   which can be added in any order.
+//
+// The terms are split into segments of predicted binade: an approximate
+// prefix sum (f32, any order) predicts the binade of each partial sum s_{k+1};
+// a term whose predicted binade differs from its predecessor's (the sum
+// crosses a power of two there), or that is a tie in its binade's grid, is a
+// "special" term. Every other term contributes r_k = rne(a_k / g) to an
+// integer scan. Then one short chain over the specials in order does, per
+// special k: s += g * (sum of r over the segment before k) -- exact -- and
+// s = fl(s + a_k) on the vector unit, the reference's own rounding. Each
+// segment is verified exactly: its start is in the predicted binade and its
+// end below the binade's top (the sums are monotone, so every partial sum in
+// between is in the binade too, and every r_k used the right grid). If any
+// check fails, if a term is not finite, if there are more than 63 specials
+// or a term is too large for its grid, the function reports failure and the
+// caller runs the serial chain (wave_chain_sum). Binade 1 is merged with the
+// subnormals (the same ulp, 2^-149), so +0 starts in it.
+//
+// One wave holds the terms lane-major (lane L: terms L*VPL .. L*VPL+VPL-1):
+// two passes of ~17 vector operations per term over 64 lanes, two scans, and
+// a chain of ~10-20 specials read from their lanes, against n dependent adds
+// for the serial chain.
+// Inclusive wave scans (lane L gets the sum over lanes 0..L).
+__device__ __forceinline__ uint32_t wave_scan_u32(uint32_t x) {
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x111, 0xf, 0xf, false);  // row_shr:1
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x112, 0xf, 0xf, false);  // row_shr:2
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x114, 0xf, 0xf, false);  // row_shr:4
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x118, 0xf, 0xf, false);  // row_shr:8
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x142, 0xa, 0xf, false);  // row_bcast:15
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x143, 0xc, 0xf, false);  // row_bcast:31
+    return x;
+}
+__device__ __forceinline__ float wave_scan_f32(float x) {
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x111, 0xf, 0xf, false));
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x112, 0xf, 0xf, false));
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x114, 0xf, 0xf, false));
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x118, 0xf, 0xf, false));
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x142, 0xa, 0xf, false));
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x143, 0xc, 0xf, false));
+    return x;
+}
+
+// Binade bucket of a non-negative float: the biased exponent, with the
+// subnormals and +0 in bucket 1 (the grid of bucket b is 2^(b - 150)).
+__device__ __forceinline__ uint32_t xs_bucket(float p) { return max((uint32_t)__float_as_uint(p), 0x00800000u) >> 23; }
+
+// LDS scratch of one exact sum: the specials' steps in order (up to 64 and
+// the tail, then 8 no-op steps the chain may read past the last one), one
+// dump slot per lane for the branch-free compaction, the waves' totals.
+template <int W>
+struct XsScratch {
+    uint4 rec[72 + 64];
+    float wtot[W];
+    uint32_t wq[W], wc[W], wbad[W];
+};
+
+// e: 16-byte aligned LDS holding n <= 64 W VPL non-negative values, with
+// e[n .. round4(n)) == +0; xs: scratch private to this sum. W == 1: one wave
+// calls it (all 64 lanes); W > 1: every thread of the workgroup calls it
+// (three workgroup barriers) and waves 0..W-1 share the terms. The result is
+// valid in wave 0: true and the sum in `out`, or false, after which wave 0
+// runs the chain.
+template <int VPL, int W>
+__device__ __forceinline__ bool block_exact_sum(const float* __restrict__ e, uint32_t n, XsScratch<W>* __restrict__ xs,
+                                                float& out) {
+    static_assert(VPL % 4 == 0 && VPL <= 32 && (W & (W - 1)) == 0 && W <= 16, "values per lane, waves");
+    const uint32_t lane = threadIdx.x & 63, wave = W == 1 ? 0u : threadIdx.x >> 6;
+    const bool active = W == 1 || wave < (uint32_t)W;
+    const uint32_t n4 = (n + 3) & ~3u, k0 = (wave * 64 + lane) * VPL;
+    auto sync = [&]() {
+        if constexpr (W > 1) __syncthreads();
+        else __builtin_amdgcn_wave_barrier();
+    };
+    float v[VPL];
+#pragma unroll
+    for (int u = 0; u < VPL / 4; u++) {
+        const uint32_t k = k0 + 4 * u;
+        const bool in = active && k < n4;
+        const float4 f = *(const float4*)(e + (in ? k : 0));  // no branch; terms past n are zeros
+        v[4 * u] = in ? f.x : 0.0f, v[4 * u + 1] = in ? f.y : 0.0f;
+        v[4 * u + 2] = in ? f.z : 0.0f, v[4 * u + 3] = in ? f.w : 0.0f;
+    }
+    // pass 1: the lane's total and the approximate prefix before it
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < VPL; j++) acc += v[j];
+    const float incl = wave_scan_f32(acc);
+    float wbase = 0.0f, tot;
+    if constexpr (W > 1) {
+        if (lane == 63 && active) xs->wtot[wave] = incl;
+        __syncthreads();
+        tot = 0.0f;
+#pragma unroll
+        for (int w = 0; w < W; w++) {
+            if ((uint32_t)w == wave) wbase = tot;
+            tot += xs->wtot[w];
+        }
+    } else {
+        tot = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(incl), 63));
+    }
+    const float base = wbase + (incl - acc);
+    // the bucket before each lane's first term: the previous lane's last, as
+    // pass 2 computes it; +0 (bucket 1) before the first term; none before a
+    // wave's first term past wave 0 (which makes that term special), unless
+    // the wave holds only zeros past n (its constant bucket: no specials)
+    uint32_t ep = xs_bucket(base + acc);
+    const int ep0 = wave == 0 ? 1 : wave * 64 * VPL < n ? -1 : (int)xs_bucket(wbase);  // a wave of zeros: none
+    ep = (uint32_t)__builtin_amdgcn_update_dpp(ep0, (int)ep, 0x138, 0xf, 0xf, false);  // wave_shr:1
+    // pass 2: buckets, specials, per-term roundings and their lane prefix; a
+    // rounding is capped at 2^24 (a term that large fails its segment check)
+    uint32_t qv[VPL], bv[VPL / 4];
+    uint32_t q = 0, spec = 0;
+    float a2 = 0.0f;
+#pragma unroll
+    for (int j = 0; j < VPL; j++) {
+        a2 += v[j];
+        const uint32_t b = xs_bucket(base + a2);
+        const float x = __builtin_amdgcn_ldexpf(v[j], 150 - (int)b);
+        const float r = __builtin_rintf(x);
+        const bool sp = b != ep || fabsf(x - r) == 0.5f;
+        q += sp ? 0u : (uint32_t)fminf(r, 16777216.0f);
+        qv[j] = q;
+        if ((j & 3) == 0) bv[j >> 2] = 0;
+        bv[j >> 2] |= b << (8 * (j & 3));
+        spec |= (uint32_t)sp << j;
+        ep = b;
+    }
+    // a term not finite or a sum that overflows; a lane below 2^26 keeps a
+    // wave's integer scan below 2^32, a total below 2^31 keeps every prefix
+    // exact (a valid sum has at most 64 segments of less than 2^23 each)
+    const bool bad = !(tot < __builtin_huge_valf()) || q >= (1u << 26);
+    const uint32_t cnt = __builtin_popcount(spec);
+    const uint32_t rin = wave_scan_u32(q), cin = wave_scan_u32(cnt);
+    uint32_t qoff = 0, coff = 0, nspec, qtot;
+    bool anybad = __builtin_amdgcn_ballot_w64(bad) != 0;
+    if constexpr (W > 1) {
+        if (lane == 63 && active) xs->wq[wave] = rin, xs->wc[wave] = cin, xs->wbad[wave] = anybad ? 1u : 0u;
+        __syncthreads();
+        uint64_t q64 = 0;
+        uint32_t nb = 0;
+        nspec = 0;
+#pragma unroll
+        for (int w = 0; w < W; w++) {
+            if ((uint32_t)w == wave) qoff = (uint32_t)q64, coff = nspec;
+            q64 += xs->wq[w], nspec += xs->wc[w], nb |= xs->wbad[w];
+        }
+        anybad = nb != 0 || q64 >= (1ull << 31);
+        qtot = (uint32_t)q64;
+    } else {
+        nspec = __builtin_amdgcn_readlane(cin, 63), qtot = __builtin_amdgcn_readlane(rin, 63);
+        anybad |= qtot >= (1u << 31);
+    }
+    if (anybad || nspec > 63) return false;  // uniform over the workgroup
+    // the specials at their rank in term order: term index, integer prefix,
+    // the term's bucket (that of the segment after it), the term; the other
+    // terms go to the lane's dump slot (no branches)
+    if (active) {
+        uint32_t rank = coff + cin - cnt;
+        const uint32_t qb = qoff + rin - q;
+#pragma unroll
+        for (int j = 0; j < VPL; j++) {
+            const uint32_t sp = (spec >> j) & 1u;
+            xs->rec[sp ? rank : 72 + lane] =
+                make_uint4(k0 + j, qb + qv[j], (bv[j >> 2] >> (8 * (j & 3))) & 0xffu, __float_as_uint(v[j]));
+            rank += sp;
+        }
+    }
+    sync();
+    if (W > 1 && wave != 0) return false;
+    // step t (lane t): the segment before special t (from the previous
+    // special, or from +0 in bucket 1) and the special; step nspec: the tail
+    // segment, no term; later steps: no-ops. Step = (d, a, lo, top): s += d
+    // is the segment's exact sum, lo <= s and s + d <= top (the float below
+    // the bucket's end; the largest float for a no-op, so that an overflow
+    // fails) verify its bucket, then s = fl(s + a).
+    constexpr float kTopAll = 3.40282347e38f;
+    {
+        const uint4 cur = lane < nspec ? xs->rec[lane] : make_uint4(64u * W * VPL, qtot, 0u, 0u);
+        const uint4 prv = lane > 0 && lane <= nspec ? xs->rec[lane - 1] : make_uint4(0xffffffffu, 0u, 1u, 0u);
+        const uint32_t t = cur.y - prv.y, b = prv.z;
+        const bool ne = lane <= nspec && cur.x - prv.x > 1u;
+        float4 st;
+        st.x = ne ? __builtin_amdgcn_ldexpf((float)t, (int)b - 150) : 0.0f;
+        st.y = lane < nspec ? __uint_as_float(cur.w) : 0.0f;
+        st.z = ne && b > 1u ? __uint_as_float(b << 23) : 0.0f;
+        st.w = ne ? __uint_as_float(((b + 1u) << 23) - 1u) : kTopAll;
+        __builtin_amdgcn_wave_barrier();
+        ((float4*)xs->rec)[lane] = st;
+        if (lane < 8) ((float4*)xs->rec)[64 + lane] = make_float4(0.0f, 0.0f, 0.0f, kTopAll);
+    }
+    __builtin_amdgcn_wave_barrier();
+    // the chain, eight steps per LDS wait; the checks fold into
+    // m = min(s - lo, top - (s + d)) >= 0 (a difference of floats is negative
+    // exactly when the first is smaller)
+    float s = 0.0f, m = 1.0f;
+    for (uint32_t i0 = 0; i0 <= nspec; i0 += 8) {
+        float4 r8[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) r8[u] = ((const float4*)xs->rec)[i0 + u];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const float lo = s - r8[u].z;
+            s += r8[u].x;
+            m = fminf(m, fminf(lo, r8[u].w - s));
+            s += r8[u].y;
+        }
+    }
+    out = s;
+    return m >= 0.0f;
+}
+
+// The serial sum by the fast path where it applies, else by the chain (CVPL
+// values per lane) on wave 0. W > 1: every thread of the workgroup calls it;
+// the sum is valid in wave 0.
+template <int VPL, int W, int CVPL = 64>
+__device__ __forceinline__ float block_serial_sum(float* __restrict__ e, uint32_t n, XsScratch<W>* __restrict__ xs) {
+    float s = 0.0f;
+    if (n <= 64u * W * VPL) {
+        const bool ok = block_exact_sum<VPL, W>(e, n, xs, s);
+        if (W > 1 && (threadIdx.x >> 6) != 0) return 0.0f;
+        if (ok) return s;
+    } else if (W > 1 && (threadIdx.x >> 6) != 0) {
+        return 0.0f;
+    }
+    return n <= 64 * CVPL ? wave_chain_sum<CVPL>(e, n) : chain_sum(e, n);
+}
+
+// The RMS sum of squares (rms_norm_row, cpu.rs:635-641) in a workgroup of
+// four or more waves, shared by waves 0..3: sq (LDS) holds the dim squares
+// with sq[dim .. round4(dim)) == +0. Every thread calls it; the sum is valid
+// in wave 0.
+__device__ __forceinline__ float rms_sum4(float* __restrict__ sq, uint32_t dim) {
+    __shared__ XsScratch<4> xs;
+    if (dim <= 1024) return block_serial_sum<4, 4>(sq, dim, &xs);
+    if (dim <= 2048) return block_serial_sum<8, 4>(sq, dim, &xs);
+    return block_serial_sum<16, 4>(sq, dim, &xs);
+}
+
 // Lane k (0..3) of each quad, to every lane of the quad (DPP quad_perm).
 template <int K>
 __device__ __forceinline__ float quad_bcast(float v) {
@@ -476,13 +725,14 @@ static constexpr int PRO_NORM = 1, PRO_QUANT = 3;
 
 // The producer of k_gemv_pro / k_gemv_swiglu, after its inputs were loaded
 // into registers (va: the residual row or the f32 row, vb: the add, vw: the
-// norm weight): with PRO_NORM the residual add, the serial RMS sum on one
-// lane (rms_norm_row, cpu.rs:635-641) and out = w * (scale * x) (cpu.rs:643);
+// norm weight): with PRO_NORM the residual add, the serial RMS sum (in its
+// exact parallel form; rms_norm_row, cpu.rs:635-641) and out = w * (scale *
+// x) (cpu.rs:643);
 // then Q8Vec::quantize_into (quant.rs:864-873) of the row into LDS (xq, and
 // the scale values xsb: f16-rounded for the FMA-chain format, else f32), a block per 8
 // threads. Every thread of the workgroup calls this; the row is spread over
 // threads 0..255 (VPT float4 each), further threads only join the barriers.
-template <int SEM, int PRO, int VPT, int CVPL = 64>
+template <int SEM, int PRO, int VPT, int CVPL = 64, int NW = 4>
 __device__ __forceinline__ void gemv_produce(const GemvPro& pro, uint32_t K, float4 (&va)[VPT], const float4 (&vb)[VPT],
                                              const float4 (&vw)[VPT], int8_t* xq, uint32_t* xsb, float* scratch,
                                              float* s_scale_p) {
@@ -502,8 +752,18 @@ __device__ __forceinline__ void gemv_produce(const GemvPro& pro, uint32_t K, flo
             }
         }
         __syncthreads();
-        if (tid < 64) {  // rms_norm_row (cpu.rs:635-641): the serial sum on wave 0
-            float ss = K <= 64 * CVPL ? wave_chain_sum<CVPL>(scratch, K) : chain_sum(scratch, K);
+        // rms_norm_row (cpu.rs:635-641): the serial sum of the squares in its
+        // exact parallel form over the workgroup's NW waves (the chain on
+        // wave 0 where that does not apply); every thread takes part in its
+        // barriers
+        __shared__ XsScratch<NW> xs;
+        float ss = 0.0f;
+        if constexpr (NW >= 16) {
+            ss = block_serial_sum<4, NW, CVPL>(scratch, K, &xs);
+        } else {
+            ss = K <= 1024 ? block_serial_sum<4, NW, CVPL>(scratch, K, &xs) : block_serial_sum<8, NW, CVPL>(scratch, K, &xs);
+        }
+        if (tid < 64) {
             ss = div_rn(ss, (float)K);
             ss += pro.eps;
             if (tid == 0) *s_scale_p = div_rn(1.0f, sqrt_rn(ss));
@@ -775,7 +1035,7 @@ __global__ __launch_bounds__(kSwigluThreads) void k_gemv_swiglu(MatSet ms, GemvP
     if (tid < 32) etab[tid] = etv;  // read after the producer's barriers
     // 3. the producer, while the weights are in flight
     // with eight chunks per thread in flight the chain holds 32 values a lane
-    gemv_produce<SEM, PRO_NORM, VPT, CPT >= 8 ? 32 : 64>(pro, K, va, vb, vw, xq, xsb, scratch, &s_scale);
+    gemv_produce<SEM, PRO_NORM, VPT, CPT >= 8 ? 32 : 64, 4>(pro, K, va, vb, vw, xq, xsb, scratch, &s_scale);
 
     // 4. block dots against the LDS row, the epilogue operands to LDS
     const uint32_t per = gemv_out_floats(SEM, nb), q4p = gemv_q4p(nb);
@@ -1096,8 +1356,8 @@ hipError_t launch_project(hipStream_t st, int sem, const DevMatrix& w, QuantAct 
 }
 
 // ---------------------------------------------------------------------------
-// RMSNorm (cpu.rs:633-644): ss is a left-to-right f32 sum of x*x, so squares
-// are formed in parallel and one lane adds them in order.
+// RMSNorm (cpu.rs:633-644): ss is a left-to-right f32 sum of x*x; the squares
+// are formed in parallel and summed by rms_sum4 with the same bits.
 __global__ __launch_bounds__(256) void k_rms_norm(float* __restrict__ out, const float* __restrict__ x,
                                                   const float* __restrict__ w, uint32_t dim, float eps) {
     extern __shared__ __align__(16) float sq[];
@@ -1108,9 +1368,10 @@ __global__ __launch_bounds__(256) void k_rms_norm(float* __restrict__ out, const
         float v = xr[i];
         sq[i] = v * v;
     }
+    if (threadIdx.x < ((dim + 3) & ~3u) - dim) sq[dim + threadIdx.x] = 0.0f;
     __syncthreads();
-    if (threadIdx.x < 64) {  // the register chain across wave 0 where dim allows
-        float ss = dim <= 64 * 64 ? wave_chain_sum(sq, dim) : chain_sum(sq, dim);
+    float ss = rms_sum4(sq, dim);  // the sum in its exact parallel form
+    if (threadIdx.x < 64) {
         ss = div_rn(ss, (float)dim);
         ss += eps;
         if (threadIdx.x == 0) s_scale = div_rn(1.0f, sqrt_rn(ss));
@@ -2755,11 +3016,10 @@ __global__ __launch_bounds__(256) void k_add_rms_quant(float* __restrict__ x, co
         }
     }
     __syncthreads();
+    // rms_norm_row (cpu.rs:635-641): ss = sum of squares left to right (in its
+    // exact parallel form), ss /= dim, ss += eps, scale = 1 / sqrt(ss)
+    float ss = rms_sum4(sq, dim);
     if (tid < 64) {
-        // rms_norm_row (cpu.rs:635-641): ss = sum of squares left to right,
-        // ss /= dim, ss += eps, scale = 1 / sqrt(ss); the sum as the
-        // register chain across wave 0 where dim allows
-        float ss = dim <= 64 * 64 ? wave_chain_sum(sq, dim) : chain_sum(sq, dim);
         ss = div_rn(ss, (float)dim);
         ss += eps;
         if (tid == 0) s_scale = div_rn(1.0f, sqrt_rn(ss));
@@ -2997,6 +3257,59 @@ __global__ __launch_bounds__(256) void k_stream_read(const v4i* __restrict__ p, 
         for (int c = 0; c < CPL; c++) acc ^= r[c];
     }
     if (acc.x == 0x7eadbeef && acc.y == 0x1b2c3d4e && acc.z == acc.w) sink[0] = acc.x;
+}
+
+// One wave per vector of n values: the serial sum by wave_exact_sum and by
+// the chain, with the shader clocks each took (a test and timing probe).
+// out[5 g ..]: fast-path sum bits, 1 if the fast path applied, chain sum
+// bits, clocks of the fast path, clocks of the chain.
+template <int VPL, int W>
+__global__ __launch_bounds__(64 * W) void k_serial_sum_probe(const float* __restrict__ x, uint32_t n,
+                                                             uint32_t* __restrict__ out) {
+    __shared__ __align__(16) float e[64 * 32 + 4];
+    __shared__ XsScratch<W> xs;
+    const uint32_t g = blockIdx.x, tid = threadIdx.x;
+    for (uint32_t i = tid; i < n; i += 64 * W) e[i] = x[(size_t)g * n + i];
+    if (tid < 4) e[n + tid] = 0.0f;
+    __syncthreads();
+    float fast = 0.0f;
+    const uint64_t t0 = __builtin_amdgcn_s_memtime();
+    const bool ok = block_exact_sum<VPL, W>(e, n, &xs, fast);
+    const uint64_t t1 = __builtin_amdgcn_s_memtime();
+    if (tid < 64) {
+        const float chain = wave_chain_sum(e, n);
+        const uint64_t t2 = __builtin_amdgcn_s_memtime();
+        if (tid == 0) {
+            out[5 * g] = __float_as_uint(fast);
+            out[5 * g + 1] = ok ? 1u : 0u;
+            out[5 * g + 2] = __float_as_uint(chain);
+            out[5 * g + 3] = (uint32_t)(t1 - t0);
+            out[5 * g + 4] = (uint32_t)(t2 - t1);
+        }
+    }
+}
+
+hipError_t launch_serial_sum_probe(hipStream_t st, const float* x, size_t n, size_t count, int waves,
+                                   uint32_t* out) {
+    if (n == 0 || n > 2048 || count == 0) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)count);
+#define KR_SSP(V, W) hipLaunchKernelGGL((k_serial_sum_probe<V, W>), grid, dim3(64 * W), 0, st, x, (uint32_t)n, out)
+    if (waves == 1) {
+        if (n <= 1024) KR_SSP(16, 1);
+        else KR_SSP(32, 1);
+    } else if (waves == 2) {
+        if (n <= 1024) KR_SSP(8, 2);
+        else KR_SSP(16, 2);
+    } else if (waves == 4) {
+        if (n <= 1024) KR_SSP(4, 4);
+        else KR_SSP(8, 4);
+    } else if (waves == 16) {
+        KR_SSP(4, 16);
+    } else {
+        return hipErrorInvalidValue;
+    }
+#undef KR_SSP
+    return hipGetLastError();
 }
 
 hipError_t launch_stream_read(hipStream_t st, const float* p, size_t n, int* sink, int cpl, size_t workgroups) {

@@ -134,6 +134,8 @@ hipError_t launch_copy(hipStream_t st, float* dst, const float* src, size_t n);
 // reads n floats (n % 4 == 0) and discards them, cpl (1, 2, 4, 8) 16-byte
 // loads per lane per round, on `workgroups` workgroups of 256 (0: one round
 // each); `sink` is never written in practice
+hipError_t launch_serial_sum_probe(hipStream_t st, const float* x, size_t n, size_t count, int waves,
+                                   uint32_t* out);
 hipError_t launch_stream_read(hipStream_t st, const float* p, size_t n, int* sink, int cpl = 2,
                               size_t workgroups = 0);
 hipError_t launch_silu_mul(hipStream_t st, float* g, const float* u, size_t n);

@@ -121,6 +121,12 @@ struct kr_ctx {
     float* ws = nullptr;
     uint16_t* wh = nullptr;
     size_t cap_q = 0, cap_s = 0;
+    // a second one: SiLU(gate) * up quantized by the gate/up GEMM while that
+    // GEMM still reads the first
+    int8_t* wq2 = nullptr;
+    float* ws2 = nullptr;
+    uint16_t* wh2 = nullptr;
+    size_t cap_q2 = 0, cap_s2 = 0;
     float* tmp = nullptr;
     size_t cap_tmp = 0;
     IdxStage st_pos, st_slots, st_win, st_tok;
@@ -200,6 +206,27 @@ int ensure_workspace(kr_ctx* c, size_t rows, size_t k) {
         HIPCHK(c, hipMalloc(&c->ws, ns * sizeof(float)));
         HIPCHK(c, hipMalloc(&c->wh, ns * sizeof(uint16_t)));
         c->cap_s = ns;
+    }
+    return KR_OK;
+}
+
+static int ensure_workspace2(kr_ctx* c, size_t rows, size_t k) {
+    const size_t nq = rows * k, ns = rows * (k / 32);
+    if (nq > c->cap_q2 || ns > c->cap_s2) c->epoch++;
+    if (nq > c->cap_q2) {
+        if (c->wq2) HIPCHK(c, hipFree(c->wq2));
+        c->wq2 = nullptr;
+        HIPCHK(c, hipMalloc(&c->wq2, nq));
+        c->cap_q2 = nq;
+    }
+    if (ns > c->cap_s2) {
+        if (c->ws2) HIPCHK(c, hipFree(c->ws2));
+        if (c->wh2) HIPCHK(c, hipFree(c->wh2));
+        c->ws2 = nullptr;
+        c->wh2 = nullptr;
+        HIPCHK(c, hipMalloc(&c->ws2, ns * sizeof(float)));
+        HIPCHK(c, hipMalloc(&c->wh2, ns * sizeof(uint16_t)));
+        c->cap_s2 = ns;
     }
     return KR_OK;
 }
@@ -512,7 +539,8 @@ void kr_close(kr_ctx* c) {
     free_stage(c->st_slots);
     free_stage(c->st_win);
     free_stage(c->st_tok);
-    void* ptrs[] = {c->kc, c->vc, c->wq, c->ws, c->wh, c->tmp, c->tokens, c->counter, c->attn_scratch};
+    void* ptrs[] = {c->kc, c->vc, c->wq, c->ws, c->wh, c->wq2, c->ws2, c->wh2, c->tmp, c->tokens, c->counter,
+                    c->attn_scratch};
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
     if (c->t0) (void)hipEventDestroy(c->t0);
@@ -1359,6 +1387,36 @@ int project_q(kr_ctx* c, size_t layer, const int* projs, const kr_buf* ys, int n
             HIPCHK(c, kr::launch_project(c->stream, sem_for_project(*ms[i]), *ms[i], act(c), rows, yp[i], ms[i]->n,
                                          nullptr));
     }
+    return KR_OK;
+}
+
+// The FFN of a prefill batch after the norm's quantization (the workspace
+// holds `rows` rows of in_dim): gate and up as one Q8_0 GEMM whose epilogue
+// forms h = SiLU(gate) * up and h's Q8 blocks (silu_quant's arithmetic) into
+// the second workspace, then down from there into `out` -- the bits of
+// project_q(gate, up), silu_quant and project_q(down), one launch fewer and
+// no f32 gate/up round trip. The workspace still holds the norm's rows after.
+bool ffn_swiglu_ok(kr_ctx* c, size_t layer, size_t rows) {
+    if (!c->prepared || layer >= c->n_layers || rows < 8) return false;
+    const Mat* g = proj_mat(c, layer, KR_PROJ_GATE);
+    const Mat* u = proj_mat(c, layer, KR_PROJ_UP);
+    const Mat* d = proj_mat(c, layer, KR_PROJ_DOWN);
+    return g && u && d && g->m.storage == KR_STORAGE_Q8_0 && u->m.storage == KR_STORAGE_Q8_0 &&
+           g->m.n == u->m.n && g->m.k == u->m.k && g->m.n % 32 == 0 && d->m.k == g->m.n &&
+           sem_for_project(g->m) == kr::SEM_FOUR_PARTIALS_F32 && rows <= c->q_rows && g->m.k == c->q_width;
+}
+
+int ffn_swiglu_down(kr_ctx* c, size_t layer, size_t rows, kr_buf out) {
+    CHECK(c, ffn_swiglu_ok(c, layer, rows), "the fused gate/up + SiLU GEMM does not apply to layer %zu", layer);
+    const Mat* g = proj_mat(c, layer, KR_PROJ_GATE);
+    const Mat* u = proj_mat(c, layer, KR_PROJ_UP);
+    const Mat* d = proj_mat(c, layer, KR_PROJ_DOWN);
+    BUF(ob, out, rows * d->m.n);
+    int rc = ensure_workspace2(c, rows, g->m.n);
+    if (rc) return rc;
+    HIPCHK(c, kr::launch_gate_up_silu_q8(c->stream, g->m, u->m, act(c), rows, c->wq2, c->ws2, c->wh2));
+    HIPCHK(c, kr::launch_project(c->stream, sem_for_project(d->m), d->m, kr::QuantAct{c->wq2, c->ws2, c->wh2}, rows,
+                                 ob->p, d->m.n, nullptr));
     return KR_OK;
 }
 

@@ -36,6 +36,7 @@
 // four, else through LDS) and are summed as ((t0 + t1) + t2) + t3.
 #include <hip/hip_runtime.h>
 
+#include "kernrt_hip.h"
 #include "device.hpp"
 #include "kernels.hpp"
 #include "numerics.hpp"
@@ -54,23 +55,37 @@ __device__ __forceinline__ uint32_t gemm_xcd_tile(uint32_t id, uint32_t count) {
     return xcd < rem ? xcd * (per + 1) + k : rem * (per + 1) + (xcd - rem) * per + k;
 }
 
-template <int SEM, int TM, int TN, int NJ, int CPW, int KC, int NS, int RS, int WPE, bool DBG>
+// SWI: the gate/up launch of a SwiGLU FFN with SiLU(gate) * up and its Q8
+// blocks as the epilogue (silu_quant's arithmetic, elementwise.rs / quant.rs:
+// 864-873): the tile's 64 columns are gate rows 32 t .. 32 t + 31 (ms.q[0])
+// and up rows 32 t .. 32 t + 31 (ms.q[1]) of the same hidden block t, and the
+// outputs are h's int8 quants and block scales in `so` instead of f32 gate/up.
+struct SwiOut {
+    int8_t* q;
+    float* s;
+    uint16_t* h;
+};
+
+template <int SEM, int TM, int TN, int NJ, int CPW, int KC, int NS, int RS, int WPE, bool DBG, bool SWI = false>
 __global__ __launch_bounds__(64 * (TM / 32) * (TN / (32 * NJ)) * (4 / CPW), WPE) void k_gemm_q8(
-    MatSet ms, QuantAct x, uint32_t M, uint32_t K, uint32_t mtiles, int32_t* __restrict__ dbg) {
+    MatSet ms, QuantAct x, uint32_t M, uint32_t K, uint32_t mtiles, int32_t* __restrict__ dbg, SwiOut so) {
     constexpr int WN = 32 * NJ, SM = TM / 32, NSUB = SM * (TN / WN), CG = 4 / CPW, NT = 64 * NSUB * CG;
     constexpr int ROW = KC * 32 + 16, PPR = KC * 2;
     constexpr int A_BYTES = TM * ROW, B_BYTES = TN * ROW;
     constexpr int BUF_BYTES = A_BYTES + B_BYTES + KC * (TM + TN) * 4;
     constexpr int PART_BYTES = CPW == 4 ? 0 : 4 * TM * TN * 4;
-    constexpr int LDS_BYTES = 3 * BUF_BYTES > PART_BYTES ? 3 * BUF_BYTES : PART_BYTES;
+    constexpr int RING_BYTES = 3 * BUF_BYTES > PART_BYTES ? 3 * BUF_BYTES : PART_BYTES;
+    constexpr int LDS_BYTES = RING_BYTES + (SWI ? 32 * 8 : 0);  // + the exp table
     constexpr int NQ = (TM + TN) * PPR, NP = (NQ + NT - 1) / NT;  // 16-byte pieces per chunk, per thread
     constexpr int NSC = ((TM + TN) * KC + NT - 1) / NT;         // scales per thread per chunk
     static_assert(TM % 32 == 0 && TN % WN == 0 && KC % (NJ == 2 || CPW >= 2 ? 4 : 8) == 0, "tile shape");
     static_assert(NJ == 1 || NJ == 2, "unit columns per wave");
     static_assert(CPW == 1 || CPW == 2 || CPW == 4, "chains per wave");
     static_assert(NT % PPR == 0, "a thread's pieces share their column");
+    static_assert(!SWI || (TN == 64 && NJ == 2 && CPW < 4), "the SwiGLU epilogue needs one gate and one up unit per wave");
     constexpr bool WF16 = SEM == SEM_FOUR_PARTIALS_F16;
     __shared__ __align__(16) int8_t lds[LDS_BYTES];
+    uint64_t* const etab = (uint64_t*)(lds + RING_BYTES);
     auto sA = [&](int buf) { return lds + buf * BUF_BYTES; };
     auto sB = [&](int buf) { return lds + buf * BUF_BYTES + A_BYTES; };
     auto sX = [&](int buf) { return (float*)(lds + buf * BUF_BYTES + A_BYTES + B_BYTES); };  // [block][row]
@@ -79,12 +94,13 @@ __global__ __launch_bounds__(64 * (TM / 32) * (TN / (32 * NJ)) * (4 / CPW), WPE)
     const uint32_t nb = K >> 5, nchunks = (nb + KC - 1) / KC;
     const uint32_t L = gemm_xcd_tile(blockIdx.x, gridDim.x);
     const uint32_t mt = L % mtiles, nt = L / mtiles;
-    const int mi_ = nt < ms.tile_end[0] ? 0 : (nt < ms.tile_end[1] ? 1 : 2);
-    const uint32_t m0 = mt * TM, n0 = (nt - (mi_ == 0 ? 0 : ms.tile_end[mi_ - 1])) * TN;
+    const int mi_ = SWI ? 0 : nt < ms.tile_end[0] ? 0 : (nt < ms.tile_end[1] ? 1 : 2);
+    const uint32_t m0 = mt * TM, n0 = SWI ? nt * 32 : (nt - (mi_ == 0 ? 0 : ms.tile_end[mi_ > 0 ? mi_ - 1 : 0])) * TN;
     const int8_t* __restrict__ W = ms.q[mi_];
     const void* __restrict__ WS = ms.s[mi_];
     const uint32_t N = ms.n[mi_];
     const uint32_t tid = threadIdx.x, lane = tid & 63, r32 = lane & 31, half = lane >> 5;
+    if (SWI && tid < 32) etab[tid] = kExp2Tab[tid];  // read after the loop's barriers
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t cg = wave % CG, sub = wave / CG;                // chains cg*CPW .. +CPW-1
     const uint32_t wm0 = (sub % SM) * 32, wn0 = (sub / SM) * WN;  // the wave's sub-tile
@@ -100,7 +116,11 @@ __global__ __launch_bounds__(64 * (TM / 32) * (TN / (32 * NJ)) * (4 / CPW), WPE)
     for (int i = 0; i < NP; i++) {
         const uint32_t q = min(tid + NT * i, (uint32_t)NQ - 1), isb = q >= PPR * TM;
         const uint32_t row = (isb ? q - PPR * TM : q) / PPR;
-        gp[i] = isb ? W + (size_t)min(n0 + row, N - 1) * K : x.q + (size_t)min(m0 + row, M - 1) * K;
+        if (SWI)  // B rows 0..31: gate, 32..63: up, of the hidden block's rows
+            gp[i] = isb ? (row >= 32 ? ms.q[1] : ms.q[0]) + (size_t)min(n0 + (row & 31), N - 1) * K
+                        : x.q + (size_t)min(m0 + row, M - 1) * K;
+        else
+            gp[i] = isb ? W + (size_t)min(n0 + row, N - 1) * K : x.q + (size_t)min(m0 + row, M - 1) * K;
         lp[i] = (isb ? A_BYTES : 0) + row * ROW + (q % PPR) * 16;
     }
     const uint32_t pc = (tid % PPR) * 16;
@@ -122,7 +142,11 @@ __global__ __launch_bounds__(64 * (TM / 32) * (TN / (32 * NJ)) * (4 / CPW), WPE)
                 st.sc[i] = f2u(x.s[(size_t)min(m0 + sidx / KC, M - 1) * nb + blk]);
             } else if (sidx < KC * (TM + TN)) {
                 const uint32_t col2 = (sidx - KC * TM) / KC;
-                st.sc[i] = scale_bits(WF16, WS, (size_t)min(n0 + col2, N - 1) * nb + blk);
+                if (SWI)
+                    st.sc[i] = scale_bits(WF16, col2 >= 32 ? ms.s[1] : ms.s[0],
+                                          (size_t)min(n0 + (col2 & 31), N - 1) * nb + blk);
+                else
+                    st.sc[i] = scale_bits(WF16, WS, (size_t)min(n0 + col2, N - 1) * nb + blk);
             }
         }
     };
@@ -317,6 +341,36 @@ __global__ __launch_bounds__(64 * (TM / 32) * (TN / (32 * NJ)) * (4 / CPW), WPE)
                     part[(((cg * CPW + c2) * NSUB + sub) * WOUT) / 4 + (j * 4 + v4) * 64 + lane] =
                         float4{t[c2][j][4 * v4], t[c2][j][4 * v4 + 1], t[c2][j][4 * v4 + 2], t[c2][j][4 * v4 + 3]};
         __syncthreads();
+        auto sum4 = [&](uint32_t o4) {
+            const float4 p0 = part[o4], p1 = part[TM * TN / 4 + o4], p2 = part[2 * TM * TN / 4 + o4];
+            const float4 p3 = part[3 * TM * TN / 4 + o4];
+            return float4{((p0.x + p1.x) + p2.x) + p3.x, ((p0.y + p1.y) + p2.y) + p3.y,
+                          ((p0.z + p1.z) + p2.z) + p3.z, ((p0.w + p1.w) + p2.w) + p3.w};
+        };
+        if constexpr (SWI) {
+            // element e: (sub, v4, lane): rows 8 v4 + 4 (lane / 32) + 0..3 of
+            // hidden column n0 + lane % 32, its gate (unit 0) and up (unit 1);
+            // the 32 lanes of a half-wave hold one row's Q8 block
+            const uint32_t nbh = N >> 5;
+#pragma unroll
+            for (int k = 0; k < TM * 8 / NT; k++) {
+                const uint32_t e = tid + NT * k, sb = e >> 8, v4 = (e >> 6) & 3, l = e & 63;
+                const uint32_t og = sb * (WOUT / 4) + v4 * 64 + l;
+                const float4 g4 = sum4(og), u4 = sum4(og + 256);
+                const float gv[4] = {g4.x, g4.y, g4.z, g4.w}, uv[4] = {u4.x, u4.y, u4.z, u4.w};
+                const uint32_t mb = m0 + (sb % SM) * 32 + 8 * v4 + 4 * (l >> 5), col = n0 + (l & 31);
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const bool live = mb + r < M;
+                    // cpu.rs:708-710: silu(g) * u
+                    const float h = div_rn(gv[r], 1.0f + glibc_expf(-gv[r], etab)) * uv[r];
+                    const size_t oi = (size_t)(live ? mb + r : 0) * N + col;
+                    quant_lane(h, live, so.q + oi, so.s + (size_t)(live ? mb + r : 0) * nbh + (n0 >> 5),
+                               so.h + (size_t)(live ? mb + r : 0) * nbh + (n0 >> 5));
+                }
+            }
+            return;
+        }
         // element o4 of a plane: (sub, j, v4, lane), the 4 outputs rows
         // 8 v4 + 4 (lane / 32) + 0..3 of column lane % 32
 #pragma unroll
@@ -348,10 +402,19 @@ static void launch_q8(hipStream_t st, MatSet ms, QuantAct x, size_t rows, size_t
     const dim3 grid(total * mtiles), block(64 * (TM / 32) * (TN / (32 * NJ)) * (4 / CPW));
     if (dbg)
         hipLaunchKernelGGL((k_gemm_q8<SEM, TM, TN, NJ, CPW, KC, NS, RS, WPE, true>), grid, block, 0, st, ms, x,
-                           (uint32_t)rows, (uint32_t)k, mtiles, dbg);
+                           (uint32_t)rows, (uint32_t)k, mtiles, dbg, SwiOut{});
     else
         hipLaunchKernelGGL((k_gemm_q8<SEM, TM, TN, NJ, CPW, KC, NS, RS, WPE, false>), grid, block, 0, st, ms, x,
-                           (uint32_t)rows, (uint32_t)k, mtiles, dbg);
+                           (uint32_t)rows, (uint32_t)k, mtiles, dbg, SwiOut{});
+}
+
+// The SwiGLU form: one tile per (row block, hidden block of 32).
+template <int TM, int NJ, int CPW, int KC, int NS, int RS, int WPE>
+static void launch_q8_swi(hipStream_t st, const MatSet& ms, QuantAct x, size_t rows, size_t k, SwiOut so) {
+    const uint32_t mtiles = (uint32_t)((rows + TM - 1) / TM), ntiles = ms.n[0] / 32;
+    const dim3 grid(ntiles * mtiles), block(64 * (TM / 32) * (64 / (32 * NJ)) * (4 / CPW));
+    hipLaunchKernelGGL((k_gemm_q8<SEM_FOUR_PARTIALS_F32, TM, 64, NJ, CPW, KC, NS, RS, WPE, false, true>), grid, block,
+                       0, st, ms, x, (uint32_t)rows, (uint32_t)k, mtiles, nullptr, so);
 }
 
 // The narrow form (few column tiles: o and down at N = 2048), on 16x16x32
@@ -613,6 +676,25 @@ __global__ __launch_bounds__(64) void k_mfma_f32_probe(const float* __restrict__
 hipError_t launch_mfma_f32_probe(hipStream_t st, const float* a, const float* b, const float* c, float* out,
                                  size_t groups) {
     hipLaunchKernelGGL(k_mfma_f32_probe, dim3((unsigned)groups), dim3(64), 0, st, a, b, c, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_gate_up_silu_q8(hipStream_t st, const DevMatrix& gate, const DevMatrix& up, QuantAct x, size_t rows,
+                                  int8_t* hq, float* hs, uint16_t* hh) {
+    if (gate.storage != KR_STORAGE_Q8_0 || up.storage != KR_STORAGE_Q8_0 || gate.n != up.n || gate.k != up.k ||
+        gate.n % 32 != 0 || rows == 0)
+        return hipErrorInvalidValue;
+    MatSet ms{};
+    ms.q[0] = gate.q, ms.q[1] = up.q;
+    ms.s[0] = gate.s, ms.s[1] = up.s;
+    ms.n[0] = ms.n[1] = (uint32_t)gate.n;
+    ms.count = 2;
+    const SwiOut so{hq, hs, hh};
+    const size_t m128 = (rows + 127) / 128, blocks = gate.n / 32;
+    if (rows > 64 && m128 * blocks >= 200)
+        launch_q8_swi<128, 2, 2, 4, 3, 1, 1>(st, ms, x, rows, gate.k, so);
+    else
+        launch_q8_swi<64, 2, 1, 8, 2, 2, 1>(st, ms, x, rows, gate.k, so);
     return hipGetLastError();
 }
 

@@ -51,6 +51,10 @@ int mul_rows(kr_ctx* c, kr_buf out, size_t oo, size_t os, kr_buf a, size_t ao, s
              size_t bs, size_t rows, size_t n);
 // gate = silu(gate) * up, quantized
 int silu_quant(kr_ctx* c, kr_buf gate, kr_buf up, size_t rows, size_t width);
+// prefill FFN after the norm's quantization: gate/up + SiLU * up + Q8 in one
+// GEMM launch, then down into `out` (Q8_0 gate/up, rows >= 8)
+bool ffn_swiglu_ok(kr_ctx* c, size_t layer, size_t rows);
+int ffn_swiglu_down(kr_ctx* c, size_t layer, size_t rows, kr_buf out);
 // rope of q and k, then k and v into the cache; positions and slots from the
 // host (pos_host/slot_host) or one device position (pos_dev, rows == 1)
 int rope_kv(kr_ctx* c, kr_buf q, kr_buf k, kr_buf v, size_t qw, size_t kvw, size_t rows, const size_t* pos_host,

@@ -62,6 +62,11 @@ hipError_t launch_rope_kv(hipStream_t st, float* q, float* k, const float* v, si
 // h = silu(gate) * up behind, quantized into (hq, hs, hh) for the down
 // projection; h itself goes to hf when non-null. Needs swiglu_fusable.
 bool swiglu_fusable(const DevMatrix& gate, const DevMatrix& up);
+// Prefill gate/up of Q8_0 matrices with SiLU(gate) * up and its Q8 blocks as
+// the GEMM's epilogue: h's quants / f32 scales / f16 scale bits [rows][n]
+// from the quantized rows x (one launch for gate/up + silu_quant).
+hipError_t launch_gate_up_silu_q8(hipStream_t st, const DevMatrix& gate, const DevMatrix& up, QuantAct x, size_t rows,
+                                  int8_t* hq, float* hs, uint16_t* hh);
 hipError_t launch_gate_up_swiglu(hipStream_t st, int sem, const DevMatrix& gate, const DevMatrix& up, const float* x,
                                  const float* add, const float* norm_w, float* x_out, float eps, int8_t* hq,
                                  float* hs, uint16_t* hh, float* hf);

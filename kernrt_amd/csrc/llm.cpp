@@ -437,12 +437,16 @@ int prefill_rows(krl_model* m, const std::vector<Row>& rows, bool stepped_conv =
                 KRC(m, kr_project(b, l, KR_PROJ_CONV_OUT, p.cy, p.o, n_tok));
             }
             KRC(m, kri::norm_quant(b, p.x, p.o, n.ffn, p.xb, n_tok, g.dim, g.eps));
-            int gu[2] = {KR_PROJ_GATE, KR_PROJ_UP};
-            kr_buf gys[2] = {p.gate, p.up};
-            KRC(m, kri::project_q(b, l, gu, gys, 2, n_tok));
-            KRC(m, kri::silu_quant(b, p.gate, p.up, n_tok, g.hidden));
-            int dn[1] = {KR_PROJ_DOWN};
-            KRC(m, kri::project_q(b, l, dn, &p.o, 1, n_tok));
+            if (kri::ffn_swiglu_ok(b, l, n_tok)) {
+                KRC(m, kri::ffn_swiglu_down(b, l, n_tok, p.o));
+            } else {
+                int gu[2] = {KR_PROJ_GATE, KR_PROJ_UP};
+                kr_buf gys[2] = {p.gate, p.up};
+                KRC(m, kri::project_q(b, l, gu, gys, 2, n_tok));
+                KRC(m, kri::silu_quant(b, p.gate, p.up, n_tok, g.hidden));
+                int dn[1] = {KR_PROJ_DOWN};
+                KRC(m, kri::project_q(b, l, dn, &p.o, 1, n_tok));
+            }
             pending = p.o;
         }
         KRC(m, kr_add_in_place(b, p.x, pending, n_tok * g.dim));

@@ -182,6 +182,21 @@ def test_decode_at_fused_swiglu_widths(storage, dim, hidden):
         assert_bits_equal(gpu.forward(tok, pos), cpu.forward(tok, pos), f"{storage} {dim} pos {pos}")
 
 
+@pytest.mark.parametrize("dim,hidden,n_tok", [(256, 3200, 200), (128, 96, 70), (128, 256, 9)])
+def test_prefill_ffn_gate_up_silu_in_one_gemm(dim, hidden, n_tok):
+    # Q8_0 prefill of 8+ rows: gate and up as one GEMM whose epilogue forms
+    # SiLU(gate) * up and its Q8 blocks (fused schedule). 200 rows x 100
+    # hidden blocks take its 128-row tiles, 70 and 9 rows its 64-row ones
+    # (two row tiles, and one partly empty); logits bitwise against the cpu
+    # backend
+    c = O.Config(dim=dim, hidden_dim=hidden, n_layers=2, n_heads=dim // 64, n_kv_heads=dim // 128, vocab_size=128,
+                 seq_len=256, rms_eps=1e-5, rope_theta=10_000.0, rope_interleaved=False, head_dim=64)
+    ow = gaussian_weights(c, "q8_0", seed=hidden + n_tok)
+    prompt = [(i * 11 + 5) % c.vocab_size for i in range(n_tok)]
+    assert_bits_equal(gpu_model(c, ow).prefill(prompt, 0), O.Model(c, ow, "cpu").prefill(prompt, 0),
+                      f"{dim}x{hidden}, {n_tok} rows")
+
+
 def test_multi_tile_shapes():
     # tests/backends.rs:436-481: a 70-row prompt against 256-wide projections
     c = O.Config(dim=128, hidden_dim=256, n_layers=2, n_heads=4, n_kv_heads=2, vocab_size=128, seq_len=128,

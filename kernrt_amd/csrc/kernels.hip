@@ -293,6 +293,39 @@ __device__ __forceinline__ float wave_chain_sum(float* __restrict__ e, uint32_t 
     return runs ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), runs - 1)) : 0.0f;
 }
 
+// Two serial sums in one pass, one per half-wave: lanes 0..31 run e0's chain
+// as wave_chain_sum<64> does and lanes 32..63 run e1's (n0, n1 <= 1024). The
+// wave-wide shift also hands lane 31's running sum to lane 32 after every
+// run; that sum only ever holds values of e0 past position 1024 (lanes 16 and
+// up, at most 16 runs), which are zeros, so lane 32 starts from +0 as lane 0
+// does. A chain that is done before the other one moves on through lanes
+// whose values are zeros, and x + (+0) = x for these non-negative sums, so
+// both end in the last lane of their half that the runs reach.
+__device__ __forceinline__ float2 wave_chain_sum2(float* __restrict__ e0, uint32_t n0, float* __restrict__ e1,
+                                                  uint32_t n1) {
+    const uint32_t lane = threadIdx.x & 63, hl = lane & 31;
+    float* e = lane < 32 ? e0 : e1;
+    const uint32_t n = lane < 32 ? n0 : n1, n4 = (n + 3) & ~3u, base = hl * 64;
+    if (hl < n4 - n) e[n + hl] = 0.0f;  // a wave's LDS accesses complete in order
+    float v[64];
+#pragma unroll
+    for (int u = 0; u < 16; u++) {
+        const float4 f = base + 4 * u < n4 ? *(const float4*)(e + base + 4 * u) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        v[4 * u] = f.x, v[4 * u + 1] = f.y, v[4 * u + 2] = f.z, v[4 * u + 3] = f.w;
+    }
+    const uint32_t r0 = (n0 + 63) / 64, r1 = (n1 + 63) / 64, runs = r0 > r1 ? r0 : r1;
+    float acc = 0.0f;
+    for (uint32_t L = 0; L < runs; L++) {
+#pragma unroll
+        for (int k = 0; k < 64; k++) acc += v[k];
+        if (L + 1 < runs)  // wave_shr:1
+            acc = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(acc), 0x138, 0xf, 0xf, false));
+    }
+    if (runs == 0) return make_float2(0.0f, 0.0f);
+    return make_float2(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), runs - 1)),
+                       __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), 32 + runs - 1)));
+}
+
 // ---- exact serial sums, evaluated in parallel --------------------------------
 //
 // The reference's serial sums of non-negative terms (the RMS sum of squares,
@@ -2306,6 +2339,20 @@ __device__ __forceinline__ void attn_tile_fetch(attn_v4f (&pre)[PT], const float
         }
     }
 }
+// As attn_tile_fetch for a stage of full rows (C = HS / 4 columns from column
+// 0), every piece addressed on its own: one code path, so the loads of
+// consecutive stages stay independent. n >= 1.
+template <uint32_t C, uint32_t PT, uint32_t NT>
+__device__ __forceinline__ void attn_tile_fetch_flat(attn_v4f (&pre)[PT], const float* base, const DevWindow& w0,
+                                                     uint32_t n_shared, uint32_t kv_dim, uint32_t i0, uint32_t n) {
+    constexpr uint32_t RS = NT / C;
+    const uint32_t prow = threadIdx.x / C, pcol = threadIdx.x % C;
+#pragma unroll
+    for (uint32_t k = 0; k < PT; k++) {
+        const uint32_t rr = prow + k * RS, rc = rr < n ? rr : n - 1;
+        pre[k] = *(const attn_v4f*)(base + (size_t)win_slot(w0, n_shared, i0 + rc) * kv_dim + 4 * pcol);
+    }
+}
 // The fetched stage into the LDS tile (row stride STRIDE floats), rows < n.
 template <uint32_t C, uint32_t PT, uint32_t NT, uint32_t ROWS, uint32_t STRIDE>
 __device__ __forceinline__ void attn_tile_put(const attn_v4f (&pre)[PT], float* kt, uint32_t n) {
@@ -2325,6 +2372,99 @@ __host__ __device__ constexpr uint32_t attn_pair_group(uint32_t rg) {
     while (p > 1 && rg % p != 0) p--;
     return p == 0 ? 1 : p;
 }
+// Softmax of k_attn_rows' pairs, each by the wave that computed its scores
+// (row rg = wave * RPW + k of sc, s_cnt[rg] values): max, exp, the serial sum
+// left to right (elementwise.rs:81-91) and the division; the probabilities go
+// back to sc and, unless `att` is null, to `att`, where the reference leaves
+// them. Two pairs per wave run side by side: their loops interleaved and
+// both sums in one pass (wave_chain_sum2).
+template <uint32_t RPW, uint32_t G>
+__device__ __forceinline__ void attn_rows_softmax(float* __restrict__ sc, uint32_t scs,
+                                                  const uint32_t* __restrict__ s_cnt, float* __restrict__ s_sum,
+                                                  const uint64_t* __restrict__ etab, uint32_t wave, uint32_t lane,
+                                                  uint32_t RG, float* __restrict__ att, uint32_t r0, uint32_t n_heads,
+                                                  uint32_t h0, uint32_t seq_len) {
+    if constexpr (RPW == 2) {
+        const uint32_t ra = wave * 2, rb = ra + 1;
+        const uint32_t na = ra < RG ? s_cnt[ra] : 0, nb = rb < RG ? s_cnt[rb] : 0;
+        if (na <= 1024 && nb <= 1024) {  // wave-uniform
+            const uint32_t nm = max(na, nb);
+            float* ea = sc + ra * scs;
+            float* eb = sc + (rb < RG ? rb : ra) * scs;
+            float ma = -INFINITY, mb = -INFINITY;
+            for (uint32_t i = lane; i < nm; i += 64) {
+                if (i < na) ma = fmaxf(ma, ea[i]);
+                if (i < nb) mb = fmaxf(mb, eb[i]);
+            }
+            ma = wave_max(ma);
+            mb = wave_max(mb);
+#pragma unroll 2
+            for (uint32_t i = lane; i < nm; i += 64) {
+                if (i < na) ea[i] = glibc_expf(ea[i] - ma, etab);
+                if (i < nb) eb[i] = glibc_expf(eb[i] - mb, etab);
+            }
+            __builtin_amdgcn_wave_barrier();
+            const float2 sum = wave_chain_sum2(ea, na, eb, nb);
+            __builtin_amdgcn_wave_barrier();
+            const uint32_t rA = ra / G, jA = ra - rA * G, rB = rb / G, jB = rb - rB * G;
+            float* aa = att + (size_t)(r0 + rA) * n_heads * seq_len + (size_t)(h0 + jA) * seq_len;
+            float* ab = att + (size_t)(r0 + rB) * n_heads * seq_len + (size_t)(h0 + jB) * seq_len;
+#pragma unroll 2
+            for (uint32_t i = lane; i < nm; i += 64) {
+                if (i < na) {
+                    const float pv = div_rn(ea[i], sum.x);
+                    ea[i] = pv;
+                    if (att) aa[i] = pv;
+                }
+                if (i < nb) {
+                    const float pv = div_rn(eb[i], sum.y);
+                    eb[i] = pv;
+                    if (att) ab[i] = pv;
+                }
+            }
+            return;
+        }
+    }
+#pragma unroll
+    for (uint32_t k = 0; k < RPW; k++) {
+        const uint32_t rg = wave * RPW + k, n = rg < RG ? s_cnt[rg] : 0;
+        float* e = sc + rg * scs;
+        float m = -INFINITY;
+        for (uint32_t i = lane; i < n; i += 64) m = fmaxf(m, e[i]);
+        m = wave_max(m);
+#pragma unroll 4
+        for (uint32_t i = lane; i < n; i += 64) e[i] = glibc_expf(e[i] - m, etab);  // independent: 4 in flight
+    }
+    __builtin_amdgcn_wave_barrier();
+    // the wave's pairs one after the other, each a register-fed chain across
+    // the wave's lanes
+#pragma unroll
+    for (uint32_t k = 0; k < RPW; k++) {
+        const uint32_t rg = wave * RPW + k;
+        if (rg < RG) {  // wave-uniform
+            const uint32_t n = s_cnt[rg];
+            const float sum = n <= 4096 ? wave_chain_sum(sc + rg * scs, n) : chain_sum(sc + rg * scs, n);
+            if (lane == 0) s_sum[rg] = sum;
+        }
+    }
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (uint32_t k = 0; k < RPW; k++) {
+        const uint32_t rg = wave * RPW + k;
+        if (rg >= RG) continue;
+        const uint32_t n = s_cnt[rg], r = rg / G, j = rg - r * G;
+        const float sj = s_sum[rg];
+        float* e = sc + rg * scs;
+        float* arow = att + (size_t)(r0 + r) * n_heads * seq_len + (size_t)(h0 + j) * seq_len;
+#pragma unroll 4
+        for (uint32_t i = lane; i < n; i += 64) {
+            const float pv = div_rn(e[i], sj);
+            e[i] = pv;
+            if (att) arow[i] = pv;
+        }
+    }
+}
+
 template <int G, int HS, int NWAVES>
 __global__ __launch_bounds__(64 * NWAVES) void k_attn_rows(const float* __restrict__ q, float* __restrict__ out,
                                                    float* __restrict__ att, const float* __restrict__ kc,
@@ -2352,38 +2492,54 @@ __global__ __launch_bounds__(64 * NWAVES) void k_attn_rows(const float* __restri
     const DevWindow w0 = windows[r0];
     const uint32_t n_shared = w0.shared_end - w0.shared_start;
 
-    // the window lengths, the exp table
+    // the window lengths, the exp table; for HS < 128 the block's q rows go to
+    // LDS here, so their load overlaps the window read (pairs past the
+    // block's end hold the last valid pair's row)
     const uint32_t wv = __builtin_amdgcn_readfirstlane(wave);
-    if (tid < NW * RPW) {
-        const uint32_t r = tid / G;
-        s_cnt[tid] = tid < RG && r < nr ? n_shared + windows[r0 + r].slot - w0.att_start + 1 : 0;
+    // (every load is issued before any store waits on one)
+    float* sq = kt + Sh::TILE;  // [RG][HS] (HS < 128)
+    attn_v4f qpiece = {0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (HS < 128) {
+        static_assert(RG * F <= NT, "one q piece per thread");
+        const uint32_t nvalid = min(RG, nr * G), f = min(tid, RG * F - 1), rg = f / F, u = f - rg * F;
+        const uint32_t rc = min(rg, nvalid - 1), r = rc / G, j = rc - r * G;
+        qpiece = *(const attn_v4f*)(q + (size_t)(r0 + r) * width + (h0 + j) * HS + 4 * u);
     }
-    if (tid < 32) etab[tid] = kExp2Tab[tid];
+    const uint32_t wslot = windows[r0 + min(tid / G, nr - 1)].slot;
+    const uint64_t et = kExp2Tab[tid & 31];
+    if constexpr (HS < 128) {
+        if (tid < RG * F) *(attn_v4f*)(sq + (tid / F) * HS + 4 * (tid % F)) = qpiece;
+    }
+    if (tid < NW * RPW) s_cnt[tid] = tid < RG && tid / G < nr ? n_shared + wslot - w0.att_start + 1 : 0;
+    if (tid < 32) etab[tid] = et;
     __syncthreads();
     uint32_t cmax = 0;
     for (uint32_t rg = 0; rg < RG; rg++) cmax = max(cmax, s_cnt[rg]);
     const float* kbase = kc + loff + kvo;
     const float* vbase = vc + loff + kvo;
-    // K (HS < 128) and V stages are fetched into registers one stage ahead
-    // (PT float4 per thread) and stored to LDS after the current stage is
-    // consumed, so the global latency overlaps the compute; the barrier after
-    // the compute waits for LDS only, leaving the fetch in flight.
+    // K (HS < 128) and V stages are fetched into registers ahead of their use
+    // (PT float4 per thread per stage) and stored to LDS after the previous
+    // stage is consumed, so the global latency overlaps the compute; the
+    // barrier after the compute waits for LDS only, leaving fetches in flight.
     constexpr uint32_t PT = TV * F / NT;
     static_assert(PT * NT == T * FK && PT * NT == TV * F, "K and V stages hold the same pieces");
-    attn_v4f pre[PT];
     const bool off32 = (uint64_t)seq_len * kv_dim * 4 <= 0xFFFFFFFFull;  // every slot's byte offset fits 32 bits
     auto tile_len = [&](uint32_t i0) { return i0 < cmax ? min(T, cmax - i0) : 0u; };
-    auto vlen = [&](uint32_t i0) { return i0 < cmax ? min(TV, cmax - i0) : 0u; };
-    // K stage s: positions of tile s / NH, dims half s % NH; V stage s: positions s TV ..
-    auto kfetch = [&](uint32_t st) {
-        const uint32_t i0 = st / NH * T;
-        attn_tile_fetch<FK, PT, NT, T>(pre, kbase, w0, n_shared, kv_dim, off32, i0, tile_len(i0), st % NH * FK);
-    };
-    auto vfetch = [&](uint32_t st) {
-        attn_tile_fetch<F, PT, NT, TV>(pre, vbase, w0, n_shared, kv_dim, off32, st * TV, vlen(st * TV), 0);
-    };
+
+    // the V lane map of phase 3: lane = (pair, 2 dims)
+    typedef float v2f __attribute__((ext_vector_type(2)));
+    const uint32_t rgv = wave * RPW + lane / LPR, e0 = 2 * (lane % LPR);
+    const uint32_t nv = rgv < RG ? s_cnt[rgv] : 0;
+    const float* pp = sc + rgv * scs;
+    float o0 = 0.0f, o1 = 0.0f;
 
     if constexpr (HS == 128) {
+        // V stage s: positions s TV .. (one stage ahead in `pre`)
+        attn_v4f pre[PT];
+        auto vlen = [&](uint32_t i0) { return i0 < cmax ? min(TV, cmax - i0) : 0u; };
+        auto vfetch = [&](uint32_t st) {
+            attn_tile_fetch<F, PT, NT, TV>(pre, vbase, w0, n_shared, kv_dim, off32, st * TV, vlen(st * TV), 0);
+        };
         vfetch(0);  // the first V stage lands while the scores and the softmax run
         // 1. scores. Wave w takes window positions 64 (NW t + w) .. + 63 of round
         // t, lane = position, for every pair of the block: the lane's K row comes
@@ -2473,147 +2629,169 @@ __global__ __launch_bounds__(64 * NWAVES) void k_attn_rows(const float* __restri
             }
         }
         __syncthreads();  // every pair's scores are in LDS
-    } else {
-        // the q rows of this wave's pairs (wave-uniform addresses: scalar
-        // loads; pairs past the block's end read the last valid pair)
-        const float* qrow[RPW];
-#pragma unroll
-        for (uint32_t k = 0; k < RPW; k++) {
-            const uint32_t rg = min(wv * RPW + k, min(RG, nr * G) - 1), r = rg / G, j = rg - r * G;
-            qrow[k] = q + (size_t)(r0 + r) * width + (size_t)(h0 + j) * HS;
-        }
-        // 1. scores of every (pair, position) of each K tile, staged through LDS
-        const uint32_t nks = (cmax + T - 1) / T * NH;
-        kfetch(0);
-        attn_tile_put<FK, PT, NT, T, KSK>(pre, kt, tile_len(0));
+
+        // 2. softmax of each pair, by the wave that computed its scores
+        attn_rows_softmax<RPW, G>(sc, scs, s_cnt, s_sum, etab, wave, lane, RG, att, r0, n_heads, h0, seq_len);
+
+        // 3. out[pair][e] = sum_i p_i * v_i[e] in position order; lane = (pair, 2 dims)
+        // the first V stage (every wave is past the last K stage)
+        const uint32_t nvs = (cmax + TV - 1) / TV;
+        attn_tile_put<F, PT, NT, TV, KSV>(pre, kt, vlen(0));
         __syncthreads();
-        float a[RPW][4];
-        for (uint32_t st = 0; st < nks; st++) {
-            const uint32_t i0 = st / NH * T, h = st % NH, nt = tile_len(i0);
-            if (st + 1 < nks)
-                kfetch(st + 1);
-            else  // the first V stage, for phase 3
-                vfetch(0);
-            {  // lane = position, wave = its RPW pairs. The pairs' q values are
-               // wave-uniform: QB float4 per pair at a time go to scalar registers
-               // (RPW QB 4 = 32), then each LDS read of 4 K values feeds 4 FMAs
-               // per pair. K is read a group of GS float4 ahead, into two register
-               // sets used in turn, so only LDS reads are waited on inside a block.
-                constexpr uint32_t QB = 8 / RPW < 2 ? 2 : 8 / RPW, GS = QB < 4 ? QB : 4, NG = QB / GS;
-                static_assert(FK % QB == 0 && QB % GS == 0, "q blocks");
-                const uint32_t ug = h * FK;  // first dim block of this stage
-                const uint32_t pos = lane;
-                if (h == 0) {
-    #pragma unroll
-                    for (uint32_t k = 0; k < RPW; k++) a[k][0] = a[k][1] = a[k][2] = a[k][3] = 0.0f;
-                }
-                const float* krow = kt + pos * KSK;
-    #pragma unroll 1
-                for (uint32_t q0 = 0; q0 < FK; q0 += QB) {
-                    float4 qv[RPW][QB];
-    #pragma unroll
-                    for (uint32_t k = 0; k < RPW; k++)
-    #pragma unroll
-                        for (uint32_t u = 0; u < QB; u++) qv[k][u] = *(const float4*)(qrow[k] + 4 * (ug + q0 + u));
-                    float4 kb[2][GS];
-    #pragma unroll
-                    for (uint32_t t = 0; t < GS; t++) kb[0][t] = *(const float4*)(krow + 4 * (q0 + t));
-    #pragma unroll
-                    for (uint32_t g = 0; g < NG; g++) {
-                        if (g + 1 < NG) {
-    #pragma unroll
-                            for (uint32_t t = 0; t < GS; t++)
-                                kb[(g + 1) & 1][t] = *(const float4*)(krow + 4 * (q0 + GS * (g + 1) + t));
-                        }
-    #pragma unroll
-                        for (uint32_t t = 0; t < GS; t++) {
-                            const float4 kk = kb[g & 1][t];
-    #pragma unroll
-                            for (uint32_t k = 0; k < RPW; k++) {
-                                const float4 qq = qv[k][GS * g + t];
-                                a[k][0] = __builtin_fmaf(qq.x, kk.x, a[k][0]);
-                                a[k][1] = __builtin_fmaf(qq.y, kk.y, a[k][1]);
-                                a[k][2] = __builtin_fmaf(qq.z, kk.z, a[k][2]);
-                                a[k][3] = __builtin_fmaf(qq.w, kk.w, a[k][3]);
-                            }
-                        }
-                    }
-                }
-    #pragma unroll
-                for (uint32_t k = 0; k < RPW; k++) {
-                    const uint32_t rg = wv * RPW + k;
-                    // dot.rs:360: (acc0 + acc1) + (acc2 + acc3), then * scale (cpu.rs:609)
-                    if (h == NH - 1 && rg < RG && pos < nt && i0 + pos < s_cnt[rg])
-                        sc[rg * scs + i0 + pos] = ((a[k][0] + a[k][1]) + (a[k][2] + a[k][3])) * scale;
-                }
-            }
-            lds_barrier();  // the stage is consumed
-            if (st + 1 < nks) {
-                attn_tile_put<FK, PT, NT, T, KSK>(pre, kt, tile_len((st + 1) / NH * T));
+        for (uint32_t st = 0; st < nvs; st++) {
+            const uint32_t i0 = st * TV, nt = vlen(i0);
+            if (st + 1 < nvs) vfetch(st + 1);
+            const uint32_t lim = nv > i0 ? min(nt, nv - i0) : 0;
+            attn_v_chain<KSV>(pp + i0, kt + e0, lim, o0, o1);
+            lds_barrier();
+            if (st + 1 < nvs) {
+                attn_tile_put<F, PT, NT, TV, KSV>(pre, kt, vlen(i0 + TV));
                 lds_barrier();
             }
         }
-    }
-
-    // 2. softmax of each pair, by the wave that computed its scores
+    } else {
+        // 1. scores of every (pair, position) of each K tile, staged through LDS.
+        // K stages s < nks and then V stages s = nks + i of the same shape
+        // (HS < 128: one K stage per 64-position tile, the same pieces as a V
+        // stage) flow through two register sets used in turn, each stage
+        // fetched two stages before it is stored to LDS: the loads of the next
+        // two stages are in flight while one is used, and the first two V
+        // stages land while the scores and the softmax run. The loops are
+        // unrolled by two so that each set is named statically, and every
+        // fetch loads its pieces unconditionally (a fetch past the last stage
+        // repeats it), so each store to LDS waits for its own loads only.
+        const uint32_t nks = (cmax + T - 1) / T, nst = nks + (cmax + TV - 1) / TV;
+        attn_v4f pa[PT], pb[PT];
+        auto fetch_into = [&](attn_v4f (&p)[PT], uint32_t s) {
+            s = min(s, nst - 1);
+            const bool isk = s < nks;
+            const uint32_t i0 = (isk ? s : s - nks) * T;
+            attn_tile_fetch_flat<F, PT, NT>(p, isk ? kbase : vbase, w0, n_shared, kv_dim, i0, tile_len(i0));
+        };
+        auto put_stage = [&](const attn_v4f (&p)[PT], uint32_t s) {
+            attn_tile_put<F, PT, NT, T, KSK>(p, kt, tile_len((s < nks ? s : s - nks) * T));
+        };
+        static_assert(NH == 1 && FK == F && KSK == KSV && TV == T, "K and V stages share one shape");
+        // this wave's pairs' q rows in LDS (the same address on every lane)
+        const float* qrow[RPW];
 #pragma unroll
-    for (uint32_t k = 0; k < RPW; k++) {
-        const uint32_t rg = wave * RPW + k, n = rg < RG ? s_cnt[rg] : 0;
-        float* e = sc + rg * scs;
-        float m = -INFINITY;
-        for (uint32_t i = lane; i < n; i += 64) m = fmaxf(m, e[i]);
-        m = wave_max(m);
-#pragma unroll 4
-        for (uint32_t i = lane; i < n; i += 64) e[i] = glibc_expf(e[i] - m, etab);  // independent: 4 in flight
-    }
-    __builtin_amdgcn_wave_barrier();
-    // sum left to right (elementwise.rs:81-91), the wave's pairs one after the
-    // other, each a register-fed chain across the wave's lanes
+        for (uint32_t k = 0; k < RPW; k++) qrow[k] = sq + min(wv * RPW + k, RG - 1) * HS;
+        auto scores = [&](uint32_t st) {
+            // lane = position, wave = its RPW pairs: QB float4 of each pair's q
+            // at a time, then each LDS read of 4 K values feeds 4 FMAs per pair.
+            // K is read a group of GS float4 ahead, into two register sets used
+            // in turn, so only LDS reads are waited on inside a block.
+            const uint32_t i0 = st * T, nt = tile_len(i0);
+            constexpr uint32_t QB = 8 / RPW < 2 ? 2 : 8 / RPW, GS = QB < 4 ? QB : 4, NG = QB / GS;
+            static_assert(FK % QB == 0 && QB % GS == 0, "q blocks");
+            const uint32_t pos = lane;
+            float a[RPW][4];
 #pragma unroll
-    for (uint32_t k = 0; k < RPW; k++) {
-        const uint32_t rg = wave * RPW + k;
-        if (rg < RG) {  // wave-uniform
-            const uint32_t n = s_cnt[rg];
-            const float sum = n <= 4096 ? wave_chain_sum(sc + rg * scs, n) : chain_sum(sc + rg * scs, n);
-            if (lane == 0) s_sum[rg] = sum;
-        }
-    }
-    __builtin_amdgcn_wave_barrier();
+            for (uint32_t k = 0; k < RPW; k++) a[k][0] = a[k][1] = a[k][2] = a[k][3] = 0.0f;
+            const float* krow = kt + pos * KSK;
+#pragma unroll 1
+            for (uint32_t q0 = 0; q0 < FK; q0 += QB) {
+                float4 qv[RPW][QB];
 #pragma unroll
-    for (uint32_t k = 0; k < RPW; k++) {
-        const uint32_t rg = wave * RPW + k;
-        if (rg >= RG) continue;
-        const uint32_t n = s_cnt[rg], r = rg / G, j = rg - r * G;
-        const float sj = s_sum[rg];
-        float* e = sc + rg * scs;
-        float* arow = att + (size_t)(r0 + r) * n_heads * seq_len + (size_t)(h0 + j) * seq_len;
-#pragma unroll 4
-        for (uint32_t i = lane; i < n; i += 64) {
-            const float pv = div_rn(e[i], sj);
-            e[i] = pv;
-            arow[i] = pv;  // the probabilities stay in `att`, as the reference leaves them
-        }
-    }
-
-    // 3. out[pair][e] = sum_i p_i * v_i[e] in position order; lane = (pair, 2 dims)
-    typedef float v2f __attribute__((ext_vector_type(2)));
-    const uint32_t rgv = wave * RPW + lane / LPR, e0 = 2 * (lane % LPR);
-    const uint32_t nv = rgv < RG ? s_cnt[rgv] : 0;
-    const float* pp = sc + rgv * scs;
-    float o0 = 0.0f, o1 = 0.0f;
-    // the first V stage (every wave is past the last K stage)
-    const uint32_t nvs = (cmax + TV - 1) / TV;
-    attn_tile_put<F, PT, NT, TV, KSV>(pre, kt, vlen(0));
-    __syncthreads();
-    for (uint32_t st = 0; st < nvs; st++) {
-        const uint32_t i0 = st * TV, nt = vlen(i0);
-        if (st + 1 < nvs) vfetch(st + 1);
-        const uint32_t lim = nv > i0 ? min(nt, nv - i0) : 0;
-        attn_v_chain<KSV>(pp + i0, kt + e0, lim, o0, o1);
-        lds_barrier();
-        if (st + 1 < nvs) {
-            attn_tile_put<F, PT, NT, TV, KSV>(pre, kt, vlen(i0 + TV));
+                for (uint32_t k = 0; k < RPW; k++)
+#pragma unroll
+                    for (uint32_t u = 0; u < QB; u++) qv[k][u] = *(const float4*)(qrow[k] + 4 * (q0 + u));
+                float4 kb[2][GS];
+#pragma unroll
+                for (uint32_t t = 0; t < GS; t++) kb[0][t] = *(const float4*)(krow + 4 * (q0 + t));
+#pragma unroll
+                for (uint32_t g = 0; g < NG; g++) {
+                    if (g + 1 < NG) {
+#pragma unroll
+                        for (uint32_t t = 0; t < GS; t++)
+                            kb[(g + 1) & 1][t] = *(const float4*)(krow + 4 * (q0 + GS * (g + 1) + t));
+                    }
+#pragma unroll
+                    for (uint32_t t = 0; t < GS; t++) {
+                        const float4 kk = kb[g & 1][t];
+#pragma unroll
+                        for (uint32_t k = 0; k < RPW; k++) {
+                            const float4 qq = qv[k][GS * g + t];
+                            a[k][0] = __builtin_fmaf(qq.x, kk.x, a[k][0]);
+                            a[k][1] = __builtin_fmaf(qq.y, kk.y, a[k][1]);
+                            a[k][2] = __builtin_fmaf(qq.z, kk.z, a[k][2]);
+                            a[k][3] = __builtin_fmaf(qq.w, kk.w, a[k][3]);
+                        }
+                    }
+                }
+            }
+#pragma unroll
+            for (uint32_t k = 0; k < RPW; k++) {
+                const uint32_t rg = wv * RPW + k;
+                // dot.rs:360: (acc0 + acc1) + (acc2 + acc3), then * scale (cpu.rs:609)
+                if (rg < RG && pos < nt && i0 + pos < s_cnt[rg])
+                    sc[rg * scs + i0 + pos] = ((a[k][0] + a[k][1]) + (a[k][2] + a[k][3])) * scale;
+            }
+        };
+        fetch_into(pa, 0);
+        fetch_into(pb, 1);
+        put_stage(pa, 0);
+        __syncthreads();
+        fetch_into(pa, 2);
+        for (uint32_t st = 0; st < nks; st += 2) {
+            scores(st);
+            lds_barrier();  // the stage is consumed
+            if (st + 1 >= nks) break;
+            put_stage(pb, st + 1);
             lds_barrier();
+            fetch_into(pb, st + 3);
+            scores(st + 1);
+            lds_barrier();
+            if (st + 2 >= nks) break;
+            put_stage(pa, st + 2);
+            lds_barrier();
+            fetch_into(pa, st + 4);
+        }
+
+        // 2. softmax of each pair, by the wave that computed its scores (the
+        // probabilities go to `att` at the end, so that no store is pending
+        // ahead of the V stages' loads)
+        attn_rows_softmax<RPW, G>(sc, scs, s_cnt, s_sum, etab, wave, lane, RG, nullptr, r0, n_heads, h0, seq_len);
+
+        // 3. out[pair][e] = sum_i p_i * v_i[e] in position order; lane = (pair, 2 dims).
+        // Stage nks (the first V stage) is in pa when nks is even, else in pb.
+        auto vphase = [&](attn_v4f (&p0)[PT], attn_v4f (&p1)[PT]) {
+            put_stage(p0, nks);
+            __syncthreads();
+            fetch_into(p0, nks + 2);
+            auto chain = [&](uint32_t sv) {
+                const uint32_t i0 = sv * TV, nt = tile_len(i0);
+                const uint32_t lim = nv > i0 ? min(nt, nv - i0) : 0;
+                attn_v_chain<KSV>(pp + i0, kt + e0, lim, o0, o1);
+            };
+            const uint32_t nvs = nst - nks;
+            for (uint32_t sv = 0; sv < nvs; sv += 2) {
+                chain(sv);
+                lds_barrier();
+                if (sv + 1 >= nvs) break;
+                put_stage(p1, nks + sv + 1);
+                lds_barrier();
+                fetch_into(p1, nks + sv + 3);
+                chain(sv + 1);
+                lds_barrier();
+                if (sv + 2 >= nvs) break;
+                put_stage(p0, nks + sv + 2);
+                lds_barrier();
+                fetch_into(p0, nks + sv + 4);
+            }
+        };
+        if (nks & 1)
+            vphase(pb, pa);
+        else
+            vphase(pa, pb);
+        // the probabilities, still in LDS, to `att` (the reference leaves them there)
+        for (uint32_t k = 0; k < RPW; k++) {
+            const uint32_t rg = wv * RPW + k;
+            if (rg >= RG) break;
+            const uint32_t n = s_cnt[rg], r = rg / G, j = rg - r * G;
+            const float* e = sc + rg * scs;
+            float* arow = att + (size_t)(r0 + r) * n_heads * seq_len + (size_t)(h0 + j) * seq_len;
+            for (uint32_t i = lane; i < n; i += 64) arow[i] = e[i];
         }
     }
     const uint32_t r = rgv / G, j = rgv - r * G;
@@ -2642,7 +2820,8 @@ __global__ __launch_bounds__(64 * NWAVES) void k_attn_rows(const float* __restri
 static size_t attn_rows_lds(size_t G, size_t hs, size_t max_count, size_t nw) {
     const size_t rpw = 128 / hs, rg = (nw * rpw / G) * G, scs = (max_count + 3) & ~(size_t)3;
     const size_t tile = hs == 128 ? std::max(64 * (hs / 2 + 4), 32 * (hs + 4)) : 64 * (hs + 4);  // AttnRowsShape::TILE
-    return (rg * scs + tile) * sizeof(float);
+    const size_t qrows = hs < 128 ? rg * hs : 0;  // the q rows (HS < 128)
+    return (rg * scs + tile + qrows) * sizeof(float);
 }
 // Waves per k_attn_rows workgroup: 8 while two workgroups fit a CU's LDS,
 // else 4 (half the rows per block) if that lets two fit, else whichever fits

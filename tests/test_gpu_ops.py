@@ -270,6 +270,19 @@ def test_attention_prefill_rows(n_heads, n_kv, hs):
     _attention_case(160, n_heads, n_kv, hs, [(90, 90 + i, 3, 71) for i in range(45)], 41 + hs)
 
 
+@pytest.mark.parametrize("n_heads,n_kv,hs", [(8, 8, 64), (6, 2, 64), (16, 2, 32), (8, 4, 128)])
+def test_attention_prefill_rows_many_tiles(n_heads, n_kv, hs):
+    # windows of 301 to 340 positions: six K and six V tiles per block, so the
+    # tiles pass through both register sets several times; kv_mul 3 leaves a
+    # block with an odd number of (row, head) pairs
+    _attention_case(400, n_heads, n_kv, hs, [(0, 300 + i, 0, 0) for i in range(40)], 42 + hs + n_heads)
+
+
+def test_attention_prefill_rows_1p7b_shape():
+    # the 128-row prefill of the 1.7B shape: 32 heads, kv_mul 1, head_dim 64
+    _attention_case(160, 32, 32, 64, [(0, i, 0, 0) for i in range(128)], 43)
+
+
 def test_attention_long_context_uses_global_scores():
     # more scores than fit in LDS: the kernel keeps them in `att`
     _attention_case(16384, 2, 1, 128, [(0, 13000, 0, 0), (100, 16383, 0, 0)], 17)

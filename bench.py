@@ -364,9 +364,11 @@ def bench_gemv(K, reps: int = 3, use_graph: bool = True):
 def bench_prefill(K, reps: int = 2):
     """128-token Q8_0 prefill at 1.7B projection shapes (`configs[2]`): the
     int8 MFMA GEMM launches the model's prefill issues per layer -- fused
-    q/k/v (one launch over 6144 rows), o, fused gate/up (16384 rows), down --
-    alone (activations quantized beforehand), and the projections with their
-    activation quantization, over all 24 layers' distinct matrices."""
+    q/k/v (one launch over 6144 rows), o, fused gate/up (16384 rows), down in
+    its chain-split form (four partial-sum planes, kr_matmul_split) -- alone
+    (activations quantized beforehand), and the projections with their
+    activation quantization, over all 24 layers' distinct matrices. The
+    planes' sum runs in the norm launch that follows down in the model."""
     log("prefill: 128-row Q8_0 projections at 1.7B shapes")
     hip = K.open("hip")
     c = K.Config(**CFG3)
@@ -378,14 +380,22 @@ def bench_prefill(K, reps: int = 2):
     rng = np.random.default_rng(4)
     ks = {k for _, shapes in groups for _, k in shapes}
     xs = {k: hip.upload(rng.normal(size=m_rows * k).astype(np.float32)) for k in ks}
-    ys = [[hip.alloc(m_rows * n) for n, _ in shapes] for _, shapes in groups]
+    split = [name == "down" for name, _ in groups]  # the model's chain-split launch
+    ys = [[hip.alloc((4 if split[g] else 1) * m_rows * n) for n, _ in shapes] for g, (_, shapes) in enumerate(groups)]
+
+    def launch(l, g, quantize):
+        k = groups[g][1][0][1]
+        if split[g]:
+            hip.matmul_split(mats[l][g][0], xs[k] if quantize else None, ys[g][0], m_rows)
+        else:
+            if quantize:
+                hip.quantize_rows(xs[k], m_rows, k)
+            hip.matmul_quantized_set(mats[l][g], ys[g], m_rows)
 
     def run():
         for l in range(c.n_layers):
-            for g, (_, shapes) in enumerate(groups):
-                k = shapes[0][1]
-                hip.quantize_rows(xs[k], m_rows, k)
-                hip.matmul_quantized_set(mats[l][g], ys[g], m_rows)
+            for g in range(len(groups)):
+                launch(l, g, True)
 
     run()
     hip.synchronize()
@@ -397,14 +407,14 @@ def bench_prefill(K, reps: int = 2):
     for g, (name, shapes) in enumerate(groups):
         k = shapes[0][1]
         n = sum(nn for nn, _ in shapes)
-        hip.quantize_rows(xs[k], m_rows, k)
+        launch(0, g, True)
         for l in range(c.n_layers):
-            hip.matmul_quantized_set(mats[l][g], ys[g], m_rows)
+            launch(l, g, False)
         hip.synchronize()
         hip.timer_start()
         for _ in range(reps):
             for l in range(c.n_layers):
-                hip.matmul_quantized_set(mats[l][g], ys[g], m_rows)
+                launch(l, g, False)
         ms = hip.timer_stop() / reps
         gemm_ms += ms
         us = ms * 1e3 / c.n_layers

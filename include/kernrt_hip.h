@@ -33,6 +33,7 @@ typedef uint32_t kr_buf;
 /* A device-resident weight matrix (one `Matrix`, quant.rs:502-520). */
 typedef uint32_t kr_mat;
 #define KR_NO_MAT ((kr_mat)0xffffffffu)
+#define KR_NO_BUF ((kr_buf)0xffffffffu)
 
 enum {
     KR_OK = 0,
@@ -176,6 +177,19 @@ int kr_matmul_quantized(kr_ctx* ctx, kr_mat w, kr_buf y, size_t rows);
  * n (1..3) matrices with the same in_dim and storage, one kernel launch over
  * all their rows, on the quantized workspace rows; y[i] gets w[i]'s output. */
 int kr_matmul_quantized_set(kr_ctx* ctx, const kr_mat* w, const kr_buf* y, int n, size_t rows);
+
+/* The chain-split form of kr_matmul for a Q8_0 matrix with in_dim % 128 == 0,
+ * the one the prefill driver runs for few rows. No counterpart in the
+ * reference: it computes the same four partial sums per output as
+ * Matrix::matmul's Q8_0 kernel (dot.rs:34-45) -- t[j] over the blocks
+ * b = j mod 4, in block order -- each on its own workgroups, and leaves them
+ * as four planes y[j][rows][out_dim] (y holds 4 * rows * out_dim floats);
+ * ((y[0] + y[1]) + y[2]) + y[3] is kr_matmul's output bit for bit. x: rows
+ * of width in_dim, quantized into the workspace in chain-major block order;
+ * KR_NO_BUF reuses the workspace as the previous kr_matmul_split left it.
+ * The matrix's chain-major copy (out_dim * in_dim * 1.125 bytes) is made on
+ * first use and kept until the matrix is freed. */
+int kr_matmul_split(kr_ctx* ctx, kr_mat w, kr_buf x, kr_buf y, size_t rows);
 
 /* A bare streaming read of len floats of src from `offset` (both multiples
  * of 4): the practical ceiling of a read-dominated kernel of that size, for

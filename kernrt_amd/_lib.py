@@ -94,6 +94,7 @@ _SIGS = {
     "kr_quantize_rows": (i32, [vp, u32, sz, sz]),
     "kr_matmul_quantized": (i32, [vp, u32, u32, sz]),
     "kr_matmul_quantized_set": (i32, [vp, C.POINTER(u32), C.POINTER(u32), i32, sz]),
+    "kr_matmul_split": (i32, [vp, u32, u32, u32, sz]),
     "kr_stream_read": (i32, [vp, u32, sz, sz]),
     "kr_stream_read_shape": (i32, [vp, u32, sz, sz, i32, sz]),
     "kr_capture_begin": (i32, [vp]),

@@ -29,6 +29,7 @@ PROJ_ALL = tuple(PROJ_INDEX)
 STORAGE_Q8_0 = 2
 STORAGE_Q8_0X4 = 3
 KR_NO_MAT = 0xFFFFFFFF
+KR_NO_BUF = 0xFFFFFFFF
 
 
 class BackendError(Exception):
@@ -372,6 +373,12 @@ class Hip:
         ws = (C.c_uint32 * n)(*mats)
         yb = (C.c_uint32 * n)(*ys)
         self._ck(self._L.kr_matmul_quantized_set(self.ctx, ws, yb, n, rows))
+
+    def matmul_split(self, mat: int, x, y: Buf, rows: int):
+        """The chain-split projection: y (4 * rows * out_dim floats) gets the
+        four partial-sum planes; x None reuses the workspace rows of the last
+        call."""
+        self._ck(self._L.kr_matmul_split(self.ctx, mat, KR_NO_BUF if x is None else x, y, rows))
 
     def stream_read(self, src: Buf, offset: int, n: int, chunks_per_lane: int = 2, workgroups: int = 0):
         """Read n floats of src and discard them (a bandwidth reference):

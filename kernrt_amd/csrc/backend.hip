@@ -42,6 +42,10 @@ struct Mat {
     // 0 the re-quantization identity holds, 1 `requant` holds the copy.
     int requant_state = -1;
     DevMatrix requant{};
+    // A Q8_0 matrix's chain-major copy for the chain-split prefill GEMM
+    // (launch_gemm_q8_cs), made on its first use; the matrix never changes
+    // after it is made, so the copy stays valid until the matrix is freed.
+    DevMatrix cm{};
 };
 
 // A host slice staged into device memory through a pinned double buffer.
@@ -138,6 +142,7 @@ struct kr_ctx {
     // (workspace, staging, rope tables): cached HIP graphs are then stale
     uint64_t epoch = 0;
     size_t q_rows = 0, q_width = 0;  // what the activation workspace holds
+    bool q_chain_major = false;      // its Q8 blocks in chain-major order (for a chain-split GEMM only)
     hipEvent_t t0 = nullptr, t1 = nullptr;
     // decode attention scratch: scores and per-chunk maxima
     float* attn_scratch = nullptr;
@@ -379,6 +384,7 @@ int quantize_rows(kr_ctx* c, const float* x, size_t rows, size_t k, size_t strid
     HIPCHK(c, kr::launch_quantize(c->stream, x, rows, k, stride, c->wq, c->ws, c->wh));
     c->q_rows = rows;
     c->q_width = k;
+    c->q_chain_major = false;
     return KR_OK;
 }
 
@@ -476,6 +482,31 @@ std::vector<uint32_t> to_u32(const size_t* v, size_t n) {
     return out;
 }
 
+// The chain-split prefill GEMM applies to a Q8_0 matrix with K % 128 == 0
+// (four equal partial sums) and few rows, where the plain tiles leave most of
+// the device idle.
+bool chain_split_ok(const DevMatrix& m, size_t rows) {
+    return m.storage == KR_STORAGE_Q8_0 && m.k % 128 == 0 && rows >= 8 && rows <= 256;
+}
+
+int ensure_chain_major(kr_ctx* c, const Mat* mt, const DevMatrix** out) {
+    Mat* m = const_cast<Mat*>(mt);
+    if (!m->cm.q) {
+        DevMatrix cm{};
+        cm.storage = KR_STORAGE_Q8_0, cm.n = m->m.n, cm.k = m->m.k;
+        hipError_t e = hipMalloc(&cm.q, cm.n * cm.k);
+        if (e == hipSuccess) e = hipMalloc(&cm.s, cm.n * (cm.k / 32) * sizeof(float));
+        if (e == hipSuccess) e = kr::launch_chain_major(c->stream, m->m, cm.q, (float*)cm.s);
+        if (e != hipSuccess) {
+            free_devmatrix(cm);
+            HIPCHK(c, e);
+        }
+        m->cm = cm;
+    }
+    *out = &m->cm;
+    return KR_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -531,6 +562,7 @@ void kr_close(kr_ctx* c) {
         if (m) {
             free_devmatrix(m->m);
             free_devmatrix(m->requant);
+            free_devmatrix(m->cm);
             delete m;
         }
     for (auto& kv : c->rope)
@@ -670,6 +702,7 @@ int kr_matrix_free(kr_ctx* c, kr_mat h) {
     HIPCHK(c, hipStreamSynchronize(c->stream));
     free_devmatrix(m->m);
     free_devmatrix(m->requant);
+    free_devmatrix(m->cm);
     delete m;
     c->mats[h] = nullptr;
     return KR_OK;
@@ -1025,11 +1058,36 @@ int kr_quantize_rows(kr_ctx* c, kr_buf x, size_t rows, size_t width) {
 int kr_matmul_quantized(kr_ctx* c, kr_mat w, kr_buf y, size_t rows) {
     Mat* m = mat_of(c, w);
     CHECK(c, m != nullptr, "unknown matrix %u", (unsigned)w);
-    CHECK(c, rows <= c->q_rows && m->m.k == c->q_width, "the workspace holds %zu rows of %zu, not %zu of %zu",
-          c->q_rows, c->q_width, rows, m->m.k);
+    CHECK(c, rows <= c->q_rows && m->m.k == c->q_width && !c->q_chain_major,
+          "the workspace holds %zu rows of %zu, not %zu of %zu", c->q_rows, c->q_width, rows, m->m.k);
     BUF(yb, y, rows * m->m.n);
     if (rows == 0) return KR_OK;
     HIPCHK(c, kr::launch_project(c->stream, sem_for_project(m->m), m->m, act(c), rows, yb->p, m->m.n, nullptr));
+    return KR_OK;
+}
+
+int kr_matmul_split(kr_ctx* c, kr_mat w, kr_buf x, kr_buf y, size_t rows) {
+    Mat* m = mat_of(c, w);
+    CHECK(c, m != nullptr, "unknown matrix %u", (unsigned)w);
+    CHECK(c, m->m.storage == KR_STORAGE_Q8_0 && m->m.k % 128 == 0,
+          "the chain-split projection needs a Q8_0 matrix with in_dim %% 128 == 0");
+    BUF(yb, y, 4 * rows * m->m.n);
+    if (x != KR_NO_BUF) {
+        BUF(xb, x, rows * m->m.k);
+        int rc = ensure_workspace(c, rows, m->m.k);
+        if (rc) return rc;
+        HIPCHK(c, kr::launch_quantize(c->stream, xb->p, rows, m->m.k, m->m.k, c->wq, c->ws, c->wh, true));
+        c->q_rows = rows;
+        c->q_width = m->m.k;
+        c->q_chain_major = true;
+    }
+    CHECK(c, rows <= c->q_rows && m->m.k == c->q_width && c->q_chain_major,
+          "the workspace does not hold %zu chain-major rows of %zu", rows, m->m.k);
+    if (rows == 0) return KR_OK;
+    const DevMatrix* cm = nullptr;
+    int rc = ensure_chain_major(c, m, &cm);
+    if (rc) return rc;
+    HIPCHK(c, kr::launch_gemm_q8_cs(c->stream, *cm, act(c), rows, yb->p));
     return KR_OK;
 }
 
@@ -1041,8 +1099,8 @@ int kr_matmul_quantized_set(kr_ctx* c, const kr_mat* w, const kr_buf* y, int n, 
         Mat* m = mat_of(c, w[i]);
         CHECK(c, m != nullptr, "unknown matrix %u", (unsigned)w[i]);
         ms[i] = &m->m;
-        CHECK(c, rows <= c->q_rows && ms[i]->k == c->q_width, "the workspace holds %zu rows of %zu, not %zu of %zu",
-              c->q_rows, c->q_width, rows, ms[i]->k);
+        CHECK(c, rows <= c->q_rows && ms[i]->k == c->q_width && !c->q_chain_major,
+              "the workspace holds %zu rows of %zu, not %zu of %zu", c->q_rows, c->q_width, rows, ms[i]->k);
         CHECK(c, ms[i]->storage == ms[0]->storage, "the matrices of one launch share their storage");
         BUF(yb, y[i], rows * ms[i]->n);
         yp[i] = yb->p;
@@ -1345,23 +1403,36 @@ int attention_dev(kr_ctx* c, kr_buf q, kr_buf out, kr_buf att, size_t layer, con
     return KR_OK;
 }
 
-int norm_quant(kr_ctx* c, kr_buf x, kr_buf add, kr_buf w, kr_buf out, size_t rows, size_t dim, float eps) {
+int norm_quant(kr_ctx* c, kr_buf x, kr_buf add, int add_planes, kr_buf w, kr_buf out, size_t rows, size_t dim,
+               float eps, bool chain_major) {
     CHECK(c, dim % 32 == 0 && dim <= 8000, "fused norm needs dim %% 32 == 0 and dim <= 8000 (got %zu)", dim);
+    CHECK(c, add_planes == 1 || add_planes == 4, "an added projection comes as 1 or 4 planes");
+    CHECK(c, !chain_major || dim % 128 == 0, "chain-major blocks need dim %% 128 == 0");
     BUF(xb, x, rows * dim);
     BUF(wb, w, dim);
     BUF(ob, out, rows * dim);
     const float* ap = nullptr;
     if (add != KR_NO_BUF) {
-        BUF(ab, add, rows * dim);
+        BUF(ab, add, add_planes * rows * dim);
         ap = ab->p;
     }
     int rc = ensure_workspace(c, rows, dim);
     if (rc) return rc;
-    HIPCHK(c, kr::launch_add_rms_quant(c->stream, xb->p, ap, wb->p, ob->p, rows, dim, eps, c->wq, c->ws, c->wh));
+    HIPCHK(c, kr::launch_add_rms_quant(c->stream, xb->p, ap, wb->p, ob->p, rows, dim, eps, c->wq, c->ws, c->wh,
+                                       add_planes, chain_major));
     c->q_rows = rows;
     c->q_width = dim;
+    c->q_chain_major = chain_major;
     return KR_OK;
 }
+
+int add_planes(kr_ctx* c, kr_buf dst, kr_buf planes, size_t len) {
+    BUF(d, dst, len);
+    BUF(p, planes, 4 * len);
+    HIPCHK(c, kr::launch_add_planes(c->stream, d->p, p->p, len));
+    return KR_OK;
+}
+
 
 int project_q(kr_ctx* c, size_t layer, const int* projs, const kr_buf* ys, int n, size_t rows) {
     CHECK(c, c->prepared && layer < c->n_layers, "layer %zu out of range", layer);
@@ -1373,8 +1444,8 @@ int project_q(kr_ctx* c, size_t layer, const int* projs, const kr_buf* ys, int n
         const Mat* m = proj_mat(c, layer, projs[i]);
         CHECK(c, m != nullptr, "projection %d is not live on layer %zu", projs[i], layer);
         ms[i] = &m->m;
-        CHECK(c, rows <= c->q_rows && ms[i]->k == c->q_width, "the workspace holds %zu rows of %zu, not %zu of %zu",
-              c->q_rows, c->q_width, rows, ms[i]->k);
+        CHECK(c, rows <= c->q_rows && ms[i]->k == c->q_width && !c->q_chain_major,
+              "the workspace holds %zu rows of %zu, not %zu of %zu", c->q_rows, c->q_width, rows, ms[i]->k);
         BUF(yb, ys[i], rows * ms[i]->n);
         yp[i] = yb->p;
         same = same && ms[i]->storage == ms[0]->storage;
@@ -1403,20 +1474,28 @@ bool ffn_swiglu_ok(kr_ctx* c, size_t layer, size_t rows) {
     const Mat* d = proj_mat(c, layer, KR_PROJ_DOWN);
     return g && u && d && g->m.storage == KR_STORAGE_Q8_0 && u->m.storage == KR_STORAGE_Q8_0 &&
            g->m.n == u->m.n && g->m.k == u->m.k && g->m.n % 32 == 0 && d->m.k == g->m.n &&
-           sem_for_project(g->m) == kr::SEM_FOUR_PARTIALS_F32 && rows <= c->q_rows && g->m.k == c->q_width;
+           sem_for_project(g->m) == kr::SEM_FOUR_PARTIALS_F32 && rows <= c->q_rows && g->m.k == c->q_width &&
+           !c->q_chain_major;
 }
 
-int ffn_swiglu_down(kr_ctx* c, size_t layer, size_t rows, kr_buf out) {
+int ffn_swiglu_down(kr_ctx* c, size_t layer, size_t rows, kr_buf out, int max_planes, int* planes) {
     CHECK(c, ffn_swiglu_ok(c, layer, rows), "the fused gate/up + SiLU GEMM does not apply to layer %zu", layer);
     const Mat* g = proj_mat(c, layer, KR_PROJ_GATE);
     const Mat* u = proj_mat(c, layer, KR_PROJ_UP);
     const Mat* d = proj_mat(c, layer, KR_PROJ_DOWN);
-    BUF(ob, out, rows * d->m.n);
+    const bool split = max_planes == 4 && chain_split_ok(d->m, rows);
+    BUF(ob, out, (split ? 4 : 1) * rows * d->m.n);
     int rc = ensure_workspace2(c, rows, g->m.n);
     if (rc) return rc;
-    HIPCHK(c, kr::launch_gate_up_silu_q8(c->stream, g->m, u->m, act(c), rows, c->wq2, c->ws2, c->wh2));
-    HIPCHK(c, kr::launch_project(c->stream, sem_for_project(d->m), d->m, kr::QuantAct{c->wq2, c->ws2, c->wh2}, rows,
-                                 ob->p, d->m.n, nullptr));
+    const DevMatrix* dc = nullptr;
+    if (split && (rc = ensure_chain_major(c, d, &dc)) != KR_OK) return rc;
+    HIPCHK(c, kr::launch_gate_up_silu_q8(c->stream, g->m, u->m, act(c), rows, c->wq2, c->ws2, c->wh2, split));
+    const kr::QuantAct h{c->wq2, c->ws2, c->wh2};
+    if (split)
+        HIPCHK(c, kr::launch_gemm_q8_cs(c->stream, *dc, h, rows, ob->p));
+    else
+        HIPCHK(c, kr::launch_project(c->stream, sem_for_project(d->m), d->m, h, rows, ob->p, d->m.n, nullptr));
+    *planes = split ? 4 : 1;
     return KR_OK;
 }
 
@@ -1429,6 +1508,7 @@ int silu_quant(kr_ctx* c, kr_buf gate, kr_buf up, size_t rows, size_t width) {
     HIPCHK(c, kr::launch_silu_quant(c->stream, g->p, u->p, rows, width, c->wq, c->ws, c->wh));
     c->q_rows = rows;
     c->q_width = width;
+    c->q_chain_major = false;
     return KR_OK;
 }
 
@@ -1524,6 +1604,7 @@ int attention_quant(kr_ctx* c, kr_buf q, kr_buf out, kr_buf att, size_t layer, c
     }
     c->q_rows = n;
     c->q_width = width;
+    c->q_chain_major = false;
     return KR_OK;
 }
 
@@ -1535,7 +1616,8 @@ int logits_q(kr_ctx* c, kr_buf y) {
     int sem;
     int rc = classifier_matrix(c, mt, &m, &sem);
     if (rc) return rc;
-    CHECK(c, c->q_rows >= 1 && c->q_width == m->k, "the workspace does not hold the classifier input");
+    CHECK(c, c->q_rows >= 1 && c->q_width == m->k && !c->q_chain_major,
+          "the workspace does not hold the classifier input");
     BUF(yb, y, m->n);
     HIPCHK(c, kr::launch_project(c->stream, sem, *m, act(c), 1, yb->p, m->n, nullptr));
     return KR_OK;
@@ -1653,6 +1735,7 @@ int norm_swiglu(kr_ctx* c, size_t layer, kr_buf x, kr_buf add, kr_buf w, kr_buf 
                                         c->wq, c->ws, c->wh, hb->p));
     c->q_rows = 1;
     c->q_width = hidden;
+    c->q_chain_major = false;
     return KR_OK;
 }
 
@@ -1728,7 +1811,8 @@ int logits_rows(kr_ctx* c, kr_buf y, size_t rows) {
     int sem;
     int rc = classifier_matrix(c, mt, &m, &sem);
     if (rc) return rc;
-    CHECK(c, c->q_rows >= rows && c->q_width == m->k, "the workspace does not hold the classifier input");
+    CHECK(c, c->q_rows >= rows && c->q_width == m->k && !c->q_chain_major,
+          "the workspace does not hold the classifier input");
     BUF(yb, y, rows * m->n);
     HIPCHK(c, kr::launch_project(c->stream, sem, *m, act(c), rows, yb->p, m->n, nullptr));
     return KR_OK;

@@ -75,6 +75,11 @@ __device__ __forceinline__ void quant_lane(float v, bool valid, int8_t* q, float
     }
 }
 
+// Position of block t in a chain-major row of nb blocks (nb % 4 == 0): the
+// blocks of the reference's partial sum 0 (t = 0, 4, 8, ..), then those of
+// sums 1, 2 and 3, each in block order.
+__device__ __forceinline__ uint32_t cm_block(uint32_t t, uint32_t nb) { return (t & 3) * (nb >> 2) + (t >> 2); }
+
 __device__ __forceinline__ uint32_t win_slot(const DevWindow& w, uint32_t n_shared, uint32_t i) {
     return i < n_shared ? w.shared_start + i : w.att_start + (i - n_shared);
 }

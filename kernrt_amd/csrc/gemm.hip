@@ -59,14 +59,24 @@ __device__ __forceinline__ uint32_t gemm_xcd_tile(uint32_t id, uint32_t count) {
 // blocks as the epilogue (silu_quant's arithmetic, elementwise.rs / quant.rs:
 // 864-873): the tile's 64 columns are gate rows 32 t .. 32 t + 31 (ms.q[0])
 // and up rows 32 t .. 32 t + 31 (ms.q[1]) of the same hidden block t, and the
-// outputs are h's int8 quants and block scales in `so` instead of f32 gate/up.
+// outputs are h's int8 quants and block scales in `so` instead of f32 gate/up,
+// in chain-major block order when `cm` is set (for a chain-split down).
 struct SwiOut {
     int8_t* q;
     float* s;
     uint16_t* h;
+    uint32_t cm;
 };
 
-template <int SEM, int TM, int TN, int NJ, int CPW, int KC, int NS, int RS, int WPE, bool DBG, bool SWI = false>
+// CS: the chain-split form for launches with few output tiles. Operands
+// are chain-major (each row holds the blocks of chain 0 -- blocks 0, 4, 8,
+// .. -- then those of chains 1, 2 and 3, with the scales in the same order),
+// a workgroup runs one chain of one tile over that chain's contiguous quarter
+// of K, all of its blocks into one accumulator in block order, and writes the
+// chain's partial sums as plane `chain` of y ([4][M][ld]); the consumer adds
+// the four planes as ((t0 + t1) + t2) + t3.
+template <int SEM, int TM, int TN, int NJ, int CPW, int KC, int NS, int RS, int WPE, bool DBG, bool SWI = false,
+          bool CS = false>
 __global__ __launch_bounds__(64 * (TM / 32) * (TN / (32 * NJ)) * (4 / CPW), WPE) void k_gemm_q8(
     MatSet ms, QuantAct x, uint32_t M, uint32_t K, uint32_t mtiles, int32_t* __restrict__ dbg, SwiOut so) {
     constexpr int WN = 32 * NJ, SM = TM / 32, NSUB = SM * (TN / WN), CG = 4 / CPW, NT = 64 * NSUB * CG;
@@ -83,6 +93,7 @@ __global__ __launch_bounds__(64 * (TM / 32) * (TN / (32 * NJ)) * (4 / CPW), WPE)
     static_assert(CPW == 1 || CPW == 2 || CPW == 4, "chains per wave");
     static_assert(NT % PPR == 0, "a thread's pieces share their column");
     static_assert(!SWI || (TN == 64 && NJ == 2 && CPW < 4), "the SwiGLU epilogue needs one gate and one up unit per wave");
+    static_assert(!CS || (CPW == 4 && !SWI && !DBG), "a chain-split wave runs its tile's one chain");
     constexpr bool WF16 = SEM == SEM_FOUR_PARTIALS_F16;
     __shared__ __align__(16) int8_t lds[LDS_BYTES];
     uint64_t* const etab = (uint64_t*)(lds + RING_BYTES);
@@ -91,9 +102,13 @@ __global__ __launch_bounds__(64 * (TM / 32) * (TN / (32 * NJ)) * (4 / CPW), WPE)
     auto sX = [&](int buf) { return (float*)(lds + buf * BUF_BYTES + A_BYTES + B_BYTES); };  // [block][row]
     auto sW = [&](int buf) { return sX(buf) + KC * TM; };                                     // [block][col]
 
-    const uint32_t nb = K >> 5, nchunks = (nb + KC - 1) / KC;
+    // K: the row length (bytes, and 32 scales per block); nb: the blocks this
+    // workgroup sums, from block koff / 32 of each row on (a chain's quarter
+    // for CS)
     const uint32_t L = gemm_xcd_tile(blockIdx.x, gridDim.x);
-    const uint32_t mt = L % mtiles, nt = L / mtiles;
+    const uint32_t mt = L % mtiles, chain = CS ? (L / mtiles) & 3 : 0, nt = CS ? L / mtiles / 4 : L / mtiles;
+    const uint32_t nbr = K >> 5, nb = CS ? nbr / 4 : nbr, nchunks = (nb + KC - 1) / KC;
+    const uint32_t kend = nb * 32, koff = chain * kend, soff = chain * nb;
     const int mi_ = SWI ? 0 : nt < ms.tile_end[0] ? 0 : (nt < ms.tile_end[1] ? 1 : 2);
     const uint32_t m0 = mt * TM, n0 = SWI ? nt * 32 : (nt - (mi_ == 0 ? 0 : ms.tile_end[mi_ > 0 ? mi_ - 1 : 0])) * TN;
     const int8_t* __restrict__ W = ms.q[mi_];
@@ -120,7 +135,7 @@ __global__ __launch_bounds__(64 * (TM / 32) * (TN / (32 * NJ)) * (4 / CPW), WPE)
             gp[i] = isb ? (row >= 32 ? ms.q[1] : ms.q[0]) + (size_t)min(n0 + (row & 31), N - 1) * K
                         : x.q + (size_t)min(m0 + row, M - 1) * K;
         else
-            gp[i] = isb ? W + (size_t)min(n0 + row, N - 1) * K : x.q + (size_t)min(m0 + row, M - 1) * K;
+            gp[i] = (isb ? W + (size_t)min(n0 + row, N - 1) * K : x.q + (size_t)min(m0 + row, M - 1) * K) + koff;
         lp[i] = (isb ? A_BYTES : 0) + row * ROW + (q % PPR) * 16;
     }
     const uint32_t pc = (tid % PPR) * 16;
@@ -131,22 +146,22 @@ __global__ __launch_bounds__(64 * (TM / 32) * (TN / (32 * NJ)) * (4 / CPW), WPE)
     };
     auto gload = [&](Stage& st, uint32_t c) {
         c = c < nchunks ? c : nchunks - 1;
-        const uint32_t col = min(c * KC * 32 + pc, K - 16);  // past the row end: a piece no block uses
+        const uint32_t col = min(c * KC * 32 + pc, kend - 16);  // past the end: a piece no block uses
 #pragma unroll
         for (int i = 0; i < NP; i++) st.p[i] = *(const g_v4i*)(gp[i] + col);
 #pragma unroll
         for (int i = 0; i < NSC; i++) {
             const uint32_t sidx = tid + NT * i;
-            const uint32_t blk = min(c * KC + sidx % KC, nb - 1);
+            const uint32_t blk = soff + min(c * KC + sidx % KC, nb - 1);
             if (sidx < KC * TM) {
-                st.sc[i] = f2u(x.s[(size_t)min(m0 + sidx / KC, M - 1) * nb + blk]);
+                st.sc[i] = f2u(x.s[(size_t)min(m0 + sidx / KC, M - 1) * nbr + blk]);
             } else if (sidx < KC * (TM + TN)) {
                 const uint32_t col2 = (sidx - KC * TM) / KC;
                 if (SWI)
                     st.sc[i] = scale_bits(WF16, col2 >= 32 ? ms.s[1] : ms.s[0],
-                                          (size_t)min(n0 + (col2 & 31), N - 1) * nb + blk);
+                                          (size_t)min(n0 + (col2 & 31), N - 1) * nbr + blk);
                 else
-                    st.sc[i] = scale_bits(WF16, WS, (size_t)min(n0 + col2, N - 1) * nb + blk);
+                    st.sc[i] = scale_bits(WF16, WS, (size_t)min(n0 + col2, N - 1) * nbr + blk);
             }
         }
     };
@@ -190,8 +205,8 @@ __global__ __launch_bounds__(64 * (TM / 32) * (TN / (32 * NJ)) * (4 / CPW), WPE)
             c2 = 0, j = 0, blk = (int)cg + 4 * (2 * p + u);
         }
     };
-    constexpr int PAIRS = NJ == 2 ? KC / 4 * CPW : KC / 8 * CPW;
-    static_assert(PAIRS % 2 == 0, "the register pipeline alternates two sets per pair");
+    constexpr int PAIRS = NJ == 2 ? KC / 4 * CPW : KC * CPW / 8;
+    static_assert(PAIRS > 0 && PAIRS % 2 == 0, "the register pipeline alternates two sets per pair");
 
     // One pair's operands (two i8 fragments per unit, the lane's 2b scale
     // operands) and results (the two units' block dots, their scale products).
@@ -240,12 +255,12 @@ __global__ __launch_bounds__(64 * (TM / 32) * (TN / (32 * NJ)) * (4 / CPW), WPE)
                 if (m < M && nn1 < N && b1 < nb) dbg[((size_t)m * N + nn1) * nb + b1] = r.d1[v];
             }
         }
-        // dot.rs: t[b & 3] += (sa * sb) * (isum as f32)
+        // dot.rs: t[b & 3] += (sa * sb) * (isum as f32); CS: every block is the chain's
 #pragma unroll
-        for (int v = 0; v < 16; v++) t[c20][j0][v] += r.P[v] * (float)r.d0[v];
+        for (int v = 0; v < 16; v++) t[CS ? 0 : c20][j0][v] += r.P[v] * (float)r.d0[v];
         if (b1 < nb) {
 #pragma unroll
-            for (int v = 0; v < 16; v++) t[c21][j1][v] += r.P[16 + v] * (float)r.d1[v];
+            for (int v = 0; v < 16; v++) t[CS ? 0 : c21][j1][v] += r.P[16 + v] * (float)r.d1[v];
         }
     };
 
@@ -318,7 +333,17 @@ __global__ __launch_bounds__(64 * (TM / 32) * (TN / (32 * NJ)) * (4 / CPW), WPE)
 
     float* Y = ms.y[mi_];
     const uint32_t ld = ms.ld[mi_];
-    if constexpr (CPW == 4) {
+    if constexpr (CS) {
+        // the chain's partial sums, plane `chain`
+        float* P = Y + (size_t)chain * M * ld;
+#pragma unroll
+        for (int j = 0; j < NJ; j++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const uint32_t m = m0 + wm0 + 8 * (v >> 2) + 4 * half + (v & 3), n = n0 + wn0 + 32 * j + r32;
+                if (m < M && n < N) P[(size_t)m * ld + n] = t[0][j][v];
+            }
+    } else if constexpr (CPW == 4) {
         // one wave holds all four chains of its outputs
 #pragma unroll
         for (int j = 0; j < NJ; j++)
@@ -351,7 +376,7 @@ __global__ __launch_bounds__(64 * (TM / 32) * (TN / (32 * NJ)) * (4 / CPW), WPE)
             // element e: (sub, v4, lane): rows 8 v4 + 4 (lane / 32) + 0..3 of
             // hidden column n0 + lane % 32, its gate (unit 0) and up (unit 1);
             // the 32 lanes of a half-wave hold one row's Q8 block
-            const uint32_t nbh = N >> 5;
+            const uint32_t nbh = N >> 5, pb = so.cm ? cm_block(n0 >> 5, nbh) : n0 >> 5;
 #pragma unroll
             for (int k = 0; k < TM * 8 / NT; k++) {
                 const uint32_t e = tid + NT * k, sb = e >> 8, v4 = (e >> 6) & 3, l = e & 63;
@@ -364,9 +389,8 @@ __global__ __launch_bounds__(64 * (TM / 32) * (TN / (32 * NJ)) * (4 / CPW), WPE)
                     const bool live = mb + r < M;
                     // cpu.rs:708-710: silu(g) * u
                     const float h = div_rn(gv[r], 1.0f + glibc_expf(-gv[r], etab)) * uv[r];
-                    const size_t oi = (size_t)(live ? mb + r : 0) * N + col;
-                    quant_lane(h, live, so.q + oi, so.s + (size_t)(live ? mb + r : 0) * nbh + (n0 >> 5),
-                               so.h + (size_t)(live ? mb + r : 0) * nbh + (n0 >> 5));
+                    const size_t orow = live ? mb + r : 0, oi = orow * N + pb * 32 + (col & 31);
+                    quant_lane(h, live, so.q + oi, so.s + orow * nbh + pb, so.h + orow * nbh + pb);
                 }
             }
             return;
@@ -406,6 +430,16 @@ static void launch_q8(hipStream_t st, MatSet ms, QuantAct x, size_t rows, size_t
     else
         hipLaunchKernelGGL((k_gemm_q8<SEM, TM, TN, NJ, CPW, KC, NS, RS, WPE, false>), grid, block, 0, st, ms, x,
                            (uint32_t)rows, (uint32_t)k, mtiles, dbg, SwiOut{});
+}
+
+// The chain-split form: tiles x 4 chains; y[0] receives [4][rows][ld].
+template <int TM, int TN, int NJ, int KC, int NS, int RS, int WPE>
+static void launch_q8_cs(hipStream_t st, MatSet ms, QuantAct x, size_t rows, size_t k) {
+    const uint32_t ntiles = (ms.n[0] + TN - 1) / TN, mtiles = (uint32_t)((rows + TM - 1) / TM);
+    ms.tile_end[0] = ms.tile_end[1] = ms.tile_end[2] = ntiles;
+    const dim3 grid(ntiles * 4 * mtiles), block(64 * (TM / 32) * (TN / (32 * NJ)));
+    hipLaunchKernelGGL((k_gemm_q8<SEM_FOUR_PARTIALS_F32, TM, TN, NJ, 4, KC, NS, RS, WPE, false, false, true>), grid,
+                       block, 0, st, ms, x, (uint32_t)rows, (uint32_t)k, mtiles, nullptr, SwiOut{});
 }
 
 // The SwiGLU form: one tile per (row block, hidden block of 32).
@@ -680,21 +714,53 @@ hipError_t launch_mfma_f32_probe(hipStream_t st, const float* a, const float* b,
 }
 
 hipError_t launch_gate_up_silu_q8(hipStream_t st, const DevMatrix& gate, const DevMatrix& up, QuantAct x, size_t rows,
-                                  int8_t* hq, float* hs, uint16_t* hh) {
+                                  int8_t* hq, float* hs, uint16_t* hh, bool chain_major) {
     if (gate.storage != KR_STORAGE_Q8_0 || up.storage != KR_STORAGE_Q8_0 || gate.n != up.n || gate.k != up.k ||
-        gate.n % 32 != 0 || rows == 0)
+        gate.n % 32 != 0 || rows == 0 || (chain_major && gate.n % 128 != 0))
         return hipErrorInvalidValue;
     MatSet ms{};
     ms.q[0] = gate.q, ms.q[1] = up.q;
     ms.s[0] = gate.s, ms.s[1] = up.s;
     ms.n[0] = ms.n[1] = (uint32_t)gate.n;
     ms.count = 2;
-    const SwiOut so{hq, hs, hh};
+    const SwiOut so{hq, hs, hh, chain_major ? 1u : 0u};
     const size_t m128 = (rows + 127) / 128, blocks = gate.n / 32;
     if (rows > 64 && m128 * blocks >= 200)
         launch_q8_swi<128, 2, 2, 4, 3, 1, 1>(st, ms, x, rows, gate.k, so);
     else
         launch_q8_swi<64, 2, 1, 8, 2, 2, 1>(st, ms, x, rows, gate.k, so);
+    return hipGetLastError();
+}
+
+// The chain-major copy of a Q8_0 matrix: each row's blocks reordered by
+// cm_block, scales with them. One thread per 16-byte half block.
+__global__ __launch_bounds__(256) void k_chain_major(const int8_t* __restrict__ q, const float* __restrict__ s,
+                                                     int8_t* __restrict__ cq, float* __restrict__ cs, uint32_t nb,
+                                                     size_t pieces) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= pieces) return;
+    const size_t row = i / (2 * nb);
+    const uint32_t rem = (uint32_t)(i - row * 2 * nb), b = rem >> 1, h = rem & 1, p = cm_block(b, nb);
+    const size_t rb = row * nb;
+    *(g_v4i*)(cq + (rb + p) * 32 + 16 * h) = *(const g_v4i*)(q + (rb + b) * 32 + 16 * h);
+    if (h == 0) cs[rb + p] = s[rb + b];
+}
+
+hipError_t launch_chain_major(hipStream_t st, const DevMatrix& m, int8_t* cq, float* cs) {
+    if (m.storage != KR_STORAGE_Q8_0 || m.k % 128 != 0) return hipErrorInvalidValue;
+    const uint32_t nb = (uint32_t)(m.k / 32);
+    const size_t pieces = m.n * nb * 2;
+    hipLaunchKernelGGL(k_chain_major, dim3((unsigned)((pieces + 255) / 256)), dim3(256), 0, st, m.q,
+                       (const float*)m.s, cq, cs, nb, pieces);
+    return hipGetLastError();
+}
+
+hipError_t launch_gemm_q8_cs(hipStream_t st, const DevMatrix& cm, QuantAct x, size_t rows, float* y4) {
+    if (cm.storage != KR_STORAGE_Q8_0 || cm.k % 128 != 0 || rows == 0) return hipErrorInvalidValue;
+    MatSet ms{};
+    ms.q[0] = cm.q, ms.s[0] = cm.s, ms.y[0] = y4, ms.n[0] = (uint32_t)cm.n, ms.ld[0] = (uint32_t)cm.n;
+    ms.count = 1;
+    launch_q8_cs<64, 64, 1, 4, 3, 2, 1>(st, ms, x, rows, cm.k);
     return hipGetLastError();
 }
 

@@ -41,8 +41,10 @@ int greedy_step(kr_ctx* c, kr_buf logits, size_t len, uint32_t* step);
 // Fused driver steps. Each leaves the Q8 quantization of its output rows in
 // the backend's activation workspace, which project_q / logits_q consume.
 // x += add (add may be KR_NO_BUF), out = rms_norm(x, w), quantize(out)
-constexpr kr_buf KR_NO_BUF = 0xffffffffu;
-int norm_quant(kr_ctx* c, kr_buf x, kr_buf add, kr_buf w, kr_buf out, size_t rows, size_t dim, float eps);
+int norm_quant(kr_ctx* c, kr_buf x, kr_buf add, int add_planes, kr_buf w, kr_buf out, size_t rows, size_t dim,
+               float eps, bool chain_major = false);
+// dst += ((p0 + p1) + p2) + p3 over the four planes of a chain-split projection
+int add_planes(kr_ctx* c, kr_buf dst, kr_buf planes, size_t len);
 // projections of the quantized workspace rows; one launch when they share in_dim and storage
 int project_q(kr_ctx* c, size_t layer, const int* projs, const kr_buf* ys, int n, size_t rows);
 // out[oo + r os + i] = a[ao + r as + i] * b[bo + r bs + i], r < rows, i < n, one launch
@@ -54,7 +56,9 @@ int silu_quant(kr_ctx* c, kr_buf gate, kr_buf up, size_t rows, size_t width);
 // prefill FFN after the norm's quantization: gate/up + SiLU * up + Q8 in one
 // GEMM launch, then down into `out` (Q8_0 gate/up, rows >= 8)
 bool ffn_swiglu_ok(kr_ctx* c, size_t layer, size_t rows);
-int ffn_swiglu_down(kr_ctx* c, size_t layer, size_t rows, kr_buf out);
+// max_planes 4: the down projection may run chain-split and leave its four
+// partial-sum planes in `out` (room for 4 x rows x dim); *planes says which
+int ffn_swiglu_down(kr_ctx* c, size_t layer, size_t rows, kr_buf out, int max_planes, int* planes);
 // rope of q and k, then k and v into the cache; positions and slots from the
 // host (pos_host/slot_host) or one device position (pos_dev, rows == 1)
 int rope_kv(kr_ctx* c, kr_buf q, kr_buf k, kr_buf v, size_t qw, size_t kvw, size_t rows, const size_t* pos_host,

@@ -118,7 +118,7 @@ __device__ __forceinline__ int dot16(const v4i& w, const v4i& x) {
 __global__ __launch_bounds__(256) void k_quantize(const float* __restrict__ x, size_t total_blocks,
                                                   uint32_t nb, uint32_t k, size_t x_stride,
                                                   int8_t* __restrict__ q, float* __restrict__ s,
-                                                  uint16_t* __restrict__ h) {
+                                                  uint16_t* __restrict__ h, uint32_t cm) {
     size_t gid = (size_t)blockIdx.x * 256 + threadIdx.x;
     size_t blk = gid >> 5;
     int lane = threadIdx.x & 31;
@@ -130,22 +130,24 @@ __global__ __launch_bounds__(256) void k_quantize(const float* __restrict__ x, s
     float d = div_rn(m, 127.0f);
     float inv = d > 0.0f ? div_rn(1.0f, d) : 0.0f;
     if (valid) {
-        q[row * k + b * 32 + lane] = q8_round(v * inv);
+        const size_t pb = row * nb + (cm ? cm_block((uint32_t)b, nb) : (uint32_t)b);  // cm: chain-major order
+        q[pb * 32 + lane] = q8_round(v * inv);
         if (lane == 0) {
-            s[blk] = d;
-            h[blk] = f16_bits(d);
+            s[pb] = d;
+            h[pb] = f16_bits(d);
         }
     }
 }
 
 hipError_t launch_quantize(hipStream_t st, const float* x, size_t rows, size_t k, size_t x_stride,
-                           int8_t* q, float* s, uint16_t* h) {
+                           int8_t* q, float* s, uint16_t* h, bool chain_major) {
     size_t nb = k / 32, total = rows * nb;
     if (total == 0) return hipSuccess;
+    if (chain_major && nb % 4 != 0) return hipErrorInvalidValue;
     size_t threads = total * 32;
     dim3 grid((unsigned)((threads + 255) / 256));
     hipLaunchKernelGGL(k_quantize, grid, dim3(256), 0, st, x, total, (uint32_t)nb, (uint32_t)k, x_stride,
-                       q, s, h);
+                       q, s, h, chain_major ? 1u : 0u);
     return hipGetLastError();
 }
 
@@ -3163,11 +3165,15 @@ hipError_t launch_attention(hipStream_t st, const float* q, float* out, float* a
 // sum, reading LDS in runs of 64 values per wait (one active lane: the same
 // loop on all 64 lanes of a wave ran 2.5x slower when other work shared the
 // CU). A Q8 block is 8 consecutive threads.
+// pstride > 0: `add` is four partial-sum planes of a chain-split projection,
+// pstride floats apart, added as ((p0 + p1) + p2) + p3 (dot.rs:45) before the
+// residual add. cm: the Q8 blocks go out in chain-major order (cm_block).
 template <bool ADD, int VPT>
 __global__ __launch_bounds__(256) void k_add_rms_quant(float* __restrict__ x, const float* __restrict__ add,
                                                        const float* __restrict__ w, float* __restrict__ out,
                                                        uint32_t dim, float eps, int8_t* __restrict__ q,
-                                                       float* __restrict__ s, uint16_t* __restrict__ h) {
+                                                       float* __restrict__ s, uint16_t* __restrict__ h,
+                                                       size_t pstride, uint32_t cm) {
     extern __shared__ __align__(16) float sq[];  // [dim]
     __shared__ float s_scale;
     const uint32_t tid = threadIdx.x, n4 = dim / 4;
@@ -3181,7 +3187,14 @@ __global__ __launch_bounds__(256) void k_add_rms_quant(float* __restrict__ x, co
             v[u] = xr[f];
             wv[u] = ((const float4*)w)[f];
             if (ADD) {
-                const float4 a = ((const float4*)(add + row * dim))[f];
+                float4 a = ((const float4*)(add + row * dim))[f];
+                if (pstride) {
+                    const float4 a1 = ((const float4*)(add + pstride + row * dim))[f];
+                    const float4 a2 = ((const float4*)(add + 2 * pstride + row * dim))[f];
+                    const float4 a3 = ((const float4*)(add + 3 * pstride + row * dim))[f];
+                    a = make_float4(((a.x + a1.x) + a2.x) + a3.x, ((a.y + a1.y) + a2.y) + a3.y,
+                                    ((a.z + a1.z) + a2.z) + a3.z, ((a.w + a1.w) + a2.w) + a3.w);
+                }
                 v[u] = make_float4(v[u].x + a.x, v[u].y + a.y, v[u].z + a.z, v[u].w + a.w);
             }
         }
@@ -3225,24 +3238,29 @@ __global__ __launch_bounds__(256) void k_add_rms_quant(float* __restrict__ x, co
             qq.y = q8_round(o.y * inv);
             qq.z = q8_round(o.z * inv);
             qq.w = q8_round(o.w * inv);
-            ((char4*)(q + row * dim))[f] = qq;
+            const uint32_t pb = cm ? cm_block(f / 8, nb) : f / 8;
+            ((char4*)(q + row * dim + pb * 32))[f & 7] = qq;
             if ((f & 7) == 0) {
-                s[row * nb + f / 8] = d;
-                h[row * nb + f / 8] = f16_bits(d);
+                s[row * nb + pb] = d;
+                h[row * nb + pb] = f16_bits(d);
             }
         }
     }
 }
 
 hipError_t launch_add_rms_quant(hipStream_t st, float* x, const float* add, const float* w, float* out,
-                                size_t rows, size_t dim, float eps, int8_t* q, float* s, uint16_t* h) {
+                                size_t rows, size_t dim, float eps, int8_t* q, float* s, uint16_t* h, int add_planes,
+                                bool chain_major) {
     if (rows == 0) return hipSuccess;
-    if (dim % 32 != 0 || dim > 8192) return hipErrorInvalidValue;
+    if (dim % 32 != 0 || dim > 8192 || (add_planes != 1 && add_planes != 4) || (chain_major && dim % 128 != 0))
+        return hipErrorInvalidValue;
+    const size_t pstride = add_planes == 4 ? rows * dim : 0;
+    const uint32_t cm = chain_major ? 1u : 0u;
     const size_t lds = dim * sizeof(float);
     const size_t vpt = (dim / 4 + 255) / 256;
 #define KR_NORM_GO(A, V)                                                                                        \
     hipLaunchKernelGGL((k_add_rms_quant<A, V>), dim3((unsigned)rows), dim3(256), lds, st, x, add, w, out,      \
-                       (uint32_t)dim, eps, q, s, h)
+                       (uint32_t)dim, eps, q, s, h, pstride, cm)
 #define KR_NORM_V(A)          \
     if (vpt <= 1)             \
         KR_NORM_GO(A, 1);     \
@@ -3359,6 +3377,18 @@ __global__ void k_add(float* __restrict__ d, const float* __restrict__ s, size_t
 hipError_t launch_add(hipStream_t st, float* d, const float* s, size_t n) {
     if (n == 0) return hipSuccess;
     hipLaunchKernelGGL(k_add, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, d, s, n);
+    return hipGetLastError();
+}
+
+// d += ((p0 + p1) + p2) + p3 over the four partial-sum planes of a
+// chain-split projection, n floats each (dot.rs:45, then the residual add)
+__global__ void k_add_planes(float* __restrict__ d, const float* __restrict__ p, size_t n) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) d[i] = d[i] + (((p[i] + p[n + i]) + p[2 * n + i]) + p[3 * n + i]);
+}
+hipError_t launch_add_planes(hipStream_t st, float* d, const float* p, size_t n) {
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_add_planes, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, d, p, n);
     return hipGetLastError();
 }
 

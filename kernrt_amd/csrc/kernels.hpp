@@ -34,7 +34,7 @@ struct DevMatrix {  // device layout of one Q8 matrix
 };
 
 hipError_t launch_quantize(hipStream_t st, const float* x, size_t rows, size_t k, size_t x_stride,
-                           int8_t* q, float* s, uint16_t* h);
+                           int8_t* q, float* s, uint16_t* h, bool chain_major = false);
 
 // One launch over up to three matrices with the same in_dim and storage
 // (q/k/v, gate/up): output y[i] gets w[i]'s rows, row stride w[i]->n.
@@ -43,8 +43,11 @@ hipError_t launch_project_set(hipStream_t st, int sem, const DevMatrix* const* w
 
 // Fused decode/prefill steps (same arithmetic as the separate ops):
 // x += add (when add != null), out = rms_norm(x) and its Q8 quantization.
+// add_planes 4: `add` holds a chain-split projection's four partial-sum planes;
+// chain_major: the Q8 blocks in chain-major order (for launch_gemm_q8_cs)
 hipError_t launch_add_rms_quant(hipStream_t st, float* x, const float* add, const float* w, float* out,
-                                size_t rows, size_t dim, float eps, int8_t* q, float* s, uint16_t* h);
+                                size_t rows, size_t dim, float eps, int8_t* q, float* s, uint16_t* h,
+                                int add_planes = 1, bool chain_major = false);
 // g = silu(g) * u and its Q8 quantization, rows of `width`
 hipError_t launch_silu_quant(hipStream_t st, float* g, const float* u, size_t rows, size_t width, int8_t* q,
                              float* s, uint16_t* h);
@@ -65,8 +68,12 @@ bool swiglu_fusable(const DevMatrix& gate, const DevMatrix& up);
 // Prefill gate/up of Q8_0 matrices with SiLU(gate) * up and its Q8 blocks as
 // the GEMM's epilogue: h's quants / f32 scales / f16 scale bits [rows][n]
 // from the quantized rows x (one launch for gate/up + silu_quant).
+// The chain-split Q8_0 GEMM (gemm.hip): `cm` is a chain-major copy (launch_chain_major),
+// x chain-major too; y4 receives the four partial-sum planes [4][rows][cm.n].
+hipError_t launch_chain_major(hipStream_t st, const DevMatrix& m, int8_t* cq, float* cs);
+hipError_t launch_gemm_q8_cs(hipStream_t st, const DevMatrix& cm, QuantAct x, size_t rows, float* y4);
 hipError_t launch_gate_up_silu_q8(hipStream_t st, const DevMatrix& gate, const DevMatrix& up, QuantAct x, size_t rows,
-                                  int8_t* hq, float* hs, uint16_t* hh);
+                                  int8_t* hq, float* hs, uint16_t* hh, bool chain_major = false);
 hipError_t launch_gate_up_swiglu(hipStream_t st, int sem, const DevMatrix& gate, const DevMatrix& up, const float* x,
                                  const float* add, const float* norm_w, float* x_out, float eps, int8_t* hq,
                                  float* hs, uint16_t* hh, float* hf);
@@ -130,6 +137,7 @@ hipError_t launch_attention_split_rows(hipStream_t st, const float* q, float* ou
 bool attention_rows_uniform(const DevWindow* host_windows, size_t n_rows, size_t max_count, size_t kv_mul,
                             size_t hs);
 hipError_t launch_add(hipStream_t st, float* dst, const float* src, size_t n);
+hipError_t launch_add_planes(hipStream_t st, float* dst, const float* planes, size_t n);
 hipError_t launch_mul(hipStream_t st, float* out, const float* a, const float* b, size_t n,
                       int sequential);
 // o[r os + i] = a[r as + i] * b[r bs + i] for r < rows, i < n (no overlap of o with a or b)

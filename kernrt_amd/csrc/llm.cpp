@@ -195,14 +195,14 @@ int decode_step_fused(krl_model* m, size_t token, size_t pos, bool dev, size_t c
         KRC(m, kr_embed(b, token, m->x, 0));
     size_t positions[1] = {pos};
     kr_window win{0, pos, 0, 0};
-    kr_buf pending = kri::KR_NO_BUF;  // the residual still to add into x
+    kr_buf pending = KR_NO_BUF;  // the residual still to add into x
     // norm(x + add) feeding the projections projs -> ys
     auto norm_then = [&](kr_buf add, kr_buf w, size_t l, const int* projs, const kr_buf* ys, int n) -> int {
         if (pro) {
             KRC(m, kri::norm_project(b, l, projs, ys, n, X[cur], add, w, X[cur ^ 1], g.dim, g.eps));
             cur ^= 1;
         } else {
-            KRC(m, kri::norm_quant(b, X[cur], add, w, m->xb, 1, g.dim, g.eps));
+            KRC(m, kri::norm_quant(b, X[cur], add, 1, w, m->xb, 1, g.dim, g.eps));
             KRC(m, kri::project_q(b, l, projs, ys, n, 1));
         }
         return KR_OK;
@@ -268,7 +268,7 @@ int decode_step_fused(krl_model* m, size_t token, size_t pos, bool dev, size_t c
         KRC(m, kri::project_q(b, l, dn, &m->mlp, 1, 1));
         pending = m->mlp;
     }
-    KRC(m, kri::norm_quant(b, X[cur], pending, m->rms_final, m->xb, 1, g.dim, g.eps));
+    KRC(m, kri::norm_quant(b, X[cur], pending, 1, m->rms_final, m->xb, 1, g.dim, g.eps));
     KRC(m, kri::logits_q(b, m->logits));
     if (dev) KRC(m, kri::greedy_step(b, m->logits, m->c.vocab_size, m->step));
     return KR_OK;
@@ -338,7 +338,7 @@ int ensure_prefill(krl_model* m, size_t n_tok) {
     TRY(alloc(m, n_tok * g.kv_dim, &p.k));
     TRY(alloc(m, n_tok * g.kv_dim, &p.v));
     TRY(alloc(m, n_tok * g.q_dim, &p.attn));
-    TRY(alloc(m, n_tok * g.dim, &p.o));
+    TRY(alloc(m, 4 * n_tok * g.dim, &p.o));  // room for a chain-split projection's four planes
     if (m->lfm2) {
         TRY(alloc(m, n_tok * 3 * g.dim, &p.bcx));
         TRY(alloc(m, n_tok * g.dim, &p.h));
@@ -401,10 +401,13 @@ int prefill_rows(krl_model* m, const std::vector<Row>& rows, bool stepped_conv =
     if (m->fused) {
         // prefill_rows with the fused kernels (see decode_step_fused); the
         // last residual add is applied here because the final norm reads one row
-        kr_buf pending = kri::KR_NO_BUF;
+        // `pending` is the last projection into the residual stream, one plane
+        // or a chain-split projection's four partial-sum planes
+        kr_buf pending = KR_NO_BUF;
+        int planes = 1;
         for (size_t l = 0; l < m->c.n_layers; l++) {
             const Norms& n = m->norms[l];
-            KRC(m, kri::norm_quant(b, p.x, pending, n.att, p.xb, n_tok, g.dim, g.eps));
+            KRC(m, kri::norm_quant(b, p.x, pending, planes, n.att, p.xb, n_tok, g.dim, g.eps));
             if (m->is_attention[l]) {
                 int qkv[3] = {KR_PROJ_Q, KR_PROJ_K, KR_PROJ_V};
                 kr_buf ys[3] = {p.q, p.k, p.v};
@@ -436,9 +439,10 @@ int prefill_rows(krl_model* m, const std::vector<Row>& rows, bool stepped_conv =
                 KRC(m, kri::mul_rows(b, p.cy, 0, g.dim, p.bcx, g.dim, 3 * g.dim, p.co, 0, g.dim, n_tok, g.dim));
                 KRC(m, kr_project(b, l, KR_PROJ_CONV_OUT, p.cy, p.o, n_tok));
             }
-            KRC(m, kri::norm_quant(b, p.x, p.o, n.ffn, p.xb, n_tok, g.dim, g.eps));
+            KRC(m, kri::norm_quant(b, p.x, p.o, 1, n.ffn, p.xb, n_tok, g.dim, g.eps));
+            planes = 1;
             if (kri::ffn_swiglu_ok(b, l, n_tok)) {
-                KRC(m, kri::ffn_swiglu_down(b, l, n_tok, p.o));
+                KRC(m, kri::ffn_swiglu_down(b, l, n_tok, p.o, 4, &planes));
             } else {
                 int gu[2] = {KR_PROJ_GATE, KR_PROJ_UP};
                 kr_buf gys[2] = {p.gate, p.up};
@@ -449,7 +453,10 @@ int prefill_rows(krl_model* m, const std::vector<Row>& rows, bool stepped_conv =
             }
             pending = p.o;
         }
-        KRC(m, kr_add_in_place(b, p.x, pending, n_tok * g.dim));
+        if (planes == 4)
+            KRC(m, kri::add_planes(b, p.x, pending, n_tok * g.dim));
+        else
+            KRC(m, kr_add_in_place(b, p.x, pending, n_tok * g.dim));
         return KR_OK;
     }
     for (size_t l = 0; l < m->c.n_layers; l++) {
@@ -630,7 +637,7 @@ int krl_decode_batch(krl_model* m, const size_t* tokens, const size_t* rope_pos,
         TRY(alloc(m, n_seq * vocab, &m->batch_logits));
         m->batch_logits_rows = n_seq;
     }
-    KRC(m, kri::norm_quant(m->b, m->pb.x, kri::KR_NO_BUF, m->rms_final, m->pb.xb, n_seq, dim, m->c.rms_eps));
+    KRC(m, kri::norm_quant(m->b, m->pb.x, KR_NO_BUF, 1, m->rms_final, m->pb.xb, n_seq, dim, m->c.rms_eps));
     KRC(m, kri::logits_rows(m->b, m->batch_logits, n_seq));
     if (logits) KRC(m, kr_read(m->b, m->batch_logits, logits, n_seq * vocab));
     return KR_OK;

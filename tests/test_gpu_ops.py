@@ -134,6 +134,47 @@ def test_gemm_at_1p7b_shapes(hip, storage, shape):
     test_matmul_matches_cpu_project(hip, storage, shape, 128)
 
 
+# The chain-split form (each of the four partial sums on its own workgroups,
+# the planes added by the consumer): partial and whole 64-row tiles, one
+# block per partial sum (k = 128) up to 64, and the 1.7B down shape.
+@pytest.mark.parametrize("shape,rows", [((960, 2560), 8), ((960, 2560), 33), ((100, 128), 64), ((36, 8192), 128),
+                                        ((100, 128), 2048), ((36, 8192), 2048), ((2048, 8192), 128)])
+def test_split_gemm_matches_cpu_project(hip, shape, rows):
+    n, k = shape
+    rng = np.random.default_rng(n + 5 * k + rows)
+    m = O.Matrix(rng.normal(0, 0.02, size=(n, k)).astype(np.float32), "q8_0")
+    x = rng.normal(size=(rows, k)).astype(np.float32)
+    x[rows // 2] = 0.0
+    mat = hip.upload_matrix(product_matrix(m))
+    y4 = hip.alloc(4 * rows * n)
+    hip.matmul_split(mat, hip.upload(x), y4, rows)
+    p = hip.read(y4, 4 * rows * n).reshape(4, rows * n)
+    got = ((p[0] + p[1]) + p[2]) + p[3]  # float32 adds, the consumer's order (dot.rs:45)
+    want = m.project_cpu(x).ravel()
+    assert_bits_equal(got, want, f"split {shape} rows={rows}")
+    # again on the workspace the first call left
+    hip.matmul_split(mat, None, y4, rows)
+    p2 = hip.read(y4, 4 * rows * n).reshape(4, rows * n)
+    assert_bits_equal(p2.ravel(), p.ravel(), "split on the kept workspace")
+    hip.free_matrix(mat)
+
+
+def test_split_gemm_contract(hip):
+    rng = np.random.default_rng(3)
+    m = O.Matrix(rng.normal(0, 0.02, size=(64, 96)).astype(np.float32), "q8_0")
+    mat = hip.upload_matrix(product_matrix(m))
+    x = hip.upload(rng.normal(size=(8, 96)).astype(np.float32))
+    with pytest.raises(RuntimeError):  # in_dim % 128 != 0: the partial sums differ in length
+        hip.matmul_split(mat, x, hip.alloc(4 * 8 * 64), 8)
+    m2 = O.Matrix(rng.normal(0, 0.02, size=(64, 128)).astype(np.float32), "q8_0")
+    mat2 = hip.upload_matrix(product_matrix(m2))
+    hip.quantize_rows(hip.upload(rng.normal(size=(8, 128)).astype(np.float32)), 8, 128)
+    with pytest.raises(RuntimeError):  # the workspace holds row-major blocks
+        hip.matmul_split(mat2, None, hip.alloc(4 * 8 * 64), 8)
+    hip.free_matrix(mat)
+    hip.free_matrix(mat2)
+
+
 @pytest.mark.parametrize("storage", ["q8_0", "q8_0x4"])
 def test_classify_matches_cpu_logits(hip, storage):
     rng = np.random.default_rng(11)

@@ -1552,6 +1552,42 @@ int rope_kv(kr_ctx* c, kr_buf q, kr_buf k, kr_buf v, size_t qw, size_t kvw, size
     return KR_OK;
 }
 
+bool qkv_rope_ok(kr_ctx* c, size_t layer, size_t rows, const kr_rope_spec* spec) {
+    if (!c->prepared || layer >= c->n_layers || !spec || spec->head_size != 64 || spec->interleaved) return false;
+    const Mat* q = proj_mat(c, layer, KR_PROJ_Q);
+    const Mat* k = proj_mat(c, layer, KR_PROJ_K);
+    const Mat* v = proj_mat(c, layer, KR_PROJ_V);
+    return q && k && v && k->m.n == c->kv_dim && rows <= c->q_rows && q->m.k == c->q_width && !c->q_chain_major &&
+           kr::qkv_rope_q8_ok(q->m, k->m, v->m, rows);
+}
+
+int project_qkv_rope(kr_ctx* c, size_t layer, kr_buf q, size_t rows, const size_t* pos_host, const size_t* slot_host,
+                     const kr_rope_spec* spec) {
+    CHECK(c, qkv_rope_ok(c, layer, rows, spec), "the q/k/v GEMM with RoPE does not apply to layer %zu", layer);
+    const Mat* qm = proj_mat(c, layer, KR_PROJ_Q);
+    const Mat* km = proj_mat(c, layer, KR_PROJ_K);
+    const Mat* vm = proj_mat(c, layer, KR_PROJ_V);
+    BUF(qb, q, rows * qm->m.n);
+    size_t maxp = 0;
+    for (size_t i = 0; i < rows; i++) {
+        maxp = pos_host[i] > maxp ? pos_host[i] : maxp;
+        CHECK(c, slot_host[i] < c->seq_len, "slot %zu out of range", slot_host[i]);
+    }
+    CHECK(c, maxp < (1u << 24), "rope position %zu too large", maxp);
+    const float2* tab;
+    int rc = rope_table(c, spec->theta, spec->head_size, maxp + 1, &tab);
+    if (rc) return rc;
+    const uint32_t* pd;
+    const uint32_t* sd;
+    std::vector<uint32_t> p = to_u32(pos_host, rows), sl = to_u32(slot_host, rows);
+    if ((rc = stage(c, c->st_pos, p.data(), rows, &pd)) != KR_OK) return rc;
+    if ((rc = stage(c, c->st_slots, sl.data(), rows, &sd)) != KR_OK) return rc;
+    const size_t base = layer * c->seq_len * c->kv_dim;
+    HIPCHK(c, kr::launch_qkv_rope_q8(c->stream, qm->m, km->m, vm->m, act(c), rows, qb->p, pd, sd, tab, c->kc + base,
+                                     c->vc + base));
+    return KR_OK;
+}
+
 int attention_quant(kr_ctx* c, kr_buf q, kr_buf out, kr_buf att, size_t layer, const kr_window* windows, size_t n,
                     const uint32_t* window_dev, const kr_attn_spec* sp) {
     CHECK(c, c->prepared && layer < c->n_layers, "layer %zu out of range", layer);

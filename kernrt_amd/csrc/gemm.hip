@@ -68,6 +68,20 @@ struct SwiOut {
     uint32_t cm;
 };
 
+// ROPE: the q/k/v launch of a prefill with head_dim 64 (one head per 64-column
+// tile) and the half-split RoPE layout: the epilogue rotates each q and k
+// head's pairs (i, i + 32) at the row's position, as k_rope_kv does
+// (cpu.rs:664-705), writes q to y[0], and k and v straight into the KV cache
+// at the row's slot (kv_write, cpu.rs:563-573); y[1] and y[2] are not written.
+struct RopeOut {
+    const uint32_t* pos;    // [M] positions
+    const uint32_t* slots;  // [M] cache slots
+    const float2* tab;      // (cos, sin) per (position, pair): [pos][32]
+    float* kc;              // the layer's keys: [seq_len][kv_dim]
+    float* vc;              // and values
+    uint32_t kv_dim;
+};
+
 // CS: the chain-split form for launches with few output tiles. Operands
 // are chain-major (each row holds the blocks of chain 0 -- blocks 0, 4, 8,
 // .. -- then those of chains 1, 2 and 3, with the scales in the same order),
@@ -76,9 +90,10 @@ struct SwiOut {
 // chain's partial sums as plane `chain` of y ([4][M][ld]); the consumer adds
 // the four planes as ((t0 + t1) + t2) + t3.
 template <int SEM, int TM, int TN, int NJ, int CPW, int KC, int NS, int RS, int WPE, bool DBG, bool SWI = false,
-          bool CS = false>
+          bool CS = false, bool ROPE = false>
 __global__ __launch_bounds__(64 * (TM / 32) * (TN / (32 * NJ)) * (4 / CPW), WPE) void k_gemm_q8(
-    MatSet ms, QuantAct x, uint32_t M, uint32_t K, uint32_t mtiles, int32_t* __restrict__ dbg, SwiOut so) {
+    MatSet ms, QuantAct x, uint32_t M, uint32_t K, uint32_t mtiles, int32_t* __restrict__ dbg, SwiOut so,
+    RopeOut ro) {
     constexpr int WN = 32 * NJ, SM = TM / 32, NSUB = SM * (TN / WN), CG = 4 / CPW, NT = 64 * NSUB * CG;
     constexpr int ROW = KC * 32 + 16, PPR = KC * 2;
     constexpr int A_BYTES = TM * ROW, B_BYTES = TN * ROW;
@@ -94,6 +109,7 @@ __global__ __launch_bounds__(64 * (TM / 32) * (TN / (32 * NJ)) * (4 / CPW), WPE)
     static_assert(NT % PPR == 0, "a thread's pieces share their column");
     static_assert(!SWI || (TN == 64 && NJ == 2 && CPW < 4), "the SwiGLU epilogue needs one gate and one up unit per wave");
     static_assert(!CS || (CPW == 4 && !SWI && !DBG), "a chain-split wave runs its tile's one chain");
+    static_assert(!ROPE || (TN == 64 && NJ == 2 && CPW < 4 && !SWI && !CS), "a RoPE tile is one 64-wide head");
     constexpr bool WF16 = SEM == SEM_FOUR_PARTIALS_F16;
     __shared__ __align__(16) int8_t lds[LDS_BYTES];
     uint64_t* const etab = (uint64_t*)(lds + RING_BYTES);
@@ -395,6 +411,37 @@ __global__ __launch_bounds__(64 * (TM / 32) * (TN / (32 * NJ)) * (4 / CPW), WPE)
             }
             return;
         }
+        if constexpr (ROPE) {
+            // element e: (sub, v4, lane): rows 8 v4 + 4 (lane / 32) + 0..3 of
+            // the head's columns i = lane % 32 (unit 0) and i + 32 (unit 1)
+#pragma unroll
+            for (int k = 0; k < TM * 8 / NT; k++) {
+                const uint32_t e = tid + NT * k, sb = e >> 8, v4 = (e >> 6) & 3, l = e & 63;
+                const uint32_t og = sb * (WOUT / 4) + v4 * 64 + l;
+                const float4 a4 = sum4(og), b4 = sum4(og + 256);
+                const float av[4] = {a4.x, a4.y, a4.z, a4.w}, bv[4] = {b4.x, b4.y, b4.z, b4.w};
+                const uint32_t mb = m0 + (sb % SM) * 32 + 8 * v4 + 4 * (l >> 5), i = l & 31, c0 = n0 + i;
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    if (mb + r >= M) continue;
+                    const uint32_t m = mb + r;
+                    if (mi_ == 2) {  // v: to the cache as it is
+                        float* vr = ro.vc + (size_t)ro.slots[m] * ro.kv_dim;
+                        vr[c0] = av[r];
+                        vr[c0 + 32] = bv[r];
+                        continue;
+                    }
+                    // k_rope_kv: r0 = a cos - b sin, r1 = a sin + b cos
+                    const float2 cs = ro.tab[(size_t)ro.pos[m] * 32 + i];
+                    const float r0 = av[r] * cs.x - bv[r] * cs.y;
+                    const float r1 = av[r] * cs.y + bv[r] * cs.x;
+                    float* dst = mi_ == 0 ? Y + (size_t)m * ld : ro.kc + (size_t)ro.slots[m] * ro.kv_dim;
+                    dst[c0] = r0;
+                    dst[c0 + 32] = r1;
+                }
+            }
+            return;
+        }
         // element o4 of a plane: (sub, j, v4, lane), the 4 outputs rows
         // 8 v4 + 4 (lane / 32) + 0..3 of column lane % 32
 #pragma unroll
@@ -426,10 +473,10 @@ static void launch_q8(hipStream_t st, MatSet ms, QuantAct x, size_t rows, size_t
     const dim3 grid(total * mtiles), block(64 * (TM / 32) * (TN / (32 * NJ)) * (4 / CPW));
     if (dbg)
         hipLaunchKernelGGL((k_gemm_q8<SEM, TM, TN, NJ, CPW, KC, NS, RS, WPE, true>), grid, block, 0, st, ms, x,
-                           (uint32_t)rows, (uint32_t)k, mtiles, dbg, SwiOut{});
+                           (uint32_t)rows, (uint32_t)k, mtiles, dbg, SwiOut{}, RopeOut{});
     else
         hipLaunchKernelGGL((k_gemm_q8<SEM, TM, TN, NJ, CPW, KC, NS, RS, WPE, false>), grid, block, 0, st, ms, x,
-                           (uint32_t)rows, (uint32_t)k, mtiles, dbg, SwiOut{});
+                           (uint32_t)rows, (uint32_t)k, mtiles, dbg, SwiOut{}, RopeOut{});
 }
 
 // The chain-split form: tiles x 4 chains; y[0] receives [4][rows][ld].
@@ -439,7 +486,7 @@ static void launch_q8_cs(hipStream_t st, MatSet ms, QuantAct x, size_t rows, siz
     ms.tile_end[0] = ms.tile_end[1] = ms.tile_end[2] = ntiles;
     const dim3 grid(ntiles * 4 * mtiles), block(64 * (TM / 32) * (TN / (32 * NJ)));
     hipLaunchKernelGGL((k_gemm_q8<SEM_FOUR_PARTIALS_F32, TM, TN, NJ, 4, KC, NS, RS, WPE, false, false, true>), grid,
-                       block, 0, st, ms, x, (uint32_t)rows, (uint32_t)k, mtiles, nullptr, SwiOut{});
+                       block, 0, st, ms, x, (uint32_t)rows, (uint32_t)k, mtiles, nullptr, SwiOut{}, RopeOut{});
 }
 
 // The SwiGLU form: one tile per (row block, hidden block of 32).
@@ -448,7 +495,7 @@ static void launch_q8_swi(hipStream_t st, const MatSet& ms, QuantAct x, size_t r
     const uint32_t mtiles = (uint32_t)((rows + TM - 1) / TM), ntiles = ms.n[0] / 32;
     const dim3 grid(ntiles * mtiles), block(64 * (TM / 32) * (64 / (32 * NJ)) * (4 / CPW));
     hipLaunchKernelGGL((k_gemm_q8<SEM_FOUR_PARTIALS_F32, TM, 64, NJ, CPW, KC, NS, RS, WPE, false, true>), grid, block,
-                       0, st, ms, x, (uint32_t)rows, (uint32_t)k, mtiles, nullptr, so);
+                       0, st, ms, x, (uint32_t)rows, (uint32_t)k, mtiles, nullptr, so, RopeOut{});
 }
 
 // The narrow form (few column tiles: o and down at N = 2048), on 16x16x32
@@ -688,6 +735,38 @@ static hipError_t gemm_q8_go(hipStream_t st, const MatSet& ms, size_t k, QuantAc
         launch_q8<SEM, 64, 64, 2, 1, 8, 2, 2, 1>(st, ms, x, rows, k, dbg);
     else
         launch_q8_s16<SEM, 32, 32, 16, 16, 1, 8, 4, 1>(st, ms, x, rows, k, dbg);
+    return hipGetLastError();
+}
+
+// Whether the q/k/v GEMM with the RoPE and kv_write epilogue applies: Q8_0,
+// head_dim 64 whole heads, and a row count at which the plain launch takes
+// the 64x64 tiles (the form the epilogue is built in).
+bool qkv_rope_q8_ok(const DevMatrix& q, const DevMatrix& k, const DevMatrix& v, size_t rows) {
+    if (q.storage != KR_STORAGE_Q8_0 || k.storage != KR_STORAGE_Q8_0 || v.storage != KR_STORAGE_Q8_0) return false;
+    if (q.k != k.k || q.k != v.k || k.n != v.n || q.n % 64 != 0 || k.n % 64 != 0 || rows < 8) return false;
+    const size_t tiles = (q.n + k.n + v.n) / 64, m128 = (rows + 127) / 128, m64 = (rows + 63) / 64;
+    return !(rows > 64 && m128 * tiles >= 200) && m64 * tiles >= 160;
+}
+
+hipError_t launch_qkv_rope_q8(hipStream_t st, const DevMatrix& q, const DevMatrix& k, const DevMatrix& v, QuantAct x,
+                              size_t rows, float* yq, const uint32_t* pos, const uint32_t* slots, const float2* tab,
+                              float* kc, float* vc) {
+    if (!qkv_rope_q8_ok(q, k, v, rows)) return hipErrorInvalidValue;
+    MatSet ms{};
+    const DevMatrix* w[3] = {&q, &k, &v};
+    uint32_t total = 0;
+    for (int i = 0; i < 3; i++) {
+        ms.q[i] = w[i]->q, ms.s[i] = w[i]->s, ms.n[i] = (uint32_t)w[i]->n;
+        total += (uint32_t)(w[i]->n / 64);
+        ms.tile_end[i] = total;
+    }
+    ms.y[0] = yq, ms.ld[0] = (uint32_t)q.n;
+    ms.count = 3;
+    const RopeOut ro{pos, slots, tab, kc, vc, (uint32_t)k.n};
+    const uint32_t mtiles = (uint32_t)((rows + 63) / 64);
+    hipLaunchKernelGGL((k_gemm_q8<SEM_FOUR_PARTIALS_F32, 64, 64, 2, 1, 8, 2, 2, 1, false, false, false, true>),
+                       dim3(total * mtiles), dim3(64 * 2 * 1 * 4), 0, st, ms, x, (uint32_t)rows, (uint32_t)q.k, mtiles,
+                       nullptr, SwiOut{}, ro);
     return hipGetLastError();
 }
 

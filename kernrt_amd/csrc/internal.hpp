@@ -59,6 +59,13 @@ bool ffn_swiglu_ok(kr_ctx* c, size_t layer, size_t rows);
 // max_planes 4: the down projection may run chain-split and leave its four
 // partial-sum planes in `out` (room for 4 x rows x dim); *planes says which
 int ffn_swiglu_down(kr_ctx* c, size_t layer, size_t rows, kr_buf out, int max_planes, int* planes);
+// prefill q/k/v after the norm's quantization with RoPE (head_dim 64, the
+// half-split layout, no q/k norm) and kv_write as the GEMM's epilogue: q
+// rotated into `q`, k and v into the layer's cache (the k and v buffers are
+// not written)
+bool qkv_rope_ok(kr_ctx* c, size_t layer, size_t rows, const kr_rope_spec* spec);
+int project_qkv_rope(kr_ctx* c, size_t layer, kr_buf q, size_t rows, const size_t* pos_host, const size_t* slot_host,
+                     const kr_rope_spec* spec);
 // rope of q and k, then k and v into the cache; positions and slots from the
 // host (pos_host/slot_host) or one device position (pos_dev, rows == 1)
 int rope_kv(kr_ctx* c, kr_buf q, kr_buf k, kr_buf v, size_t qw, size_t kvw, size_t rows, const size_t* pos_host,

@@ -71,6 +71,13 @@ bool swiglu_fusable(const DevMatrix& gate, const DevMatrix& up);
 // The chain-split Q8_0 GEMM (gemm.hip): `cm` is a chain-major copy (launch_chain_major),
 // x chain-major too; y4 receives the four partial-sum planes [4][rows][cm.n].
 hipError_t launch_chain_major(hipStream_t st, const DevMatrix& m, int8_t* cq, float* cs);
+// The q/k/v GEMM with RoPE (head_dim 64, half-split layout) and kv_write as its
+// epilogue (gemm.hip): q rotated into yq, k rotated and v into kc / vc (the
+// layer's cache) at each row's slot.
+bool qkv_rope_q8_ok(const DevMatrix& q, const DevMatrix& k, const DevMatrix& v, size_t rows);
+hipError_t launch_qkv_rope_q8(hipStream_t st, const DevMatrix& q, const DevMatrix& k, const DevMatrix& v, QuantAct x,
+                              size_t rows, float* yq, const uint32_t* pos, const uint32_t* slots, const float2* tab,
+                              float* kc, float* vc);
 hipError_t launch_gemm_q8_cs(hipStream_t st, const DevMatrix& cm, QuantAct x, size_t rows, float* y4);
 hipError_t launch_gate_up_silu_q8(hipStream_t st, const DevMatrix& gate, const DevMatrix& up, QuantAct x, size_t rows,
                                   int8_t* hq, float* hs, uint16_t* hh, bool chain_major = false);

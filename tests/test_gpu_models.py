@@ -197,6 +197,27 @@ def test_prefill_ffn_gate_up_silu_in_one_gemm(dim, hidden, n_tok):
                       f"{dim}x{hidden}, {n_tok} rows")
 
 
+@pytest.mark.parametrize("n_kv,n1,n2", [(32, 100, 90), (8, 200, 50)])
+def test_prefill_qkv_rope_kv_write_in_one_gemm(n_kv, n1, n2):
+    # the 1.7B attention width (dim 2048, head_dim 64): prefills whose q/k/v
+    # launch takes the 64-row tiles run RoPE and kv_write as the GEMM's
+    # epilogue (100 and 90 rows at kv_mul 1, 200 rows at kv_mul 4; the
+    # 50-row continuation takes the separate launches); a first prompt, a
+    # continuation at the next positions (reading the first prompt's keys and
+    # values from the cache), then two decode steps; logits bitwise against
+    # the cpu backend at each stage
+    c = O.Config(dim=2048, hidden_dim=256, n_layers=1, n_heads=32, n_kv_heads=n_kv, vocab_size=64, seq_len=256,
+                 rms_eps=1e-5, rope_theta=130_000.0, rope_interleaved=False, head_dim=64)
+    ow = gaussian_weights(c, "q8_0", seed=170 + n_kv, norms="uniform")
+    gpu, cpu = gpu_model(c, ow), O.Model(c, ow, "cpu")
+    p1 = [(i * 13 + 1) % c.vocab_size for i in range(n1)]
+    p2 = [(i * 5 + 7) % c.vocab_size for i in range(n2)]
+    assert_bits_equal(gpu.prefill(p1, 0), cpu.prefill(p1, 0), "first prompt")
+    assert_bits_equal(gpu.prefill(p2, n1), cpu.prefill(p2, n1), "continuation")
+    for i, tok in enumerate([3, 9]):
+        assert_bits_equal(gpu.forward(tok, n1 + n2 + i), cpu.forward(tok, n1 + n2 + i), f"decode {i}")
+
+
 def test_multi_tile_shapes():
     # tests/backends.rs:436-481: a 70-row prompt against 256-wide projections
     c = O.Config(dim=128, hidden_dim=256, n_layers=2, n_heads=4, n_kv_heads=2, vocab_size=128, seq_len=128,

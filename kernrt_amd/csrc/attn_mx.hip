@@ -261,7 +261,8 @@ __global__ __launch_bounds__(256, 3) void k_attn_mx_v(float* __restrict__ att, f
                                                    const DevWindow* __restrict__ windows, uint32_t n_rows,
                                                    uint32_t n_heads, uint32_t kv_mul, uint32_t kv_dim,
                                                    uint32_t seq_len, int8_t* __restrict__ qo, float* __restrict__ so,
-                                                   uint16_t* __restrict__ ho, const float* __restrict__ psum) {
+                                                   uint16_t* __restrict__ ho, const float* __restrict__ psum,
+                                                   uint32_t keep_att) {
     constexpr uint32_t VST = HS + 4, PST = 33;
     static_assert(32 % G == 0 && (HS == 64 || HS == 128), "shape");
     __shared__ __align__(16) float s_v[2][32 * VST];  // V chunk [position][dim]
@@ -312,17 +313,24 @@ __global__ __launch_bounds__(256, 3) void k_attn_mx_v(float* __restrict__ att, f
         st.p = vs4{i0 < n ? p0 : 0.0f, i0 + 1 < n ? p1 : 0.0f, i0 + 2 < n ? p2 : 0.0f, i0 + 3 < n ? p3 : 0.0f};
     };
     // the probabilities: each exp divided by its pair's sum (elementwise.rs:88-91),
-    // written back to `att` where the reference leaves them, and to LDS
+    // written back to `att` where the reference leaves them (unless the
+    // caller has no use for them: keep_att == 0), and to LDS
     const uint32_t lpair = tid >> 3, lr = lpair / G, lj = lpair - lr * G;
     const float lsum = s_cnt[lpair] > 0 ? psum[(size_t)(r0 + lr) * n_heads + h0 + lj] : 1.0f;
     uint32_t lchunk = 0;  // the chunk lstore is given next
     auto lstore = [&](VStage& st, int buf) {
         const uint32_t g0 = 32 * lchunk++ + 4 * (tid & 7), n = s_cnt[lpair];
         float* arow = att_row(min(lpair, nr * G - 1));
-        if (g0 < n) st.p.x = div_rn(st.p.x, lsum), arow[g0] = st.p.x;
-        if (g0 + 1 < n) st.p.y = div_rn(st.p.y, lsum), arow[g0 + 1] = st.p.y;
-        if (g0 + 2 < n) st.p.z = div_rn(st.p.z, lsum), arow[g0 + 2] = st.p.z;
-        if (g0 + 3 < n) st.p.w = div_rn(st.p.w, lsum), arow[g0 + 3] = st.p.w;
+        if (g0 < n) st.p.x = div_rn(st.p.x, lsum);
+        if (g0 + 1 < n) st.p.y = div_rn(st.p.y, lsum);
+        if (g0 + 2 < n) st.p.z = div_rn(st.p.z, lsum);
+        if (g0 + 3 < n) st.p.w = div_rn(st.p.w, lsum);
+        if (keep_att) {
+            if (g0 < n) arow[g0] = st.p.x;
+            if (g0 + 1 < n) arow[g0 + 1] = st.p.y;
+            if (g0 + 2 < n) arow[g0 + 2] = st.p.z;
+            if (g0 + 3 < n) arow[g0 + 3] = st.p.w;
+        }
 #pragma unroll
         for (uint32_t k = 0; k < HS / 32; k++) {
             const uint32_t f = tid + 256 * k, rr = f / (HS / 4), col = f - rr * (HS / 4);
@@ -444,7 +452,8 @@ bool attention_mx_ok(const DevWindow* w, size_t n_rows, size_t max_count, size_t
 hipError_t launch_attention_mx(hipStream_t st, const float* q, float* out, float* att, const float* kc,
                                const float* vc, size_t layer, const DevWindow* windows, size_t n_rows,
                                size_t max_count, size_t n_heads, size_t kv_mul, size_t hs, size_t kv_dim,
-                               size_t seq_len, float scale, int8_t* qo, float* so, uint16_t* ho, float* scratch) {
+                               size_t seq_len, float scale, int8_t* qo, float* so, uint16_t* ho, float* scratch,
+                               bool keep_att) {
     const size_t G = attn_mx_group(kv_mul), R = 32 / G;
     const dim3 grid((unsigned)(n_heads / G), (unsigned)((n_rows + R - 1) / R));
     const dim3 gsm((unsigned)((n_rows * n_heads + 63) / 64));
@@ -458,7 +467,7 @@ hipError_t launch_attention_mx(hipStream_t st, const float* q, float* out, float
                        (uint32_t)seq_len, pmax, psum);                                                             \
     hipLaunchKernelGGL((k_attn_mx_v<g, h>), grid, dim3(256), 0, st, att, out, vc, layer * seq_len * kv_dim, windows, \
                        (uint32_t)n_rows, (uint32_t)n_heads, (uint32_t)kv_mul, (uint32_t)kv_dim, (uint32_t)seq_len, \
-                       qo, so, ho, psum)
+                       qo, so, ho, psum, keep_att ? 1u : 0u)
 #define KR_ATTN_MX_G(g)     \
     if (hs == 64) {         \
         KR_ATTN_MX(g, 64);  \

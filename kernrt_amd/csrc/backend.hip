@@ -902,7 +902,7 @@ int ensure_attn_scratch(kr_ctx* c, size_t need) {
 // two-launch split form, everything else launch_attention.
 int attention_many(kr_ctx* c, const float* q, float* out, float* att, size_t layer, const uint32_t* wd,
                    const std::vector<uint32_t>& w, size_t n, size_t max_count, const kr_attn_spec* sp,
-                   int8_t* qo, float* so, uint16_t* ho) {
+                   int8_t* qo, float* so, uint16_t* ho, bool keep_att = true) {
     const kr::DevWindow* hw = (const kr::DevWindow*)w.data();
     const float scale = 1.0f / sqrtf((float)sp->head_size);  // cpu.rs:591
     if (n >= 2 && !kr::attention_rows_uniform(hw, n, max_count, sp->kv_mul, sp->head_size) &&
@@ -921,7 +921,7 @@ int attention_many(kr_ctx* c, const float* q, float* out, float* att, size_t lay
     if (rc) return rc;
     HIPCHK(c, kr::launch_attention(c->stream, q, out, att, c->kc, c->vc, layer, (const kr::DevWindow*)wd, n, max_count,
                                    sp->n_heads, sp->kv_mul, sp->head_size, sp->kv_dim, sp->seq_len, scale, qo, so, ho,
-                                   hw, c->attn_scratch));
+                                   hw, c->attn_scratch, keep_att));
     return KR_OK;
 }
 
@@ -1589,7 +1589,7 @@ int project_qkv_rope(kr_ctx* c, size_t layer, kr_buf q, size_t rows, const size_
 }
 
 int attention_quant(kr_ctx* c, kr_buf q, kr_buf out, kr_buf att, size_t layer, const kr_window* windows, size_t n,
-                    const uint32_t* window_dev, const kr_attn_spec* sp) {
+                    const uint32_t* window_dev, const kr_attn_spec* sp, bool keep_att) {
     CHECK(c, c->prepared && layer < c->n_layers, "layer %zu out of range", layer);
     CHECK(c, sp && sp->kv_dim == c->kv_dim && sp->seq_len == c->seq_len,
           "attention spec does not match the prepared cache");
@@ -1635,7 +1635,7 @@ int attention_quant(kr_ctx* c, kr_buf q, kr_buf out, kr_buf att, size_t layer, c
                                        n, max_count, sp->n_heads, sp->kv_mul, sp->head_size, sp->kv_dim, sp->seq_len,
                                        scale, c->wq, c->ws, c->wh));
     } else {
-        rc = attention_many(c, qb->p, ob->p, ab->p, layer, wd, w, n, max_count, sp, c->wq, c->ws, c->wh);
+        rc = attention_many(c, qb->p, ob->p, ab->p, layer, wd, w, n, max_count, sp, c->wq, c->ws, c->wh, keep_att);
         if (rc) return rc;
     }
     c->q_rows = n;

@@ -71,9 +71,11 @@ int project_qkv_rope(kr_ctx* c, size_t layer, kr_buf q, size_t rows, const size_
 int rope_kv(kr_ctx* c, kr_buf q, kr_buf k, kr_buf v, size_t qw, size_t kvw, size_t rows, const size_t* pos_host,
             const size_t* slot_host, const uint32_t* pos_dev, size_t layer, const kr_rope_spec* spec);
 // attention whose output rows are also quantized; windows from the host, or
-// one device window (window_dev, n == 1)
+// one device window (window_dev, n == 1). keep_att false: the prefill forms
+// may leave `att` without the final probabilities (the driver never reads
+// its scratch rows back); every output is unchanged
 int attention_quant(kr_ctx* c, kr_buf q, kr_buf out, kr_buf att, size_t layer, const kr_window* windows,
-                    size_t n, const uint32_t* window_dev, const kr_attn_spec* spec);
+                    size_t n, const uint32_t* window_dev, const kr_attn_spec* spec, bool keep_att = true);
 // the classifier over the quantized workspace row
 int logits_q(kr_ctx* c, kr_buf y);
 // the classifier over the first `rows` quantized workspace rows -> y [rows][vocab]

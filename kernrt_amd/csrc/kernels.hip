@@ -2786,8 +2786,9 @@ __global__ __launch_bounds__(64 * NWAVES) void k_attn_rows(const float* __restri
             vphase(pb, pa);
         else
             vphase(pa, pb);
-        // the probabilities, still in LDS, to `att` (the reference leaves them there)
-        for (uint32_t k = 0; k < RPW; k++) {
+        // the probabilities, still in LDS, to `att` (the reference leaves them
+        // there; null: the caller has no use for them)
+        for (uint32_t k = 0; att && k < RPW; k++) {
             const uint32_t rg = wv * RPW + k;
             if (rg >= RG) break;
             const uint32_t n = s_cnt[rg], r = rg / G, j = rg - r * G;
@@ -3051,7 +3052,7 @@ hipError_t launch_attention(hipStream_t st, const float* q, float* out, float* a
                             const float* vc, size_t layer, const DevWindow* windows, size_t n_rows,
                             size_t max_count, size_t n_heads, size_t kv_mul, size_t hs, size_t kv_dim,
                             size_t seq_len, float scale, int8_t* qo, float* so, uint16_t* ho,
-                            const DevWindow* host_windows, float* mx_scratch) {
+                            const DevWindow* host_windows, float* mx_scratch, bool keep_att) {
     if (n_rows == 0) return hipSuccess;
     if (hs == 0 || hs > 256 || hs % 4 != 0 || kv_mul == 0 || n_heads % kv_mul != 0) return hipErrorInvalidValue;
     if (qo && hs % 32 != 0) return hipErrorInvalidValue;
@@ -3059,7 +3060,7 @@ hipError_t launch_attention(hipStream_t st, const float* q, float* out, float* a
     if (host_windows && mx_scratch && attention_mx_ok(host_windows, n_rows, max_count, kv_mul, hs)) {
         // blocks of 32 (row, head) pairs on the matrix core (attn_mx.hip)
         return launch_attention_mx(st, q, out, att, kc, vc, layer, windows, n_rows, max_count, n_heads, kv_mul, hs,
-                                   kv_dim, seq_len, scale, qo, so, ho, mx_scratch);
+                                   kv_dim, seq_len, scale, qo, so, ho, mx_scratch, keep_att);
     }
     if (host_windows && attention_rows_uniform(host_windows, n_rows, max_count, kv_mul, hs)) {
         // many rows whose blocks share a window layout: k_attn_rows
@@ -3069,9 +3070,9 @@ hipError_t launch_attention(hipStream_t st, const float* q, float* out, float* a
         const uint32_t scs = (uint32_t)((max_count + 3) & ~(size_t)3);
         const dim3 grid((unsigned)(n_heads / G), (unsigned)((n_rows + R - 1) / R));
 #define KR_ATTN_ROWS(g, h, w)                                                                                 \
-    hipLaunchKernelGGL((k_attn_rows<g, h, w>), grid, dim3(64 * w), lds, st, q, out, att, kc, vc,              \
-                       layer * seq_len * kv_dim, windows, (uint32_t)n_rows, (uint32_t)n_heads, (uint32_t)kv_mul, \
-                       (uint32_t)kv_dim, (uint32_t)seq_len, scale, scs, qo, so, ho)
+    hipLaunchKernelGGL((k_attn_rows<g, h, w>), grid, dim3(64 * w), lds, st, q, out, keep_att ? att : nullptr, kc,   \
+                       vc, layer * seq_len * kv_dim, windows, (uint32_t)n_rows, (uint32_t)n_heads,              \
+                       (uint32_t)kv_mul, (uint32_t)kv_dim, (uint32_t)seq_len, scale, scs, qo, so, ho)
 #define KR_ATTN_ROWS_W(g, h)         \
     if (nw == 8)                     \
         KR_ATTN_ROWS(g, h, 8);       \

@@ -109,7 +109,7 @@ hipError_t launch_attention(hipStream_t st, const float* q, float* out, float* a
                             size_t max_count, size_t n_heads, size_t kv_mul, size_t head_size,
                             size_t kv_dim, size_t seq_len, float scale, int8_t* qo = nullptr,
                             float* so = nullptr, uint16_t* ho = nullptr, const DevWindow* host_windows = nullptr,
-                            float* mx_scratch = nullptr);
+                            float* mx_scratch = nullptr, bool keep_att = true);
 // Prefill attention on the matrix core (attn_mx.hip): whether a launch can
 // take it (head size 64 or 128, a longest window of 1024 to 4096 positions,
 // every block of 32 / G rows sharing one window layout), and the launch.
@@ -118,7 +118,8 @@ bool attention_mx_ok(const DevWindow* w, size_t n_rows, size_t max_count, size_t
 hipError_t launch_attention_mx(hipStream_t st, const float* q, float* out, float* att, const float* kc,
                                const float* vc, size_t layer, const DevWindow* windows, size_t n_rows,
                                size_t max_count, size_t n_heads, size_t kv_mul, size_t hs, size_t kv_dim,
-                               size_t seq_len, float scale, int8_t* qo, float* so, uint16_t* ho, float* scratch);
+                               size_t seq_len, float scale, int8_t* qo, float* so, uint16_t* ho, float* scratch,
+                               bool keep_att = true);
 // Decode attention of one row in two launches (scores by 64-row chunks with
 // RoPE and the kv_write of k/v folded in, then softmax + V by head slices of
 // 4 dims); `scratch` holds

@@ -426,8 +426,9 @@ int prefill_rows(krl_model* m, const std::vector<Row>& rows, bool stepped_conv =
                                         nullptr, l, &g.rs));
                 }
                 if (g.hs % 32 == 0) {
+                    // the probabilities in p.att are scratch here: not written back
                     KRC(m, kri::attention_quant(b, p.q, p.attn, p.att, l, windows.data(), windows.size(), nullptr,
-                                                &g.as));
+                                                &g.as, false));
                 } else {
                     KRC(m, kr_attention(b, p.q, p.attn, p.att, l, windows.data(), windows.size(), &g.as));
                     KRC(m, kr_quantize_rows(b, p.attn, n_tok, g.q_dim));

@@ -225,11 +225,16 @@ __global__ __launch_bounds__(256) void k_attn_softmax_att(float* __restrict__ at
     for (uint32_t k = 0; k < PW; k++) m[k] = pmax[pidx(k)];
     float sum = 0.0f;
     float* tw = s_e + PW * wave * TS;
-    for (uint32_t c = 0; c < nch; c++) {
+    // chunk c + 1's loads are issued before chunk c's exps and chains run
+    // (two register sets in turn; a load past the last chunk re-reads a
+    // position inside the window and is not used)
+    auto load = [&](float (&x)[PW], uint32_t c) {
         const uint32_t i = c * C + lane;
-        float x[PW];
 #pragma unroll
         for (uint32_t k = 0; k < PW; k++) x[k] = row(k)[at(i)];
+    };
+    auto process = [&](const float (&x)[PW], uint32_t c) {
+        const uint32_t i = c * C + lane;
 #pragma unroll
         for (uint32_t k = 0; k < PW; k++) {
             const bool live = i < s_n[PW * wave + k];
@@ -251,7 +256,17 @@ __global__ __launch_bounds__(256) void k_attn_softmax_att(float* __restrict__ at
             }
         }
         __builtin_amdgcn_wave_barrier();  // the chains have read the tile before it is rewritten
+    };
+    float xa[PW], xb[PW];
+    load(xa, 0);
+    uint32_t c = 0;
+    for (; c + 2 <= nch; c += 2) {
+        load(xb, c + 1);
+        process(xa, c);
+        load(xa, c + 2);
+        process(xb, c + 1);
     }
+    if (c < nch) process(xa, c);
     if (lane < PW && p0 + PW * wave + lane < n_pairs) psum[p0 + PW * wave + lane] = sum;
 }
 

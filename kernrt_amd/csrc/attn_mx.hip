@@ -60,7 +60,10 @@ __device__ __forceinline__ MxBlock mx_block(const DevWindow* windows, uint32_t n
                                             uint32_t* s_cnt) {
     constexpr uint32_t R = 32 / G;
     MxBlock b;
-    b.r0 = blockIdx.y * R;
+    // the last row blocks first: a causal prefill's windows grow with the
+    // row, so the longest blocks start first and the short ones fill in
+    // behind them, instead of leaving the long ones for the tail
+    b.r0 = (gridDim.y - 1 - blockIdx.y) * R;
     b.nr = min(R, n_rows - b.r0);
     b.h0 = blockIdx.x * G;
     b.kvo = (b.h0 / kv_mul) * hs;
@@ -200,7 +203,8 @@ __global__ __launch_bounds__(256) void k_attn_softmax_att(float* __restrict__ at
     __shared__ uint64_t etab[32];
     __shared__ uint32_t s_n[64];
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t n_pairs = n_rows * n_heads, p0 = blockIdx.x * 64;
+    // the last pairs first (the longest windows of a causal prefill; see mx_block)
+    const uint32_t n_pairs = n_rows * n_heads, p0 = (gridDim.x - 1 - blockIdx.x) * 64;
     if (tid < 32) etab[tid] = kExp2Tab[tid];
     if (tid < 64) {
         uint32_t n = 0;

@@ -2487,7 +2487,9 @@ __global__ __launch_bounds__(64 * NWAVES) void k_attn_rows(const float* __restri
     __shared__ float s_sum[NW * RPW];
     __shared__ uint64_t etab[32];
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t r0 = blockIdx.y * R;
+    // the last row blocks first: a causal prefill's windows grow with the
+    // row, so the longest blocks start first and the short ones fill in behind
+    const uint32_t r0 = (gridDim.y - 1 - blockIdx.y) * R;
     const uint32_t nr = min(R, n_rows - r0);
     // query heads h0 .. h0 + G - 1 of KV head h0 / kv_mul (G divides kv_mul)
     const uint32_t width = n_heads * HS, h0 = blockIdx.x * G, kvo = (h0 / kv_mul) * HS;

@@ -484,9 +484,12 @@ std::vector<uint32_t> to_u32(const size_t* v, size_t n) {
 
 // The chain-split prefill GEMM applies to a Q8_0 matrix with K % 128 == 0
 // (four equal partial sums) and few rows, where the plain tiles leave most of
-// the device idle.
+// the device idle, and where its own grid (64x64 tiles x 4 partial sums) still
+// has a workgroup for every CU (at 64 rows of a 1024-wide output it has 64,
+// and the plain 32x32 tiles are faster).
 bool chain_split_ok(const DevMatrix& m, size_t rows) {
-    return m.storage == KR_STORAGE_Q8_0 && m.k % 128 == 0 && rows >= 8 && rows <= 256;
+    return m.storage == KR_STORAGE_Q8_0 && m.k % 128 == 0 && rows >= 8 && rows <= 256 &&
+           ((rows + 63) / 64) * ((m.n + 63) / 64) * 4 >= 256;
 }
 
 int ensure_chain_major(kr_ctx* c, const Mat* mt, const DevMatrix** out) {

@@ -202,11 +202,13 @@ def test_prefill_qkv_rope_kv_write_in_one_gemm(n_kv, n1, n2):
     # the 1.7B attention width (dim 2048, head_dim 64): prefills whose q/k/v
     # launch takes the 64-row tiles run RoPE and kv_write as the GEMM's
     # epilogue (100 and 90 rows at kv_mul 1, 200 rows at kv_mul 4; the
-    # 50-row continuation takes the separate launches); a first prompt, a
-    # continuation at the next positions (reading the first prompt's keys and
-    # values from the cache), then two decode steps; logits bitwise against
-    # the cpu backend at each stage
-    c = O.Config(dim=2048, hidden_dim=256, n_layers=1, n_heads=32, n_kv_heads=n_kv, vocab_size=64, seq_len=256,
+    # 50-row continuation takes the separate launches), and their down
+    # projections run chain-split (65-256 rows at dim 2048), the planes summed
+    # by the next layer's norm and by the final residual add; a first prompt,
+    # a continuation at the next positions (reading the first prompt's keys
+    # and values from the cache), then two decode steps; logits bitwise
+    # against the cpu backend at each stage
+    c = O.Config(dim=2048, hidden_dim=256, n_layers=2, n_heads=32, n_kv_heads=n_kv, vocab_size=64, seq_len=256,
                  rms_eps=1e-5, rope_theta=130_000.0, rope_interleaved=False, head_dim=64)
     ow = gaussian_weights(c, "q8_0", seed=170 + n_kv, norms="uniform")
     gpu, cpu = gpu_model(c, ow), O.Model(c, ow, "cpu")

@@ -1924,6 +1924,12 @@ __global__ __launch_bounds__(512) void k_attention_fast(
 // every query head; the scores go to a scratch row per head, and each
 // chunk's maximum per head to a second scratch array.
 // The new position's key is taken from LDS, not from the cache being written.
+// The key rows are read with P consecutive lanes on each row's P 16-byte
+// pieces of one phase (P = 16: 256 contiguous bytes per row, four rows per
+// load), then passed through LDS (XOR-swizzled, conflict-free both ways) to
+// the lane that owns the row: one lane per row reading its own 16-byte
+// pieces spreads every load over 64 cache lines and streams at about two
+// thirds of the rate of the same bytes read this way.
 template <int G, int HS, bool ROPE>
 __global__ __launch_bounds__(64) void k_attn_scores(const float* __restrict__ q, const float* __restrict__ kin,
                                                     const float* __restrict__ vin, float* __restrict__ kc,
@@ -1932,9 +1938,13 @@ __global__ __launch_bounds__(64) void k_attn_scores(const float* __restrict__ q,
                                                     const float2* __restrict__ tab, int interleaved, uint32_t kv_dim,
                                                     float scale, float* __restrict__ sc, uint32_t ss,
                                                     float* __restrict__ mxp, uint32_t ms, uint32_t width) {
+    typedef float v4f __attribute__((ext_vector_type(4)));
     constexpr uint32_t F = HS / 4, HALF = HS / 2;
+    constexpr uint32_t P = F < 16 ? F : 16, NP = F / P, SPL = 64 / P;  // pieces per phase, phases, rows per load
+    static_assert(F % P == 0 && (P & (P - 1)) == 0, "head size");
     __shared__ __align__(16) float qs[G * HS];
     __shared__ __align__(16) float kn[HS];
+    __shared__ __align__(16) v4f kt[64 * (P + 1)];  // one phase of the 64 key rows, rows padded by one piece
     const uint32_t lane = threadIdx.x, hk = blockIdx.x, chunk = blockIdx.y, row = blockIdx.z;
     const uint32_t n_heads = width / HS;
     const DevWindow w = win[row];
@@ -1944,16 +1954,26 @@ __global__ __launch_bounds__(64) void k_attn_scores(const float* __restrict__ q,
     const uint32_t count = n_shared + w.slot - w.att_start + 1;
     const uint32_t r0 = chunk * 64;
     if (r0 >= count && (chunk != 0 || !ROPE)) return;
-    // this lane's key row, issued first so that its latency overlaps the q
-    // and RoPE loads (the new position's key is replaced below by the one
-    // rotated here, so reading its cache slot before the write is harmless)
+    // the 64 key rows, issued first so that their latency overlaps the q and
+    // RoPE loads (the new position's key is replaced below by the one rotated
+    // here, so reading its cache slot before the write is harmless); load u
+    // of phase h brings piece h * P + lane % P of row SPL * u + lane / P, rows
+    // past the window read the window's last row
     const uint32_t i = r0 + lane;
     const bool live = i < count;
     const uint32_t ic = live ? i : count - 1;
-    float4 kk[F];
-    const float4* krow = (const float4*)(kc + loff + (size_t)win_slot(w, n_shared, ic) * kv_dim + (size_t)hk * HS);
+    const uint32_t pc = lane % P, pr = lane / P;
+    // a uniform base and 32-bit offsets (one layer's cache is far below 4 GB)
+    const char* kbase = (const char*)(kc + loff + (size_t)hk * HS);
+    v4f kr[F];
 #pragma unroll
-    for (uint32_t u = 0; u < F; u++) kk[u] = krow[u];
+    for (uint32_t h = 0; h < NP; h++) {
+#pragma unroll
+        for (uint32_t u = 0; u < P; u++) {
+            const uint32_t ri = min(r0 + SPL * u + pr, count - 1);
+            kr[h * P + u] = *(const v4f*)(kbase + (win_slot(w, n_shared, ri) * kv_dim + 4 * (P * h + pc)) * 4u);
+        }
+    }
     const float* qh = q + (size_t)row * width + (size_t)hk * G * HS;
     if (!ROPE) {  // q is already rotated, and every key is in the cache
         for (uint32_t t = lane; t < G * F; t += 64) ((float4*)qs)[t] = ((const float4*)qh)[t];
@@ -1978,23 +1998,57 @@ __global__ __launch_bounds__(64) void k_attn_scores(const float* __restrict__ q,
         }
         if (r0 >= count) return;
     }
-    if (ROPE && ic == count - 1) {  // the new position: its key is the one just rotated
+    // the four chains of every query head, dims in order (dot.rs:350-366),
+    // one phase of P pieces at a time through LDS: piece t of row r sits at
+    // r * (P + 1) + t (the padding keeps both the row-wise stores and the
+    // lane-per-row reads free of bank conflicts)
+    float a[G][4];
 #pragma unroll
-        for (uint32_t u = 0; u < F; u++) kk[u] = ((const float4*)kn)[u];
+    for (int j = 0; j < G; j++) a[j][0] = a[j][1] = a[j][2] = a[j][3] = 0.0f;
+    const bool fresh = ROPE && ic == count - 1;  // the new position: its key is the one just rotated
+#pragma unroll
+    for (uint32_t h = 0; h < NP; h++) {
+        if (h) __syncthreads();  // the previous phase is read
+#pragma unroll
+        for (uint32_t u = 0; u < P; u++) {
+            const uint32_t r = SPL * u + pr;
+            kt[r * (P + 1) + pc] = kr[h * P + u];
+        }
+        __syncthreads();
+        v4f kk[P];
+#pragma unroll
+        for (uint32_t t = 0; t < P; t++) kk[t] = fresh ? ((const v4f*)kn)[h * P + t] : kt[lane * (P + 1) + t];
+        // q (the same for every lane) in groups of Q pieces, each group read
+        // while the previous one's FMAs run; the empty asm statements pin that
+        // order, so the compiler does not hold every head's q in registers
+        constexpr uint32_t Q = P < 4 ? P : 4, NG = G * (P / Q);
+        const v4f* qv = (const v4f*)qs + h * P;
+        v4f qg[2][Q];
+#pragma unroll
+        for (uint32_t t = 0; t < Q; t++) qg[0][t] = qv[t];
+#pragma unroll
+        for (uint32_t g = 0; g < NG; g++) {
+            const uint32_t j = g / (P / Q), t0 = (g % (P / Q)) * Q;
+            if (g + 1 < NG) {
+                const uint32_t jn = (g + 1) / (P / Q), tn = ((g + 1) % (P / Q)) * Q;
+#pragma unroll
+                for (uint32_t t = 0; t < Q; t++) qg[(g + 1) & 1][t] = qv[jn * F + tn + t];
+            }
+#pragma unroll
+            for (uint32_t t = 0; t < Q; t++) {
+                const v4f qq = qg[g & 1][t];
+                a[j][0] = __builtin_fmaf(qq.x, kk[t0 + t].x, a[j][0]);
+                a[j][1] = __builtin_fmaf(qq.y, kk[t0 + t].y, a[j][1]);
+                a[j][2] = __builtin_fmaf(qq.z, kk[t0 + t].z, a[j][2]);
+                a[j][3] = __builtin_fmaf(qq.w, kk[t0 + t].w, a[j][3]);
+            }
+            __asm__ __volatile__("" : "+v"(a[j][0]), "+v"(a[j][1]), "+v"(a[j][2]), "+v"(a[j][3])::"memory");
+        }
     }
 #pragma unroll
     for (int j = 0; j < G; j++) {
-        float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
-#pragma unroll
-        for (uint32_t u = 0; u < F; u++) {
-            const float4 qq = ((const float4*)(qs + j * HS))[u];
-            a0 = __builtin_fmaf(qq.x, kk[u].x, a0);
-            a1 = __builtin_fmaf(qq.y, kk[u].y, a1);
-            a2 = __builtin_fmaf(qq.z, kk[u].z, a2);
-            a3 = __builtin_fmaf(qq.w, kk[u].w, a3);
-        }
         // dot.rs:360: (acc0 + acc1) + (acc2 + acc3), then * scale (cpu.rs:609)
-        const float sv = ((a0 + a1) + (a2 + a3)) * scale;
+        const float sv = ((a[j][0] + a[j][1]) + (a[j][2] + a[j][3])) * scale;
         if (live) sc[(size_t)(hk * G + j) * ss + i] = sv;
         // the chunk's maximum (order-free), so the softmax launch need not scan the scores for it
         const float m = wave_max(live ? sv : -INFINITY);

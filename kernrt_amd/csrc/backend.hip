@@ -914,7 +914,7 @@ int attention_many(kr_ctx* c, const float* q, float* out, float* att, size_t lay
         if (rc) return rc;
         HIPCHK(c, kr::launch_attention_split_rows(c->stream, q, out, att, c->kc, c->vc, layer, (const kr::DevWindow*)wd,
                                                   n, max_count, sp->n_heads, sp->kv_mul, sp->head_size, sp->kv_dim,
-                                                  sp->seq_len, scale, c->attn_scratch));
+                                                  sp->seq_len, scale, c->attn_scratch, keep_att));
         const size_t width = sp->n_heads * sp->head_size;
         if (qo) HIPCHK(c, kr::launch_quantize(c->stream, out, n, width, width, qo, so, ho));
         return KR_OK;

@@ -2904,10 +2904,15 @@ static size_t attn_rows_group(size_t kv_mul) {  // query heads per workgroup
 // row), G * HS threads, lane (j, e) = one output value. The G score rows and
 // their chunk maxima come from k_attn_scores; the max, exp, serial sum (one
 // lane per head) and division are as in k_attn_softmax_v; then V streams
-// through LDS in tiles of 64 positions (fetched into registers one tile
-// ahead) and every lane runs its own position-order chain. All lanes carry a
-// chain, which suits many rows in flight (k_attn_softmax_v instead spreads
-// one row over many CUs).
+// through LDS in tiles of 64 positions and every lane runs its own
+// position-order chain. All lanes carry a chain, which suits many rows in
+// flight (k_attn_softmax_v instead spreads one row over many CUs). The V
+// tiles come through two register sets, each tile fetched two tiles ahead of
+// its use, the first two before the softmax starts (so their latency runs
+// beside the exps and the serial sums); the loop is unrolled by two so that
+// each set is named statically and each wait covers its own loads only.
+// Fetches past the window read its last row again (never summed). `att` may
+// be null: the probabilities are then not written back.
 template <int G, int HS>
 __global__ __launch_bounds__(G * HS < 64 ? 64 : G * HS) void k_attn_softmax_v_rows(
     const float* __restrict__ sc_in, uint32_t ss, const float* __restrict__ mxp, uint32_t ms,
@@ -2941,7 +2946,35 @@ __global__ __launch_bounds__(G * HS < 64 ? 64 : G * HS) void k_attn_softmax_v_ro
         s_max[tid] = m;
     }
     if (tid < 32) etab[tid] = kExp2Tab[tid];
+    // V tiles: piece f = (position f / F, float4 f % F) of a 64-position tile
+    v4f pa[PT], pb[PT];
+    auto fetch = [&](v4f(&buf)[PT], uint32_t i0) {
+#pragma unroll
+        for (uint32_t k = 0; k < PT; k++) {
+            const uint32_t f = min(tid + NT * k, T * F - 1), rr = f / F, u = f - rr * F;
+            const uint32_t i = min(i0 + rr, count - 1);
+            buf[k] = *(const v4f*)(vbase + (size_t)win_slot(w, n_shared, i) * kv_dim + 4 * u);
+        }
+    };
+    auto put = [&](const v4f(&buf)[PT]) {
+#pragma unroll
+        for (uint32_t k = 0; k < PT; k++) {
+            const uint32_t f = tid + NT * k, rr = f / F, u = f - rr * F;
+            if (NT * PT == T * F || f < T * F) *(v4f*)(vt + rr * HS + 4 * u) = buf[k];
+        }
+    };
+    // lane (vj, ve): o += p_i * v_i[ve] of head vj over the tile at i0, in
+    // position order (cpu.rs:614-628)
+    const uint32_t vj = tid / HS, ve = tid - vj * HS;
+    auto vsum = [&](float& acc, const float* pr, uint32_t i0) {
+        const uint32_t nt = i0 < count ? min(T, count - i0) : 0u;
+#pragma unroll 8
+        for (uint32_t ii = 0; ii < nt; ii++) acc += pr[i0 + ii] * vt[ii * HS + ve];
+    };
     __syncthreads();
+    fetch(pa, 0);
+    __builtin_amdgcn_sched_barrier(0);  // all of tile 0's loads before tile 1's: the waits count on that order
+    fetch(pb, T);
     // the G heads of a position together: independent exps (and divisions) per thread
     float mj[G];
 #pragma unroll
@@ -2966,44 +2999,28 @@ __global__ __launch_bounds__(G * HS < 64 ? 64 : G * HS) void k_attn_softmax_v_ro
 #pragma unroll
         for (int j = 0; j < G; j++) {
             ps[j * scs + i] = pv[j];
-            att[(size_t)j * seq_len + i] = pv[j];  // the probabilities stay in `att`, as the reference leaves them
+            // the probabilities stay in `att`, as the reference leaves them
+            if (att) att[(size_t)j * seq_len + i] = pv[j];
         }
     }
-    // V tiles: piece f = (position f / F, float4 f % F)
-    v4f pre[PT];
-    auto tile_len = [&](uint32_t i0) { return i0 < count ? min(T, count - i0) : 0u; };
-#define KR_VROWS_FETCH(i0, nt)                                                                             \
-    _Pragma("unroll") for (uint32_t k = 0; k < PT; k++) {                                                  \
-        const uint32_t f = min(tid + NT * k, (nt) * F - 1), rr = f / F, u = f - rr * F;                   \
-        pre[k] = *(const v4f*)(vbase + (size_t)win_slot(w, n_shared, (i0) + rr) * kv_dim + 4 * u);       \
-    }
-#define KR_VROWS_PUT(nt)                                                                                   \
-    _Pragma("unroll") for (uint32_t k = 0; k < PT; k++) {                                                  \
-        const uint32_t f = tid + NT * k, rr = f / F, u = f - rr * F;                                       \
-        if (f < (nt) * F) *(v4f*)(vt + rr * HS + 4 * u) = pre[k];                                          \
-    }
-    KR_VROWS_FETCH(0, tile_len(0))
     __syncthreads();  // the probabilities are in LDS
-    KR_VROWS_PUT(tile_len(0))
-    __syncthreads();
-    const uint32_t j = tid / HS, e = tid - j * HS;
-    const float* pp = ps + (j < G ? j : 0) * scs;
+    const float* pp = ps + (vj < G ? vj : 0) * scs;
     float o = 0.0f;
-    for (uint32_t i0 = 0; i0 < count; i0 += T) {
-        const uint32_t nt = tile_len(i0), ntn = tile_len(i0 + T);
-        if (ntn) {
-            KR_VROWS_FETCH(i0 + T, ntn)
-        }
-#pragma unroll 8
-        for (uint32_t ii = 0; ii < nt; ii++) o += pp[i0 + ii] * vt[ii * HS + e];
-        lds_barrier();  // the tile is consumed; the next fetch stays in flight
-        if (ntn) {
-            KR_VROWS_PUT(ntn)
-            lds_barrier();
-        }
+    // one exit, at the end of the pair (a window of an odd number of tiles
+    // runs one empty sum): every path into the loop head has the same order
+    // of loads in flight, tile i0 + 2T's before i0 + 3T's
+    for (uint32_t i0 = 0; i0 < count; i0 += 2 * T) {
+        put(pa);
+        lds_barrier();
+        fetch(pa, i0 + 2 * T);
+        vsum(o, pp, i0);
+        lds_barrier();  // the tile is consumed
+        put(pb);
+        lds_barrier();
+        fetch(pb, i0 + 3 * T);
+        vsum(o, pp, i0 + T);
+        lds_barrier();
     }
-#undef KR_VROWS_FETCH
-#undef KR_VROWS_PUT
     if (tid < G * HS) out[tid] = o;
 }
 
@@ -3014,7 +3031,7 @@ __global__ __launch_bounds__(G * HS < 64 ? 64 : G * HS) void k_attn_softmax_v_ro
 hipError_t launch_attention_split_rows(hipStream_t st, const float* q, float* out, float* att, const float* kc,
                                        const float* vc, size_t layer, const DevWindow* windows, size_t n_rows,
                                        size_t max_count, size_t n_heads, size_t kv_mul, size_t hs, size_t kv_dim,
-                                       size_t seq_len, float scale, float* scratch) {
+                                       size_t seq_len, float scale, float* scratch, bool keep_att) {
     if (n_rows == 0) return hipSuccess;
     if (!attention_split_rows_ok(max_count, kv_mul, hs) || n_heads % kv_mul != 0 || max_count > seq_len)
         return hipErrorInvalidValue;
@@ -3034,7 +3051,7 @@ hipError_t launch_attention_split_rows(hipStream_t st, const float* q, float* ou
                            (uint32_t)(n_heads * hs));                                                                \
         hipLaunchKernelGGL((k_attn_softmax_v_rows<G, H>), g2, dim3(G * H < 64 ? 64 : G * H), lds, st, sc, ss, mxp, ms, \
                            vc, loff, windows, (uint32_t)kv_dim, (uint32_t)seq_len, (uint32_t)scs, (uint32_t)n_heads,  \
-                           att, out);                                                                               \
+                           keep_att ? att : nullptr, out);                                                            \
     } while (0)
 #define KR_SPLIT_ROWS_H(G)       \
     if (hs == 32)                \

@@ -139,7 +139,7 @@ hipError_t launch_attention_split(hipStream_t st, const float* q, const float* k
 hipError_t launch_attention_split_rows(hipStream_t st, const float* q, float* out, float* att, const float* kc,
                                        const float* vc, size_t layer, const DevWindow* windows, size_t n_rows,
                                        size_t max_count, size_t n_heads, size_t kv_mul, size_t hs, size_t kv_dim,
-                                       size_t seq_len, float scale, float* scratch);
+                                       size_t seq_len, float scale, float* scratch, bool keep_att = true);
 // whether the rows' windows let launch_attention use its block-of-rows
 // (prefill) kernel: each block of rows shares att_start and the shared range
 bool attention_rows_uniform(const DevWindow* host_windows, size_t n_rows, size_t max_count, size_t kv_mul,

@@ -1516,8 +1516,11 @@ int silu_quant(kr_ctx* c, kr_buf gate, kr_buf up, size_t rows, size_t width) {
 }
 
 int rope_kv(kr_ctx* c, kr_buf q, kr_buf k, kr_buf v, size_t qw, size_t kvw, size_t rows, const size_t* pos_host,
-            const size_t* slot_host, const uint32_t* pos_dev, size_t layer, const kr_rope_spec* spec) {
+            const size_t* slot_host, const uint32_t* pos_dev, size_t layer, const kr_rope_spec* spec, kr_buf nq,
+            kr_buf nk, float eps) {
     CHECK(c, c->prepared && layer < c->n_layers, "layer %zu out of range", layer);
+    const bool norms = nq != KR_NO_BUF || nk != KR_NO_BUF;
+    CHECK(c, !norms || (nq != KR_NO_BUF && nk != KR_NO_BUF), "the fused q/k norms take both weights");
     CHECK(c, spec && spec->head_size >= 2 && spec->head_size % 2 == 0, "rope head_size must be even");
     CHECK(c, kvw == c->kv_dim && kvw % spec->head_size == 0 && qw % spec->head_size == 0,
           "fused rope/kv_write needs whole heads and kv_width == kv_dim");
@@ -1549,6 +1552,15 @@ int rope_kv(kr_ctx* c, kr_buf q, kr_buf k, kr_buf v, size_t qw, size_t kvw, size
         if (rc) return rc;
         rc = stage(c, c->st_slots, sl.data(), rows, &sd);
         if (rc) return rc;
+    }
+    if (norms) {
+        CHECK(c, spec->head_size <= 256, "head_size must be in 1..=256");
+        BUF(wqb, nq, spec->head_size);
+        BUF(wkb, nk, spec->head_size);
+        HIPCHK(c, kr::launch_qk_norm_rope_kv(c->stream, qb->p, kb->p, vb->p, qw, kvw, rows, wqb->p, wkb->p, eps, pd,
+                                             sd, tab, spec->head_size, spec->interleaved, c->kc, c->vc, layer,
+                                             c->seq_len));
+        return KR_OK;
     }
     HIPCHK(c, kr::launch_rope_kv(c->stream, qb->p, kb->p, vb->p, qw, kvw, rows, pd, sd, tab, spec->head_size,
                                  spec->interleaved, c->kc, c->vc, layer, c->seq_len));

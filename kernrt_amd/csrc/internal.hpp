@@ -67,9 +67,12 @@ bool qkv_rope_ok(kr_ctx* c, size_t layer, size_t rows, const kr_rope_spec* spec)
 int project_qkv_rope(kr_ctx* c, size_t layer, kr_buf q, size_t rows, const size_t* pos_host, const size_t* slot_host,
                      const kr_rope_spec* spec);
 // rope of q and k, then k and v into the cache; positions and slots from the
-// host (pos_host/slot_host) or one device position (pos_dev, rows == 1)
+// host (pos_host/slot_host) or one device position (pos_dev, rows == 1).
+// With the weights nq and nk, the per-head RMSNorms of q and k (eps) come
+// first, in the same launch.
 int rope_kv(kr_ctx* c, kr_buf q, kr_buf k, kr_buf v, size_t qw, size_t kvw, size_t rows, const size_t* pos_host,
-            const size_t* slot_host, const uint32_t* pos_dev, size_t layer, const kr_rope_spec* spec);
+            const size_t* slot_host, const uint32_t* pos_dev, size_t layer, const kr_rope_spec* spec,
+            kr_buf nq = KR_NO_BUF, kr_buf nk = KR_NO_BUF, float eps = 0.0f);
 // attention whose output rows are also quantized; windows from the host, or
 // one device window (window_dev, n == 1). keep_att false: the prefill forms
 // may leave `att` without the final probabilities (the driver never reads

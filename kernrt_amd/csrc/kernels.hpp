@@ -55,6 +55,12 @@ hipError_t launch_silu_quant(hipStream_t st, float* g, const float* u, size_t ro
 hipError_t launch_rope_kv(hipStream_t st, float* q, float* k, const float* v, size_t qw, size_t kvw,
                           size_t rows, const uint32_t* positions, const uint32_t* slots, const float2* table,
                           size_t head_size, int interleaved, float* kc, float* vc, size_t layer, size_t seq_len);
+// per-head RMSNorm of q (weight wq) and k (wk), then launch_rope_kv's work, in one launch
+hipError_t launch_qk_norm_rope_kv(hipStream_t st, float* q, float* k, const float* v, size_t qw, size_t kvw,
+                                  size_t rows, const float* wq, const float* wk, float eps,
+                                  const uint32_t* positions, const uint32_t* slots, const float2* table,
+                                  size_t head_size, int interleaved, float* kc, float* vc, size_t layer,
+                                  size_t seq_len);
 
 // y[m*ldy + n] for m < rows. Uses the GEMV path (rows <= 4) or the MFMA GEMM.
 // One decode row (M = 1) of 1-3 projections with the producer of their input

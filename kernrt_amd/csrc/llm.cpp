@@ -416,14 +416,16 @@ int prefill_rows(krl_model* m, const std::vector<Row>& rows, bool stepped_conv =
                     int qkv[3] = {KR_PROJ_Q, KR_PROJ_K, KR_PROJ_V};
                     kr_buf ys[3] = {p.q, p.k, p.v};
                     KRC(m, kri::project_q(b, l, qkv, ys, 3, n_tok));
-                    if (n.has_q && n.has_k) {
-                        KRC(m, kri::qk_norm_pair(b, p.q, p.k, n_tok, g.q_dim, g.kv_dim, g.hs, n.q, n.k, g.eps));
+                    if (n.has_q && n.has_k && g.hs <= 256) {
+                        // q/k norms, RoPE and kv_write in one launch
+                        KRC(m, kri::rope_kv(b, p.q, p.k, p.v, g.q_dim, g.kv_dim, n_tok, positions.data(),
+                                            slots.data(), nullptr, l, &g.rs, n.q, n.k, g.eps));
                     } else {
                         if (n.has_q) KRC(m, kr_qk_norm(b, p.q, n_tok, g.q_dim, g.hs, n.q, g.eps));
                         if (n.has_k) KRC(m, kr_qk_norm(b, p.k, n_tok, g.kv_dim, g.hs, n.k, g.eps));
+                        KRC(m, kri::rope_kv(b, p.q, p.k, p.v, g.q_dim, g.kv_dim, n_tok, positions.data(),
+                                            slots.data(), nullptr, l, &g.rs));
                     }
-                    KRC(m, kri::rope_kv(b, p.q, p.k, p.v, g.q_dim, g.kv_dim, n_tok, positions.data(), slots.data(),
-                                        nullptr, l, &g.rs));
                 }
                 if (g.hs % 32 == 0) {
                     // the probabilities in p.att are scratch here: not written back

@@ -914,9 +914,10 @@ int attention_many(kr_ctx* c, const float* q, float* out, float* att, size_t lay
         if (rc) return rc;
         HIPCHK(c, kr::launch_attention_split_rows(c->stream, q, out, att, c->kc, c->vc, layer, (const kr::DevWindow*)wd,
                                                   n, max_count, sp->n_heads, sp->kv_mul, sp->head_size, sp->kv_dim,
-                                                  sp->seq_len, scale, c->attn_scratch, keep_att));
+                                                  sp->seq_len, scale, c->attn_scratch, keep_att,
+                                                  sp->head_size % 32 == 0 ? qo : nullptr, so, ho));
         const size_t width = sp->n_heads * sp->head_size;
-        if (qo) HIPCHK(c, kr::launch_quantize(c->stream, out, n, width, width, qo, so, ho));
+        if (qo && sp->head_size % 32 != 0) HIPCHK(c, kr::launch_quantize(c->stream, out, n, width, width, qo, so, ho));
         return KR_OK;
     }
     // the matrix-core prefill attention keeps each pair's max and sum in the scratch

@@ -2917,7 +2917,8 @@ template <int G, int HS>
 __global__ __launch_bounds__(G * HS < 64 ? 64 : G * HS) void k_attn_softmax_v_rows(
     const float* __restrict__ sc_in, uint32_t ss, const float* __restrict__ mxp, uint32_t ms,
     const float* __restrict__ vc, size_t loff, const DevWindow* __restrict__ win, uint32_t kv_dim, uint32_t seq_len,
-    uint32_t scs, uint32_t n_heads, float* __restrict__ att, float* __restrict__ out) {
+    uint32_t scs, uint32_t n_heads, float* __restrict__ att, float* __restrict__ out, int8_t* __restrict__ qo,
+    float* __restrict__ so, uint16_t* __restrict__ ho) {
     constexpr uint32_t NT = G * HS < 64 ? 64 : G * HS, T = 64, F = HS / 4, PT = (T * F + NT - 1) / NT;
     typedef float v4f __attribute__((ext_vector_type(4)));
     extern __shared__ __align__(16) float sm[];  // probabilities [G][scs] | V tile [T][HS]
@@ -2931,7 +2932,8 @@ __global__ __launch_bounds__(G * HS < 64 ? 64 : G * HS) void k_attn_softmax_v_ro
     sc_in += (size_t)row * n_heads * ss + (size_t)hk * G * ss;
     mxp += (size_t)row * n_heads * ms + (size_t)hk * G * ms;
     att += (size_t)row * n_heads * seq_len + (size_t)hk * G * seq_len;
-    out += (size_t)row * n_heads * HS + (size_t)hk * G * HS;
+    const size_t ob = (size_t)row * n_heads * HS + (size_t)hk * G * HS;  // this workgroup's first output
+    out += ob;
     float* ps = sm;
     float* vt = sm + G * scs;
     const float* vbase = vc + loff + (size_t)hk * HS;
@@ -3022,6 +3024,8 @@ __global__ __launch_bounds__(G * HS < 64 ? 64 : G * HS) void k_attn_softmax_v_ro
         lds_barrier();
     }
     if (tid < G * HS) out[tid] = o;
+    // HS % 32 == 0: each 32-lane group is one Q8 block of the row's output
+    if (qo) quant_lane(o, tid < G * HS, qo + ob + tid, so + (ob + tid) / 32, ho + (ob + tid) / 32);
 }
 
 // Many rows with windows of their own (batched decode of independent
@@ -3031,9 +3035,11 @@ __global__ __launch_bounds__(G * HS < 64 ? 64 : G * HS) void k_attn_softmax_v_ro
 hipError_t launch_attention_split_rows(hipStream_t st, const float* q, float* out, float* att, const float* kc,
                                        const float* vc, size_t layer, const DevWindow* windows, size_t n_rows,
                                        size_t max_count, size_t n_heads, size_t kv_mul, size_t hs, size_t kv_dim,
-                                       size_t seq_len, float scale, float* scratch, bool keep_att) {
+                                       size_t seq_len, float scale, float* scratch, bool keep_att, int8_t* qo,
+                                       float* so, uint16_t* ho) {
     if (n_rows == 0) return hipSuccess;
-    if (!attention_split_rows_ok(max_count, kv_mul, hs) || n_heads % kv_mul != 0 || max_count > seq_len)
+    if (!attention_split_rows_ok(max_count, kv_mul, hs) || n_heads % kv_mul != 0 || max_count > seq_len ||
+        (qo && hs % 32 != 0))
         return hipErrorInvalidValue;
     const size_t n_kv = n_heads / kv_mul, nchunks = (max_count + 63) / 64, loff = layer * seq_len * kv_dim;
     const size_t scs = (max_count + 3) & ~(size_t)3;
@@ -3051,7 +3057,7 @@ hipError_t launch_attention_split_rows(hipStream_t st, const float* q, float* ou
                            (uint32_t)(n_heads * hs));                                                                \
         hipLaunchKernelGGL((k_attn_softmax_v_rows<G, H>), g2, dim3(G * H < 64 ? 64 : G * H), lds, st, sc, ss, mxp, ms, \
                            vc, loff, windows, (uint32_t)kv_dim, (uint32_t)seq_len, (uint32_t)scs, (uint32_t)n_heads,  \
-                           keep_att ? att : nullptr, out);                                                            \
+                           keep_att ? att : nullptr, out, qo, so, ho);                                                \
     } while (0)
 #define KR_SPLIT_ROWS_H(G)       \
     if (hs == 32)                \

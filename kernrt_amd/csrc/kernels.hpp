@@ -141,11 +141,14 @@ hipError_t launch_attention_split(hipStream_t st, const float* q, const float* k
                                   float scale, float* scratch);
 // The same two launches for many rows with windows of their own (batched
 // decode): q rows already rotated, keys already in the cache; `scratch`
-// holds n_rows * attention_split_scratch(n_heads, seq_len) floats.
+// holds n_rows * attention_split_scratch(n_heads, seq_len) floats. keep_att
+// false leaves `att` unwritten; qo/so/ho (head size a multiple of 32) take
+// the output rows' Q8 blocks as well.
 hipError_t launch_attention_split_rows(hipStream_t st, const float* q, float* out, float* att, const float* kc,
                                        const float* vc, size_t layer, const DevWindow* windows, size_t n_rows,
                                        size_t max_count, size_t n_heads, size_t kv_mul, size_t hs, size_t kv_dim,
-                                       size_t seq_len, float scale, float* scratch, bool keep_att = true);
+                                       size_t seq_len, float scale, float* scratch, bool keep_att = true,
+                                       int8_t* qo = nullptr, float* so = nullptr, uint16_t* ho = nullptr);
 // whether the rows' windows let launch_attention use its block-of-rows
 // (prefill) kernel: each block of rows shares att_start and the shared range
 bool attention_rows_uniform(const DevWindow* host_windows, size_t n_rows, size_t max_count, size_t kv_mul,

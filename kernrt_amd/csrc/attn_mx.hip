@@ -10,22 +10,6 @@
 
 namespace kr {
 
-// Serial f32 sum of VPL register values per lane, lane 0's first (values
-// past the end are +0.0, which leaves a sum of non-negative terms
-// unchanged): each lane adds its values to the running sum, which passes
-// from lane L to lane L + 1 by DPP (wave_shr:1), as in wave_chain_sum.
-template <int VPL>
-__device__ __forceinline__ float reg_chain_sum(const float (&v)[VPL], uint32_t n) {
-    const uint32_t runs = (n + VPL - 1) / VPL;
-    float acc = 0.0f;
-    for (uint32_t L = 0; L < runs; L++) {
-#pragma unroll
-        for (int k = 0; k < VPL; k++) acc += v[k];
-        if (L + 1 < runs) acc = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(acc), 0x138, 0xf, 0xf, false));
-    }
-    return runs ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), runs - 1)) : 0.0f;
-}
-
 typedef float mx_v32f __attribute__((ext_vector_type(32)));
 // Attention of prefill rows on the matrix core, in three launches over
 // blocks of 32 (row, head) pairs (G query heads of one KV head x 32 / G
@@ -40,11 +24,12 @@ typedef float mx_v32f __attribute__((ext_vector_type(32)));
 //     brings dims 4s + 2h and 4s + 2h + 1 of its pair's q and of its
 //     position's key), then ((a0 + a1) + (a2 + a3)) * scale (cpu.rs:609) on
 //     the vector unit. Raw scores go to `att`.
-//  2. k_attn_softmax_att: a wave per pair (elementwise.rs:65-91): the row
-//     from `att` into registers, VPL values per lane; max, exp, the serial
-//     sum (reg_chain_sum), the division; the probabilities back to `att`,
-//     where the reference leaves them.
-//  3. k_attn_mx_v: per two positions one instruction forms the 32 pairs x
+//  2. k_attn_softmax_att (elementwise.rs:65-91): with each pair's max from
+//     the scores launch, the exps back to `att` and each pair's serial sum,
+//     64 pairs per workgroup over 64-position chunks.
+//  3. k_attn_mx_v: each exp divided by its pair's sum as the chunk is staged
+//     (the probabilities back to `att` where the caller keeps them, as the
+//     reference leaves them); per two positions one instruction forms the 32 pairs x
 //     32 dims products p_i * v_i[e] (each the correctly rounded product), and
 //     the vector unit adds them to the chains in position order. Positions a
 //     pair's window does not reach get p = 0; the zero products leave the
@@ -88,6 +73,10 @@ __global__ __launch_bounds__(256) void k_attn_mx_scores(const float* __restrict_
     constexpr uint32_t NS = HS / 4, KCH = 8, QST = HS + 4;
     static_assert(32 % G == 0 && (HS == 64 || HS == 128) && NS % KCH == 0, "shape");
     __shared__ __align__(16) float s_q[32 * QST];  // the pairs' q rows
+    // each wave's key chunk: [32 positions][KCH steps x 4 dims], rows padded to
+    // KST floats so that the lane-per-position float2 reads meet distinct banks
+    constexpr uint32_t KST = 4 * KCH + 2;
+    __shared__ __align__(16) float s_k[4][32 * KST];
     __shared__ uint32_t s_cnt[32];
     __shared__ float s_mx[4][32];
     const uint32_t tid = threadIdx.x, lane = tid & 63, h = lane >> 5, pr = lane & 31;
@@ -114,29 +103,48 @@ __global__ __launch_bounds__(256) void k_attn_mx_scores(const float* __restrict_
         // this lane's pair's q dims 4s + 2h, 4s + 2h + 1, from LDS
         const float* qrow = s_q + pr * QST + 2 * h;
         const uint32_t ntile = (cmax + 31) / 32;
-        // this wave's tiles t = wave, wave + 4, ...; key chunks of KCH steps in
-        // two register sets used in turn, the next chunk (the next tile's first
-        // at a tile's end) in flight while one is used
-        constexpr uint32_t NCH = NS / KCH;
-        static_assert(NCH % 2 == 0, "a tile starts in the first register set");
-        auto krow_of = [&](uint32_t t) {
-            const uint32_t pos = min(32 * t + pr, cmax - 1);
-            return kbase + (size_t)win_slot(w0, n_shared, pos) * kv_dim + 2 * h;
-        };
-        auto kload = [&](float2(&k)[KCH], const float* krow, uint32_t c) {
+        // this wave's tiles t = wave, wave + 4, ...; key chunks of KCH steps
+        // (32 positions x 4 KCH dims) read with 4 KCH / 4 lanes on each
+        // position's contiguous 16 KCH bytes (a lane per position reading its
+        // own 8 bytes per step would spread every load over 32 rows), through
+        // two register sets used in turn, the next chunk (the next tile's
+        // first at a tile's end) in flight while one is used; each chunk goes
+        // through the wave's LDS rows to the lane of its position
+        constexpr uint32_t NCH = NS / KCH, SEG = KCH, RPL = 64 / SEG, NLD = 32 / RPL;
+        static_assert(NCH % 2 == 0 && 64 % SEG == 0, "a tile starts in the first register set");
+        typedef float kv4 __attribute__((ext_vector_type(4)));
+        const uint32_t lrow = lane / SEG, lseg = lane - lrow * SEG;
+        auto kload = [&](kv4(&k)[NLD], uint32_t t, uint32_t c) {
 #pragma unroll
-            for (uint32_t u = 0; u < KCH; u++) k[u] = *(const float2*)(krow + 4 * (c * KCH + u));
+            for (uint32_t i = 0; i < NLD; i++) {
+                const uint32_t pos = min(32 * t + RPL * i + lrow, cmax - 1);
+                k[i] = *(const kv4*)(kbase + (size_t)win_slot(w0, n_shared, pos) * kv_dim + 4 * (c * KCH + lseg));
+            }
         };
-        float2 ka[KCH], kb[KCH];
+        float* kt = s_k[wave];
+        auto kput = [&](const kv4(&k)[NLD]) {
+#pragma unroll
+            for (uint32_t i = 0; i < NLD; i++) {
+                float* d = kt + (RPL * i + lrow) * KST + 4 * lseg;
+                *(float2*)d = float2{k[i].x, k[i].y};
+                *(float2*)(d + 2) = float2{k[i].z, k[i].w};
+            }
+            __builtin_amdgcn_wave_barrier();  // one wave's LDS accesses complete in order
+        };
         float mloc[16];  // the max of element v's pair over this lane's positions (order-free)
 #pragma unroll
         for (uint32_t v = 0; v < 16; v++) mloc[v] = -INFINITY;
-        const float* krow = krow_of(wave);
-        if (wave < ntile) kload(ka, krow, 0);
+        kv4 ka[NLD], kb[NLD];
+        if (wave < ntile) kload(ka, wave, 0);
         for (uint32_t t = wave; t < ntile; t += 4) {
-            const float* knext = krow_of(min(t + 4, ntile - 1));
+            const uint32_t tnext = min(t + 4, ntile - 1);
             mx_v32f a02 = {}, a13 = {};
-            auto steps = [&](const float2(&k)[KCH], uint32_t c) {
+            auto steps = [&](uint32_t c) {
+                // this lane's position pr, dims 4 (c KCH + u) + 2 h and + 1
+                float2 k[KCH];
+#pragma unroll
+                for (uint32_t u = 0; u < KCH; u++) k[u] = *(const float2*)(kt + pr * KST + 4 * u + 2 * h);
+                __builtin_amdgcn_wave_barrier();  // the reads come before the next chunk's stores
 #pragma unroll
                 for (uint32_t u = 0; u < KCH; u++) {
                     const float2 qq = *(const float2*)(qrow + 4 * (c * KCH + u));
@@ -147,15 +155,16 @@ __global__ __launch_bounds__(256) void k_attn_mx_scores(const float* __restrict_
             };
 #pragma unroll
             for (uint32_t c = 0; c < NCH; c += 2) {
-                kload(kb, krow, c + 1);
-                steps(ka, c);
+                kload(kb, t, c + 1);
+                kput(ka);
+                steps(c);
                 if (c + 2 < NCH)
-                    kload(ka, krow, c + 2);
+                    kload(ka, t, c + 2);
                 else
-                    kload(ka, knext, 0);  // the next tile's first chunk (the last tile's again at the end)
-                steps(kb, c + 1);
+                    kload(ka, tnext, 0);  // the next tile's first chunk (the last tile's again at the end)
+                kput(kb);
+                steps(c + 1);
             }
-            krow = knext;
             // element v: pair 8 (v / 4) + 4 h + v % 4, position 32 t + pr; a02 = chains 0 | 2, a13 = 1 | 3
             const uint32_t pos = 32 * t + pr;
 #pragma unroll

@@ -193,29 +193,34 @@ __global__ __launch_bounds__(256) void k_attn_mx_scores(const float* __restrict_
     }
 }
 
-// Exps and sums of the softmax of 64 (row, head) pairs of `att` per
-// workgroup (elementwise.rs:65-91), over 64-position chunks; wave w serves
-// pairs 16 w .. +15, one pair per load (lane = position: 256 contiguous
-// bytes). With each pair's max from k_attn_mx_scores, the exps go to `att`
-// and to the wave's rows of an LDS tile [pair][position], and lane k < 16
-// runs pair 16 w + k's serial sum over its row in position order. The
+// Exps and sums of the softmax of kMxSmPairs (row, head) pairs of `att`
+// per workgroup (elementwise.rs:65-91), over 64-position chunks; wave w
+// serves pairs PW w .. + PW - 1, one pair per load (lane = position: 256
+// contiguous bytes). With each pair's max from k_attn_mx_scores, the exps go
+// to `att` and to the wave's rows of an LDS tile [pair][position], and lane
+// k < PW runs pair PW w + k's serial sum over its row in position order. The
 // division by the sum happens where the probabilities are next read
-// (k_attn_mx_v).
+// (k_attn_mx_v). A wave's time is PW times its pairs' longest window in
+// exps, and the waves of the longest windows set the launch's length: with
+// 4 pairs a wave they do a quarter of the work they did with 16 (cfg5
+// 2048-token prefill 106.8k -> 113.6k tok/s at 8 pairs, 116.7k at 4;
+// 2 and 1 are slower again, the serial sums then dominating).
+static constexpr uint32_t kMxSmPW = 4, kMxSmPairs = 4 * kMxSmPW;
 __global__ __launch_bounds__(256) void k_attn_softmax_att(float* __restrict__ att,
                                                           const DevWindow* __restrict__ windows, uint32_t n_rows,
                                                           uint32_t n_heads, uint32_t seq_len,
                                                           const float* __restrict__ pmax, float* __restrict__ psum) {
     // chunk positions, tile row stride (16-byte rows, each 16 bytes further
     // along the banks than the one above), pairs per wave
-    constexpr uint32_t C = 64, TS = C + 4, PW = 16;
-    __shared__ __align__(16) float s_e[64 * TS];
+    constexpr uint32_t C = 64, TS = C + 4, PW = kMxSmPW, PP = kMxSmPairs;
+    __shared__ __align__(16) float s_e[PP * TS];
     __shared__ uint64_t etab[32];
-    __shared__ uint32_t s_n[64];
+    __shared__ uint32_t s_n[PP];
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     // the last pairs first (the longest windows of a causal prefill; see mx_block)
-    const uint32_t n_pairs = n_rows * n_heads, p0 = (gridDim.x - 1 - blockIdx.x) * 64;
+    const uint32_t n_pairs = n_rows * n_heads, p0 = (gridDim.x - 1 - blockIdx.x) * PP;
     if (tid < 32) etab[tid] = kExp2Tab[tid];
-    if (tid < 64) {
+    if (tid < PP) {
         uint32_t n = 0;
         if (p0 + tid < n_pairs) {
             const DevWindow w = windows[(p0 + tid) / n_heads];
@@ -225,7 +230,7 @@ __global__ __launch_bounds__(256) void k_attn_softmax_att(float* __restrict__ at
     }
     __syncthreads();
     uint32_t nmax = 0;
-    for (uint32_t k = 0; k < 64; k++) nmax = max(nmax, s_n[k]);
+    for (uint32_t k = 0; k < PP; k++) nmax = max(nmax, s_n[k]);
     const uint32_t nch = (nmax + C - 1) / C;
     auto pidx = [&](uint32_t k) { return min(p0 + PW * wave + k, n_pairs - 1); };
     auto row = [&](uint32_t k) { return att + (size_t)pidx(k) * seq_len; };
@@ -484,7 +489,7 @@ hipError_t launch_attention_mx(hipStream_t st, const float* q, float* out, float
                                bool keep_att) {
     const size_t G = attn_mx_group(kv_mul), R = 32 / G;
     const dim3 grid((unsigned)(n_heads / G), (unsigned)((n_rows + R - 1) / R));
-    const dim3 gsm((unsigned)((n_rows * n_heads + 63) / 64));
+    const dim3 gsm((unsigned)((n_rows * n_heads + kMxSmPairs - 1) / kMxSmPairs));
     float* pmax = scratch;                  // each pair's max
     float* psum = scratch + n_rows * n_heads;  // and its sum of exps
 #define KR_ATTN_MX(g, h)                                                                                         \

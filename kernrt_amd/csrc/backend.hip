@@ -1555,7 +1555,8 @@ int rope_kv(kr_ctx* c, kr_buf q, kr_buf k, kr_buf v, size_t qw, size_t kvw, size
         if (rc) return rc;
     }
     if (norms) {
-        CHECK(c, spec->head_size <= 256, "head_size must be in 1..=256");
+        CHECK(c, spec->head_size <= 128 && spec->head_size % 4 == 0,
+              "the fused q/k norms take head sizes that are multiples of 4, at most 128");
         BUF(wqb, nq, spec->head_size);
         BUF(wkb, nk, spec->head_size);
         HIPCHK(c, kr::launch_qk_norm_rope_kv(c->stream, qb->p, kb->p, vb->p, qw, kvw, rows, wqb->p, wkb->p, eps, pd,

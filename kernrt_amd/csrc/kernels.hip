@@ -3437,11 +3437,17 @@ __global__ __launch_bounds__(256) void k_rope_kv(float* __restrict__ q, float* _
 
 // Per-head RMSNorm of q and k (cpu.rs:647-661, as k_qk_norm), then their
 // RoPE (as k_rope_kv), then k and v into the cache at slots[row]: the three
-// steps of a layer with q and k norms in one launch. 16 lanes per item, an
-// item being one (row, head) of q, of k or of v (v is only copied): the
-// squares go to an LDS row, one lane runs the serial sum, the normalized
-// values replace the squares, and the lanes rotate the head's pairs from
-// there.
+// steps of a layer with q and k norms in one launch. LP lanes per item (an
+// item is one (row, head) of q, of k or of v, which is only copied): 4 for
+// a prefill's many items, so that a wave runs 16 of the serial sums side by
+// side, 16 for a few rows (a batched-decode step), so that the launch still
+// spreads over the CUs:
+// the lanes load the head in 16-byte pieces and put the squares in an LDS
+// row, the item's first lane runs the serial sum, the normalized values
+// replace the squares, each lane rotates its pairs in place (a pair's two
+// values are read and written by one lane only), and the lanes store the
+// head from LDS in 16-byte pieces.
+template <uint32_t LP>
 __global__ __launch_bounds__(256) void k_qk_norm_rope_kv(float* __restrict__ q, float* __restrict__ k,
                                                          const float* __restrict__ v, uint32_t qh, uint32_t kh,
                                                          uint32_t rows, uint32_t hs, const float* __restrict__ wq,
@@ -3450,66 +3456,69 @@ __global__ __launch_bounds__(256) void k_qk_norm_rope_kv(float* __restrict__ q, 
                                                          const uint32_t* __restrict__ slots,
                                                          const float2* __restrict__ tab, int interleaved,
                                                          float* __restrict__ kc, float* __restrict__ vc, size_t base) {
-    constexpr uint32_t MAXV = 16;  // values per lane: head <= 256
-    extern __shared__ __align__(16) float sq[];  // [16 items][round4(hs) + 4]
-    __shared__ float s_scale[16];
-    const uint32_t slot16 = threadIdx.x >> 4, l16 = threadIdx.x & 15;
-    const uint32_t stride = ((hs + 3) & ~3u) + 4, per_row = qh + 2 * kh;
-    const uint32_t item = blockIdx.x * 16 + slot16;
+    constexpr uint32_t ITEMS = 256 / LP, MAXV4 = 128 / 4 / LP;  // 16-byte pieces per lane: head <= 128
+    extern __shared__ __align__(16) float sq[];                   // [ITEMS][hs + 4]
+    __shared__ float s_scale[ITEMS];
+    const uint32_t slot = threadIdx.x / LP, l = threadIdx.x % LP;
+    const uint32_t stride = ((hs + 3) & ~3u) + 4, per_row = qh + 2 * kh, h4 = hs / 4;
+    const uint32_t item = blockIdx.x * ITEMS + slot;
     const bool live = item < rows * per_row;
     const uint32_t row = live ? item / per_row : 0, hd = live ? item % per_row : 0;
     const uint32_t kvw = kh * hs;
-    float* cache_k = kc + base + (size_t)slots[row] * kvw;
     if (hd >= qh + kh) {  // v: copied into the cache
         const uint32_t e0 = (hd - qh - kh) * hs;
-        float* cv = vc + base + (size_t)slots[row] * kvw + e0;
-        const float* src = v + (size_t)row * kvw + e0;
-        for (uint32_t i = l16; live && i < hs; i += 16) cv[i] = src[i];
-        return;  // the whole 16-lane group leaves together; no barrier follows for it
+        float4* cv = (float4*)(vc + base + (size_t)slots[row] * kvw + e0);
+        const float4* src = (const float4*)(v + (size_t)row * kvw + e0);
+        for (uint32_t i = l; live && i < h4; i += LP) cv[i] = src[i];
+        return;  // the item's lanes leave together; only wave-level ordering follows for the others
     }
     const bool is_k = hd >= qh;
     float* vec = is_k ? k + (size_t)row * kvw + (size_t)(hd - qh) * hs : q + (size_t)row * qh * hs + (size_t)hd * hs;
     const float* w = is_k ? wk : wq;
-    float* rowl = sq + slot16 * stride;
-    float a[MAXV];
+    float* rowl = sq + slot * stride;
+    float4 a[MAXV4];
 #pragma unroll
-    for (uint32_t t = 0; t < MAXV; t++) {
-        const uint32_t i = l16 + 16 * t;
-        a[t] = live && i < hs ? vec[i] : 0.0f;
-        if (i < hs) rowl[i] = a[t] * a[t];
+    for (uint32_t t = 0; t < MAXV4; t++) {
+        const uint32_t i = l + LP * t;
+        a[t] = live && i < h4 ? ((const float4*)vec)[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (i < h4) ((float4*)rowl)[i] = make_float4(a[t].x * a[t].x, a[t].y * a[t].y, a[t].z * a[t].z, a[t].w * a[t].w);
     }
-    __builtin_amdgcn_wave_barrier();  // an item's 16 lanes are in one wave: LDS order within the wave suffices
-    if (l16 == 0) {  // rms of the head (cpu.rs:635-641 on one head)
+    __builtin_amdgcn_wave_barrier();  // an item's lanes are in one wave: LDS order within the wave suffices
+    if (l == 0) {  // rms of the head (cpu.rs:635-641 on one head)
         float ss = chain_sum(rowl, hs);
         ss = div_rn(ss, (float)hs);
         ss += eps;
-        s_scale[slot16] = div_rn(1.0f, sqrt_rn(ss));
+        s_scale[slot] = div_rn(1.0f, sqrt_rn(ss));
     }
     __builtin_amdgcn_wave_barrier();
-    const float scale = s_scale[slot16];
+    const float scale = s_scale[slot];
 #pragma unroll
-    for (uint32_t t = 0; t < MAXV; t++) {
-        const uint32_t i = l16 + 16 * t;
-        if (i < hs) rowl[i] = w[i] * (scale * a[t]);
+    for (uint32_t t = 0; t < MAXV4; t++) {
+        const uint32_t i = l + LP * t;
+        if (i < h4) {
+            const float4 wv = ((const float4*)w)[i];
+            ((float4*)rowl)[i] = make_float4(wv.x * (scale * a[t].x), wv.y * (scale * a[t].y),
+                                             wv.z * (scale * a[t].z), wv.w * (scale * a[t].w));
+        }
     }
     __builtin_amdgcn_wave_barrier();
     // RoPE of the normalized head (cpu.rs:664-705): pair p is (p, p + half),
     // or (2p, 2p + 1) interleaved; two products and a difference/sum, unfused
     const uint32_t half = hs / 2;
     const float2* tr = tab + (size_t)pos[row] * half;
-    for (uint32_t pi = l16; live && pi < half; pi += 16) {
+    for (uint32_t pi = l; pi < half; pi += LP) {
         const uint32_t i0 = interleaved ? 2 * pi : pi, i1 = interleaved ? 2 * pi + 1 : pi + half;
         const float2 cs = tr[pi];
         const float x0 = rowl[i0], x1 = rowl[i1];
-        const float r0 = x0 * cs.x - x1 * cs.y;
-        const float r1 = x0 * cs.y + x1 * cs.x;
-        vec[i0] = r0;
-        vec[i1] = r1;
-        if (is_k) {
-            const uint32_t e = (hd - qh) * hs;
-            cache_k[e + i0] = r0;
-            cache_k[e + i1] = r1;
-        }
+        rowl[i0] = x0 * cs.x - x1 * cs.y;
+        rowl[i1] = x0 * cs.y + x1 * cs.x;
+    }
+    __builtin_amdgcn_wave_barrier();
+    float4* ck = (float4*)(kc + base + (size_t)slots[row] * kvw + (size_t)(is_k ? hd - qh : 0) * hs);
+    for (uint32_t i = l; live && i < h4; i += LP) {
+        const float4 r = ((const float4*)rowl)[i];
+        ((float4*)vec)[i] = r;
+        if (is_k) ck[i] = r;
     }
 }
 
@@ -3518,12 +3527,16 @@ hipError_t launch_qk_norm_rope_kv(hipStream_t st, float* q, float* k, const floa
                                   const uint32_t* positions, const uint32_t* slots, const float2* table,
                                   size_t head_size, int interleaved, float* kc, float* vc, size_t layer,
                                   size_t seq_len) {
-    if (head_size == 0 || head_size > 256 || head_size % 2 || qw % head_size || kvw % head_size)
+    if (head_size == 0 || head_size > 128 || head_size % 4 || qw % head_size || kvw % head_size)
         return hipErrorInvalidValue;
     const size_t n = rows * (qw / head_size + 2 * (kvw / head_size));
     if (n == 0) return hipSuccess;
-    const size_t stride = ((head_size + 3) & ~(size_t)3) + 4;
-    hipLaunchKernelGGL(k_qk_norm_rope_kv, dim3((unsigned)((n + 15) / 16)), dim3(256), 16 * stride * sizeof(float), st,
+    const size_t stride = head_size + 4;
+    // 4 lanes an item where that still leaves 512 or more workgroups
+    const bool four = n >= 512 * 64;
+    const size_t items = four ? 64 : 16;
+    hipLaunchKernelGGL(four ? k_qk_norm_rope_kv<4> : k_qk_norm_rope_kv<16>, dim3((unsigned)((n + items - 1) / items)),
+                       dim3(256), items * stride * sizeof(float), st,
                        q, k, v, (uint32_t)(qw / head_size), (uint32_t)(kvw / head_size), (uint32_t)rows,
                        (uint32_t)head_size, wq, wk, eps, positions, slots, table, interleaved, kc, vc,
                        layer * seq_len * kvw);

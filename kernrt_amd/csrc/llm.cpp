@@ -416,7 +416,7 @@ int prefill_rows(krl_model* m, const std::vector<Row>& rows, bool stepped_conv =
                     int qkv[3] = {KR_PROJ_Q, KR_PROJ_K, KR_PROJ_V};
                     kr_buf ys[3] = {p.q, p.k, p.v};
                     KRC(m, kri::project_q(b, l, qkv, ys, 3, n_tok));
-                    if (n.has_q && n.has_k && g.hs <= 256) {
+                    if (n.has_q && n.has_k && g.hs <= 128 && g.hs % 4 == 0) {
                         // q/k norms, RoPE and kv_write in one launch
                         KRC(m, kri::rope_kv(b, p.q, p.k, p.v, g.q_dim, g.kv_dim, n_tok, positions.data(),
                                             slots.data(), nullptr, l, &g.rs, n.q, n.k, g.eps));

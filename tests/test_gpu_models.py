@@ -329,6 +329,24 @@ def test_long_prefill_attention_on_the_matrix_core(n_heads, n_kv, hs, storage):
         assert_bits_equal(gpu.forward(9 + t, 1250 + t), cpu.forward(9 + t, 1250 + t), f"decode at {1250 + t}")
 
 
+@pytest.mark.parametrize("n_heads,n_kv,interleaved", [(16, 8, False), (24, 8, True)])
+def test_long_prefill_with_qk_norm(n_heads, n_kv, interleaved):
+    # q/k norms + RoPE + kv_write in one launch at 4 lanes per head item, the
+    # form a prefill of 32768 or more (row, head) items takes (1100 rows x
+    # 32 or 40 items of q, k and v): two layers, so every row's layer-1 q
+    # (through its attention output) reaches the layer-2 cache that the
+    # decode steps read, and every row's layer-1 k through the layer-1 cache
+    c = O.Config(dim=n_heads * 32, hidden_dim=128, n_layers=2, n_heads=n_heads, n_kv_heads=n_kv, vocab_size=64,
+                 seq_len=1200, rms_eps=1e-6, rope_theta=1_000_000.0, rope_interleaved=interleaved, head_dim=32)
+    ow = gaussian_weights(c, "q8_0", seed=n_heads + 7, qk_norm=True, norms="uniform")
+    prompt = [(i * 5 + 1) % c.vocab_size for i in range(1150)]
+    gpu, cpu = gpu_model(c, ow), O.Model(c, ow, "cpu")
+    assert_bits_equal(gpu.prefill(prompt[:1100], 0), cpu.prefill(prompt[:1100], 0), "prefill 1100")
+    assert_bits_equal(gpu.prefill(prompt[1100:], 1100), cpu.prefill(prompt[1100:], 1100), "chunk at 1100")
+    for t in range(2):
+        assert_bits_equal(gpu.forward(9 + t, 1150 + t), cpu.forward(9 + t, 1150 + t), f"decode at {1150 + t}")
+
+
 def test_greedy_graph_per_window_bucket():
     # The captured step is sized for a window bucket (a power of two from 512
     # covering the generation): three query heads per KV head on a 4100-slot

@@ -416,22 +416,22 @@ __global__ __launch_bounds__(256, 3) void k_attn_mx_v(float* __restrict__ att, f
             if (k + 1 < 16) d = dn;
         }
     };
-    // two register stages, named (not an array), so they stay in registers:
-    // chunk c + 2 is in flight while chunk c is computed from LDS
-    VStage sa, sb;
+    // one register stage: chunk c + 1 is in flight while chunk c is
+    // computed from LDS (a second stage, chunk c + 2 in flight, cost 13
+    // spilled registers at three waves per SIMD and ran 1.2% slower)
+    VStage sa;
     gload(sa, 0);
-    gload(sb, 1);
     lstore(sa, 0);
-    gload(sa, 2);
+    gload(sa, 1);
     __syncthreads();
     for (uint32_t c = 0; c < nch; c += 2) {
         compute(0, c);
-        lstore(sb, 1);  // chunk c + 1
-        gload(sb, c + 3);
+        lstore(sa, 1);  // chunk c + 1
+        gload(sa, c + 2);
         __syncthreads();
         compute(1, c + 1);
         lstore(sa, 0);  // chunk c + 2
-        gload(sa, c + 4);
+        gload(sa, c + 3);
         __syncthreads();
     }
     if (__syncthreads_or(vbad) && vwave) {

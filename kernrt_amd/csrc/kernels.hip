@@ -2463,19 +2463,20 @@ __device__ __forceinline__ void attn_rows_softmax(float* __restrict__ sc, uint32
             const float2 sum = wave_chain_sum2(ea, na, eb, nb);
             __builtin_amdgcn_wave_barrier();
             const uint32_t rA = ra / G, jA = ra - rA * G, rB = rb / G, jB = rb - rB * G;
-            float* aa = att + (size_t)(r0 + rA) * n_heads * seq_len + (size_t)(h0 + jA) * seq_len;
-            float* ab = att + (size_t)(r0 + rB) * n_heads * seq_len + (size_t)(h0 + jB) * seq_len;
+            // null att: nothing is written back (and no offset is taken from it)
+            float* aa = att ? att + (size_t)(r0 + rA) * n_heads * seq_len + (size_t)(h0 + jA) * seq_len : nullptr;
+            float* ab = att ? att + (size_t)(r0 + rB) * n_heads * seq_len + (size_t)(h0 + jB) * seq_len : nullptr;
 #pragma unroll 2
             for (uint32_t i = lane; i < nm; i += 64) {
                 if (i < na) {
                     const float pv = div_rn(ea[i], sum.x);
                     ea[i] = pv;
-                    if (att) aa[i] = pv;
+                    if (aa) aa[i] = pv;
                 }
                 if (i < nb) {
                     const float pv = div_rn(eb[i], sum.y);
                     eb[i] = pv;
-                    if (att) ab[i] = pv;
+                    if (ab) ab[i] = pv;
                 }
             }
             return;
@@ -2511,12 +2512,12 @@ __device__ __forceinline__ void attn_rows_softmax(float* __restrict__ sc, uint32
         const uint32_t n = s_cnt[rg], r = rg / G, j = rg - r * G;
         const float sj = s_sum[rg];
         float* e = sc + rg * scs;
-        float* arow = att + (size_t)(r0 + r) * n_heads * seq_len + (size_t)(h0 + j) * seq_len;
+        float* arow = att ? att + (size_t)(r0 + r) * n_heads * seq_len + (size_t)(h0 + j) * seq_len : nullptr;
 #pragma unroll 4
         for (uint32_t i = lane; i < n; i += 64) {
             const float pv = div_rn(e[i], sj);
             e[i] = pv;
-            if (att) arow[i] = pv;
+            if (arow) arow[i] = pv;
         }
     }
 }
@@ -2931,7 +2932,8 @@ __global__ __launch_bounds__(G * HS < 64 ? 64 : G * HS) void k_attn_softmax_v_ro
     const uint32_t count = n_shared + w.slot - w.att_start + 1, nch = (count + 63) / 64;
     sc_in += (size_t)row * n_heads * ss + (size_t)hk * G * ss;
     mxp += (size_t)row * n_heads * ms + (size_t)hk * G * ms;
-    att += (size_t)row * n_heads * seq_len + (size_t)hk * G * seq_len;
+    // null att: the probabilities are not written back (no offset is taken from it)
+    float* const arow = att ? att + (size_t)row * n_heads * seq_len + (size_t)hk * G * seq_len : nullptr;
     const size_t ob = (size_t)row * n_heads * HS + (size_t)hk * G * HS;  // this workgroup's first output
     out += ob;
     float* ps = sm;
@@ -3002,7 +3004,7 @@ __global__ __launch_bounds__(G * HS < 64 ? 64 : G * HS) void k_attn_softmax_v_ro
         for (int j = 0; j < G; j++) {
             ps[j * scs + i] = pv[j];
             // the probabilities stay in `att`, as the reference leaves them
-            if (att) att[(size_t)j * seq_len + i] = pv[j];
+            if (arow) arow[(size_t)j * seq_len + i] = pv[j];
         }
     }
     __syncthreads();  // the probabilities are in LDS

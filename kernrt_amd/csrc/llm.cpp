@@ -421,8 +421,12 @@ int prefill_rows(krl_model* m, const std::vector<Row>& rows, bool stepped_conv =
                         KRC(m, kri::rope_kv(b, p.q, p.k, p.v, g.q_dim, g.kv_dim, n_tok, positions.data(),
                                             slots.data(), nullptr, l, &g.rs, n.q, n.k, g.eps));
                     } else {
-                        if (n.has_q) KRC(m, kr_qk_norm(b, p.q, n_tok, g.q_dim, g.hs, n.q, g.eps));
-                        if (n.has_k) KRC(m, kr_qk_norm(b, p.k, n_tok, g.kv_dim, g.hs, n.k, g.eps));
+                        if (n.has_q && n.has_k) {
+                            KRC(m, kri::qk_norm_pair(b, p.q, p.k, n_tok, g.q_dim, g.kv_dim, g.hs, n.q, n.k, g.eps));
+                        } else {
+                            if (n.has_q) KRC(m, kr_qk_norm(b, p.q, n_tok, g.q_dim, g.hs, n.q, g.eps));
+                            if (n.has_k) KRC(m, kr_qk_norm(b, p.k, n_tok, g.kv_dim, g.hs, n.k, g.eps));
+                        }
                         KRC(m, kri::rope_kv(b, p.q, p.k, p.v, g.q_dim, g.kv_dim, n_tok, positions.data(),
                                             slots.data(), nullptr, l, &g.rs));
                     }

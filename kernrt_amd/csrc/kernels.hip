@@ -1963,7 +1963,6 @@ __global__ __launch_bounds__(64) void k_attn_scores(const float* __restrict__ q,
     const bool live = i < count;
     const uint32_t ic = live ? i : count - 1;
     const uint32_t pc = lane % P, pr = lane / P;
-    // a uniform base and 32-bit offsets (one layer's cache is far below 4 GB)
     const char* kbase = (const char*)(kc + loff + (size_t)hk * HS);
     v4f kr[F];
 #pragma unroll
@@ -1971,7 +1970,7 @@ __global__ __launch_bounds__(64) void k_attn_scores(const float* __restrict__ q,
 #pragma unroll
         for (uint32_t u = 0; u < P; u++) {
             const uint32_t ri = min(r0 + SPL * u + pr, count - 1);
-            kr[h * P + u] = *(const v4f*)(kbase + (win_slot(w, n_shared, ri) * kv_dim + 4 * (P * h + pc)) * 4u);
+            kr[h * P + u] = *(const v4f*)(kbase + ((size_t)win_slot(w, n_shared, ri) * kv_dim + 4 * (P * h + pc)) * 4);
         }
     }
     const float* qh = q + (size_t)row * width + (size_t)hk * G * HS;

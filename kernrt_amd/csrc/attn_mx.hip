@@ -460,7 +460,13 @@ __global__ __launch_bounds__(256, 3) void k_attn_mx_v(float* __restrict__ att, f
     }
 }
 
-static constexpr size_t kAttnMxMinWindow = 1024;
+// the shortest longest-window the matrix-core launches take: for head_dim
+// 128 they overtake k_attn_rows between 128 and 192 positions (cfg5 prefill
+// of 128 tokens 54.6k against 50.5k tok/s, of 192 tokens 59.5k against 61.7k,
+// of 1000 tokens 69k against 125k); for head_dim 64 k_attn_rows stages its
+// keys through LDS and stays faster up to 1024 (the 1.7B 128-token prefill
+// 53.1k tok/s against 45.1k at a 128-position threshold)
+static constexpr size_t kAttnMxMinWindow128 = 160, kAttnMxMinWindow64 = 1024;
 // k_attn_mx: query heads per workgroup (the largest of 8, 4, 2, 1 dividing
 // kv_mul), and whether a launch can take it: head size 64 or 128, windows
 // of at most 4096 positions, n_rows >= 2 and every block of 32 / G rows
@@ -472,7 +478,8 @@ static size_t attn_mx_group(size_t kv_mul) {
 }
 bool attention_mx_ok(const DevWindow* w, size_t n_rows, size_t max_count, size_t kv_mul, size_t hs) {
     // shorter windows run faster on k_attn_rows (one launch, more workgroups)
-    if ((hs != 64 && hs != 128) || max_count < kAttnMxMinWindow || max_count > 64 * 64 || n_rows < 2) return false;
+    const size_t min_window = hs == 128 ? kAttnMxMinWindow128 : kAttnMxMinWindow64;
+    if ((hs != 64 && hs != 128) || max_count < min_window || max_count > 64 * 64 || n_rows < 2) return false;
     const size_t R = 32 / attn_mx_group(kv_mul);
     for (size_t r = 0; r < n_rows; r++) {
         const DevWindow& a = w[r - r % R];

@@ -464,9 +464,10 @@ __global__ __launch_bounds__(256, 3) void k_attn_mx_v(float* __restrict__ att, f
 // 128 they overtake k_attn_rows between 128 and 192 positions (cfg5 prefill
 // of 128 tokens 54.6k against 50.5k tok/s, of 192 tokens 59.5k against 61.7k,
 // of 1000 tokens 69k against 125k); for head_dim 64 k_attn_rows stages its
-// keys through LDS and stays faster up to 1024 (the 1.7B 128-token prefill
-// 53.1k tok/s against 45.1k at a 128-position threshold)
-static constexpr size_t kAttnMxMinWindow128 = 160, kAttnMxMinWindow64 = 1024;
+// keys through LDS and stays faster up to about 768 (1.7B-shaped prefills:
+// 256 / 640 tokens 65.1k / 71.0k on k_attn_rows against 57.6k / 69.7k, 768
+// even, 896 / 1000 tokens 74.9k / 72.0k against 78.1k / 78.4k)
+static constexpr size_t kAttnMxMinWindow128 = 160, kAttnMxMinWindow64 = 768;
 // k_attn_mx: query heads per workgroup (the largest of 8, 4, 2, 1 dividing
 // kv_mul), and whether a launch can take it: head size 64 or 128, windows
 // of at most 4096 positions, n_rows >= 2 and every block of 32 / G rows

@@ -6,8 +6,8 @@
  * reference drivers drive `dyn Backend`.
  *
  * The reference is Rust; with no Rust toolchain in this build's image the
- * driver is C++, and the Rust `backends/hip.rs` arm that a maintainer would
- * add over kernrt_hip.h is shown in INTEGRATION.md.
+ * driver is C++. A Rust `backends/hip.rs` arm over kernrt_hip.h forwards
+ * each `Backend` method to the kr_* call of the same name and arguments.
  */
 #ifndef KERNRT_LLM_H
 #define KERNRT_LLM_H

@@ -2220,12 +2220,13 @@ bool attention_split_ok(size_t max_count, size_t kv_mul, size_t hs) {
     return max_count >= 1 && max_count <= 64 * 64 && attn_split_lds(scs, kv_mul, kAttnSplitDW) <= kAttnSplitLds;
 }
 
-// k_attn_softmax_v_rows: scores [G][scs] | V [64][HS]; at most 2048 positions
+// k_attn_softmax_v_rows: scores [G][scs] | V [64][HS] in LDS, so the window
+// is bounded by what those take (at most 16384 positions)
 bool attention_split_rows_ok(size_t max_count, size_t kv_mul, size_t hs) {
     if (kv_mul != 1 && kv_mul != 2 && kv_mul != 3 && kv_mul != 4 && kv_mul != 8) return false;
     if (hs != 32 && hs != 64 && hs != 128) return false;
     const size_t scs = (max_count + 3) & ~(size_t)3;
-    return max_count >= 1 && max_count <= 2048 && (kv_mul * scs + 64 * hs) * sizeof(float) <= kAttnSplitLds;
+    return max_count >= 1 && max_count <= 16384 && (kv_mul * scs + 64 * hs) * sizeof(float) <= kAttnSplitLds;
 }
 
 // scores [n_heads][round4(seq_len)] | chunk maxima [n_heads][attn_split_ms(seq_len)]

@@ -229,6 +229,34 @@ def test_decode_batch_head_dim_128(n_seq):
             assert_bits_equal(got[s], cpus[s].forward(toks[s], ctx[s] + t), f"step {t} sequence {s}")
 
 
+def test_decode_batch_windows_past_2048():
+    # the batched decode's split attention with windows of 2100-2600
+    # positions (past the 2048 of its first form; the LDS holds the score rows
+    # and one V tile): each step's rows must equal forward() of each sequence
+    room = 2700
+    n_seq = 3
+    c = O.Config(seq_len=room * n_seq, **QWEN3_SMALL)
+    ow = gaussian_weights(c, "q8_0", seed=91, qk_norm=True, norms="uniform")
+    rng = np.random.default_rng(92)
+    ctx = [2100, 2400, 2650]
+    g = gpu_model(c, ow)
+    cpus = [O.Model(c, ow, "cpu") for _ in range(n_seq)]
+    kv = c.n_kv_heads * c.head_dim
+    for s in range(n_seq):
+        keys = rng.normal(size=ctx[s] * kv).astype(np.float32)
+        vals = rng.normal(size=ctx[s] * kv).astype(np.float32)
+        g.backend.kv_upload(0, s * room * kv, keys)
+        g.backend.kv_upload(1, s * room * kv, vals)
+        cpus[s].kv_upload(0, 0, keys)
+        cpus[s].kv_upload(1, 0, vals)
+    for t in range(2):
+        toks = [int(v) for v in rng.integers(0, c.vocab_size, size=n_seq)]
+        got = g.decode_batch(toks, [ctx[s] + t for s in range(n_seq)], [s * room + ctx[s] + t for s in range(n_seq)],
+                             [s * room for s in range(n_seq)])
+        for s in range(n_seq):
+            assert_bits_equal(got[s], cpus[s].forward(toks[s], ctx[s] + t), f"step {t} sequence {s}")
+
+
 SMOLLM2_360M = dict(dim=960, hidden_dim=2560, n_layers=32, n_heads=15, n_kv_heads=5, vocab_size=49152, seq_len=1024,
                     rms_eps=1e-5, rope_theta=100_000.0, rope_interleaved=False, head_dim=64)
 

@@ -2071,9 +2071,11 @@ __global__ __launch_bounds__(64) void k_attn_scores(const float* __restrict__ q,
 // vst = round64(scs) + 4 (the 16 rows of a transposed read start 16 bytes
 // apart, on distinct banks).
 static constexpr uint32_t kAttnVRegs = 8;  // V float4 per thread held in registers
-__host__ __device__ inline size_t attn_split_vst(size_t scs) { return ((scs + 63) & ~(size_t)63) + 4; }
-__host__ __device__ inline size_t attn_split_lds(size_t scs, size_t G, size_t DW) {
-    return (G * scs + (DW + G * DW) * attn_split_vst(scs)) * sizeof(float);
+__host__ __device__ inline size_t attn_split_vst(size_t pw) { return ((pw + 63) & ~(size_t)63) + 4; }
+// pw: the positions of one pass of the V slice and product table (the whole
+// window in one pass where that fits)
+__host__ __device__ inline size_t attn_split_lds(size_t scs, size_t G, size_t DW, size_t pw) {
+    return (G * scs + (DW + G * DW) * attn_split_vst(pw)) * sizeof(float);
 }
 __host__ __device__ inline size_t attn_split_ms(size_t seq_len) { return ((seq_len + 63) / 64 + 3) & ~(size_t)3; }
 template <int G, int HS, int DW>
@@ -2082,7 +2084,7 @@ __global__ __launch_bounds__(1024) void k_attn_softmax_v(const float* __restrict
                                                          const float* __restrict__ vc, size_t loff,
                                                          const DevWindow* __restrict__ win, uint32_t kv_dim,
                                                          uint32_t seq_len, uint32_t scs, float* __restrict__ att,
-                                                         float* __restrict__ out) {
+                                                         float* __restrict__ out, uint32_t pw) {
     constexpr uint32_t S = HS / DW, FV = DW / 4, T = 1024, TV = 512;
     extern __shared__ __align__(16) float sm[];
     __shared__ float s_sum[G];
@@ -2097,7 +2099,7 @@ __global__ __launch_bounds__(1024) void k_attn_softmax_v(const float* __restrict
     out += (size_t)row * n_heads * HS;
     const uint32_t n_shared = w.shared_end - w.shared_start;
     const uint32_t count = n_shared + w.slot - w.att_start + 1;  // <= scs
-    const uint32_t vst = (uint32_t)attn_split_vst(scs), nch = (count + 63) / 64;
+    const uint32_t vst = (uint32_t)attn_split_vst(pw), nch = (count + 63) / 64;
     float* ps = sm;
     float* vt = sm + G * scs;
     // 1. the chunk maxima of the G heads (every wave; nch <= 64), the exp
@@ -2134,90 +2136,113 @@ __global__ __launch_bounds__(1024) void k_attn_softmax_v(const float* __restrict
     // float4 f % FV); it lands while the softmax sum runs (issued before the
     // exp, it held up the exp phase's barrier)
     const float* vbase = vc + loff + (size_t)hk * HS + d0;
-    const uint32_t units = count * FV, tv = tid - TV;
+    const uint32_t units0 = min(count, pw) * FV, tv = tid - TV;  // the first pass's V units
     float4 vr[kAttnVRegs];
     if (wave >= 8) {
 #pragma unroll
         for (int u = 0; u < (int)kAttnVRegs; u++) {
             const uint32_t f = tv + TV * u;
-            if (f < units) {
+            if (f < units0) {
                 const uint32_t r = f / FV, col = f - r * FV;
                 vr[u] = *(const float4*)(vbase + (size_t)win_slot(w, n_shared, r) * kv_dim + 4 * col);
             }
         }
     }
-    // 3. softmax sum, left to right (elementwise.rs:81-91), one wave per head,
-    // while waves 8-15 store the V slice transposed
+    // 3. softmax sum, left to right (elementwise.rs:81-91), one wave per head
     if (wave < G) {
         const float sj = wave_chain_sum(ps + wave * scs, count);
         if (lane == 0) s_sum[wave] = sj;
     }
-    if (wave >= 8) {
-        auto put = [&](uint32_t f, float4 v) {
-            const uint32_t r = f / FV, c = 4 * (f - r * FV);
-            vt[c * vst + r] = v.x, vt[(c + 1) * vst + r] = v.y, vt[(c + 2) * vst + r] = v.z, vt[(c + 3) * vst + r] = v.w;
-        };
-#pragma unroll
-        for (int u = 0; u < (int)kAttnVRegs; u++)
-            if (tv + TV * u < units) put(tv + TV * u, vr[u]);
-        for (uint32_t f = tv + TV * kAttnVRegs; f < units; f += TV) {  // windows past the register capacity
-            const uint32_t r = f / FV, col = f - r * FV;
-            put(f, *(const float4*)(vbase + (size_t)win_slot(w, n_shared, r) * kv_dim + 4 * col));
-        }
-    }
-    __syncthreads();
-    // 4. probabilities, the G heads of a position together (elementwise.rs:88-91),
-    // and at once the products p_i * v_i[e] of out[h][d0 + e] = sum_i p_i *
-    // v_i[e] into row j * DW + e; +0.0 from count to round32(count) (adding
-    // +0.0 leaves every reachable running sum unchanged: it starts at +0.0
-    // and so is never -0.0)
+    // 4-5 in passes of pw positions (one pass where the LDS holds the whole
+    // window): waves 8-15 store the pass's V slice transposed (the first pass
+    // while the softmax sums run), all waves form the pass's probabilities
+    // and products, and the chain lanes continue their sums over them
     constexpr uint32_t NL = G * DW;
     float* prod = vt + DW * vst;
-    const uint32_t n32 = (count + 31) & ~31u;
+    float acc = 0.0f;  // lane tid < NL: the running V sum of (head tid / DW, dim tid % DW)
     float sj[G];
+    for (uint32_t p0 = 0; p0 < count; p0 += pw) {
+        const uint32_t pn = min(pw, count - p0), units = pn * FV;
+        if (wave >= 8) {
+            auto put = [&](uint32_t f, float4 v) {
+                const uint32_t r = f / FV, c = 4 * (f - r * FV);
+                vt[c * vst + r] = v.x, vt[(c + 1) * vst + r] = v.y, vt[(c + 2) * vst + r] = v.z, vt[(c + 3) * vst + r] = v.w;
+            };
+            uint32_t f0 = tv;
+            if (p0 == 0) {
 #pragma unroll
-    for (int j = 0; j < G; j++) sj[j] = s_sum[j];
-    for (uint32_t i = tid; i < n32; i += T) {
-        const bool live = i < count;
-        const uint32_t ii = live ? i : 0;
-        float pv[G], vv[DW];
-#pragma unroll
-        for (int e = 0; e < (int)DW; e++) vv[e] = vt[e * vst + ii];
-#pragma unroll
-        for (int j = 0; j < G; j++) pv[j] = div_rn(ps[j * scs + ii], sj[j]);
-#pragma unroll
-        for (int j = 0; j < G; j++) {
-            if (live) ps[j * scs + i] = pv[j];
-#pragma unroll
-            for (int e = 0; e < (int)DW; e++) prod[(j * DW + e) * vst + i] = live ? pv[j] * vv[e] : 0.0f;
+                for (int u = 0; u < (int)kAttnVRegs; u++)
+                    if (tv + TV * u < units) put(tv + TV * u, vr[u]);
+                f0 = tv + TV * kAttnVRegs;
+            }
+            for (uint32_t f = f0; f < units; f += TV) {  // past the register capacity, and later passes
+                const uint32_t r = f / FV, col = f - r * FV;
+                put(f, *(const float4*)(vbase + (size_t)win_slot(w, n_shared, p0 + r) * kv_dim + 4 * col));
+            }
         }
-    }
-    // 5. the chains, i in order
-    __syncthreads();
-    if (tid < NL) {
-        const uint32_t j = tid / DW, e = tid % DW;
-        out[(size_t)(hk * G + j) * HS + d0 + e] = chain_sum(prod + tid * vst, n32);
-    } else if (sidx == 0 && tid >= 64) {
-        // the probabilities to `att` while the chains run (global stores
-        // issued earlier would hold up every later wait on the memory counter)
-        for (uint32_t t = tid - 64; t < G * count; t += T - 64) {
-            const uint32_t j = t / count, i = t - j * count;
-            att[(size_t)(hk * G + j) * seq_len + i] = ps[j * scs + i];
+        __syncthreads();
+        // 4. probabilities, the G heads of a position together (elementwise.rs:88-91),
+        // and at once the products p_i * v_i[e] of out[h][d0 + e] = sum_i p_i *
+        // v_i[e] into row j * DW + e; +0.0 from count to round32(count) (adding
+        // +0.0 leaves every reachable running sum unchanged: it starts at +0.0
+        // and so is never -0.0)
+        const uint32_t n32 = (pn + 31) & ~31u;
+#pragma unroll
+        for (int j = 0; j < G; j++) sj[j] = s_sum[j];
+        for (uint32_t i = tid; i < n32; i += T) {
+            const bool live = i < pn;
+            const uint32_t ii = live ? i : 0;
+            float pv[G], vv[DW];
+#pragma unroll
+            for (int e = 0; e < (int)DW; e++) vv[e] = vt[e * vst + ii];
+#pragma unroll
+            for (int j = 0; j < G; j++) pv[j] = div_rn(ps[j * scs + p0 + ii], sj[j]);
+#pragma unroll
+            for (int j = 0; j < G; j++) {
+                if (live) ps[j * scs + p0 + i] = pv[j];
+#pragma unroll
+                for (int e = 0; e < (int)DW; e++) prod[(j * DW + e) * vst + i] = live ? pv[j] * vv[e] : 0.0f;
+            }
         }
+        // 5. the chains, i in order
+        __syncthreads();
+        const bool last = p0 + pw >= count;
+        if (tid < NL) {
+            acc = chain_sum(prod + tid * vst, n32, acc);
+        } else if (last && sidx == 0 && tid >= 64) {
+            // the probabilities to `att` while the chains run (global stores
+            // issued earlier would hold up every later wait on the memory counter)
+            for (uint32_t t = tid - 64; t < G * count; t += T - 64) {
+                const uint32_t j = t / count, i = t - j * count;
+                att[(size_t)(hk * G + j) * seq_len + i] = ps[j * scs + i];
+            }
+        }
+        if (!last) __syncthreads();  // the chains have read the table before the next pass rewrites it
     }
+    if (tid < NL) out[(size_t)(hk * G + tid / DW) * HS + d0 + tid % DW] = acc;
 }
 
 static constexpr size_t kAttnSplitLds = 150 * 1024;
 // dims per k_attn_softmax_v workgroup: 4 (twice the workgroups of 8, each
 // with half the products to form; measured faster)
 static constexpr size_t kAttnSplitDW = 4;
+// positions per pass of k_attn_softmax_v's V slice and product table: the
+// whole window in one pass where the LDS holds it, else the fewest passes
+// (of whole 64-position chunks) that fit beside the G score rows; 0: none do
+static size_t attn_split_pass(size_t scs, size_t G) {
+    for (size_t np = 1; np <= 8; np++) {
+        const size_t pw = ((scs + np - 1) / np + 63) & ~(size_t)63;
+        if (attn_split_lds(scs, G, kAttnSplitDW, pw) <= kAttnSplitLds) return pw;
+    }
+    return 0;
+}
 
 bool attention_split_ok(size_t max_count, size_t kv_mul, size_t hs) {
     if (kv_mul != 1 && kv_mul != 2 && kv_mul != 3 && kv_mul != 4 && kv_mul != 8) return false;
     if (hs != 32 && hs != 64 && hs != 128) return false;
     const size_t scs = (max_count + 3) & ~(size_t)3;
     // max_count <= 4096: one chunk maximum per lane of a wave in k_attn_softmax_v
-    return max_count >= 1 && max_count <= 64 * 64 && attn_split_lds(scs, kv_mul, kAttnSplitDW) <= kAttnSplitLds;
+    return max_count >= 1 && max_count <= 64 * 64 && attn_split_pass(scs, kv_mul) > 0;
 }
 
 // k_attn_softmax_v_rows: scores [G][scs] | V [64][HS] in LDS, so the window
@@ -2247,14 +2272,15 @@ hipError_t launch_attention_split(hipStream_t st, const float* q, const float* k
     const uint32_t ss = (uint32_t)((seq_len + 3) & ~(size_t)3);  // scratch row stride
     const uint32_t ms = (uint32_t)attn_split_ms(seq_len);
     float* mxp = scratch + n_heads * ss;
-    const size_t lds = attn_split_lds(scs, kv_mul, kAttnSplitDW);
+    const size_t pw = attn_split_pass(scs, kv_mul), lds = attn_split_lds(scs, kv_mul, kAttnSplitDW, pw);
     const dim3 g1((unsigned)n_kv, (unsigned)nchunks), g2((unsigned)(n_kv * (hs / kAttnSplitDW)));
 #define KR_SPLIT(G, H)                                                                                              \
     do {                                                                                                            \
         hipLaunchKernelGGL((k_attn_scores<G, H, true>), g1, dim3(64), 0, st, q, k, v, kc, vc, loff, window, pos,    \
                            table, interleaved, (uint32_t)kv_dim, scale, sc, ss, mxp, ms, (uint32_t)(n_heads * hs)); \
         hipLaunchKernelGGL((k_attn_softmax_v<G, H, kAttnSplitDW>), g2, dim3(1024), lds, st, sc, ss, mxp, ms, vc,   \
-                           loff, window, (uint32_t)kv_dim, (uint32_t)seq_len, (uint32_t)scs, att, out);             \
+                           loff, window, (uint32_t)kv_dim, (uint32_t)seq_len, (uint32_t)scs, att, out,              \
+                           (uint32_t)pw);                                                                           \
     } while (0)
 #define KR_SPLIT_H(G)              \
     if (hs == 32)                  \

@@ -294,6 +294,29 @@ def test_split_decode_attention_windows(n_heads, n_kv, hs, ctx):
         assert_bits_equal(gpu.forward(5 + t, ctx + t), cpu.forward(5 + t, ctx + t), f"decode at {ctx + t}")
 
 
+@pytest.mark.parametrize("n_heads,n_kv,hs,ctx", [(6, 2, 64, 3000), (8, 4, 128, 3500), (4, 2, 128, 4000),
+                                                 (8, 1, 64, 3000)])
+def test_split_decode_attention_in_passes(n_heads, n_kv, hs, ctx):
+    # decode windows whose V slice and product table do not fit the LDS in
+    # one piece beside the score rows: the softmax+V launch runs them in 2
+    # (G = 3 and 2) up to 8 (G = 8) passes, the chains continuing across
+    # passes; the cache is filled directly, then two decode steps
+    c = O.Config(dim=n_heads * hs, hidden_dim=128, n_layers=1, n_heads=n_heads, n_kv_heads=n_kv, vocab_size=64,
+                 seq_len=ctx + 4, rms_eps=1e-5, rope_theta=10_000.0, rope_interleaved=False, head_dim=hs)
+    ow = gaussian_weights(c, "q8_0", seed=ctx + hs + n_kv)
+    gpu, cpu = gpu_model(c, ow), O.Model(c, ow, "cpu")
+    rng = np.random.default_rng(ctx + n_heads)
+    kv = n_kv * hs
+    keys = rng.normal(size=ctx * kv).astype(np.float32)
+    vals = rng.normal(size=ctx * kv).astype(np.float32)
+    gpu.backend.kv_upload(0, 0, keys)
+    gpu.backend.kv_upload(1, 0, vals)
+    cpu.kv_upload(0, 0, keys)
+    cpu.kv_upload(1, 0, vals)
+    for t in range(2):
+        assert_bits_equal(gpu.forward(5 + t, ctx + t), cpu.forward(5 + t, ctx + t), f"decode at {ctx + t}")
+
+
 def test_greedy_256_tokens_at_360m_width():
     # SmolLM2-360M widths (dim 960, 15/5 heads, hd 64, hidden 2560, theta 1e5)
     # with 2 layers and an 8192-token vocabulary so the oracle finishes fast:

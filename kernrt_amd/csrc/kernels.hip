@@ -2078,7 +2078,7 @@ __host__ __device__ inline size_t attn_split_lds(size_t scs, size_t G, size_t DW
     return (G * scs + (DW + G * DW) * attn_split_vst(pw)) * sizeof(float);
 }
 __host__ __device__ inline size_t attn_split_ms(size_t seq_len) { return ((seq_len + 63) / 64 + 3) & ~(size_t)3; }
-template <int G, int HS, int DW>
+template <int G, int HS, int DW, bool LONG = false>
 __global__ __launch_bounds__(1024) void k_attn_softmax_v(const float* __restrict__ sc_in, uint32_t ss,
                                                          const float* __restrict__ mxp, uint32_t ms,
                                                          const float* __restrict__ vc, size_t loff,
@@ -2102,11 +2102,19 @@ __global__ __launch_bounds__(1024) void k_attn_softmax_v(const float* __restrict
     const uint32_t vst = (uint32_t)attn_split_vst(pw), nch = (count + 63) / 64;
     float* ps = sm;
     float* vt = sm + G * scs;
-    // 1. the chunk maxima of the G heads (every wave; nch <= 64), the exp
-    // table, ...
+    // 1. the chunk maxima of the G heads (every wave, a lane per chunk; LONG:
+    // windows past 4096 positions, 64 chunks apart), the exp table, ...
     float pm[G];
 #pragma unroll
-    for (int j = 0; j < G; j++) pm[j] = lane < nch ? mxp[(size_t)(hk * G + j) * ms + lane] : -INFINITY;
+    for (int j = 0; j < G; j++) {
+        if constexpr (LONG) {
+            float m = -INFINITY;
+            for (uint32_t c = lane; c < nch; c += 64) m = fmaxf(m, mxp[(size_t)(hk * G + j) * ms + c]);
+            pm[j] = m;
+        } else {
+            pm[j] = lane < nch ? mxp[(size_t)(hk * G + j) * ms + lane] : -INFINITY;
+        }
+    }
     const uint64_t et = kExp2Tab[tid & 31];
     __asm__ __volatile__("" ::: "memory");
     // ... and the G score rows by LDS DMA (16-byte units; rows padded to a multiple of 4 floats in both places)
@@ -2149,8 +2157,12 @@ __global__ __launch_bounds__(1024) void k_attn_softmax_v(const float* __restrict
         }
     }
     // 3. softmax sum, left to right (elementwise.rs:81-91), one wave per head
-    if (wave < G) {
-        const float sj = wave_chain_sum(ps + wave * scs, count);
+    if (wave < G) {  // register-fed across the wave up to 4096 values, else (LONG) one LDS-fed lane
+        float sj;
+        if constexpr (LONG)
+            sj = lane == 0 ? chain_sum(ps + wave * scs, count) : 0.0f;
+        else
+            sj = wave_chain_sum(ps + wave * scs, count);
         if (lane == 0) s_sum[wave] = sj;
     }
     // 4-5 in passes of pw positions (one pass where the LDS holds the whole
@@ -2230,7 +2242,7 @@ static constexpr size_t kAttnSplitDW = 4;
 // whole window in one pass where the LDS holds it, else the fewest passes
 // (of whole 64-position chunks) that fit beside the G score rows; 0: none do
 static size_t attn_split_pass(size_t scs, size_t G) {
-    for (size_t np = 1; np <= 8; np++) {
+    for (size_t np = 1; np <= 16; np++) {
         const size_t pw = ((scs + np - 1) / np + 63) & ~(size_t)63;
         if (attn_split_lds(scs, G, kAttnSplitDW, pw) <= kAttnSplitLds) return pw;
     }
@@ -2241,8 +2253,7 @@ bool attention_split_ok(size_t max_count, size_t kv_mul, size_t hs) {
     if (kv_mul != 1 && kv_mul != 2 && kv_mul != 3 && kv_mul != 4 && kv_mul != 8) return false;
     if (hs != 32 && hs != 64 && hs != 128) return false;
     const size_t scs = (max_count + 3) & ~(size_t)3;
-    // max_count <= 4096: one chunk maximum per lane of a wave in k_attn_softmax_v
-    return max_count >= 1 && max_count <= 64 * 64 && attn_split_pass(scs, kv_mul) > 0;
+    return max_count >= 1 && max_count <= 16384 && attn_split_pass(scs, kv_mul) > 0;
 }
 
 // k_attn_softmax_v_rows: scores [G][scs] | V [64][HS] in LDS, so the window
@@ -2278,9 +2289,14 @@ hipError_t launch_attention_split(hipStream_t st, const float* q, const float* k
     do {                                                                                                            \
         hipLaunchKernelGGL((k_attn_scores<G, H, true>), g1, dim3(64), 0, st, q, k, v, kc, vc, loff, window, pos,    \
                            table, interleaved, (uint32_t)kv_dim, scale, sc, ss, mxp, ms, (uint32_t)(n_heads * hs)); \
-        hipLaunchKernelGGL((k_attn_softmax_v<G, H, kAttnSplitDW>), g2, dim3(1024), lds, st, sc, ss, mxp, ms, vc,   \
-                           loff, window, (uint32_t)kv_dim, (uint32_t)seq_len, (uint32_t)scs, att, out,              \
-                           (uint32_t)pw);                                                                           \
+        if (max_count > 64 * 64)                                                                                    \
+            hipLaunchKernelGGL((k_attn_softmax_v<G, H, kAttnSplitDW, true>), g2, dim3(1024), lds, st, sc, ss, mxp,  \
+                               ms, vc, loff, window, (uint32_t)kv_dim, (uint32_t)seq_len, (uint32_t)scs, att, out,  \
+                               (uint32_t)pw);                                                                       \
+        else                                                                                                        \
+            hipLaunchKernelGGL((k_attn_softmax_v<G, H, kAttnSplitDW>), g2, dim3(1024), lds, st, sc, ss, mxp, ms,    \
+                               vc, loff, window, (uint32_t)kv_dim, (uint32_t)seq_len, (uint32_t)scs, att, out,      \
+                               (uint32_t)pw);                                                                       \
     } while (0)
 #define KR_SPLIT_H(G)              \
     if (hs == 32)                  \

@@ -295,12 +295,14 @@ def test_split_decode_attention_windows(n_heads, n_kv, hs, ctx):
 
 
 @pytest.mark.parametrize("n_heads,n_kv,hs,ctx", [(6, 2, 64, 3000), (8, 4, 128, 3500), (4, 2, 128, 4000),
-                                                 (8, 1, 64, 3000)])
+                                                 (8, 1, 64, 3000), (4, 2, 64, 5000), (6, 2, 64, 6000)])
 def test_split_decode_attention_in_passes(n_heads, n_kv, hs, ctx):
     # decode windows whose V slice and product table do not fit the LDS in
     # one piece beside the score rows: the softmax+V launch runs them in 2
     # (G = 3 and 2) up to 8 (G = 8) passes, the chains continuing across
-    # passes; the cache is filled directly, then two decode steps
+    # passes; past 4096 positions the softmax sums run on one lane and the
+    # chunk maxima 64 apart per lane; the cache is filled directly, then two
+    # decode steps
     c = O.Config(dim=n_heads * hs, hidden_dim=128, n_layers=1, n_heads=n_heads, n_kv_heads=n_kv, vocab_size=64,
                  seq_len=ctx + 4, rms_eps=1e-5, rope_theta=10_000.0, rope_interleaved=False, head_dim=hs)
     ow = gaussian_weights(c, "q8_0", seed=ctx + hs + n_kv)

@@ -468,9 +468,14 @@ __global__ __launch_bounds__(256, 3) void k_attn_mx_v(float* __restrict__ att, f
 // 256 / 640 tokens 65.1k / 71.0k on k_attn_rows against 57.6k / 69.7k, 768
 // even, 896 / 1000 tokens 74.9k / 72.0k against 78.1k / 78.4k)
 static constexpr size_t kAttnMxMinWindow128 = 160, kAttnMxMinWindow64 = 768;
+// the launches loop over the window in chunks, so the longest window is a
+// choice, not a limit of the kernels (k_attn_rows and k_attention_fast, which
+// took the windows past 4096 before, ran 2048 -> 4200-token prefills at a
+// third of the rate)
+static constexpr size_t kAttnMxMaxWindow = 16384;
 // k_attn_mx: query heads per workgroup (the largest of 8, 4, 2, 1 dividing
 // kv_mul), and whether a launch can take it: head size 64 or 128, windows
-// of at most 4096 positions, n_rows >= 2 and every block of 32 / G rows
+// of at most kAttnMxMaxWindow positions, n_rows >= 2 and every block of 32 / G rows
 // sharing one window layout (prefill).
 static size_t attn_mx_group(size_t kv_mul) {
     for (size_t g : {8, 4, 2})
@@ -480,7 +485,7 @@ static size_t attn_mx_group(size_t kv_mul) {
 bool attention_mx_ok(const DevWindow* w, size_t n_rows, size_t max_count, size_t kv_mul, size_t hs) {
     // shorter windows run faster on k_attn_rows (one launch, more workgroups)
     const size_t min_window = hs == 128 ? kAttnMxMinWindow128 : kAttnMxMinWindow64;
-    if ((hs != 64 && hs != 128) || max_count < min_window || max_count > 64 * 64 || n_rows < 2) return false;
+    if ((hs != 64 && hs != 128) || max_count < min_window || max_count > kAttnMxMaxWindow || n_rows < 2) return false;
     const size_t R = 32 / attn_mx_group(kv_mul);
     for (size_t r = 0; r < n_rows; r++) {
         const DevWindow& a = w[r - r % R];

@@ -7,7 +7,7 @@ matrix-core prefill attention at the op level.
   rounded product), and the prefill attention runs the reference's score and
   V chains on it. Checked here against the host's fmaf on typical,
   subnormal, cancelling, overflowing and infinite operands.
-* k_attn_mx_* (windows of 1024..4096 positions in the prefill layout): every
+* k_attn_mx_* (windows of 1024..4570 positions in the prefill layout): every
   row's output and probabilities against the oracle, several 32-pair blocks
   and a partial one, with and without a shared prefix, kv_mul 1, 2, 3, 4, 8
   and head size 64 and 128; and a V row holding an infinity just past a
@@ -180,6 +180,12 @@ def test_matrix_core_attention_every_row(n_heads, n_kv, hs):
     _mx_case(1400, n_heads, n_kv, hs, [(0, 1100 + i, 0, 0) for i in range(70)], 101 + hs + n_heads)
     # a shared prefix of 300 slots, then each row's own suffix
     _mx_case(1500, n_heads, n_kv, hs, [(600, 1400 + i, 0, 300) for i in range(45)], 102 + hs + n_heads)
+
+
+@pytest.mark.parametrize("n_heads,n_kv,hs", [(8, 8, 64), (16, 8, 128)])
+def test_matrix_core_attention_past_4096_positions(n_heads, n_kv, hs):
+    # windows of 4500-4570 positions in 32-pair blocks and a partial one
+    _mx_case(4700, n_heads, n_kv, hs, [(0, 4500 + i, 0, 0) for i in range(70)], 301 + hs)
 
 
 @pytest.mark.parametrize("hs", [64, 128])

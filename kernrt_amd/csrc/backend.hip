@@ -1798,7 +1798,8 @@ bool split_attention_ok(kr_ctx* c, const kr_attn_spec* sp, size_t max_count) {
 }
 
 int rope_attention(kr_ctx* c, kr_buf q, kr_buf k, kr_buf v, kr_buf out, kr_buf att, size_t layer, size_t pos_host,
-                   const uint32_t* step_dev, const kr_attn_spec* sp, const kr_rope_spec* rs, size_t dev_max_count) {
+                   const uint32_t* step_dev, const kr_attn_spec* sp, const kr_rope_spec* rs, size_t dev_max_count,
+                   kr_buf nq, kr_buf nk, float eps) {
     CHECK(c, c->prepared && layer < c->n_layers, "layer %zu out of range", layer);
     const size_t cap = step_dev ? dev_max_count : pos_host + 1;
     CHECK(c, split_attention_ok(c, sp, cap) && sp->kv_dim == c->kv_dim && sp->n_heads % sp->kv_mul == 0,
@@ -1810,6 +1811,16 @@ int rope_attention(kr_ctx* c, kr_buf q, kr_buf k, kr_buf v, kr_buf out, kr_buf a
     BUF(vb, v, c->kv_dim);
     BUF(ob, out, width);
     BUF(ab, att, sp->n_heads * sp->seq_len);
+    const float* wq = nullptr;
+    const float* wk = nullptr;
+    if (nq != KR_NO_BUF) {
+        BUF(wqb, nq, sp->head_size);
+        wq = wqb->p;
+    }
+    if (nk != KR_NO_BUF) {
+        BUF(wkb, nk, sp->head_size);
+        wk = wkb->p;
+    }
     int rc0 = ensure_attn_scratch(c, kr::attention_split_scratch(sp->n_heads, c->seq_len));
     if (rc0) return rc0;
     const float2* tab;
@@ -1838,7 +1849,8 @@ int rope_attention(kr_ctx* c, kr_buf q, kr_buf k, kr_buf v, kr_buf out, kr_buf a
     const float scale = 1.0f / sqrtf((float)sp->head_size);  // cpu.rs:591
     HIPCHK(c, kr::launch_attention_split(c->stream, qb->p, kb->p, vb->p, ob->p, ab->p, c->kc, c->vc, layer,
                                          (const kr::DevWindow*)wd, pd, tab, rs->interleaved, max_count, sp->n_heads,
-                                         sp->kv_mul, sp->head_size, c->kv_dim, c->seq_len, scale, c->attn_scratch));
+                                         sp->kv_mul, sp->head_size, c->kv_dim, c->seq_len, scale, c->attn_scratch,
+                                         wq, wk, eps));
     return KR_OK;
 }
 

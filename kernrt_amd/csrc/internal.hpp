@@ -117,8 +117,10 @@ bool split_attention_ok(kr_ctx* c, const kr_attn_spec* spec, size_t max_count);
 // window {0, pos, 0, 0} and position from the host (pos_host), or from the
 // device step record (step_dev: window at step[1..4], position at step[2],
 // the window at most dev_max_count positions: the launch is sized for it)
+// nq / nk: per-head RMSNorm weights of q / k applied before the rotation
+// (either may be KR_NO_BUF)
 int rope_attention(kr_ctx* c, kr_buf q, kr_buf k, kr_buf v, kr_buf out, kr_buf att, size_t layer, size_t pos_host,
                    const uint32_t* step_dev, const kr_attn_spec* spec, const kr_rope_spec* rope,
-                   size_t dev_max_count);
+                   size_t dev_max_count, kr_buf nq = KR_NO_BUF, kr_buf nk = KR_NO_BUF, float eps = 0.0f);
 
 }  // namespace kri

@@ -1919,7 +1919,8 @@ __global__ __launch_bounds__(512) void k_attention_fast(
 //
 // k_attn_scores, workgroup = (KV head, 64 cache rows): RoPE of the head's
 // query heads and of the new key (cpu.rs:274-302, the host-built cos/sin
-// table), the kv_write of the new key and value (cpu.rs:238-246, by the
+// table; with qnw / knw given, after their per-head RMSNorm, so that the
+// q/k norms of a decode step need no launch of their own), the kv_write of the new key and value (cpu.rs:238-246, by the
 // chunk-0 workgroup), then one lane per cache row runs the four-chain dot for
 // every query head; the scores go to a scratch row per head, and each
 // chunk's maximum per head to a second scratch array.
@@ -1937,7 +1938,9 @@ __global__ __launch_bounds__(64) void k_attn_scores(const float* __restrict__ q,
                                                     const DevWindow* __restrict__ win, const uint32_t* __restrict__ pos,
                                                     const float2* __restrict__ tab, int interleaved, uint32_t kv_dim,
                                                     float scale, float* __restrict__ sc, uint32_t ss,
-                                                    float* __restrict__ mxp, uint32_t ms, uint32_t width) {
+                                                    float* __restrict__ mxp, uint32_t ms, uint32_t width,
+                                                    const float* __restrict__ qnw, const float* __restrict__ knw,
+                                                    float eps) {
     typedef float v4f __attribute__((ext_vector_type(4)));
     constexpr uint32_t F = HS / 4, HALF = HS / 2;
     constexpr uint32_t P = F < 16 ? F : 16, NP = F / P, SPL = 64 / P;  // pieces per phase, phases, rows per load
@@ -1945,6 +1948,7 @@ __global__ __launch_bounds__(64) void k_attn_scores(const float* __restrict__ q,
     __shared__ __align__(16) float qs[G * HS];
     __shared__ __align__(16) float kn[HS];
     __shared__ __align__(16) v4f kt[64 * (P + 1)];  // one phase of the 64 key rows, rows padded by one piece
+    __shared__ float s_nsc[G + 1];                   // the heads' RMSNorm scales
     const uint32_t lane = threadIdx.x, hk = blockIdx.x, chunk = blockIdx.y, row = blockIdx.z;
     const uint32_t n_heads = width / HS;
     const DevWindow w = win[row];
@@ -1977,11 +1981,44 @@ __global__ __launch_bounds__(64) void k_attn_scores(const float* __restrict__ q,
     if (!ROPE) {  // q is already rotated, and every key is in the cache
         for (uint32_t t = lane; t < G * F; t += 64) ((float4*)qs)[t] = ((const float4*)qh)[t];
     }
+    // per-head RMSNorm of the query heads (qnw) and of the new key (knw)
+    // before the rotation (cpu.rs:647-661, k_qk_norm's arithmetic): the
+    // squares into the key tile (free until the first phase), one lane per
+    // head runs the serial sum, every lane scales the values in LDS
+    const bool nrm = ROPE && (qnw != nullptr || knw != nullptr);
+    if (nrm) {
+        float* sq = (float*)kt;
+        for (uint32_t t = lane; t < (G + 1) * HS; t += 64) {
+            const uint32_t hh = t / HS, i = t - hh * HS;
+            const float x = hh < G ? qh[hh * HS + i] : kin[(size_t)hk * HS + i];
+            (hh < G ? qs + hh * HS : kn)[i] = x;
+            sq[t] = x * x;
+        }
+        __syncthreads();
+        if (lane <= (uint32_t)G) {
+            float sc1 = 1.0f;
+            if (lane < (uint32_t)G ? qnw != nullptr : knw != nullptr) {
+                float ssq = chain_sum(sq + lane * HS, HS);
+                ssq = div_rn(ssq, (float)HS);
+                ssq += eps;
+                sc1 = div_rn(1.0f, sqrt_rn(ssq));
+            }
+            s_nsc[lane] = sc1;
+        }
+        __syncthreads();
+        for (uint32_t t = lane; t < (G + 1) * HS; t += 64) {
+            const uint32_t hh = t / HS, i = t - hh * HS;
+            const float* nw = hh < G ? qnw : knw;
+            float* d = hh < G ? qs + hh * HS : kn;
+            if (nw) d[i] = nw[i] * (s_nsc[hh] * d[i]);
+        }
+        __syncthreads();
+    }
     const float2* tr = ROPE ? tab + (size_t)pos[0] * HALF : tab;
     for (uint32_t t = lane; ROPE && t < (G + 1) * HALF; t += 64) {
         const uint32_t hh = t / HALF, i = t - hh * HALF;
-        const float* src = hh < G ? qh + hh * HS : kin + (size_t)hk * HS;
         float* dst = hh < G ? qs + hh * HS : kn;
+        const float* src = nrm ? dst : hh < G ? qh + hh * HS : kin + (size_t)hk * HS;
         const uint32_t i0 = interleaved ? 2 * i : i, i1 = interleaved ? 2 * i + 1 : i + HALF;
         const float2 cs = tr[i];
         const float a = src[i0], b = src[i1];
@@ -2274,7 +2311,7 @@ hipError_t launch_attention_split(hipStream_t st, const float* q, const float* k
                                   float* att, float* kc, float* vc, size_t layer, const DevWindow* window,
                                   const uint32_t* pos, const float2* table, int interleaved, size_t max_count,
                                   size_t n_heads, size_t kv_mul, size_t hs, size_t kv_dim, size_t seq_len,
-                                  float scale, float* scratch) {
+                                  float scale, float* scratch, const float* qnw, const float* knw, float eps) {
     if (!attention_split_ok(max_count, kv_mul, hs) || n_heads % kv_mul != 0 || max_count > seq_len)
         return hipErrorInvalidValue;
     const size_t n_kv = n_heads / kv_mul, nchunks = (max_count + 63) / 64, loff = layer * seq_len * kv_dim;
@@ -2288,7 +2325,8 @@ hipError_t launch_attention_split(hipStream_t st, const float* q, const float* k
 #define KR_SPLIT(G, H)                                                                                              \
     do {                                                                                                            \
         hipLaunchKernelGGL((k_attn_scores<G, H, true>), g1, dim3(64), 0, st, q, k, v, kc, vc, loff, window, pos,    \
-                           table, interleaved, (uint32_t)kv_dim, scale, sc, ss, mxp, ms, (uint32_t)(n_heads * hs)); \
+                           table, interleaved, (uint32_t)kv_dim, scale, sc, ss, mxp, ms, (uint32_t)(n_heads * hs),  \
+                           qnw, knw, eps);                                                                          \
         if (max_count > 64 * 64)                                                                                    \
             hipLaunchKernelGGL((k_attn_softmax_v<G, H, kAttnSplitDW, true>), g2, dim3(1024), lds, st, sc, ss, mxp,  \
                                ms, vc, loff, window, (uint32_t)kv_dim, (uint32_t)seq_len, (uint32_t)scs, att, out,  \
@@ -3098,7 +3136,7 @@ hipError_t launch_attention_split_rows(hipStream_t st, const float* q, float* ou
     do {                                                                                                             \
         hipLaunchKernelGGL((k_attn_scores<G, H, false>), g1, dim3(64), 0, st, q, nullptr, nullptr, kcw, vcw, loff,   \
                            windows, nullptr, nullptr, 0, (uint32_t)kv_dim, scale, sc, ss, mxp, ms,                   \
-                           (uint32_t)(n_heads * hs));                                                                \
+                           (uint32_t)(n_heads * hs), nullptr, nullptr, 0.0f);                                        \
         hipLaunchKernelGGL((k_attn_softmax_v_rows<G, H>), g2, dim3(G * H < 64 ? 64 : G * H), lds, st, sc, ss, mxp, ms, \
                            vc, loff, windows, (uint32_t)kv_dim, (uint32_t)seq_len, (uint32_t)scs, (uint32_t)n_heads,  \
                            keep_att ? att : nullptr, out, qo, so, ho);                                                \

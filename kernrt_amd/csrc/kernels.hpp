@@ -127,8 +127,9 @@ hipError_t launch_attention_mx(hipStream_t st, const float* q, float* out, float
                                size_t seq_len, float scale, int8_t* qo, float* so, uint16_t* ho, float* scratch,
                                bool keep_att = true);
 // Decode attention of one row in two launches (scores by 64-row chunks with
-// RoPE and the kv_write of k/v folded in, then softmax + V by head slices of
-// 4 dims); `scratch` holds
+// RoPE and the kv_write of k/v folded in, and the per-head q / k RMSNorm
+// where qnw / knw are given, then softmax + V by head slices of 4 dims);
+// `scratch` holds
 // attention_split_scratch(n_heads, seq_len) floats.
 bool attention_split_ok(size_t max_count, size_t kv_mul, size_t hs);
 // launch_attention_split_rows's geometry check (k_attn_softmax_v_rows).
@@ -138,7 +139,8 @@ hipError_t launch_attention_split(hipStream_t st, const float* q, const float* k
                                   float* att, float* kc, float* vc, size_t layer, const DevWindow* window,
                                   const uint32_t* pos, const float2* table, int interleaved, size_t max_count,
                                   size_t n_heads, size_t kv_mul, size_t hs, size_t kv_dim, size_t seq_len,
-                                  float scale, float* scratch);
+                                  float scale, float* scratch, const float* qnw = nullptr,
+                                  const float* knw = nullptr, float eps = 0.0f);
 // The same two launches for many rows with windows of their own (batched
 // decode): q rows already rotated, keys already in the cache; `scratch`
 // holds n_rows * attention_split_scratch(n_heads, seq_len) floats. keep_att

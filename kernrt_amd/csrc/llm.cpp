@@ -213,18 +213,19 @@ int decode_step_fused(krl_model* m, size_t token, size_t pos, bool dev, size_t c
             int qkv[3] = {KR_PROJ_Q, KR_PROJ_K, KR_PROJ_V};
             kr_buf ys[3] = {m->q, m->k, m->v};
             TRY(norm_then(pending, n.att, l, qkv, ys, 3));
-            if (n.has_q && n.has_k) {
-                KRC(m, kri::qk_norm_pair(b, m->q, m->k, 1, g.q_dim, g.kv_dim, g.hs, n.q, n.k, g.eps));
-            } else {
-                if (n.has_q) KRC(m, kr_qk_norm(b, m->q, 1, g.q_dim, g.hs, n.q, g.eps));
-                if (n.has_k) KRC(m, kr_qk_norm(b, m->k, 1, g.kv_dim, g.hs, n.k, g.eps));
-            }
             if (split && pro) {
-                // rope + kv_write + attention in two launches; O quantizes its input
+                // q/k norms + rope + kv_write + attention in two launches; O quantizes its input
                 KRC(m, kri::rope_attention(b, m->q, m->k, m->v, m->attn, m->att, l, pos, dev ? s : nullptr, &g.as,
-                                           &g.rs, wmax));
+                                           &g.rs, wmax, n.has_q ? n.q : KR_NO_BUF, n.has_k ? n.k : KR_NO_BUF,
+                                           g.eps));
                 KRC(m, kri::quant_project(b, l, KR_PROJ_O, m->attn, m->o, g.q_dim));
             } else {
+                if (n.has_q && n.has_k) {
+                    KRC(m, kri::qk_norm_pair(b, m->q, m->k, 1, g.q_dim, g.kv_dim, g.hs, n.q, n.k, g.eps));
+                } else {
+                    if (n.has_q) KRC(m, kr_qk_norm(b, m->q, 1, g.q_dim, g.hs, n.q, g.eps));
+                    if (n.has_k) KRC(m, kr_qk_norm(b, m->k, 1, g.kv_dim, g.hs, n.k, g.eps));
+                }
                 KRC(m, kri::rope_kv(b, m->q, m->k, m->v, g.q_dim, g.kv_dim, 1, dev ? nullptr : positions,
                                     dev ? nullptr : positions, dev ? s + 2 : nullptr, l, &g.rs));
                 if (g.hs % 32 == 0) {

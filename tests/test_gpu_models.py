@@ -372,6 +372,27 @@ def test_long_prefill_with_qk_norm(n_heads, n_kv, interleaved):
         assert_bits_equal(gpu.forward(9 + t, 1150 + t), cpu.forward(9 + t, 1150 + t), f"decode at {1150 + t}")
 
 
+@pytest.mark.parametrize("n_heads,n_kv,hs,interleaved,storage",
+                         [(16, 8, 128, False, "q8_0x4"), (6, 2, 64, True, "q8_0"), (8, 8, 64, False, "q8_0x4")])
+def test_decode_with_qk_norm_in_the_scores_launch(n_heads, n_kv, hs, interleaved, storage):
+    # the per-head q/k RMSNorm runs inside the decode scores launch: each
+    # 64-row chunk's workgroup normalizes its query heads and the new key
+    # before the rotation; eager steps, then a captured greedy generation,
+    # over windows across 64-row chunks
+    c = O.Config(dim=n_heads * hs, hidden_dim=128, n_layers=2, n_heads=n_heads, n_kv_heads=n_kv, vocab_size=64,
+                 seq_len=400, rms_eps=1e-6, rope_theta=1_000_000.0, rope_interleaved=interleaved, head_dim=hs)
+    ow = gaussian_weights(c, storage, seed=hs + n_heads, qk_norm=True, norms="uniform")
+    prompt = [(i * 7 + 2) % c.vocab_size for i in range(130)]
+    gpu, cpu = gpu_model(c, ow), O.Model(c, ow, "cpu")
+    assert_bits_equal(gpu.prefill(prompt, 0), cpu.prefill(prompt, 0), "prefill")
+    for t in range(3):
+        p = len(prompt) + t
+        assert_bits_equal(gpu.forward(5 + t, p), cpu.forward(5 + t, p), f"decode at {p}")
+    pos = len(prompt) + 3
+    got = gpu.generate_greedy(11, pos, 40, use_graph=True)
+    assert list(got) == _oracle_greedy(cpu, 11, pos, 40)
+
+
 def test_greedy_graph_per_window_bucket():
     # The captured step is sized for a window bucket (a power of two from 512
     # covering the generation): three query heads per KV head on a 4100-slot

@@ -1931,7 +1931,7 @@ __global__ __launch_bounds__(512) void k_attention_fast(
 // the lane that owns the row: one lane per row reading its own 16-byte
 // pieces spreads every load over 64 cache lines and streams at about two
 // thirds of the rate of the same bytes read this way.
-template <int G, int HS, bool ROPE>
+template <int G, int HS, bool ROPE, bool NORM = false>
 __global__ __launch_bounds__(64) void k_attn_scores(const float* __restrict__ q, const float* __restrict__ kin,
                                                     const float* __restrict__ vin, float* __restrict__ kc,
                                                     float* __restrict__ vc, size_t loff,
@@ -1968,6 +1968,31 @@ __global__ __launch_bounds__(64) void k_attn_scores(const float* __restrict__ q,
     const uint32_t ic = live ? i : count - 1;
     const uint32_t pc = lane % P, pr = lane / P;
     const char* kbase = (const char*)(kc + loff + (size_t)hk * HS);
+    // the RoPE operands, loaded ahead of the key rows so that their latency
+    // overlaps the keys' (global loads complete in issue order): the raw
+    // query heads and new key (element t = lane + 64 u of the G + 1 heads),
+    // their norm weights, and the (cos, sin) of the pairs this lane rotates
+    constexpr uint32_t NX = ROPE ? ((G + 1) * HS + 63) / 64 : 1, NR = ROPE ? ((G + 1) * HALF + 63) / 64 : 1;
+    const float* qh = q + (size_t)row * width + (size_t)hk * G * HS;
+    const bool nrm = ROPE && NORM && (qnw != nullptr || knw != nullptr);  // NORM: the instantiation with the norms
+    float xr[NX], wr[NX];
+    float2 cs[NR];
+    if (ROPE) {
+        const float2* tr = tab + (size_t)pos[0] * HALF;
+#pragma unroll
+        for (uint32_t u = 0; u < NX; u++) {
+            const uint32_t t = lane + 64 * u, hh = t / HS, e = t - hh * HS;
+            const bool in = t < (G + 1) * HS;
+            const float* nw = hh < G ? qnw : knw;
+            xr[u] = in ? (hh < G ? qh[hh * HS + e] : kin[(size_t)hk * HS + e]) : 0.0f;
+            wr[u] = NORM && in && nw != nullptr ? nw[e] : 1.0f;
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < NR; u++) {
+            const uint32_t t = lane + 64 * u, hh = t / HALF;
+            cs[u] = t < (G + 1) * HALF ? tr[t - hh * HALF] : make_float2(0.0f, 0.0f);
+        }
+    }
     v4f kr[F];
 #pragma unroll
     for (uint32_t h = 0; h < NP; h++) {
@@ -1977,53 +2002,57 @@ __global__ __launch_bounds__(64) void k_attn_scores(const float* __restrict__ q,
             kr[h * P + u] = *(const v4f*)(kbase + ((size_t)win_slot(w, n_shared, ri) * kv_dim + 4 * (P * h + pc)) * 4);
         }
     }
-    const float* qh = q + (size_t)row * width + (size_t)hk * G * HS;
     if (!ROPE) {  // q is already rotated, and every key is in the cache
         for (uint32_t t = lane; t < G * F; t += 64) ((float4*)qs)[t] = ((const float4*)qh)[t];
     }
-    // per-head RMSNorm of the query heads (qnw) and of the new key (knw)
-    // before the rotation (cpu.rs:647-661, k_qk_norm's arithmetic): the
-    // squares into the key tile (free until the first phase), one lane per
-    // head runs the serial sum, every lane scales the values in LDS
-    const bool nrm = ROPE && (qnw != nullptr || knw != nullptr);
-    if (nrm) {
+    if (ROPE) {
+        // the raw heads to LDS, with the squares into the key tile (free
+        // until the first phase) for the per-head RMSNorm of the query heads
+        // (qnw) and of the new key (knw) before the rotation (cpu.rs:647-661,
+        // k_qk_norm's arithmetic: one lane per head runs the serial sum);
+        // LDS-only barriers, so the key rows stay in flight
         float* sq = (float*)kt;
-        for (uint32_t t = lane; t < (G + 1) * HS; t += 64) {
-            const uint32_t hh = t / HS, i = t - hh * HS;
-            const float x = hh < G ? qh[hh * HS + i] : kin[(size_t)hk * HS + i];
-            (hh < G ? qs + hh * HS : kn)[i] = x;
-            sq[t] = x * x;
-        }
-        __syncthreads();
-        if (lane <= (uint32_t)G) {
-            float sc1 = 1.0f;
-            if (lane < (uint32_t)G ? qnw != nullptr : knw != nullptr) {
-                float ssq = chain_sum(sq + lane * HS, HS);
-                ssq = div_rn(ssq, (float)HS);
-                ssq += eps;
-                sc1 = div_rn(1.0f, sqrt_rn(ssq));
+#pragma unroll
+        for (uint32_t u = 0; u < NX; u++) {
+            const uint32_t t = lane + 64 * u, hh = t / HS, e = t - hh * HS;
+            if (t < (G + 1) * HS) {
+                (hh < G ? qs + hh * HS : kn)[e] = xr[u];
+                if (nrm) sq[t] = xr[u] * xr[u];
             }
-            s_nsc[lane] = sc1;
         }
-        __syncthreads();
-        for (uint32_t t = lane; t < (G + 1) * HS; t += 64) {
-            const uint32_t hh = t / HS, i = t - hh * HS;
-            const float* nw = hh < G ? qnw : knw;
-            float* d = hh < G ? qs + hh * HS : kn;
-            if (nw) d[i] = nw[i] * (s_nsc[hh] * d[i]);
+        lds_barrier();
+        if (nrm) {
+            if (lane <= (uint32_t)G) {
+                float sc1 = 1.0f;
+                if (lane < (uint32_t)G ? qnw != nullptr : knw != nullptr) {
+                    float ssq = chain_sum(sq + lane * HS, HS);
+                    ssq = div_rn(ssq, (float)HS);
+                    ssq += eps;
+                    sc1 = div_rn(1.0f, sqrt_rn(ssq));
+                }
+                s_nsc[lane] = sc1;
+            }
+            lds_barrier();
+#pragma unroll
+            for (uint32_t u = 0; u < NX; u++) {
+                const uint32_t t = lane + 64 * u, hh = t / HS, e = t - hh * HS;
+                if (t < (G + 1) * HS && (hh < G ? qnw != nullptr : knw != nullptr))
+                    (hh < G ? qs + hh * HS : kn)[e] = wr[u] * (s_nsc[hh] * xr[u]);
+            }
+            lds_barrier();
         }
-        __syncthreads();
-    }
-    const float2* tr = ROPE ? tab + (size_t)pos[0] * HALF : tab;
-    for (uint32_t t = lane; ROPE && t < (G + 1) * HALF; t += 64) {
-        const uint32_t hh = t / HALF, i = t - hh * HALF;
-        float* dst = hh < G ? qs + hh * HS : kn;
-        const float* src = nrm ? dst : hh < G ? qh + hh * HS : kin + (size_t)hk * HS;
-        const uint32_t i0 = interleaved ? 2 * i : i, i1 = interleaved ? 2 * i + 1 : i + HALF;
-        const float2 cs = tr[i];
-        const float a = src[i0], b = src[i1];
-        dst[i0] = a * cs.x - b * cs.y;
-        dst[i1] = a * cs.y + b * cs.x;
+        // the rotation in place: one lane reads and writes both values of a pair
+#pragma unroll
+        for (uint32_t u = 0; u < NR; u++) {
+            const uint32_t t = lane + 64 * u, hh = t / HALF, e = t - hh * HALF;
+            if (t < (G + 1) * HALF) {
+                float* dst = hh < G ? qs + hh * HS : kn;
+                const uint32_t i0 = interleaved ? 2 * e : e, i1 = interleaved ? 2 * e + 1 : e + HALF;
+                const float a = dst[i0], b = dst[i1];
+                dst[i0] = a * cs[u].x - b * cs[u].y;
+                dst[i1] = a * cs[u].y + b * cs[u].x;
+            }
+        }
     }
     __syncthreads();
     if (ROPE && chunk == 0) {
@@ -2324,9 +2353,14 @@ hipError_t launch_attention_split(hipStream_t st, const float* q, const float* k
     const dim3 g1((unsigned)n_kv, (unsigned)nchunks), g2((unsigned)(n_kv * (hs / kAttnSplitDW)));
 #define KR_SPLIT(G, H)                                                                                              \
     do {                                                                                                            \
-        hipLaunchKernelGGL((k_attn_scores<G, H, true>), g1, dim3(64), 0, st, q, k, v, kc, vc, loff, window, pos,    \
-                           table, interleaved, (uint32_t)kv_dim, scale, sc, ss, mxp, ms, (uint32_t)(n_heads * hs),  \
-                           qnw, knw, eps);                                                                          \
+        if (qnw || knw)                                                                                             \
+            hipLaunchKernelGGL((k_attn_scores<G, H, true, true>), g1, dim3(64), 0, st, q, k, v, kc, vc, loff, window, \
+                               pos, table, interleaved, (uint32_t)kv_dim, scale, sc, ss, mxp, ms,                   \
+                               (uint32_t)(n_heads * hs), qnw, knw, eps);                                            \
+        else                                                                                                        \
+            hipLaunchKernelGGL((k_attn_scores<G, H, true>), g1, dim3(64), 0, st, q, k, v, kc, vc, loff, window, pos, \
+                               table, interleaved, (uint32_t)kv_dim, scale, sc, ss, mxp, ms, (uint32_t)(n_heads * hs), \
+                               nullptr, nullptr, 0.0f);                                                             \
         if (max_count > 64 * 64)                                                                                    \
             hipLaunchKernelGGL((k_attn_softmax_v<G, H, kAttnSplitDW, true>), g2, dim3(1024), lds, st, sc, ss, mxp,  \
                                ms, vc, loff, window, (uint32_t)kv_dim, (uint32_t)seq_len, (uint32_t)scs, att, out,  \
